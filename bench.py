@@ -1,0 +1,264 @@
+"""Benchmark of the table-search path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one MoE layer of the table path on the config-2 workload of
+BASELINE.json (Qwen3-VL-30B-A3B-shaped prefill: N=4096 tokens, hidden 2048
+bf16, PCA 2048x128 per modality, C=8192 centroids with cached outputs
+8192x2048, router 128 experts top-8, keep_rate 0.6, 70 % near / 30 % outlier
+tokens): router top-k softmax -> projection -> nearest centroid -> keep-rate
+selection -> gather + combine + residual.  Inputs are resident in HBM before
+timing; steps rotate over replicas of the workload totalling > 2x the 256 MB
+Infinity Cache so reads come from HBM.
+
+Prints ONE JSON line: tokens/s per MoE layer (value), per-stage device times
+from HIP events recorded on the stream the kernels run on, the roofline of the
+dominant kernel, the decode (N=32, C=16384, top-4) layer, and the reference
+path restated on the host CPU (oracle, numpy fp32) as the CPU baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "tablemoe-sc26_amd"))
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "table-search tokens/s per MoE layer (N=4096 prefill, N=32 decode) + HBM GB/s"
+N_REPLICAS = 4
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _stage_bytes(cfg, n, n_keep, nn, top_k):
+    """Algorithmic HBM bytes of each stage of one layer (bf16 = 2 bytes)."""
+    H, d, C, E = cfg["hidden"], cfg["dim"], cfg["n_cent"], cfg["n_experts"]
+    n_reuse = n - n_keep
+    return {
+        "router": n * E * 4 + n * top_k * (4 + 8),
+        "project": n * H * 2 + 2 * H * d * 2 + 2 * d * 2 + n * d * 2 + n * 4,
+        "search": n * d * 2 + C * d * 2 + C * 4 + n * 4 + n * nn * (4 + 8),
+        "keep": n * nn * 4 + n,
+        "combine": (n + n_keep * top_k * 4 + n_reuse * nn * (8 + (4 if nn > 1 else 0))
+                    + n_reuse * nn * H * 2 + n_keep * top_k * H * 2 + 2 * n * H * 2),
+    }
+
+
+def run_layer_bench(cfg_id, steps, warmup, n=None):
+    import torch
+
+    from table_moe.cache_engine import GlobalTable
+    from table_moe.synth import make_workload
+
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    wl = make_workload(cfg_id, n=n)
+    log(f"config {cfg_id}: workload generated in {time.time() - t0:.1f}s")
+    cfg = wl.cfg
+    base = wl.to(dev)
+    reps = [base] + [base.to(dev) for _ in range(N_REPLICAS - 1)]
+    for r in reps[1:]:
+        for k, v in r.__dict__.items():
+            if isinstance(v, torch.Tensor):
+                setattr(r, k, v.clone())
+    tables = [GlobalTable(r.centroids, r.values, (r.proj_vis, r.bias_vis), (r.proj_txt, r.bias_txt)) for r in reps]
+    outs = [torch.empty_like(r.residual) for r in reps]
+    topk, nn, kr = cfg["router_top_k"], cfg["n_nearest"], cfg["keep_rate"]
+    N = cfg["n"]
+
+    stage_names = ["router", "project", "search", "keep", "combine"]
+
+    def step(i, ev=None):
+        r, t, o = reps[i % N_REPLICAS], tables[i % N_REPLICAS], outs[i % N_REPLICAS]
+        if ev is not None:
+            ev[0].record()
+        w, _ = t.route(r.logits, topk)
+        if ev is not None:
+            ev[1].record()
+        q, qn = t.project(r.x, r.is_vision)
+        if ev is not None:
+            ev[2].record()
+        dist, idx = t.search(q, nn, qn)
+        if ev is not None:
+            ev[3].record()
+        keep = t.keep_select(dist[:, 0], t.keep_count(N, kr))
+        if ev is not None:
+            ev[4].record()
+        t.gather_combine(keep, r.slot_out, w, idx, dist, r.residual, o)
+        if ev is not None:
+            ev[5].record()
+        return keep
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    stage_ms = {s: 0.0 for s in stage_names}
+    for e in evs:
+        for j, s in enumerate(stage_names):
+            stage_ms[s] += e[j].elapsed_time(e[j + 1])
+    stage_us = {s: 1000.0 * v / steps for s, v in stage_ms.items()}
+    keep = step(0)
+    torch.cuda.synchronize()
+    n_keep = int(keep.sum().item())
+    return dict(cfg=cfg, wl=wl, elapsed=elapsed, ms_per_step=1000.0 * elapsed / steps, stage_us=stage_us,
+                n_keep=n_keep, bytes=_stage_bytes(cfg, N, n_keep, nn, topk))
+
+
+def cpu_baseline(wl, budget_s=12.0):
+    """The reference op sequence restated in numpy fp32 (oracle), on a bounded sample."""
+    import numpy as np
+
+    from oracle import tm_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info, threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_info = threadpool_limits = None
+    f = lambda t: t.detach().cpu().float().numpy()  # noqa: E731
+    cfg = wl.cfg
+    n_sample = min(cfg["n"], 1024)
+    args = (f(wl.x[:n_sample]), wl.is_vision[:n_sample].cpu().numpy(), (f(wl.proj_vis), f(wl.bias_vis)),
+            (f(wl.proj_txt), f(wl.bias_txt)), f(wl.centroids), f(wl.values), f(wl.logits[:n_sample]),
+            f(wl.slot_out[:n_sample]), f(wl.residual[:n_sample]), cfg["router_top_k"], cfg["n_nearest"],
+            cfg["keep_rate"])
+    cores = len(os.sched_getaffinity(0))
+    threads = cores
+    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
+    try:
+        O.layer_forward_g_fp32(*args)  # warm-up
+        times = []
+        t_all = time.perf_counter()
+        while time.perf_counter() - t_all < budget_s or len(times) < 3:
+            t0 = time.perf_counter()
+            O.layer_forward_g_fp32(*args)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 50:
+                break
+        if threadpool_info:
+            info = threadpool_info()
+            if info:
+                threads = max(int(i.get("num_threads", 1)) for i in info)
+    finally:
+        if ctx is not None:
+            ctx.unregister() if hasattr(ctx, "unregister") else None
+    med = float(np.median(times))
+    return {
+        "value": n_sample / med,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n_sample} tokens of the config-2 layer (all C={cfg['n_cent']} centroids), "
+                  f"median of {len(times)} runs, numpy fp32, {threads} threads on {cores} host cores",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the table-search path runs on a single device in this build "
+              "(multi-GPU sharding is a design note only); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from table_moe import _native
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    _native.load()
+    torch.cuda.set_device(0)
+    log(f"device {torch.cuda.get_device_name(0)}")
+
+    pre = run_layer_bench(2, args.steps, args.warmup)
+    log(f"prefill: {pre['ms_per_step'] * 1000:.1f} us/layer, stages {json.dumps(pre['stage_us'])}")
+    dec = run_layer_bench(3, args.steps, args.warmup, n=32)
+    log(f"decode N=32: {dec['ms_per_step'] * 1000:.1f} us/layer, stages {json.dumps(dec['stage_us'])}")
+
+    cfg = pre["cfg"]
+    N, C, d = cfg["n"], cfg["n_cent"], cfg["dim"]
+    st, by = pre["stage_us"], pre["bytes"]
+    # dominant kernel and its roofline
+    dom = max(st, key=st.get)
+    if dom == "search":
+        flops = 2.0 * N * C * d
+        achieved = flops / (st[dom] * 1e-6) / 1e12
+        roof = {"kernel": "tm_search_global (search + merge launches)", "bound": "mfma", "achieved": achieved,
+                "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None}
+    else:
+        achieved = by[dom] / (st[dom] * 1e-6) / 1e9
+        roof = {"kernel": {"combine": "tm_gather_combine", "project": "tm_project", "router": "tm_topk_softmax",
+                           "keep": "tm_keep_select"}[dom], "bound": "hbm", "achieved": achieved,
+                "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": None}
+    roof["algorithmic_per_launch"] = by[dom] if roof["bound"] == "hbm" else 2.0 * N * C * d
+    roof["avg_launch_us"] = st[dom]
+
+    total_bytes = sum(by.values())
+    ds = dec["stage_us"]
+    search_tflops = 2.0 * N * C * d / (st["search"] * 1e-6) / 1e12
+    result = {
+        "metric": METRIC,
+        "value": N / (pre["ms_per_step"] * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": pre["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "config 2: Qwen3-VL-30B-A3B-shaped single MoE layer, prefill N=4096 (3584 vision + 512 "
+                        "text), hidden 2048, PCA 2048x128 per modality, C=8192 centroids, cached outputs "
+                        "8192x2048, router 128 experts top-8, top-1 search, keep_rate 0.6, 70% near / 30% outliers",
+            "tokens": N, "centroids": C, "pca_dim": d, "hidden": cfg["hidden"], "n_keep": pre["n_keep"],
+            "replicas": N_REPLICAS,
+        },
+        "stages_us": {k: round(v, 2) for k, v in st.items()},
+        "layer_hbm_GBps": total_bytes / (sum(st.values()) * 1e-6) / 1e9,
+        "search_mfma_tflops": search_tflops,
+        "search_mfma_frac": search_tflops / BF16_PEAK_TFLOPS,
+        "roofline": roof,
+        "decode": {
+            "workload": "config 3: N=32 text tokens, C=16384 x 128 bf16, cached outputs 16384x2048, top-4 "
+                        "inverse-distance blend, keep_rate 0.6",
+            "us_per_layer": dec["ms_per_step"] * 1000.0,
+            "tokens_per_s": 32 / (dec["ms_per_step"] * 1e-3),
+            "stages_us": {k: round(v, 2) for k, v in ds.items()},
+            "search_hbm_GBps": dec["bytes"]["search"] / (ds["search"] * 1e-6) / 1e9,
+            "layer_hbm_GBps": sum(dec["bytes"].values()) / (sum(ds.values()) * 1e-6) / 1e9,
+        },
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(pre["wl"])
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

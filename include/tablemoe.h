@@ -1,0 +1,303 @@
+/*
+ * tablemoe.h -- C ABI of the MI355X (gfx950) table-search path of TableMoE.
+ *
+ * Every entry point takes device pointers, element counts, element strides
+ * and a HIP stream (hipStream_t passed as void*; NULL = the legacy default
+ * stream), enqueues its kernels on that stream and returns without a host
+ * synchronisation.  Nothing here allocates device memory: outputs and
+ * workspaces are caller-provided.  No global mutable state; calls on
+ * different streams are independent as long as their buffers are.
+ *
+ * Return value: TM_OK or one of the TM_E* codes below; tm_last_error()
+ * gives a message for the calling thread's last failure.
+ *
+ * Booleans are bytes (0/1), as torch.bool.  Indices are int64 (torch.long).
+ * "dtype" selects the element type of the model-dtype operands:
+ * TM_DT_F32, TM_DT_F16 or TM_DT_BF16.
+ *
+ * Two families of entry points:
+ *   - reference semantics ("mode R"): the per-(expert, modality) tables of
+ *     table_moe/cache_engine (keys [E,2,K,d], values [E,2,K,H]), gated
+ *     dot/cosine search, expert keep masks, slot combine, online window.
+ *   - global-table semantics ("mode G"): one table of C centroids [C,d] with
+ *     cached outputs [C,H]; L2 top-k search, token keep-by-distance, gather +
+ *     combine + residual.  These serve the north-star configs; the reference
+ *     has no counterpart beyond the reference entry points they generalise,
+ *     cited on each.
+ */
+#ifndef TABLEMOE_H
+#define TABLEMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define TM_OK 0
+#define TM_EINVAL_SHAPE 1 /* a size or stride is out of range             */
+#define TM_EINVAL_DTYPE 2 /* unsupported dtype tag for this entry point   */
+#define TM_EINVAL_ARG 3   /* a required pointer is NULL, bad enum value   */
+#define TM_EHIP 4         /* a HIP runtime call failed (launch error)     */
+#define TM_EWORKSPACE 5   /* workspace missing or too small               */
+
+/* ---- dtype tags ------------------------------------------------------ */
+#define TM_DT_F32 0
+#define TM_DT_F16 1
+#define TM_DT_BF16 2
+
+/* ---- hit comparators (max score vs threshold) ------------------------ */
+#define TM_CMP_GE 0 /* hit = max >= threshold */
+#define TM_CMP_GT 1 /* hit = max >  threshold */
+
+/* ---- metrics of the global table ------------------------------------- */
+#define TM_METRIC_L2 0  /* ascending ||q - c||^2 */
+#define TM_METRIC_DOT 1 /* descending q . c      */
+
+/* ---- renormalisation targets ----------------------------------------- */
+#define TM_TARGET_ONE 0      /* surviving weights rescaled to sum 1           */
+#define TM_TARGET_ORIG_SUM 1 /* rescaled to the row's original sum (DeepSeek) */
+#define TM_TARGET_GIVEN 2    /* rescaled to a caller-given per-row target     */
+
+typedef void *tm_stream_t;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int tm_version(void);
+/* Static string naming a status code. */
+const char *tm_status_string(int status);
+/* Message of the calling thread's last failing call ("" if none). */
+const char *tm_last_error(void);
+
+/* ======================================================================
+ * a1 -- router softmax + top-k.
+ * Replaces qwen_topk_softmax (table_moe/ops/qwen_topk_softmax.py:122-154;
+ * binding table_moe/ops/csrc/qwen_topk_softmax/qwen_topk_softmax_bindings.cpp:5-23).
+ * logits [n_tokens, n_experts] fp32 (row stride ld_logits); outputs
+ * [n_tokens, top_k] contiguous: fp32 softmax probabilities in descending
+ * order (ties -> lower expert id) and int64 expert ids.  renormalize != 0
+ * divides the k weights by their sum (clamped to 1e-20), as normalize_topk.
+ * Limits: 1 <= top_k <= min(n_experts, 32), n_experts <= 4096.
+ * ====================================================================== */
+int tm_topk_softmax(const float *logits, int64_t n_tokens, int32_t n_experts, int64_t ld_logits,
+                    int32_t top_k, int32_t renormalize, float *out_weights, int64_t *out_ids,
+                    tm_stream_t stream);
+
+/* ======================================================================
+ * a4 -- projection of hidden states into the PCA space.
+ * Replaces VectorSearchEngine._project_queries_into + _normalize_last_dim
+ * (table_moe/cache_engine/search.py:476-498, :12-21).
+ * q[b] = dtype(x[b] @ P_m + bias_m), m = vision if is_vision[b] else text
+ * (is_vision NULL: all vision; proj_txt/bias_txt NULL: the vision pair is
+ * shared).  normalize != 0: q = dtype(fp32(q / dtype(||q||))) and rows with
+ * ||q|| <= eps become 0.  x [n, hidden] (row stride ld_x), bias_m [dim],
+ * P_m element (h, j) at P_m[h*ps_h + j*ps_d] with ps_d == 1 (the reference's
+ * row-major [hidden, dim]) or ps_h == 1 (a k-contiguous transposed copy),
+ * q_out [n, dim] (row stride ld_q).  q_sqnorm (nullable) receives
+ * sum_j q[b,j]^2 in fp32 of the stored (rounded) q.
+ * Limits: dim <= 256; hidden % 8 == 0 and dim in {16, 32, 64, 128, 256} for
+ * F16/BF16 (MFMA path).
+ * ====================================================================== */
+int tm_project(int32_t dtype, const void *x, int64_t n_tokens, int32_t hidden, int64_t ld_x,
+               const uint8_t *is_vision, const void *proj_vis, const void *bias_vis,
+               const void *proj_txt, const void *bias_txt, int64_t ps_h, int64_t ps_d,
+               int32_t dim, int32_t normalize, float eps, void *q_out, int64_t ld_q, float *q_sqnorm,
+               tm_stream_t stream);
+
+/* ======================================================================
+ * a5/a6/a7 -- gated search of each reused (token, slot) in the table of its
+ * routed expert and modality.
+ * Replaces the prefill/decode offline search of VectorSearchEngine
+ * (table_moe/cache_engine/search.py:515-602 cosine, :661-697 dot, Triton
+ * kernels :35-256).
+ * For b < n_tokens, s < top_k: searched = reuse[b,s] (reuse NULL: all) and
+ * s >= col_offset and 0 <= sel[b,s] < n_experts.  If searched:
+ * score_c = q[b] . keys[sel[b,s], m(b), c] (fp32 accumulation), max over
+ * c < n_centroids (first index on ties), hit = max >= thr (TM_CMP_GE) or
+ * > thr (TM_CMP_GT), thr = thr_vision or thr_text by modality.
+ * Writes every (b, s): (1, argmax) on a hit, (0, 0) otherwise.
+ * keys element strides (ks_e, ks_m, ks_c), unit stride along dim.
+ * Limits: dim <= 256, n_centroids <= 65536.
+ * ====================================================================== */
+int tm_search_gated(int32_t dtype, const void *q_low, int64_t n_tokens, int64_t ld_q,
+                    const void *keys, int64_t n_experts, int64_t n_centroids, int32_t dim,
+                    int64_t ks_e, int64_t ks_m, int64_t ks_c, const int64_t *sel, int32_t top_k,
+                    int64_t ss_b, int64_t ss_s, const uint8_t *is_vision, const uint8_t *reuse,
+                    int64_t rs_b, int64_t rs_s, int32_t col_offset, float thr_vision,
+                    float thr_text, int32_t cmp, uint8_t *out_hit, int64_t *out_idx,
+                    int64_t os_b, int64_t os_s, tm_stream_t stream);
+
+/* ======================================================================
+ * a8 -- decode hybrid search: online window first, offline table second.
+ * Replaces VectorSearchEngine.search_decode_hybrid /
+ * search_decode_hybrid_bs1_into (table_moe/cache_engine/search.py:839-954,
+ * :987-1105; Triton kernel :258-385; fallback :778-806).
+ * Slots s >= keep_k of each token b are searched.  Online (n_online_valid > 0):
+ * score_j = x[b] . online_keys[j] for j < n_online_valid, (max, first argmax j*);
+ * if max > 0: on_idx[b] = j*, and slot s is an online hit when sel[b,s] is
+ * among online_ids[j*, 0:online_topk] (on_slot = first matching position).
+ * Slots that are not online hits are searched offline with the raw
+ * projection q = dtype(x @ P_m + bias_m) against keys with hit = max >= 0.
+ * All outputs are written for every (b, s): on_hit/off_hit 0, on_slot/off_idx
+ * 0, on_idx -1 where nothing was found.
+ * workspace: >= n_tokens * dim * sizeof(dtype) bytes (the projected queries).
+ * Limits: n_online_valid <= 1024, online_topk <= 64, dim <= 256.
+ * ====================================================================== */
+int tm_search_hybrid(int32_t dtype, const void *x, int64_t n_tokens, int32_t hidden, int64_t ld_x,
+                     const uint8_t *is_vision, const void *proj_vis, const void *bias_vis,
+                     const void *proj_txt, const void *bias_txt, int64_t ps_h, int64_t ps_d,
+                     int32_t dim, const void *online_keys, int64_t ld_online, int32_t n_online_valid,
+                     const int64_t *online_ids, int32_t online_topk, int64_t ld_online_ids,
+                     const void *keys, int64_t n_experts, int64_t n_centroids, int64_t ks_e,
+                     int64_t ks_m, int64_t ks_c, const int64_t *sel, int32_t top_k, int64_t ss_b,
+                     int64_t ss_s, int32_t keep_k, uint8_t *on_hit, int64_t *on_idx,
+                     uint8_t *off_hit, int64_t *off_idx, int64_t *on_slot, int64_t os_b,
+                     int64_t os_s, void *workspace, size_t workspace_bytes, tm_stream_t stream);
+
+/* ======================================================================
+ * a3 -- keep masks.
+ * tm_fixed_keep_mask replaces build_fixed_keep_mask / build_decode_keep_mask
+ * (table_moe/skip/pruning.py:4-15, :51-52): out[b,s] = s < keep_k.
+ * tm_expert_keep_mask replaces build_prefill_keep_mask
+ * (table_moe/skip/pruning.py:18-48): score[e] = sum of attn[b]*w[b,s] over
+ * slots routed to e (attn NULL: w[b,s]/n_tokens), summed in a fixed order;
+ * the max(1, int(n_active*keep_rate)) highest-scoring activated experts are
+ * kept (equal scores: lower id first); out[b,s] = kept(sel[b,s]).
+ * workspace: >= tm_expert_keep_mask_workspace_size(n_tokens, n_experts).
+ * Limits: n_experts <= 1024.
+ * ====================================================================== */
+int tm_fixed_keep_mask(int64_t n_tokens, int32_t top_k, int32_t keep_k, uint8_t *out,
+                       tm_stream_t stream);
+size_t tm_expert_keep_mask_workspace_size(int64_t n_tokens, int32_t n_experts);
+int tm_expert_keep_mask(const int64_t *sel, const float *weights, const float *attn,
+                        int64_t n_tokens, int32_t top_k, int32_t n_experts, double keep_rate,
+                        uint8_t *out_mask, float *out_expert_scores, void *workspace,
+                        size_t workspace_bytes, tm_stream_t stream);
+
+/* ======================================================================
+ * a11 -- surviving-weight renormalisation.
+ * Replaces renormalize_surviving_weights (table_moe/skip/pruning.py:55-73).
+ * out[b,:] = (w*m) / sum(w*m) * target, 0 for rows whose kept sum is not > 0;
+ * target = 1 (TM_TARGET_ONE), the row's original sum (TM_TARGET_ORIG_SUM) or
+ * target[b * ld_t] (TM_TARGET_GIVEN, dtype of the weights).
+ * Each step rounds to the weights' dtype as the torch ops do.
+ * w [n, k] (row stride ld_w), mask [n, k] (row stride ld_m), out contiguous.
+ * ====================================================================== */
+int tm_renormalize(int32_t dtype, const void *weights, int64_t ld_w, const uint8_t *mask,
+                   int64_t ld_m, int64_t n_tokens, int32_t top_k, int32_t target_mode,
+                   const void *target, int64_t ld_t, void *out, tm_stream_t stream);
+
+/* ======================================================================
+ * a10 -- gather of cached rows.
+ * Replaces HybridStorageManager.gather_values / gather_values_decode_bs1
+ * (table_moe/cache_engine/manager.py:212-228).
+ * out[dst(i)] = values[eids[i], mids[i], cids[i]] (a row of `hidden`
+ * elements), dst(i) = dst_rows[i] (NULL: i).  mids NULL: modality
+ * `modality`.  values element strides (vs_e, vs_m, vs_c), unit along hidden.
+ * out has n_out_rows rows of stride ld_out; a destination outside
+ * [0, n_out_rows) is skipped, a source index out of range zero-fills its row.
+ * ====================================================================== */
+int tm_gather_rows(int32_t dtype, const void *values, int64_t n_experts, int64_t n_centroids,
+                   int32_t hidden, int64_t vs_e, int64_t vs_m, int64_t vs_c, const int64_t *eids,
+                   const int64_t *mids, int32_t modality, const int64_t *cids, int64_t n_rows,
+                   const int64_t *dst_rows, void *out, int64_t n_out_rows, int64_t ld_out,
+                   tm_stream_t stream);
+
+/* ======================================================================
+ * a10+a11 -- fused gather + combine of one MoE layer's slots (reference
+ * semantics), with optional residual.
+ * Fuses the collected-buffer fill and the weighted sum of
+ * QwenMoeWrapperCached.forward (table_moe/models/qwen3_vl_moe/cached_layers.py:
+ * 439-465) and DeepSeekMoeWrapperCached.forward
+ * (table_moe/models/deepseek_vl2/deepseek_layers.py:695-729):
+ * slot (b,s) source = computed[b,s] if compute_mask, else
+ * online_values[on_idx[b], on_slot[b,s]] if on_hit, else
+ * values[sel[b,s], m(b), off_idx[b,s]] if off_hit, else dropped.
+ * Surviving weights renormalised per target_mode (rounded to dtype for
+ * TM_TARGET_ONE, as the reference's .to(dtype)), y = sum_s w~ * source in fp32,
+ * out = dtype(y) or dtype(residual + y).
+ * computed [n, k, hidden] (strides cs_b, cs_s), weights fp32 [n, k]
+ * (row stride ld_w), masks/indices [n, k] with row stride ld_m,
+ * online_values [W, online_topk, hidden] (strides ov_w, ov_s) or NULL.
+ * ====================================================================== */
+int tm_slot_combine(int32_t dtype, int64_t n_tokens, int32_t top_k, int32_t hidden,
+                    const float *weights, int64_t ld_w, const uint8_t *compute_mask,
+                    const void *computed, int64_t cs_b, int64_t cs_s, const uint8_t *off_hit,
+                    const int64_t *off_idx, const int64_t *sel, int64_t ld_m,
+                    const uint8_t *is_vision, const void *values, int64_t n_experts,
+                    int64_t n_centroids, int64_t vs_e, int64_t vs_m, int64_t vs_c,
+                    const uint8_t *on_hit, const int64_t *on_idx, const int64_t *on_slot,
+                    const void *online_values, int64_t n_online, int32_t online_topk,
+                    int64_t ov_w, int64_t ov_s, int32_t target_mode, const void *residual,
+                    int64_t ld_r, void *out, int64_t ld_out, tm_stream_t stream);
+
+/* ======================================================================
+ * a12 -- online window ring-buffer write.
+ * Replaces the copies of HybridStorageManager.update_online_cache /
+ * update_online_cache_bs1 (table_moe/cache_engine/manager.py:89-155).
+ * Row i < n_rows goes to ring row (start + i) % ring_size: keys <- hidden[i],
+ * ids <- ids[i] (-1 where valid[i,s] == 0), values <- outputs[i] (0 where
+ * invalid).  valid NULL: all valid.  n_rows <= ring_size.  The caller keeps
+ * the host-side ring pointer (as the reference does).
+ * ====================================================================== */
+int tm_online_update(int32_t dtype, const void *hidden, int64_t ld_h, const int64_t *ids,
+                     int64_t ld_ids, const void *outputs, int64_t os_b, int64_t os_s,
+                     const uint8_t *valid, int64_t ld_valid, int64_t n_rows, int32_t top_k,
+                     int32_t hidden_dim, int64_t start, int64_t ring_size, void *ring_keys,
+                     int64_t *ring_ids, void *ring_values, tm_stream_t stream);
+
+/* ======================================================================
+ * Mode G (global table) -- north-star kernels (1)-(4).
+ * ====================================================================== */
+
+/* ||c||^2 of each centroid in fp32 (table load time). */
+int tm_centroid_sqnorms(int32_t dtype, const void *cents, int64_t n_cent, int32_t dim,
+                        int64_t ld_c, float *out, tm_stream_t stream);
+
+/* (1)+(2): nearest centroids of each query.
+ * Generalises the offline search (table_moe/cache_engine/search.py:566-602)
+ * to one global table with L2 or dot metric and top-k.
+ * q [n, dim] dtype (row stride ld_q); cents [C, dim] (row stride ld_c);
+ * q_sqnorm (nullable: computed) and c_sqnorm (required for L2) fp32.
+ * L2: dist = ||q||^2 - 2 q.c + ||c||^2 in fp32, ascending; DOT: q.c
+ * descending; ties -> lower centroid index.  out_dist/out_idx [n, top_k].
+ * workspace >= tm_search_global_workspace_size(...).
+ * Limits: dim in {64, 128, 256}, 1 <= top_k <= 8, dtype F16 or BF16. */
+size_t tm_search_global_workspace_size(int64_t n_tokens, int64_t n_cent, int32_t dim,
+                                       int32_t top_k);
+int tm_search_global(int32_t dtype, const void *q, int64_t n_tokens, int64_t ld_q,
+                     const float *q_sqnorm, const void *cents, int64_t n_cent, int64_t ld_c,
+                     const float *c_sqnorm, int32_t dim, int32_t top_k, int32_t metric,
+                     float *out_dist, int64_t *out_idx, void *workspace, size_t workspace_bytes,
+                     tm_stream_t stream);
+
+/* (3): keep the n_keep tokens of largest score (ties -> lower token index);
+ * out_keep[i] = 1 for kept tokens.  tm_keep_count gives
+ * max(1, floor(n * keep_rate)) clamped to n (table_moe/skip/pruning.py:45).
+ * score: fp32 [n] with row stride ld_score (e.g. column 0 of [n, top_k]). */
+int64_t tm_keep_count(int64_t n, double keep_rate);
+size_t tm_keep_select_workspace_size(int64_t n);
+int tm_keep_select(const float *score, int64_t n, int64_t ld_score, int64_t n_keep,
+                   uint8_t *out_keep, void *workspace, size_t workspace_bytes,
+                   tm_stream_t stream);
+
+/* (4): gather + combine + residual.
+ * out[i] = dtype(residual[i] + y_i), y_i = sum_s w~[i,s] * slot_out[i,s]
+ * (w~ = w / sum w) for kept tokens; y_i = sum_j beta_ij values[idx[i,j]]
+ * (beta ~ 1/(dist+1e-6), normalised; beta = 1 for n_nearest = 1) otherwise.
+ * residual NULL: no residual.  slot_out is read only for kept tokens.
+ * Strides: slot_out (so_b, so_s), values ld_v, residual ld_r, out ld_o,
+ * weights ld_w, idx/dist ld_idx. */
+int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden, const uint8_t *keep,
+                      const void *slot_out, int64_t so_b, int64_t so_s, const float *weights,
+                      int64_t ld_w, int32_t top_k, const void *values, int64_t n_cent,
+                      int64_t ld_v, const int64_t *idx, const float *dist, int64_t ld_idx,
+                      int32_t n_nearest, const void *residual, int64_t ld_r, void *out,
+                      int64_t ld_o, tm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TABLEMOE_H */

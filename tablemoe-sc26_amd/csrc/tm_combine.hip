@@ -1,0 +1,374 @@
+// Gather / combine kernels: cached-row gather (a10), the mode-G gather +
+// combine + residual (north-star kernel (4)), the reference-semantics fused
+// slot combine (a10+a11) and the online-window ring write (a12).
+//
+// All are HBM-bound row streams: one workgroup of 256 threads per output row,
+// 16-byte vector loads/stores (8 bf16/fp16 or 2x4 fp32 per thread per step)
+// when every row pointer is 16-byte aligned, element loops otherwise.
+#include "tm_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxSrc = 64;
+
+// y[h] = sum_j coef[j] * src_j[h] (+ residual), for one row, fp32 accumulate.
+template <int DT, bool VEC>
+__device__ __forceinline__ void combine_row(const typename Elem<DT>::T *const *src, const float *coef,
+                                            int nsrc, const typename Elem<DT>::T *residual,
+                                            typename Elem<DT>::T *dst, int hidden) {
+  if constexpr (VEC) {
+    for (int h0 = threadIdx.x * 8; h0 < hidden; h0 += kThreads * 8) {
+      float acc[8];
+      if (residual) {
+        tm_load8<DT>(residual + h0, acc);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+      }
+      for (int j = 0; j < nsrc; ++j) {
+        float v[8];
+        tm_load8<DT>(src[j] + h0, v);
+        const float c = coef[j];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(c, v[i], acc[i]);
+      }
+      tm_store8<DT>(dst + h0, acc);
+    }
+  } else {
+    for (int h = threadIdx.x; h < hidden; h += kThreads) {
+      float acc = residual ? Elem<DT>::to_f(residual[h]) : 0.f;
+      for (int j = 0; j < nsrc; ++j) acc = fmaf(coef[j], Elem<DT>::to_f(src[j][h]), acc);
+      dst[h] = Elem<DT>::from_f(acc);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a10: out[dst(i)] = values[e, m, c]
+// ---------------------------------------------------------------------------
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(
+    const typename Elem<DT>::T *__restrict__ values, int64_t n_exp, int64_t n_cent, int hidden,
+    int64_t vs_e, int64_t vs_m, int64_t vs_c, const int64_t *__restrict__ eids,
+    const int64_t *__restrict__ mids, int modality, const int64_t *__restrict__ cids,
+    const int64_t *__restrict__ dst_rows, typename Elem<DT>::T *__restrict__ out, int64_t n_out,
+    int64_t ld_out) {
+  using T = typename Elem<DT>::T;
+  const int64_t i = blockIdx.x;
+  const int64_t e = eids[i], c = cids[i];
+  const int64_t m = mids ? mids[i] : modality;
+  const int64_t d = dst_rows ? dst_rows[i] : i;
+  if (d < 0 || d >= n_out) return;  // whole workgroup
+  T *dst = out + d * ld_out;
+  const bool ok = e >= 0 && e < n_exp && m >= 0 && m < 2 && c >= 0 && c < n_cent;
+  const T *src = values + e * vs_e + m * vs_m + c * vs_c;
+  const float one = 1.f;
+  combine_row<DT, VEC>(&src, &one, ok ? 1 : 0, nullptr, dst, hidden);
+}
+
+// ---------------------------------------------------------------------------
+// (4) mode G: out[b] = residual[b] + (keep ? sum_s w~ E[b,s] : sum_j beta V[idx])
+// ---------------------------------------------------------------------------
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kThreads) void gather_combine_kernel(
+    int hidden, const uint8_t *__restrict__ keep, const typename Elem<DT>::T *__restrict__ slot_out,
+    int64_t so_b, int64_t so_s, const float *__restrict__ w, int64_t ld_w, int top_k,
+    const typename Elem<DT>::T *__restrict__ values, int64_t n_cent, int64_t ld_v,
+    const int64_t *__restrict__ idx, const float *__restrict__ dist, int64_t ld_idx, int nn,
+    const typename Elem<DT>::T *__restrict__ residual, int64_t ld_r,
+    typename Elem<DT>::T *__restrict__ out, int64_t ld_o) {
+  using T = typename Elem<DT>::T;
+  __shared__ const T *s_src[kMaxSrc];
+  __shared__ float s_coef[kMaxSrc];
+  __shared__ int s_nsrc;
+  const int64_t b = blockIdx.x;
+  if (threadIdx.x == 0) {
+    int ns = 0;
+    if (keep[b]) {
+      float sum = 0.f;
+      for (int s = 0; s < top_k; ++s) sum += w[b * ld_w + s];
+      if (sum > 0.f) {
+        for (int s = 0; s < top_k; ++s) {
+          s_src[ns] = slot_out + b * so_b + s * so_s;
+          s_coef[ns] = w[b * ld_w + s] / sum;
+          ++ns;
+        }
+      }
+    } else if (nn == 1) {
+      const int64_t c = idx[b * ld_idx];
+      if (c >= 0 && c < n_cent) {
+        s_src[0] = values + c * ld_v;
+        s_coef[0] = 1.f;
+        ns = 1;
+      }
+    } else {
+      float inv_sum = 0.f;
+      for (int j = 0; j < nn; ++j) {
+        const int64_t c = idx[b * ld_idx + j];
+        if (c >= 0 && c < n_cent) inv_sum += 1.f / (dist[b * ld_idx + j] + 1e-6f);
+      }
+      for (int j = 0; j < nn; ++j) {
+        const int64_t c = idx[b * ld_idx + j];
+        if (c >= 0 && c < n_cent) {
+          s_src[ns] = values + c * ld_v;
+          s_coef[ns] = (1.f / (dist[b * ld_idx + j] + 1e-6f)) / inv_sum;
+          ++ns;
+        }
+      }
+    }
+    s_nsrc = ns;
+  }
+  __syncthreads();
+  combine_row<DT, VEC>(s_src, s_coef, s_nsrc, residual ? residual + b * ld_r : nullptr, out + b * ld_o,
+                       hidden);
+}
+
+// ---------------------------------------------------------------------------
+// a10+a11 reference-semantics slot combine (cached_layers.py:439-465,
+// deepseek_layers.py:695-729).
+// ---------------------------------------------------------------------------
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kThreads) void slot_combine_kernel(
+    int top_k, int hidden, const float *__restrict__ w, int64_t ld_w,
+    const uint8_t *__restrict__ compute_mask, const typename Elem<DT>::T *__restrict__ computed,
+    int64_t cs_b, int64_t cs_s, const uint8_t *__restrict__ off_hit, const int64_t *__restrict__ off_idx,
+    const int64_t *__restrict__ sel, int64_t ld_m, const uint8_t *__restrict__ is_vision,
+    const typename Elem<DT>::T *__restrict__ values, int64_t n_exp, int64_t n_cent, int64_t vs_e,
+    int64_t vs_m, int64_t vs_c, const uint8_t *__restrict__ on_hit, const int64_t *__restrict__ on_idx,
+    const int64_t *__restrict__ on_slot, const typename Elem<DT>::T *__restrict__ online_values,
+    int64_t n_online, int online_topk, int64_t ov_w, int64_t ov_s, int target_mode,
+    const typename Elem<DT>::T *__restrict__ residual, int64_t ld_r, typename Elem<DT>::T *__restrict__ out,
+    int64_t ld_o) {
+  using T = typename Elem<DT>::T;
+  __shared__ const T *s_src[kMaxSrc];
+  __shared__ float s_coef[kMaxSrc];
+  __shared__ int s_nsrc;
+  const int64_t b = blockIdx.x;
+  if (threadIdx.x == 0) {
+    const T *src[kMaxSrc];
+    float wv[kMaxSrc];
+    float kept = 0.f, full = 0.f;
+    const int m = (is_vision == nullptr || is_vision[b]) ? 0 : 1;
+    for (int s = 0; s < top_k; ++s) {
+      const int64_t mi = b * ld_m + s;
+      const T *p = nullptr;
+      if (off_hit && off_hit[mi]) {
+        const int64_t e = sel[mi], c = off_idx[mi];
+        if (e >= 0 && e < n_exp && c >= 0 && c < n_cent) p = values + e * vs_e + m * vs_m + c * vs_c;
+      } else if (on_hit && on_hit[mi]) {
+        const int64_t r = on_idx[b], j = on_slot[mi];
+        if (r >= 0 && r < n_online && j >= 0 && j < online_topk) p = online_values + r * ov_w + j * ov_s;
+      } else if (compute_mask && compute_mask[mi]) {
+        p = computed + b * cs_b + s * cs_s;
+      }
+      const float ws = w[b * ld_w + s];
+      full += ws;
+      src[s] = p;
+      wv[s] = ws;
+      if (p) kept += ws;
+    }
+    int ns = 0;
+    if (kept > 0.f) {
+      for (int s = 0; s < top_k; ++s) {
+        if (!src[s]) continue;
+        float c = wv[s] / kept;
+        if (target_mode == TM_TARGET_ORIG_SUM) c = c * full;
+        else c = tm_round<DT>(c);
+        s_src[ns] = src[s];
+        s_coef[ns] = c;
+        ++ns;
+      }
+    }
+    s_nsrc = ns;
+  }
+  __syncthreads();
+  combine_row<DT, VEC>(s_src, s_coef, s_nsrc, residual ? residual + b * ld_r : nullptr, out + b * ld_o,
+                       hidden);
+}
+
+// ---------------------------------------------------------------------------
+// a12: ring write of the online window
+// ---------------------------------------------------------------------------
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kThreads) void online_update_kernel(
+    const typename Elem<DT>::T *__restrict__ hidden_in, int64_t ld_h, const int64_t *__restrict__ ids,
+    int64_t ld_ids, const typename Elem<DT>::T *__restrict__ outputs, int64_t os_b, int64_t os_s,
+    const uint8_t *__restrict__ valid, int64_t ld_valid, int top_k, int hidden, int64_t start,
+    int64_t ring_size, typename Elem<DT>::T *__restrict__ ring_keys, int64_t *__restrict__ ring_ids,
+    typename Elem<DT>::T *__restrict__ ring_values) {
+  using T = typename Elem<DT>::T;
+  const int64_t i = blockIdx.x;
+  const int64_t r = (start + i) % ring_size;
+  if (threadIdx.x < top_k) {
+    const int s = threadIdx.x;
+    const bool ok = valid == nullptr || valid[i * ld_valid + s];
+    ring_ids[r * top_k + s] = ok ? ids[i * ld_ids + s] : -1;
+  }
+  const float one = 1.f;
+  const T *hsrc = hidden_in + i * ld_h;
+  combine_row<DT, VEC>(&hsrc, &one, 1, nullptr, ring_keys + r * hidden, hidden);
+  for (int s = 0; s < top_k; ++s) {
+    const bool ok = valid == nullptr || valid[i * ld_valid + s];
+    const T *src = outputs + i * os_b + s * os_s;
+    combine_row<DT, VEC>(&src, &one, ok ? 1 : 0, nullptr, ring_values + (r * top_k + s) * hidden, hidden);
+  }
+}
+
+template <int DT>
+constexpr int64_t vec_elems() { return 16 / Elem<DT>::kBytes; }
+
+// True when rows starting at `base` with element stride `ld` are 16-byte aligned.
+static bool rows_aligned(const void *base, int64_t ld, int elem_bytes) {
+  return base == nullptr || (tm_aligned16(base) && ((ld * elem_bytes) % 16 == 0));
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" int tm_gather_rows(int32_t dtype, const void *values, int64_t n_experts, int64_t n_centroids,
+                              int32_t hidden, int64_t vs_e, int64_t vs_m, int64_t vs_c,
+                              const int64_t *eids, const int64_t *mids, int32_t modality,
+                              const int64_t *cids, int64_t n_rows, const int64_t *dst_rows, void *out,
+                              int64_t n_out_rows, int64_t ld_out, tm_stream_t stream) {
+  TM_REQUIRE(n_rows >= 0 && hidden > 0 && ld_out >= hidden && n_out_rows >= 0, TM_EINVAL_SHAPE,
+             "tm_gather_rows: bad sizes");
+  if (n_rows == 0) return TM_OK;
+  TM_REQUIRE(values && eids && cids && out, TM_EINVAL_ARG, "tm_gather_rows: null pointer");
+  TM_REQUIRE(n_rows < (int64_t)0x7fffffff, TM_EINVAL_SHAPE, "tm_gather_rows: too many rows");
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    using T = typename Elem<DT>::T;
+    const int E = Elem<DT>::kBytes;
+    const bool vec = hidden % 8 == 0 && tm_aligned16(values) && (vs_e * E) % 16 == 0 &&
+                     (vs_m * E) % 16 == 0 && (vs_c * E) % 16 == 0 && rows_aligned(out, ld_out, E);
+    auto V = static_cast<const T *>(values);
+    auto O = static_cast<T *>(out);
+    if (vec)
+      hipLaunchKernelGGL((gather_rows_kernel<DT, true>), dim3((unsigned)n_rows), dim3(kThreads), 0,
+                         tm_hip_stream(stream), V, n_experts, n_centroids, hidden, vs_e, vs_m, vs_c,
+                         eids, mids, modality, cids, dst_rows, O, n_out_rows, ld_out);
+    else
+      hipLaunchKernelGGL((gather_rows_kernel<DT, false>), dim3((unsigned)n_rows), dim3(kThreads), 0,
+                         tm_hip_stream(stream), V, n_experts, n_centroids, hidden, vs_e, vs_m, vs_c,
+                         eids, mids, modality, cids, dst_rows, O, n_out_rows, ld_out);
+    TM_LAUNCH_CHECK("tm_gather_rows");
+    return TM_OK;
+  });
+}
+
+extern "C" int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden, const uint8_t *keep,
+                                 const void *slot_out, int64_t so_b, int64_t so_s, const float *weights,
+                                 int64_t ld_w, int32_t top_k, const void *values, int64_t n_cent,
+                                 int64_t ld_v, const int64_t *idx, const float *dist, int64_t ld_idx,
+                                 int32_t n_nearest, const void *residual, int64_t ld_r, void *out,
+                                 int64_t ld_o, tm_stream_t stream) {
+  TM_REQUIRE(n_tokens >= 0 && hidden > 0 && top_k >= 1 && top_k <= kMaxSrc && n_nearest >= 1 &&
+                 n_nearest <= kMaxSrc && ld_o >= hidden && ld_v >= hidden && ld_w >= top_k &&
+                 ld_idx >= n_nearest,
+             TM_EINVAL_SHAPE, "tm_gather_combine: bad sizes");
+  TM_REQUIRE(n_tokens < (int64_t)0x7fffffff, TM_EINVAL_SHAPE, "tm_gather_combine: too many tokens");
+  if (n_tokens == 0) return TM_OK;
+  TM_REQUIRE(keep && slot_out && weights && values && idx && out && (n_nearest == 1 || dist),
+             TM_EINVAL_ARG, "tm_gather_combine: null pointer");
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    using T = typename Elem<DT>::T;
+    const int E = Elem<DT>::kBytes;
+    const bool vec = hidden % 8 == 0 && tm_aligned16(slot_out) && (so_b * E) % 16 == 0 &&
+                     (so_s * E) % 16 == 0 && rows_aligned(values, ld_v, E) &&
+                     rows_aligned(residual, ld_r, E) && rows_aligned(out, ld_o, E);
+    auto launch = [&](auto vec_tag) {
+      constexpr bool VEC = decltype(vec_tag)::value;
+      hipLaunchKernelGGL((gather_combine_kernel<DT, VEC>), dim3((unsigned)n_tokens), dim3(kThreads), 0,
+                         tm_hip_stream(stream), hidden, keep, static_cast<const T *>(slot_out), so_b,
+                         so_s, weights, ld_w, top_k, static_cast<const T *>(values), n_cent, ld_v, idx,
+                         dist, ld_idx, n_nearest, static_cast<const T *>(residual), ld_r,
+                         static_cast<T *>(out), ld_o);
+    };
+    if (vec) launch(std::true_type{});
+    else launch(std::false_type{});
+    TM_LAUNCH_CHECK("tm_gather_combine");
+    return TM_OK;
+  });
+}
+
+extern "C" int tm_slot_combine(int32_t dtype, int64_t n_tokens, int32_t top_k, int32_t hidden,
+                               const float *weights, int64_t ld_w, const uint8_t *compute_mask,
+                               const void *computed, int64_t cs_b, int64_t cs_s, const uint8_t *off_hit,
+                               const int64_t *off_idx, const int64_t *sel, int64_t ld_m,
+                               const uint8_t *is_vision, const void *values, int64_t n_experts,
+                               int64_t n_centroids, int64_t vs_e, int64_t vs_m, int64_t vs_c,
+                               const uint8_t *on_hit, const int64_t *on_idx, const int64_t *on_slot,
+                               const void *online_values, int64_t n_online, int32_t online_topk,
+                               int64_t ov_w, int64_t ov_s, int32_t target_mode, const void *residual,
+                               int64_t ld_r, void *out, int64_t ld_out, tm_stream_t stream) {
+  TM_REQUIRE(n_tokens >= 0 && top_k >= 1 && top_k <= kMaxSrc && hidden > 0 && ld_w >= top_k &&
+                 ld_m >= top_k && ld_out >= hidden,
+             TM_EINVAL_SHAPE, "tm_slot_combine: bad sizes");
+  TM_REQUIRE(target_mode == TM_TARGET_ONE || target_mode == TM_TARGET_ORIG_SUM, TM_EINVAL_ARG,
+             "tm_slot_combine: bad target mode %d", target_mode);
+  TM_REQUIRE(n_tokens < (int64_t)0x7fffffff, TM_EINVAL_SHAPE, "tm_slot_combine: too many tokens");
+  if (n_tokens == 0) return TM_OK;
+  TM_REQUIRE(weights && out, TM_EINVAL_ARG, "tm_slot_combine: null pointer");
+  TM_REQUIRE(!compute_mask || computed, TM_EINVAL_ARG, "tm_slot_combine: compute_mask needs computed");
+  TM_REQUIRE(!off_hit || (off_idx && sel && values), TM_EINVAL_ARG,
+             "tm_slot_combine: off_hit needs off_idx, sel and values");
+  TM_REQUIRE(!on_hit || (on_idx && on_slot && online_values), TM_EINVAL_ARG,
+             "tm_slot_combine: on_hit needs on_idx, on_slot and online_values");
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    using T = typename Elem<DT>::T;
+    const int E = Elem<DT>::kBytes;
+    const bool vec = hidden % 8 == 0 && (computed == nullptr || (tm_aligned16(computed) && (cs_b * E) % 16 == 0 &&
+                                                                  (cs_s * E) % 16 == 0)) &&
+                     (values == nullptr || (tm_aligned16(values) && (vs_e * E) % 16 == 0 &&
+                                            (vs_m * E) % 16 == 0 && (vs_c * E) % 16 == 0)) &&
+                     (online_values == nullptr || (tm_aligned16(online_values) && (ov_w * E) % 16 == 0 &&
+                                                   (ov_s * E) % 16 == 0)) &&
+                     rows_aligned(residual, ld_r, E) && rows_aligned(out, ld_out, E);
+    auto launch = [&](auto vec_tag) {
+      constexpr bool VEC = decltype(vec_tag)::value;
+      hipLaunchKernelGGL((slot_combine_kernel<DT, VEC>), dim3((unsigned)n_tokens), dim3(kThreads), 0,
+                         tm_hip_stream(stream), top_k, hidden, weights, ld_w, compute_mask,
+                         static_cast<const T *>(computed), cs_b, cs_s, off_hit, off_idx, sel, ld_m,
+                         is_vision, static_cast<const T *>(values), n_experts, n_centroids, vs_e, vs_m,
+                         vs_c, on_hit, on_idx, on_slot, static_cast<const T *>(online_values), n_online,
+                         online_topk, ov_w, ov_s, target_mode, static_cast<const T *>(residual), ld_r,
+                         static_cast<T *>(out), ld_out);
+    };
+    if (vec) launch(std::true_type{});
+    else launch(std::false_type{});
+    TM_LAUNCH_CHECK("tm_slot_combine");
+    return TM_OK;
+  });
+}
+
+extern "C" int tm_online_update(int32_t dtype, const void *hidden, int64_t ld_h, const int64_t *ids,
+                                int64_t ld_ids, const void *outputs, int64_t os_b, int64_t os_s,
+                                const uint8_t *valid, int64_t ld_valid, int64_t n_rows, int32_t top_k,
+                                int32_t hidden_dim, int64_t start, int64_t ring_size, void *ring_keys,
+                                int64_t *ring_ids, void *ring_values, tm_stream_t stream) {
+  TM_REQUIRE(n_rows >= 0 && ring_size > 0 && n_rows <= ring_size && top_k >= 0 && top_k <= kThreads &&
+                 hidden_dim > 0 && start >= 0 && start < ring_size,
+             TM_EINVAL_SHAPE, "tm_online_update: bad sizes (rows %lld, ring %lld, start %lld)",
+             (long long)n_rows, (long long)ring_size, (long long)start);
+  if (n_rows == 0) return TM_OK;
+  TM_REQUIRE(hidden && ids && outputs && ring_keys && ring_ids && ring_values, TM_EINVAL_ARG,
+             "tm_online_update: null pointer");
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    using T = typename Elem<DT>::T;
+    const int E = Elem<DT>::kBytes;
+    const bool vec = hidden_dim % 8 == 0 && rows_aligned(hidden, ld_h, E) && tm_aligned16(outputs) &&
+                     (os_b * E) % 16 == 0 && (os_s * E) % 16 == 0 && tm_aligned16(ring_keys) &&
+                     tm_aligned16(ring_values);
+    auto launch = [&](auto vec_tag) {
+      constexpr bool VEC = decltype(vec_tag)::value;
+      hipLaunchKernelGGL((online_update_kernel<DT, VEC>), dim3((unsigned)n_rows), dim3(kThreads), 0,
+                         tm_hip_stream(stream), static_cast<const T *>(hidden), ld_h, ids, ld_ids,
+                         static_cast<const T *>(outputs), os_b, os_s, valid, ld_valid, top_k, hidden_dim,
+                         start, ring_size, static_cast<T *>(ring_keys), ring_ids, static_cast<T *>(ring_values));
+    };
+    if (vec) launch(std::true_type{});
+    else launch(std::false_type{});
+    TM_LAUNCH_CHECK("tm_online_update");
+    return TM_OK;
+  });
+}

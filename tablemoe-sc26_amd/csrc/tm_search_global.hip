@@ -1,0 +1,351 @@
+// Mode G (global table) nearest-centroid search: north-star kernels (1)+(2).
+//
+// dist(q, c) = ||q||^2 - 2 q.c + ||c||^2 with q.c on bf16/fp16 MFMA (fp32
+// accumulation); only d' = ||c||^2 - 2 q.c is ranked (||q||^2 is constant per
+// query) and the n x C score matrix is never written.
+//
+// Layout of the contraction: D^T = C . Q^T with v_mfma_f32_32x32x16.  The A
+// operand is a 32-centroid slab read from LDS, the B operand is the wave's 32
+// queries held in registers for the whole kernel (DIM/16 k-steps).  In the
+// result each lane owns ONE query (column l%32) and 16 centroids, so the
+// running top-k is a per-lane register list and needs no cross-lane traffic
+// until the very end.
+//
+// Grid = (row blocks) x (centroid splits).  Each workgroup writes its top-k
+// per query as packed keys (orderable(d') << 32 | c) into the workspace;
+// tm_merge_kernel reduces the splits.  Packed keys make the order total:
+// smaller distance first, then lower centroid index.
+#include "tm_mfma.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kStage = 128;  // centroids per LDS stage (4 slabs of 32)
+constexpr int kPad = 8;
+
+struct SplitPlan {
+  int rw;        // query slabs (of 32) per workgroup: 4, or 1 for small n
+  int64_t row_blocks;
+  int64_t nsplit;
+  int64_t chunk;  // centroids per split (multiple of kStage)
+};
+
+SplitPlan plan_split(int64_t n, int64_t c) {
+  SplitPlan p;
+  p.rw = (n <= 32) ? 1 : 4;
+  p.row_blocks = tm_cdiv(n, 32 * p.rw);
+  const int64_t max_split = tm_cdiv(c, kStage);
+  int64_t want = tm_cdiv(1024, p.row_blocks);  // aim at ~1024 workgroups (4 per CU)
+  if (want < 1) want = 1;
+  if (want > max_split) want = max_split;
+  p.chunk = tm_cdiv(tm_cdiv(c, want), kStage) * kStage;
+  p.nsplit = tm_cdiv(c, p.chunk);
+  return p;
+}
+
+// Register-list length used for a requested top_k (the first top_k entries
+// of a longer list are the same top_k).
+static inline int list_len(int top_k) { return top_k <= 1 ? 1 : (top_k <= 4 ? 4 : 8); }
+
+__device__ __forceinline__ uint64_t make_key(float dprime, int c) {
+  return ((uint64_t)tm_orderable(dprime) << 32) | (uint32_t)c;
+}
+
+// Insert `x` into the ascending list `l` of length K (compare-swap chain).
+template <int K>
+__device__ __forceinline__ void list_insert(uint64_t (&l)[K], uint64_t x) {
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const uint64_t lo = l[j] < x ? l[j] : x;
+    x = l[j] < x ? x : l[j];
+    l[j] = lo;
+  }
+}
+
+template <int DT, int DIM, int K, int RW, int METRIC>
+__global__ __launch_bounds__(kThreads) void search_global_kernel(
+    const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
+    const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
+    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws) {
+  using T = typename Elem<DT>::T;
+  constexpr int KS = DIM / 16;  // k-steps of the 32x32x16 MFMA
+  __shared__ __attribute__((aligned(16))) T cs[kStage][DIM + kPad];
+  __shared__ float cn[kStage];
+  __shared__ uint64_t merge_buf[(RW == 1) ? 4 * 32 * K : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int slab = (RW == 4) ? wave : 0;
+  const int64_t split = blockIdx.y;
+  const int64_t row_base = (int64_t)blockIdx.x * (32 * RW) + slab * 32;
+  const int64_t c_begin = split * chunk;
+  const int64_t c_end = (c_begin + chunk < n_cent) ? c_begin + chunk : n_cent;
+
+  // B operand: this wave's 32 queries, all k-steps, in registers.
+  uint4 qf[KS];
+  {
+    const int64_t r = row_base + (lane & 31);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks] = make_uint4(0, 0, 0, 0);
+      if (r < n) qf[ks] = *reinterpret_cast<const uint4 *>(q + r * ld_q + ks * 16 + 8 * (lane >> 5));
+    }
+  }
+
+  float best_d = __builtin_huge_valf();
+  int best_i = 0x7fffffff;
+  uint64_t lst[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) lst[j] = ~0ull;
+
+  for (int64_t s0 = c_begin; s0 < c_end; s0 += kStage) {
+    // Stage kStage centroids (rows beyond c_end are zero and skipped later).
+    constexpr int CH = DIM / 8;  // 16-byte chunks per centroid row
+    for (int ci = tid; ci < kStage * CH; ci += kThreads) {
+      const int r = ci / CH, c8 = (ci % CH) * 8;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (s0 + r < c_end) v = *reinterpret_cast<const uint4 *>(cents + (s0 + r) * ld_c + c8);
+      *reinterpret_cast<uint4 *>(&cs[r][c8]) = v;
+    }
+    if (tid < kStage) cn[tid] = (METRIC == TM_METRIC_L2 && s0 + tid < c_end) ? c_sqnorm[s0 + tid] : 0.f;
+    __syncthreads();
+
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      if (RW == 1 && sub != wave) continue;
+      tm_f32x16 acc = {};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(&cs[sub * 32 + (lane & 31)][ks * 16 + 8 * (lane >> 5)]);
+        acc = tm_mfma32x32x16<DT>(a, qf[ks], acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = sub * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        const int64_t c = s0 + m;
+        const float dp = (METRIC == TM_METRIC_L2) ? fmaf(-2.f, acc[i], cn[m]) : -acc[i];
+        if (c < c_end) {
+          if constexpr (K == 1) {
+            if (dp < best_d) { best_d = dp; best_i = (int)c; }
+          } else {
+            const uint64_t key = make_key(dp, (int)c);
+            if (key < lst[K - 1]) list_insert<K>(lst, key);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  if constexpr (K == 1) lst[0] = (best_i == 0x7fffffff) ? ~0ull : make_key(best_d, best_i);
+
+  // Merge the two half-waves (same query column, disjoint centroids).
+  {
+    uint64_t other[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) other[j] = __shfl_xor(lst[j], 32, 64);
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+      if (other[j] < lst[K - 1]) list_insert<K>(lst, other[j]);
+  }
+
+  if constexpr (RW == 1) {
+    // Waves share the queries but saw disjoint centroid slabs: merge via LDS.
+    if (lane < 32) {
+#pragma unroll
+      for (int j = 0; j < K; ++j) merge_buf[(wave * 32 + lane) * K + j] = lst[j];
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 32) {
+      for (int w = 1; w < 4; ++w) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+          const uint64_t o = merge_buf[(w * 32 + lane) * K + j];
+          if (o < lst[K - 1]) list_insert<K>(lst, o);
+        }
+      }
+    } else {
+      return;
+    }
+  }
+
+  const int64_t r = row_base + (lane & 31);
+  if (lane < 32 && r < n) {
+    uint64_t *dst = ws + (split * n + r) * K;
+#pragma unroll
+    for (int j = 0; j < K; ++j) dst[j] = lst[j];
+  }
+}
+
+// One wave per query: reduce nsplit partial lists to the final top-k.
+template <int DT, int K, int METRIC>
+__global__ __launch_bounds__(kThreads) void merge_kernel(
+    const uint64_t *__restrict__ ws, int64_t n, int64_t nsplit, const typename Elem<DT>::T *__restrict__ q,
+    int64_t ld_q, int dim, const float *__restrict__ q_sqnorm, int top_k, float *__restrict__ out_dist,
+    int64_t *__restrict__ out_idx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (r >= n) return;  // whole wave exits together
+  uint64_t lst[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) lst[j] = ~0ull;
+  for (int64_t s = lane; s < nsplit; s += 64) {
+    const uint64_t *src = ws + (s * n + r) * K;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const uint64_t v = src[j];
+      if (v < lst[K - 1]) list_insert<K>(lst, v);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t other[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) other[j] = __shfl_xor(lst[j], o, 64);
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+      if (other[j] < lst[K - 1]) list_insert<K>(lst, other[j]);
+  }
+  float qn = 0.f;
+  if (METRIC == TM_METRIC_L2) {
+    if (q_sqnorm != nullptr) {
+      qn = q_sqnorm[r];
+    } else {
+      for (int j = lane; j < dim; j += 64) {
+        const float v = Elem<DT>::to_f(q[r * ld_q + j]);
+        qn = fmaf(v, v, qn);
+      }
+      qn = tm_wave_sum(qn);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      if (j >= top_k) break;
+      const uint64_t key = lst[j];
+      if (key == ~0ull) {
+        out_idx[r * top_k + j] = -1;
+        out_dist[r * top_k + j] = (METRIC == TM_METRIC_L2) ? __builtin_huge_valf() : -__builtin_huge_valf();
+      } else {
+        const float dp = tm_from_orderable((uint32_t)(key >> 32));
+        out_idx[r * top_k + j] = (int64_t)(uint32_t)key;
+        out_dist[r * top_k + j] = (METRIC == TM_METRIC_L2) ? fmaxf(qn + dp, 0.f) : -dp;
+      }
+    }
+  }
+}
+
+template <int DT>
+__global__ void sqnorm_kernel(const typename Elem<DT>::T *c, int64_t n, int dim, int64_t ld, float *out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.f;
+  for (int j = 0; j < dim; ++j) {
+    const float v = Elem<DT>::to_f(c[i * ld + j]);
+    s = fmaf(v, v, s);
+  }
+  out[i] = s;
+}
+
+template <int DT, int DIM, int K, int METRIC>
+int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float *q_sqnorm,
+                  const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm,
+                  float *out_dist, int64_t *out_idx, uint64_t *ws, hipStream_t stream) {
+  using T = typename Elem<DT>::T;
+  const SplitPlan p = plan_split(n, n_cent);
+  dim3 grid((unsigned)p.row_blocks, (unsigned)p.nsplit), block(kThreads);
+  if (p.rw == 4)
+    hipLaunchKernelGGL((search_global_kernel<DT, DIM, K, 4, METRIC>), grid, block, 0, stream,
+                       static_cast<const T *>(q), n, ld_q, static_cast<const T *>(cents), n_cent,
+                       ld_c, c_sqnorm, p.chunk, ws);
+  else
+    hipLaunchKernelGGL((search_global_kernel<DT, DIM, K, 1, METRIC>), grid, block, 0, stream,
+                       static_cast<const T *>(q), n, ld_q, static_cast<const T *>(cents), n_cent,
+                       ld_c, c_sqnorm, p.chunk, ws);
+  TM_LAUNCH_CHECK("tm_search_global");
+  hipLaunchKernelGGL((merge_kernel<DT, K, METRIC>), dim3((unsigned)tm_cdiv(n, kThreads / 64)),
+                     block, 0, stream, ws, n, p.nsplit, static_cast<const T *>(q), ld_q, DIM,
+                     q_sqnorm, top_k, out_dist, out_idx);
+  TM_LAUNCH_CHECK("tm_search_global(merge)");
+  return TM_OK;
+}
+
+template <int DT, int DIM, int METRIC>
+int dispatch_k(int top_k, const void *q, int64_t n, int64_t ld_q, const float *q_sqnorm,
+               const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm,
+               float *out_dist, int64_t *out_idx, uint64_t *ws, hipStream_t stream) {
+  switch (list_len(top_k)) {
+    case 1: return launch_search<DT, DIM, 1, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
+    case 4: return launch_search<DT, DIM, 4, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
+    default: return launch_search<DT, DIM, 8, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
+  }
+}
+
+template <int DT, int METRIC>
+int dispatch_dim(int dim, int top_k, const void *q, int64_t n, int64_t ld_q, const float *q_sqnorm,
+                 const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm,
+                 float *out_dist, int64_t *out_idx, uint64_t *ws, hipStream_t stream) {
+  switch (dim) {
+    case 64: return dispatch_k<DT, 64, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
+    case 128: return dispatch_k<DT, 128, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
+    case 256: return dispatch_k<DT, 256, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
+    default: return tm_fail(TM_EINVAL_SHAPE, "tm_search_global: dim %d not in {64, 128, 256}", dim);
+  }
+}
+
+}  // namespace
+
+extern "C" int tm_centroid_sqnorms(int32_t dtype, const void *cents, int64_t n_cent, int32_t dim,
+                                   int64_t ld_c, float *out, tm_stream_t stream) {
+  TM_REQUIRE(n_cent >= 0 && dim > 0 && ld_c >= dim, TM_EINVAL_SHAPE, "tm_centroid_sqnorms: bad sizes");
+  TM_REQUIRE(n_cent == 0 || (cents && out), TM_EINVAL_ARG, "tm_centroid_sqnorms: null pointer");
+  if (n_cent == 0) return TM_OK;
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    hipLaunchKernelGGL((sqnorm_kernel<DT>), dim3((unsigned)tm_cdiv(n_cent, 256)), dim3(256), 0,
+                       tm_hip_stream(stream), static_cast<const typename Elem<DT>::T *>(cents),
+                       n_cent, dim, ld_c, out);
+    TM_LAUNCH_CHECK("tm_centroid_sqnorms");
+    return TM_OK;
+  });
+}
+
+extern "C" size_t tm_search_global_workspace_size(int64_t n_tokens, int64_t n_cent, int32_t dim,
+                                                  int32_t top_k) {
+  (void)dim;
+  if (n_tokens <= 0 || n_cent <= 0 || top_k <= 0) return 0;
+  const SplitPlan p = plan_split(n_tokens, n_cent);
+  return (size_t)p.nsplit * (size_t)n_tokens * (size_t)list_len(top_k) * sizeof(uint64_t);
+}
+
+extern "C" int tm_search_global(int32_t dtype, const void *q, int64_t n_tokens, int64_t ld_q,
+                                const float *q_sqnorm, const void *cents, int64_t n_cent,
+                                int64_t ld_c, const float *c_sqnorm, int32_t dim, int32_t top_k,
+                                int32_t metric, float *out_dist, int64_t *out_idx, void *workspace,
+                                size_t workspace_bytes, tm_stream_t stream) {
+  TM_REQUIRE(n_tokens >= 0 && n_cent > 0 && n_cent < (int64_t)0x7fffffff, TM_EINVAL_SHAPE,
+             "tm_search_global: bad sizes n=%lld C=%lld", (long long)n_tokens, (long long)n_cent);
+  TM_REQUIRE(ld_q >= dim && ld_c >= dim, TM_EINVAL_SHAPE, "tm_search_global: bad row strides");
+  TM_REQUIRE(top_k >= 1 && top_k <= 8, TM_EINVAL_SHAPE, "tm_search_global: top_k %d not in [1, 8]", top_k);
+  TM_REQUIRE(metric == TM_METRIC_L2 || metric == TM_METRIC_DOT, TM_EINVAL_ARG, "tm_search_global: bad metric");
+  TM_REQUIRE(dtype == TM_DT_BF16 || dtype == TM_DT_F16, TM_EINVAL_DTYPE,
+             "tm_search_global: dtype must be F16 or BF16");
+  if (n_tokens == 0) return TM_OK;
+  TM_REQUIRE(q && cents && out_dist && out_idx, TM_EINVAL_ARG, "tm_search_global: null pointer");
+  TM_REQUIRE(metric != TM_METRIC_L2 || c_sqnorm, TM_EINVAL_ARG, "tm_search_global: L2 needs c_sqnorm");
+  TM_REQUIRE(tm_aligned16(q) && tm_aligned16(cents) && (ld_q * 2) % 16 == 0 && (ld_c * 2) % 16 == 0,
+             TM_EINVAL_SHAPE, "tm_search_global: q and centroid rows must be 16-byte aligned");
+  const size_t need = tm_search_global_workspace_size(n_tokens, n_cent, dim, top_k);
+  TM_REQUIRE(workspace != nullptr && workspace_bytes >= need, TM_EWORKSPACE,
+             "tm_search_global: workspace %zu bytes < %zu", workspace_bytes, need);
+  uint64_t *ws = static_cast<uint64_t *>(workspace);
+  hipStream_t s = tm_hip_stream(stream);
+  if (dtype == TM_DT_BF16) {
+    if (metric == TM_METRIC_L2)
+      return dispatch_dim<TM_DT_BF16, TM_METRIC_L2>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, s);
+    return dispatch_dim<TM_DT_BF16, TM_METRIC_DOT>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, s);
+  }
+  if (metric == TM_METRIC_L2)
+    return dispatch_dim<TM_DT_F16, TM_METRIC_L2>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, s);
+  return dispatch_dim<TM_DT_F16, TM_METRIC_DOT>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, s);
+}

@@ -1,0 +1,333 @@
+// Selection kernels: keep-rate radix select (north-star kernel (3)), the
+// reference's keep masks (table_moe/skip/pruning.py) and surviving-weight
+// renormalisation.
+#include "tm_common.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// block-wide exclusive scan of one uint32 per thread (blockDim.x % 64 == 0)
+// ---------------------------------------------------------------------------
+template <int NT>
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *wave_tot, uint32_t &total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) wave_tot[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < NT / 64; ++w) {
+      const uint32_t t = wave_tot[w];
+      wave_tot[w] = run;
+      run += t;
+    }
+    wave_tot[NT / 64] = run;
+  }
+  __syncthreads();
+  total = wave_tot[NT / 64];
+  return wave_tot[wave] + inc - v;
+}
+
+// ---------------------------------------------------------------------------
+// (3) keep the n_keep largest scores; ties -> lower token index.
+// One workgroup.  Four 8-bit radix passes over order-preserving uint32 keys
+// find the boundary key T and how many copies of T are kept; a scan over the
+// tokens in index order then keeps the first of the tied ones.
+// ---------------------------------------------------------------------------
+constexpr int kSelThreads = 1024;
+
+__global__ __launch_bounds__(kSelThreads) void keep_select_kernel(const float *__restrict__ score,
+                                                                  int64_t n, int64_t ld,
+                                                                  int64_t n_keep,
+                                                                  uint8_t *__restrict__ out) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_prefix, s_mask;
+  __shared__ int64_t s_remaining;
+  __shared__ uint32_t wave_tot[kSelThreads / 64 + 1];
+  const int tid = threadIdx.x;
+  const int64_t per = (n + kSelThreads - 1) / kSelThreads;
+  const int64_t lo = tid * per;
+  const int64_t hi = (lo + per < n) ? lo + per : n;
+
+  if (n_keep <= 0 || n_keep >= n) {
+    const uint8_t v = n_keep > 0 ? 1 : 0;
+    for (int64_t i = lo; i < hi; ++i) out[i] = v;
+    return;
+  }
+  if (tid == 0) { s_prefix = 0; s_mask = 0; s_remaining = n_keep; }
+  __syncthreads();
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int b = tid; b < 256; b += kSelThreads) hist[b] = 0;
+    __syncthreads();
+    const uint32_t prefix = s_prefix, mask = s_mask;
+    for (int64_t i = lo; i < hi; ++i) {
+      const uint32_t key = tm_orderable(score[i * ld]);
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int64_t above = 0;
+      int b = 255;
+      for (; b > 0; --b) {
+        if (above + hist[b] >= s_remaining) break;
+        above += hist[b];
+      }
+      s_remaining -= above;
+      s_prefix = prefix | ((uint32_t)b << shift);
+      s_mask = mask | (255u << shift);
+    }
+    __syncthreads();
+  }
+  const uint32_t T = s_prefix;
+  const int64_t keep_eq = s_remaining;  // copies of T to keep, >= 1
+  uint32_t cnt = 0;
+  for (int64_t i = lo; i < hi; ++i) cnt += (tm_orderable(score[i * ld]) == T);
+  uint32_t total;
+  uint32_t rank = block_exclusive_scan<kSelThreads>(cnt, wave_tot, total);
+  for (int64_t i = lo; i < hi; ++i) {
+    const uint32_t key = tm_orderable(score[i * ld]);
+    uint8_t k = 0;
+    if (key > T) {
+      k = 1;
+    } else if (key == T) {
+      k = ((int64_t)rank < keep_eq) ? 1 : 0;
+      ++rank;
+    }
+    out[i] = k;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a3: build_fixed_keep_mask (pruning.py:4-15)
+// ---------------------------------------------------------------------------
+__global__ void fixed_keep_kernel(int64_t total, int top_k, int keep_k, uint8_t *out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < total) out[i] = ((int)(i % top_k) < keep_k) ? 1 : 0;
+}
+
+// ---------------------------------------------------------------------------
+// a3: build_prefill_keep_mask (pruning.py:18-48), deterministic.
+// Pass 1: per token chunk, each expert's partial score sum (fixed entry
+// order) and selection count.  Pass 2 (one workgroup): chunk sums in chunk
+// order, ranking, mask.
+// ---------------------------------------------------------------------------
+constexpr int kEntries = 2048;  // (token, slot) entries per chunk
+
+__global__ __launch_bounds__(256) void expert_partial_kernel(
+    const int64_t *__restrict__ sel, const float *__restrict__ w, const float *__restrict__ attn,
+    int64_t n, int top_k, int n_experts, int64_t tok_per_chunk, float *__restrict__ part_sum,
+    uint32_t *__restrict__ part_cnt) {
+  __shared__ int s_sel[kEntries];
+  __shared__ float s_val[kEntries];
+  const int64_t t0 = (int64_t)blockIdx.x * tok_per_chunk;
+  const int64_t t1 = (t0 + tok_per_chunk < n) ? t0 + tok_per_chunk : n;
+  const int ne = (int)((t1 - t0) * top_k);
+  const float nf = (float)n;
+  for (int j = threadIdx.x; j < ne; j += blockDim.x) {
+    const int64_t b = t0 + j / top_k;
+    const int s = j % top_k;
+    const int64_t e = sel[b * top_k + s];
+    s_sel[j] = (e >= 0 && e < n_experts) ? (int)e : -1;
+    const float wv = w[b * top_k + s];
+    s_val[j] = attn ? attn[b] * wv : wv / nf;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
+    float acc = 0.f;
+    uint32_t cnt = 0;
+    for (int j = 0; j < ne; ++j) {
+      if (s_sel[j] == e) { acc += s_val[j]; ++cnt; }
+    }
+    part_sum[(int64_t)blockIdx.x * n_experts + e] = acc;
+    part_cnt[(int64_t)blockIdx.x * n_experts + e] = cnt;
+  }
+}
+
+constexpr int kRankThreads = 1024;
+constexpr int kMaxExperts = 1024;
+
+__global__ __launch_bounds__(kRankThreads) void expert_rank_kernel(
+    const int64_t *__restrict__ sel, int64_t n, int top_k, int n_experts, int64_t nchunk,
+    const float *__restrict__ part_sum, const uint32_t *__restrict__ part_cnt, double keep_rate,
+    uint8_t *__restrict__ out_mask, float *__restrict__ out_scores) {
+  __shared__ float score[kMaxExperts];
+  __shared__ uint8_t active[kMaxExperts];
+  __shared__ uint8_t kept[kMaxExperts];
+  __shared__ uint32_t wave_tot[kRankThreads / 64 + 1];
+  const int tid = threadIdx.x;
+  uint32_t my_active = 0;
+  for (int e = tid; e < n_experts; e += kRankThreads) {
+    float s = 0.f;
+    uint32_t c = 0;
+    for (int64_t k = 0; k < nchunk; ++k) {
+      s += part_sum[k * n_experts + e];
+      c += part_cnt[k * n_experts + e];
+    }
+    score[e] = s;
+    active[e] = c > 0;
+    my_active += (c > 0);
+    if (out_scores) out_scores[e] = s;
+  }
+  uint32_t n_active;
+  (void)block_exclusive_scan<kRankThreads>(my_active, wave_tot, n_active);
+  int64_t num_keep = (int64_t)((double)n_active * keep_rate);
+  if (num_keep < 1) num_keep = 1;
+  if (num_keep > (int64_t)n_active) num_keep = n_active;
+  for (int e = tid; e < n_experts; e += kRankThreads) {
+    uint8_t k = 0;
+    if (active[e]) {
+      const float se = score[e];
+      int64_t rank = 0;
+      for (int o = 0; o < n_experts; ++o)
+        rank += (active[o] && (score[o] > se || (score[o] == se && o < e)));
+      k = rank < num_keep;
+    }
+    kept[e] = k;
+  }
+  __syncthreads();
+  const int64_t total = n * top_k;
+  for (int64_t i = tid; i < total; i += kRankThreads) {
+    const int64_t e = sel[i];
+    out_mask[i] = (e >= 0 && e < n_experts) ? kept[e] : 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a11: renormalize_surviving_weights (pruning.py:55-73), one thread per row.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ void renormalize_kernel(const typename Elem<DT>::T *__restrict__ w, int64_t ld_w,
+                                   const uint8_t *__restrict__ mask, int64_t ld_m, int64_t n,
+                                   int top_k, int target_mode, const typename Elem<DT>::T *__restrict__ target,
+                                   int64_t ld_t, typename Elem<DT>::T *__restrict__ out) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= n) return;
+  const typename Elem<DT>::T *wr = w + b * ld_w;
+  const uint8_t *mr = mask + b * ld_m;
+  float kept = 0.f, full = 0.f;
+  for (int s = 0; s < top_k; ++s) {
+    const float v = Elem<DT>::to_f(wr[s]);
+    full += v;
+    if (mr[s]) kept += v;
+  }
+  kept = tm_round<DT>(kept);
+  float tgt = 1.f;
+  if (target_mode == TM_TARGET_ORIG_SUM) tgt = tm_round<DT>(full);
+  else if (target_mode == TM_TARGET_GIVEN) tgt = Elem<DT>::to_f(target[b * ld_t]);
+  typename Elem<DT>::T *o = out + b * top_k;
+  const bool valid = kept > 0.f;
+  for (int s = 0; s < top_k; ++s) {
+    float r = 0.f;
+    if (valid && mr[s]) {
+      r = tm_round<DT>(Elem<DT>::to_f(wr[s]) / kept);
+      if (target_mode != TM_TARGET_ONE) r = tm_round<DT>(r * tgt);
+    }
+    o[s] = Elem<DT>::from_f(r);
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" int64_t tm_keep_count(int64_t n, double keep_rate) {
+  if (n <= 0) return 0;
+  int64_t k = (int64_t)((double)n * keep_rate);
+  if (k < 1) k = 1;
+  if (k > n) k = n;
+  return k;
+}
+
+extern "C" size_t tm_keep_select_workspace_size(int64_t n) {
+  (void)n;
+  return 0;
+}
+
+extern "C" int tm_keep_select(const float *score, int64_t n, int64_t ld_score, int64_t n_keep,
+                              uint8_t *out_keep, void *workspace, size_t workspace_bytes,
+                              tm_stream_t stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  TM_REQUIRE(n >= 0 && n < ((int64_t)1 << 31) && ld_score >= 1, TM_EINVAL_SHAPE,
+             "tm_keep_select: bad sizes n=%lld", (long long)n);
+  if (n == 0) return TM_OK;
+  TM_REQUIRE(score && out_keep, TM_EINVAL_ARG, "tm_keep_select: null pointer");
+  hipLaunchKernelGGL(keep_select_kernel, dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
+                     score, n, ld_score, n_keep, out_keep);
+  TM_LAUNCH_CHECK("tm_keep_select");
+  return TM_OK;
+}
+
+extern "C" int tm_fixed_keep_mask(int64_t n_tokens, int32_t top_k, int32_t keep_k, uint8_t *out,
+                                  tm_stream_t stream) {
+  TM_REQUIRE(n_tokens >= 0 && top_k >= 0, TM_EINVAL_SHAPE, "tm_fixed_keep_mask: bad sizes");
+  const int64_t total = n_tokens * top_k;
+  if (total == 0) return TM_OK;
+  TM_REQUIRE(out, TM_EINVAL_ARG, "tm_fixed_keep_mask: null pointer");
+  hipLaunchKernelGGL(fixed_keep_kernel, dim3((unsigned)tm_cdiv(total, 256)), dim3(256), 0,
+                     tm_hip_stream(stream), total, top_k, keep_k, out);
+  TM_LAUNCH_CHECK("tm_fixed_keep_mask");
+  return TM_OK;
+}
+
+static int64_t expert_tok_per_chunk(int32_t top_k) {
+  int64_t t = kEntries / (top_k > 0 ? top_k : 1);
+  return t < 1 ? 1 : t;
+}
+
+extern "C" size_t tm_expert_keep_mask_workspace_size(int64_t n_tokens, int32_t n_experts) {
+  // sized for the largest chunk count (top_k = 32)
+  if (n_tokens <= 0 || n_experts <= 0) return 0;
+  const int64_t nchunk = tm_cdiv(n_tokens, expert_tok_per_chunk(32));
+  return (size_t)nchunk * (size_t)n_experts * (sizeof(float) + sizeof(uint32_t));
+}
+
+extern "C" int tm_expert_keep_mask(const int64_t *sel, const float *weights, const float *attn,
+                                   int64_t n_tokens, int32_t top_k, int32_t n_experts,
+                                   double keep_rate, uint8_t *out_mask, float *out_expert_scores,
+                                   void *workspace, size_t workspace_bytes, tm_stream_t stream) {
+  TM_REQUIRE(n_tokens >= 0 && top_k >= 1 && top_k <= 32 && n_experts >= 1 && n_experts <= kMaxExperts,
+             TM_EINVAL_SHAPE, "tm_expert_keep_mask: bad sizes (top_k %d, experts %d)", top_k, n_experts);
+  if (n_tokens == 0) return TM_OK;
+  TM_REQUIRE(sel && weights && out_mask, TM_EINVAL_ARG, "tm_expert_keep_mask: null pointer");
+  const int64_t tpc = expert_tok_per_chunk(top_k);
+  const int64_t nchunk = tm_cdiv(n_tokens, tpc);
+  const size_t need = (size_t)nchunk * (size_t)n_experts * (sizeof(float) + sizeof(uint32_t));
+  TM_REQUIRE(workspace && workspace_bytes >= need, TM_EWORKSPACE,
+             "tm_expert_keep_mask: workspace %zu bytes < %zu", workspace_bytes, need);
+  float *part_sum = static_cast<float *>(workspace);
+  uint32_t *part_cnt = reinterpret_cast<uint32_t *>(part_sum + nchunk * n_experts);
+  hipStream_t s = tm_hip_stream(stream);
+  hipLaunchKernelGGL(expert_partial_kernel, dim3((unsigned)nchunk), dim3(256), 0, s, sel, weights,
+                     attn, n_tokens, top_k, n_experts, tpc, part_sum, part_cnt);
+  TM_LAUNCH_CHECK("tm_expert_keep_mask(partial)");
+  hipLaunchKernelGGL(expert_rank_kernel, dim3(1), dim3(kRankThreads), 0, s, sel, n_tokens, top_k,
+                     n_experts, nchunk, part_sum, part_cnt, keep_rate, out_mask, out_expert_scores);
+  TM_LAUNCH_CHECK("tm_expert_keep_mask(rank)");
+  return TM_OK;
+}
+
+extern "C" int tm_renormalize(int32_t dtype, const void *weights, int64_t ld_w, const uint8_t *mask,
+                              int64_t ld_m, int64_t n_tokens, int32_t top_k, int32_t target_mode,
+                              const void *target, int64_t ld_t, void *out, tm_stream_t stream) {
+  TM_REQUIRE(n_tokens >= 0 && top_k >= 0 && ld_w >= top_k && ld_m >= top_k, TM_EINVAL_SHAPE,
+             "tm_renormalize: bad sizes");
+  TM_REQUIRE(target_mode >= TM_TARGET_ONE && target_mode <= TM_TARGET_GIVEN, TM_EINVAL_ARG,
+             "tm_renormalize: bad target mode %d", target_mode);
+  if (n_tokens == 0 || top_k == 0) return TM_OK;
+  TM_REQUIRE(weights && mask && out && (target_mode != TM_TARGET_GIVEN || target), TM_EINVAL_ARG,
+             "tm_renormalize: null pointer");
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    using T = typename Elem<DT>::T;
+    hipLaunchKernelGGL((renormalize_kernel<DT>), dim3((unsigned)tm_cdiv(n_tokens, 256)), dim3(256), 0,
+                       tm_hip_stream(stream), static_cast<const T *>(weights), ld_w, mask, ld_m,
+                       n_tokens, top_k, target_mode, static_cast<const T *>(target), ld_t,
+                       static_cast<T *>(out));
+    TM_LAUNCH_CHECK("tm_renormalize");
+    return TM_OK;
+  });
+}

@@ -1,0 +1,153 @@
+"""ctypes binding of libtablemoe_hip.so (the C ABI in include/tablemoe.h).
+
+The library is loaded lazily on first use.  torch is imported first so the
+library's libamdhip64.so.7 dependency resolves to the HIP runtime torch has
+already loaded: torch streams and device pointers are then valid in our
+kernels.  There is no fallback: a missing library or a non-HIP tensor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtablemoe_hip.so"
+
+TM_OK, TM_EINVAL_SHAPE, TM_EINVAL_DTYPE, TM_EINVAL_ARG, TM_EHIP, TM_EWORKSPACE = range(6)
+TM_DT_F32, TM_DT_F16, TM_DT_BF16 = 0, 1, 2
+TM_CMP_GE, TM_CMP_GT = 0, 1
+TM_METRIC_L2, TM_METRIC_DOT = 0, 1
+TM_TARGET_ONE, TM_TARGET_ORIG_SUM, TM_TARGET_GIVEN = 0, 1, 2
+
+_DTYPE_TAG = {torch.float32: TM_DT_F32, torch.float16: TM_DT_F16, torch.bfloat16: TM_DT_BF16}
+
+i32, i64, f32, f64, vp, sz = C.c_int32, C.c_int64, C.c_float, C.c_double, C.c_void_p, C.c_size_t
+
+# name -> (restype, argtypes); mirrors include/tablemoe.h
+PROTOTYPES = {
+    "tm_version": (C.c_int, []),
+    "tm_status_string": (C.c_char_p, [C.c_int]),
+    "tm_last_error": (C.c_char_p, []),
+    "tm_topk_softmax": (C.c_int, [vp, i64, i32, i64, i32, i32, vp, vp, vp]),
+    "tm_project": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, vp, vp, i64, i64, i32, i32, f32, vp, i64, vp, vp]),
+    "tm_search_gated": (C.c_int, [i32, vp, i64, i64, vp, i64, i64, i32, i64, i64, i64, vp, i32, i64, i64, vp, vp,
+                                  i64, i64, i32, f32, f32, i32, vp, vp, i64, i64, vp]),
+    "tm_search_hybrid": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, vp, vp, i64, i64, i32, vp, i64, i32, vp, i32,
+                                   i64, vp, i64, i64, i64, i64, i64, vp, i32, i64, i64, i32, vp, vp, vp, vp, vp, i64,
+                                   i64, vp, sz, vp]),
+    "tm_fixed_keep_mask": (C.c_int, [i64, i32, i32, vp, vp]),
+    "tm_expert_keep_mask_workspace_size": (sz, [i64, i32]),
+    "tm_expert_keep_mask": (C.c_int, [vp, vp, vp, i64, i32, i32, f64, vp, vp, vp, sz, vp]),
+    "tm_renormalize": (C.c_int, [i32, vp, i64, vp, i64, i64, i32, i32, vp, i64, vp, vp]),
+    "tm_gather_rows": (C.c_int, [i32, vp, i64, i64, i32, i64, i64, i64, vp, vp, i32, vp, i64, vp, vp, i64, i64, vp]),
+    "tm_slot_combine": (C.c_int, [i32, i64, i32, i32, vp, i64, vp, vp, i64, i64, vp, vp, vp, i64, vp, vp, i64, i64,
+                                  i64, i64, i64, vp, vp, vp, vp, i64, i32, i64, i64, i32, vp, i64, vp, i64, vp]),
+    "tm_online_update": (C.c_int, [i32, vp, i64, vp, i64, vp, i64, i64, vp, i64, i64, i32, i32, i64, i64, vp, vp,
+                                   vp, vp]),
+    "tm_centroid_sqnorms": (C.c_int, [i32, vp, i64, i32, i64, vp, vp]),
+    "tm_search_global_workspace_size": (sz, [i64, i64, i32, i32]),
+    "tm_search_global": (C.c_int, [i32, vp, i64, i64, vp, vp, i64, i64, vp, i32, i32, i32, vp, vp, vp, sz, vp]),
+    "tm_keep_count": (i64, [i64, f64]),
+    "tm_keep_select_workspace_size": (sz, [i64]),
+    "tm_keep_select": (C.c_int, [vp, i64, i64, i64, vp, vp, sz, vp]),
+    "tm_gather_combine": (C.c_int, [i32, i64, i32, vp, vp, i64, i64, vp, i64, i32, vp, i64, i64, vp, vp, i64, i32,
+                                    vp, i64, vp, i64, vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def load(path: str | os.PathLike | None = None) -> C.CDLL:
+    """Load (once) and return the library; raise if it is not built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise NativeLibraryMissing(
+                f"{p} is not built; run `python tablemoe-sc26_amd/build_lib.py` (or __graft_entry__.build())"
+            )
+        lib = C.CDLL(str(p))
+        for name, (res, args) in PROTOTYPES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def lib() -> C.CDLL:
+    return _lib if _lib is not None else load()
+
+
+def check(status: int, what: str) -> None:
+    if status == TM_OK:
+        return
+    L = lib()
+    msg = (L.tm_last_error() or b"").decode(errors="replace")
+    name = (L.tm_status_string(status) or b"?").decode()
+    if status == TM_EHIP:
+        raise RuntimeError(f"{what}: {name}: {msg}")
+    raise ValueError(f"{what}: {name}: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)
+
+
+def dtype_tag(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_TAG[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16") from None
+
+
+def require_hip(*tensors: torch.Tensor | None) -> torch.device:
+    """All given tensors must live on the same HIP device; return it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"table_moe kernels run on a HIP device only; got a tensor on {t.device} "
+                "(there is no CPU fallback)"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no tensor given")
+    return dev
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def as_u8(mask: torch.Tensor) -> torch.Tensor:
+    """A bool/uint8 mask viewed as bytes (no copy for torch.bool)."""
+    if mask.dtype == torch.bool:
+        return mask.view(torch.uint8) if mask.is_contiguous() or mask.dim() == 0 else mask.to(torch.uint8)
+    if mask.dtype == torch.uint8:
+        return mask
+    return (mask != 0).to(torch.uint8)
+
+
+def exported_symbols() -> list[str]:
+    return [n for n in PROTOTYPES]

@@ -1,0 +1,317 @@
+"""VectorSearchEngine: the reference search surface over HIP kernels.
+
+Same class, method names, argument meaning, return conventions (fresh tensors,
+workspace views for ``search_decode_hybrid``, caller buffers for ``*_into``)
+and error types as the reference (table_moe/cache_engine/search.py:388-1105).
+The work runs in ``tm_project`` + ``tm_search_gated`` (offline searches) and
+``tm_search_hybrid`` (decode window + offline), enqueued on torch's current
+stream with no host synchronisation.
+
+Semantics follow the reference's torch path (the one its unit tests pin):
+cosine searches hit on ``max >= threshold``, raw-dot searches on
+``max > OFFLINE_DOT_THRESHOLD``, decode searches against normalised keys on
+``max >= 0``; scores are fp32 sums of the model-dtype products.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _native as N
+from .config import CacheConfig
+
+# The reference exports whether its Triton kernels are active; this
+# implementation has none.
+HAS_TRITON = False
+
+
+def _round_cap(batch_size: int) -> int:
+    cap = max(batch_size, 128)
+    return ((cap + 127) // 128) * 128
+
+
+class VectorSearchEngine:
+    def __init__(self, manager):
+        self.manager = manager
+        self.device = manager.device
+        self.workspace_capacity = 0
+        self.workspace = {}
+        self.prefill_query_workspace_capacity = 0
+        self.prefill_query_workspace = None
+        self.decode_query_workspace_capacity = 0
+        self.decode_query_workspace = None
+        self.search_dims_cache = None
+        self._workspace_top_k = None
+
+    # ------------------------------------------------------------------ setup
+    def _get_pca_pair(self):
+        pca_map = getattr(self.manager, "pca", None)
+        if not isinstance(pca_map, dict) or not pca_map:
+            raise ValueError("manager.pca must be a non-empty dict")
+        if "vision" in pca_map and "text" in pca_map:
+            return pca_map["vision"], pca_map["text"]
+        shared = pca_map[next(iter(pca_map))]
+        return shared, shared
+
+    def _get_search_dims(self):
+        if self.search_dims_cache is not None:
+            return self.search_dims_cache
+        pca_vis, pca_txt = self._get_pca_pair()
+        compressed_dim = int(pca_vis["proj"].shape[1])
+        if int(pca_txt["proj"].shape[1]) != compressed_dim:
+            raise ValueError("vision/text PCA projection dims must match")
+        online_topk = None
+        if getattr(self.manager, "online_expert_ids", None) is not None:
+            online_topk = int(self.manager.online_expert_ids.shape[1])
+        self.search_dims_cache = {
+            "pca_vis": pca_vis,
+            "pca_txt": pca_txt,
+            "compressed_dim": compressed_dim,
+            "fixed_k": int(self.manager.keys_buffer.shape[2]),
+            "online_topk": online_topk,
+            # k-contiguous copies of the projections for the MFMA projection
+            "proj_t": (self._transposed(pca_vis["proj"]), self._transposed(pca_txt["proj"])),
+        }
+        return self.search_dims_cache
+
+    @staticmethod
+    def _transposed(proj: torch.Tensor) -> torch.Tensor:
+        return proj.t().contiguous()  # [dim, hidden]
+
+    def _ensure_workspace(self, batch_size, top_k):
+        if batch_size > self.workspace_capacity or top_k != self._workspace_top_k:
+            cap = _round_cap(max(batch_size, self.workspace_capacity))
+            dev = self.device
+            self.workspace["on_hit"] = torch.zeros((cap, top_k), dtype=torch.bool, device=dev)
+            self.workspace["off_hit"] = torch.zeros((cap, top_k), dtype=torch.bool, device=dev)
+            self.workspace["off_idx"] = torch.zeros((cap, top_k), dtype=torch.long, device=dev)
+            self.workspace["on_idx"] = torch.full((cap,), -1, dtype=torch.long, device=dev)
+            self.workspace["on_slot"] = torch.zeros((cap, top_k), dtype=torch.long, device=dev)
+            self.workspace["reuse"] = torch.zeros((cap, top_k), dtype=torch.bool, device=dev)
+            self.workspace_capacity = cap
+            self._workspace_top_k = top_k
+
+    def _query_workspace(self, attr_ws, attr_cap, batch_size, compressed_dim):
+        dtype = self.manager.keys_buffer.dtype
+        ws = getattr(self, attr_ws)
+        if (
+            ws is None
+            or batch_size > getattr(self, attr_cap)
+            or ws.shape[1] != compressed_dim
+            or ws.dtype != dtype
+        ):
+            cap = _round_cap(batch_size)
+            ws = torch.zeros((cap, compressed_dim), dtype=dtype, device=self.device)
+            setattr(self, attr_ws, ws)
+            setattr(self, attr_cap, cap)
+        return ws[:batch_size]
+
+    def _ensure_prefill_query_workspace(self, batch_size, compressed_dim):
+        return self._query_workspace(
+            "prefill_query_workspace", "prefill_query_workspace_capacity", batch_size, compressed_dim
+        )
+
+    def _ensure_decode_query_workspace(self, batch_size, compressed_dim):
+        return self._query_workspace(
+            "decode_query_workspace", "decode_query_workspace_capacity", batch_size, compressed_dim
+        )
+
+    # ------------------------------------------------------------ projection
+    def _project_queries_into(self, hidden_states, is_vision_mask, search_dims, query_low, normalize):
+        """q = dtype(x @ P_m + bias_m) (+ L2 normalisation) into ``query_low``
+        (reference search.py:476-498)."""
+        dev = N.require_hip(hidden_states, query_low)
+        dtype = self.manager.keys_buffer.dtype
+        if hidden_states.dtype != dtype:
+            raise RuntimeError(f"hidden_states dtype {hidden_states.dtype} != table dtype {dtype}")
+        x = hidden_states if hidden_states.stride(-1) == 1 else hidden_states.contiguous()
+        n, hidden = x.shape
+        pv, pt = search_dims["pca_vis"], search_dims["pca_txt"]
+        tv, tt = search_dims["proj_t"]
+        isv = N.as_u8(is_vision_mask.reshape(-1).to(device=dev, dtype=torch.bool))
+        N.call(
+            "tm_project", N.dtype_tag(dtype), N.ptr(x), n, hidden, x.stride(0), N.ptr(isv),
+            N.ptr(tv), N.ptr(pv["bias"]), N.ptr(tt), N.ptr(pt["bias"]), 1, hidden,
+            search_dims["compressed_dim"], 1 if normalize else 0, float(CacheConfig.OFFLINE_COSINE_EPS),
+            N.ptr(query_low), query_low.stride(0), None, N.stream(dev),
+        )
+        return query_low
+
+    def _build_prefill_queries(self, hidden_states, is_vision_mask, search_dims):
+        q = self._ensure_prefill_query_workspace(hidden_states.shape[0], search_dims["compressed_dim"])
+        return self._project_queries_into(hidden_states, is_vision_mask, search_dims, q, normalize=True)
+
+    def _build_prefill_queries_offline_dot(self, hidden_states, is_vision_mask, search_dims):
+        q = self._ensure_prefill_query_workspace(hidden_states.shape[0], search_dims["compressed_dim"])
+        return self._project_queries_into(hidden_states, is_vision_mask, search_dims, q, normalize=False)
+
+    def _build_decode_queries(self, hidden_states, is_vision_mask, search_dims):
+        q = self._ensure_decode_query_workspace(hidden_states.shape[0], search_dims["compressed_dim"])
+        return self._project_queries_into(hidden_states, is_vision_mask, search_dims, q, normalize=False)
+
+    # ----------------------------------------------------------- gated search
+    def _gated_into(self, query_low, keys, selected_experts, is_vision_mask, reuse_mask, out_hit, out_idx,
+                    thr_vision, thr_text, cmp, col_offset=0):
+        dev = N.require_hip(query_low, keys, selected_experts, out_hit, out_idx)
+        n, top_k = selected_experts.shape
+        sel = selected_experts if selected_experts.dtype == torch.long else selected_experts.long()
+        isv = N.as_u8(is_vision_mask.reshape(-1).to(device=dev, dtype=torch.bool))
+        rs = None if reuse_mask is None else N.as_u8(reuse_mask.to(device=dev, dtype=torch.bool))
+        if keys.stride(-1) != 1:
+            raise ValueError("keys must have a unit stride along the PCA dimension")
+        N.call(
+            "tm_search_gated", N.dtype_tag(keys.dtype), N.ptr(query_low), n, query_low.stride(0), N.ptr(keys),
+            keys.shape[0], keys.shape[2], keys.shape[3], keys.stride(0), keys.stride(1), keys.stride(2),
+            N.ptr(sel), top_k, sel.stride(0), sel.stride(1), N.ptr(isv), N.ptr(rs),
+            0 if rs is None else rs.stride(0), 0 if rs is None else rs.stride(1), col_offset,
+            float(thr_vision), float(thr_text), cmp, N.ptr(N.as_u8(out_hit)), N.ptr(out_idx),
+            out_hit.stride(0), out_hit.stride(1), N.stream(dev),
+        )
+
+    def _search_prefill_offline_into(self, query_low, selected_experts, is_vision_mask, reuse_mask,
+                                     out_hit_mask, out_cluster_indices):
+        self._gated_into(
+            query_low, self.manager.keys_buffer, selected_experts, is_vision_mask, reuse_mask,
+            out_hit_mask, out_cluster_indices, CacheConfig.OFFLINE_COSINE_THRESHOLD_VISION,
+            CacheConfig.OFFLINE_COSINE_THRESHOLD_TEXT, N.TM_CMP_GE,
+        )
+
+    def _search_decode_offline_from_low_into(self, query_low, selected_experts, is_vision_mask, reuse_mask,
+                                             out_hit_mask, out_cluster_indices, threshold_vision=0.0,
+                                             threshold_text=0.0):
+        self._gated_into(
+            query_low, self.manager.keys_buffer, selected_experts, is_vision_mask, reuse_mask,
+            out_hit_mask, out_cluster_indices, threshold_vision, threshold_text, N.TM_CMP_GE,
+        )
+
+    def _search_offline_dot_from_low_into(self, query_low, selected_experts, is_vision_mask, reuse_mask,
+                                          out_hit_mask, out_cluster_indices):
+        thr = float(CacheConfig.OFFLINE_DOT_THRESHOLD)
+        self._gated_into(
+            query_low, self.manager.raw_keys_buffer, selected_experts, is_vision_mask, reuse_mask,
+            out_hit_mask, out_cluster_indices, thr, thr, N.TM_CMP_GT,
+        )
+
+    def _search_decode_offline_into(self, hidden_states, selected_experts, is_vision_mask, reuse_mask,
+                                    out_hit_mask, out_cluster_indices):
+        q = self._build_decode_queries(hidden_states, is_vision_mask, self._get_search_dims())
+        self._search_decode_offline_from_low_into(
+            q, selected_experts, is_vision_mask, reuse_mask, out_hit_mask, out_cluster_indices
+        )
+
+    def _fresh_outputs(self, selected_experts):
+        bs, top_k = selected_experts.shape
+        return (
+            torch.empty((bs, top_k), dtype=torch.bool, device=self.device),
+            torch.empty((bs, top_k), dtype=torch.long, device=self.device),
+        )
+
+    # ------------------------------------------------------- public searches
+    def search_prefill_offline(self, layer_idx, hidden_states, selected_experts, is_vision_mask, reuse_mask):
+        hit, idx = self._fresh_outputs(selected_experts)
+        q = self._build_prefill_queries(hidden_states, is_vision_mask, self._get_search_dims())
+        self._search_prefill_offline_into(q, selected_experts, is_vision_mask, reuse_mask, hit, idx)
+        return hit, idx
+
+    def search_prefill_offline_dot(self, layer_idx, hidden_states, selected_experts, is_vision_mask, reuse_mask):
+        hit, idx = self._fresh_outputs(selected_experts)
+        q = self._build_prefill_queries_offline_dot(hidden_states, is_vision_mask, self._get_search_dims())
+        self._search_offline_dot_from_low_into(q, selected_experts, is_vision_mask, reuse_mask, hit, idx)
+        return hit, idx
+
+    def search_decode_offline(self, layer_idx, hidden_states, selected_experts, is_vision_mask, reuse_mask):
+        hit, idx = self._fresh_outputs(selected_experts)
+        self._search_decode_offline_into(hidden_states, selected_experts, is_vision_mask, reuse_mask, hit, idx)
+        return hit, idx
+
+    def search_decode_offline_dot(self, layer_idx, hidden_states, selected_experts, is_vision_mask, reuse_mask):
+        hit, idx = self._fresh_outputs(selected_experts)
+        q = self._build_decode_queries(hidden_states, is_vision_mask, self._get_search_dims())
+        self._search_offline_dot_from_low_into(q, selected_experts, is_vision_mask, reuse_mask, hit, idx)
+        return hit, idx
+
+    # ---------------------------------------------------------- hybrid search
+    def _online_state(self):
+        m = self.manager
+        valid = m.online_size if getattr(m, "online_full", False) else getattr(m, "online_ptr", 0)
+        keys = getattr(m, "online_keys", None)
+        ids = getattr(m, "online_expert_ids", None)
+        if keys is None or ids is None or valid <= 0:
+            return None, None, 0
+        return keys, ids, int(valid)
+
+    def _hybrid_into(self, hidden_states, selected_experts, is_vision_mask, keep_k, on_hit, on_idx, off_hit,
+                     off_idx, on_slot):
+        dev = N.require_hip(hidden_states, selected_experts, on_hit, off_idx)
+        dims = self._get_search_dims()
+        dtype = self.manager.keys_buffer.dtype
+        if hidden_states.dtype != dtype:
+            raise RuntimeError(f"hidden_states dtype {hidden_states.dtype} != table dtype {dtype}")
+        x = hidden_states if hidden_states.stride(-1) == 1 else hidden_states.contiguous()
+        n, hidden = x.shape
+        top_k = selected_experts.shape[1]
+        sel = selected_experts if selected_experts.dtype == torch.long else selected_experts.long()
+        num_search = max(top_k - keep_k, 0)
+        on_keys, on_ids, n_valid = self._online_state()
+        if num_search <= 0:
+            n_valid = 0  # nothing is searched: outputs are only cleared
+        if on_ids is not None and on_ids.stride(-1) != 1:
+            raise ValueError("online_expert_ids must have a unit stride along slots")
+        keys = self.manager.keys_buffer
+        isv = N.as_u8(is_vision_mask.reshape(-1).to(device=dev, dtype=torch.bool))
+        q_ws = self._ensure_decode_query_workspace(n, dims["compressed_dim"])
+        pv, pt = dims["pca_vis"], dims["pca_txt"]
+        tv, tt = dims["proj_t"]
+        N.call(
+            "tm_search_hybrid", N.dtype_tag(dtype), N.ptr(x), n, hidden, x.stride(0), N.ptr(isv),
+            N.ptr(tv), N.ptr(pv["bias"]), N.ptr(tt), N.ptr(pt["bias"]), 1, hidden, dims["compressed_dim"],
+            N.ptr(on_keys), 0 if on_keys is None else on_keys.stride(0), n_valid, N.ptr(on_ids),
+            0 if on_ids is None else on_ids.shape[1], 0 if on_ids is None else on_ids.stride(0),
+            N.ptr(keys), keys.shape[0], keys.shape[2], keys.stride(0), keys.stride(1), keys.stride(2),
+            N.ptr(sel), top_k, sel.stride(0), sel.stride(1), int(keep_k), N.ptr(N.as_u8(on_hit)), N.ptr(on_idx),
+            N.ptr(N.as_u8(off_hit)), N.ptr(off_idx), N.ptr(on_slot), on_hit.stride(0), on_hit.stride(1),
+            N.ptr(q_ws), q_ws.numel() * q_ws.element_size(), N.stream(dev),
+        )
+
+    def search_decode_hybrid(self, layer_idx, hidden_states, selected_experts, is_vision_mask, keep_k=None):
+        batch_size, top_k = selected_experts.shape
+        if keep_k is None:
+            keep_k = CacheConfig.KEEP_K
+        keep_k = max(0, min(int(keep_k), top_k))
+        self._ensure_workspace(batch_size, top_k)
+        ws = self.workspace
+        on_hit = ws["on_hit"][:batch_size, :top_k]
+        off_hit = ws["off_hit"][:batch_size, :top_k]
+        off_idx = ws["off_idx"][:batch_size, :top_k]
+        on_idx = ws["on_idx"][:batch_size]
+        on_slot = ws["on_slot"][:batch_size, :top_k]
+        self._hybrid_into(hidden_states, selected_experts, is_vision_mask, keep_k, on_hit, on_idx, off_hit,
+                          off_idx, on_slot)
+        return on_hit, on_idx, off_hit, off_idx, on_slot
+
+    def search_decode_offline_bs1_into(self, hidden_state, selected_experts_row, is_vision, keep_k,
+                                       out_off_hit, out_off_idx):
+        top_k = int(selected_experts_row.shape[0])
+        if top_k == 0:
+            return
+        keep_k = max(0, min(int(keep_k), top_k))
+        hidden = hidden_state.view(1, -1)
+        q = self._build_decode_queries(hidden, is_vision.view(1), self._get_search_dims())
+        thr = float(CacheConfig.OFFLINE_DOT_THRESHOLD)
+        self._gated_into(
+            q, self.manager.raw_keys_buffer, selected_experts_row.view(1, top_k), is_vision.view(1), None,
+            out_off_hit.view(1, top_k), out_off_idx.view(1, top_k), thr, thr, N.TM_CMP_GT, col_offset=keep_k,
+        )
+
+    def search_decode_hybrid_bs1_into(self, hidden_state, selected_experts_row, is_vision, keep_k, out_on_hit,
+                                      out_on_idx, out_off_hit, out_off_idx, out_on_slot):
+        top_k = int(selected_experts_row.shape[0])
+        if top_k == 0:
+            out_on_idx.fill_(-1)
+            return
+        keep_k = max(0, min(int(keep_k), top_k))
+        self._hybrid_into(
+            hidden_state.view(1, -1), selected_experts_row.view(1, top_k), is_vision.view(1), keep_k,
+            out_on_hit.view(1, top_k), out_on_idx.view(1), out_off_hit.view(1, top_k), out_off_idx.view(1, top_k),
+            out_on_slot.view(1, top_k),
+        )

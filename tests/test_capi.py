@@ -1,0 +1,99 @@
+"""CPU checks of the C ABI: the library loads, exports every entry point that
+include/tablemoe.h declares with the same arity as the ctypes prototypes, and
+validates arguments before touching a device (no compute call needs a GPU)."""
+
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from table_moe import _native as N
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "tablemoe.h"
+
+
+def _declarations():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(?:int|int64_t|size_t|const char \*)\s*\*?\s*(tm_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.S):
+        args = m.group(2).strip()
+        n = 0 if args in ("", "void") else len([a for a in args.split(",") if a.strip()])
+        decls[m.group(1)] = n
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return N.load()
+
+
+def test_header_declares_all_prototypes():
+    decls = _declarations()
+    assert len(decls) >= 20
+    assert set(decls) == set(N.PROTOTYPES), set(decls) ^ set(N.PROTOTYPES)
+    for name, nargs in decls.items():
+        assert len(N.PROTOTYPES[name][1]) == nargs, name
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(N.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    for name in _declarations():
+        assert name in exported, name
+        assert getattr(lib, name) is not None
+
+
+def test_library_links_one_hip_runtime():
+    out = subprocess.run(["readelf", "-d", str(N.LIB_PATH)], capture_output=True, text=True, check=True).stdout
+    needed = re.findall(r"NEEDED.*\[(.*)\]", out)
+    hip = [n for n in needed if "amdhip64" in n]
+    assert hip == ["libamdhip64.so.7"], needed  # resolves to the runtime torch already loaded
+
+
+def test_status_strings(lib):
+    assert lib.tm_version() >= 100
+    assert lib.tm_status_string(N.TM_OK) == b"TM_OK"
+    assert lib.tm_status_string(N.TM_EWORKSPACE) == b"TM_EWORKSPACE"
+
+
+def test_keep_count_matches_reference_rule(lib):
+    from oracle import tm_oracle as O
+
+    for n in (0, 1, 2, 5, 32, 255, 256, 4096, 10007):
+        for r in (0.0, 0.1, 0.25, 0.5, 0.6, 0.75, 0.9, 1.0):
+            assert lib.tm_keep_count(n, r) == O.keep_count(n, r), (n, r)
+
+
+def test_argument_validation_without_device(lib):
+    # empty inputs are no-ops
+    assert lib.tm_keep_select(None, 0, 1, 0, None, None, 0, None) == N.TM_OK
+    assert lib.tm_project(N.TM_DT_BF16, None, 0, 2048, 2048, None, C.c_void_p(16), C.c_void_p(16), None, None,
+                          1, 2048, 128, 0, 1e-6, C.c_void_p(16), 128, None, None) == N.TM_OK
+    # bad sizes / enums / dtypes are rejected before any launch
+    assert lib.tm_search_global(N.TM_DT_BF16, None, 10, 128, None, None, 100, 128, None, 128, 9, 0, None, None,
+                                None, 0, None) == N.TM_EINVAL_SHAPE
+    assert b"top_k 9" in lib.tm_last_error()
+    assert lib.tm_search_global(N.TM_DT_F32, None, 10, 128, None, None, 100, 128, None, 128, 1, 0, None, None,
+                                None, 0, None) == N.TM_EINVAL_DTYPE
+    assert lib.tm_search_gated(7, C.c_void_p(16), 4, 64, C.c_void_p(16), 8, 256, 64, 0, 0, 64, C.c_void_p(16), 8,
+                               8, 1, None, None, 0, 0, 0, 0.6, 0.7, 0, C.c_void_p(16), C.c_void_p(16), 8, 1,
+                               None) == N.TM_EINVAL_DTYPE
+    assert lib.tm_search_gated(N.TM_DT_BF16, C.c_void_p(16), 4, 64, C.c_void_p(16), 8, 256, 64, 0, 0, 64,
+                               C.c_void_p(16), 8, 8, 1, None, None, 0, 0, 0, 0.6, 0.7, 5, C.c_void_p(16),
+                               C.c_void_p(16), 8, 1, None) == N.TM_EINVAL_ARG
+    assert lib.tm_renormalize(N.TM_DT_F32, C.c_void_p(16), 8, C.c_void_p(16), 8, 4, 8, 9, None, 0,
+                              C.c_void_p(16), None) == N.TM_EINVAL_ARG
+    assert lib.tm_online_update(N.TM_DT_BF16, C.c_void_p(16), 8, C.c_void_p(16), 8, C.c_void_p(16), 64, 8, None, 0,
+                                65, 8, 8, 0, 64, C.c_void_p(16), C.c_void_p(16), C.c_void_p(16),
+                                None) == N.TM_EINVAL_SHAPE
+    # workspace checks
+    need = lib.tm_search_global_workspace_size(4096, 8192, 128, 1)
+    assert need > 0
+    assert lib.tm_search_global(N.TM_DT_BF16, C.c_void_p(16), 4096, 128, None, C.c_void_p(16), 8192, 128,
+                                C.c_void_p(16), 128, 1, 0, C.c_void_p(16), C.c_void_p(16), C.c_void_p(16),
+                                need - 1, None) == N.TM_EWORKSPACE
+    assert lib.tm_expert_keep_mask_workspace_size(4096, 128) > 0

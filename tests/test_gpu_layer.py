@@ -1,0 +1,410 @@
+"""GPU parity of the router, selection, gather/combine and online-window
+kernels, the drop-in Python surface, and the full mode-G layer at the
+config-2 (Qwen3-VL-30B-A3B prefill) shape."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tm_oracle as O
+from parity_util import ODT, assert_within_ulps, check_pick, check_topk_rows, np64
+from table_moe import _native as N
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def test_single_hip_runtime_in_process(hip_device):
+    """Our library and torch share one HIP runtime instance."""
+    torch.zeros(1, device=hip_device)
+    N.load()
+    paths = set()
+    with open("/proc/self/maps") as f:
+        for line in f:
+            if "libamdhip64" in line:
+                paths.add(line.split()[-1])
+    assert len(paths) == 1, paths
+
+
+# ---------------------------------------------------------------- a1 router
+@pytest.mark.parametrize("n,e,k,renorm", [(4096, 128, 8, False), (300, 64, 6, True), (77, 300, 5, False),
+                                          (5, 2048, 32, False), (1, 8, 8, True)])
+def test_topk_softmax_vs_oracle(hip_device, n, e, k, renorm):
+    from table_moe.ops import qwen_topk_softmax
+
+    g = _gen(61 + e)
+    logits = torch.randn(n, e, generator=g) * 2
+    logits[0, :4] = 20.0  # exact ties above every other logit: lower id first
+    w, ids = qwen_topk_softmax(logits.to(hip_device), k, normalize_topk=renorm)
+    torch.cuda.synchronize()
+    ww, wids, p = O.topk_softmax(np64(logits), k, renorm)
+    gi = np64(ids)
+    check_topk_rows(p, gi, wids, larger_is_better=True, what="router")
+    np.testing.assert_array_equal(gi[0, : min(4, k)], np.arange(min(4, k)))
+    got_p = np.take_along_axis(p, gi, axis=1)
+    if renorm:
+        got_p = got_p / got_p.sum(1, keepdims=True)
+    np.testing.assert_allclose(np64(w), got_p, rtol=2e-6, atol=1e-9)
+
+
+# ------------------------------------------------------------ a3 keep masks
+def test_fixed_keep_mask_reference_kat(hip_device):
+    from table_moe.skip import build_decode_keep_mask, build_fixed_keep_mask
+
+    sel = torch.tensor([[0, 1, 2, 3], [4, 5, 6, 7]], device=hip_device)
+    want = torch.tensor([[True, True, False, False], [True, True, False, False]], device=hip_device)
+    assert torch.equal(build_fixed_keep_mask(sel, 2), want)
+    assert torch.equal(build_decode_keep_mask(sel, None), torch.ones_like(want))
+    assert torch.equal(build_fixed_keep_mask(sel, 0), torch.zeros_like(want))
+
+
+@pytest.mark.parametrize("n,k,e,use_attn,keep_rate", [(4096, 8, 128, True, 0.6), (4096, 8, 128, False, 0.6),
+                                                      (513, 6, 64, True, 0.25), (7, 2, 1000, True, 0.9),
+                                                      (1, 8, 128, False, 0.6)])
+def test_expert_keep_mask_vs_oracle(hip_device, n, k, e, use_attn, keep_rate):
+    from table_moe.skip import build_prefill_keep_mask
+
+    g = _gen(71 + n)
+    sel = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)])
+    w = torch.rand(n, k, generator=g)
+    attn = torch.rand(n, generator=g) if use_attn else None
+    dev = hip_device
+    mask = build_prefill_keep_mask(sel.to(dev), w.to(dev), None if attn is None else attn.to(dev), e, keep_rate)
+    torch.cuda.synchronize()
+    want, sums = O.build_prefill_keep_mask(sel.numpy(), np64(w), None if attn is None else np64(attn), e, keep_rate)
+    got = np64(mask)
+    if not np.array_equal(got, want):
+        # only experts whose exact scores tie the keep boundary within fp32 summation error may differ
+        kept_got = set(sel.numpy()[got].tolist())
+        kept_want = set(sel.numpy()[want].tolist())
+        diff = kept_got ^ kept_want
+        boundary = min(sums[list(kept_want)])
+        for ex in diff:
+            assert abs(sums[ex] - boundary) <= 1e-5 * abs(boundary), (ex, sums[ex], boundary)
+        assert len(kept_got) == len(kept_want)
+
+
+@pytest.mark.parametrize("dtype,target", [(torch.float32, None), (torch.float32, "orig"), (torch.bfloat16, None),
+                                          (torch.float16, "orig")])
+def test_renormalize_vs_oracle(hip_device, dtype, target):
+    from table_moe.skip import renormalize_surviving_weights
+
+    g = _gen(81)
+    n, k = 1000, 8
+    w = torch.rand(n, k, generator=g).to(dtype)
+    m = torch.rand(n, k, generator=g) < 0.5
+    m[:3] = False  # zero-survivor rows
+    dev = hip_device
+    tgt = w.float().sum(-1, keepdim=True).to(dtype) if target else None
+    out = renormalize_surviving_weights(w.to(dev), m.to(dev), None if tgt is None else tgt.to(dev))
+    torch.cuda.synchronize()
+    want = O.renormalize_surviving_weights(np64(w), m.numpy(), None if tgt is None else np64(tgt), dt=ODT[dtype])
+    got = np64(out)
+    assert (got[:3] == 0).all()
+    if dtype == torch.float32:
+        np.testing.assert_allclose(got, want, rtol=5e-7, atol=0)
+    else:
+        assert_within_ulps(got, want, dtype, n_ulp=1, min_exact=0.95)
+
+
+def test_renormalize_reference_kat(hip_device):
+    from table_moe.skip import renormalize_surviving_weights
+
+    dev = hip_device
+    out = renormalize_surviving_weights(torch.tensor([[0.4, 0.3, 0.2, 0.1]], device=dev),
+                                        torch.tensor([[True, True, False, False]], device=dev))
+    torch.testing.assert_close(out.cpu(), torch.tensor([[4 / 7, 3 / 7, 0.0, 0.0]]), atol=1e-6, rtol=0)
+
+
+# ----------------------------------------------------------- a10 gather rows
+@pytest.mark.parametrize("dtype,hidden", [(torch.bfloat16, 2048), (torch.float16, 1004), (torch.float32, 64)])
+def test_gather_rows_bit_exact(hip_device, dtype, hidden):
+    from table_moe.cache_engine import CacheConfig, HybridStorageManager
+
+    g = _gen(91)
+    dev = hip_device
+    old = CacheConfig.MODEL_DTYPE
+    CacheConfig.MODEL_DTYPE = dtype
+    try:
+        mgr = HybridStorageManager(0, 8, hidden, dev)
+    finally:
+        CacheConfig.MODEL_DTYPE = old
+    mgr.values_buffer.copy_(torch.randn(mgr.values_buffer.shape, generator=g).to(dtype))
+    n = 300
+    e = torch.randint(0, 8, (n,), generator=g)
+    m = torch.randint(0, 2, (n,), generator=g)
+    c = torch.randint(0, mgr.values_buffer.shape[2], (n,), generator=g)
+    got = mgr.gather_values(e, m, c)  # host indices, as the reference caller passes them
+    torch.cuda.synchronize()
+    assert got.device.type == "cuda"
+    assert torch.equal(got.cpu(), mgr.values_buffer.cpu()[e, m, c])
+    out = torch.zeros(8, hidden, dtype=dtype, device=dev)
+    slots = torch.tensor([1, 5, 6])
+    mgr.gather_values_decode_bs1(e[:3].to(dev), 1, c[:3].to(dev), slots.to(dev), out)
+    torch.cuda.synchronize()
+    ref = torch.zeros(8, hidden, dtype=dtype)
+    ref[slots] = mgr.values_buffer.cpu()[e[:3], 1, c[:3]]
+    assert torch.equal(out.cpu(), ref)
+
+
+# ----------------------------------------------------------- a12 online window
+def test_online_update_vs_oracle(hip_device):
+    from table_moe.cache_engine import CacheConfig, HybridStorageManager
+
+    g = _gen(101)
+    dev = hip_device
+    H, k = 256, 8
+    saved = (CacheConfig.ONLINE_CACHE_SIZE, CacheConfig.ONLINE_TOP_K, CacheConfig.MODEL_DTYPE)
+    CacheConfig.ONLINE_CACHE_SIZE, CacheConfig.ONLINE_TOP_K, CacheConfig.MODEL_DTYPE = 16, k, torch.bfloat16
+    try:
+        mgr = HybridStorageManager(3, 8, H, dev)
+    finally:
+        CacheConfig.ONLINE_CACHE_SIZE, CacheConfig.ONLINE_TOP_K, CacheConfig.MODEL_DTYPE = saved
+    st = dict(keys=np.zeros((16, H)), ids=np.full((16, k), -1), values=np.zeros((16, k, H)), ptr=0, full=False,
+              size=16)
+    for step, n in enumerate([5, 9, 1, 20, 3, 16, 2]):
+        hid = torch.randn(n, H, generator=g).to(torch.bfloat16)
+        ids = torch.randint(0, 8, (n, k), generator=g)
+        outs = torch.randn(n, k, H, generator=g).to(torch.bfloat16)
+        valid = torch.rand(n, k, generator=g) < 0.7
+        if n == 1:
+            mgr.update_online_cache_bs1(hid[0].to(dev), ids[0].to(dev), outs[0].to(dev), valid[0].to(dev))
+        else:
+            mgr.update_online_cache(hid.to(dev), ids.to(dev), outs.to(dev), valid.to(dev))
+        st = O.online_update(st, np64(hid), ids.numpy(), np64(outs), valid.numpy())
+        torch.cuda.synchronize()
+        assert mgr.online_ptr == st["ptr"] and mgr.online_full == st["full"]
+        np.testing.assert_array_equal(np64(mgr.online_keys), st["keys"])
+        np.testing.assert_array_equal(np64(mgr.online_expert_ids), st["ids"])
+        np.testing.assert_array_equal(np64(mgr.online_values), st["values"])
+
+
+# ------------------------------------------------------- a10+a11 slot combine
+@pytest.mark.parametrize("target", ["one", "orig_sum"])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_slot_combine_vs_oracle(hip_device, target, with_residual):
+    g = _gen(111)
+    dev = hip_device
+    n, k, H, E, K, W, wk = 200, 8, 1024, 16, 64, 8, 8
+    dt = torch.bfloat16
+    w = torch.rand(n, k, generator=g)
+    compute = torch.zeros(n, k, dtype=torch.bool)
+    compute[:, :3] = True
+    off_hit = (torch.rand(n, k, generator=g) < 0.4) & ~compute
+    on_hit = (torch.rand(n, k, generator=g) < 0.3) & ~compute & ~off_hit
+    on_hit[:5] = False
+    off_hit[:5] = False
+    compute[:2] = False  # rows with no survivor
+    sel = torch.randint(0, E, (n, k), generator=g)
+    off_idx = torch.randint(0, K, (n, k), generator=g)
+    on_idx = torch.randint(0, W, (n,), generator=g)
+    on_slot = torch.randint(0, wk, (n, k), generator=g)
+    vis = torch.rand(n, generator=g) < 0.5
+    computed = torch.randn(n, k, H, generator=g).to(dt)
+    values = torch.randn(E, 2, K, H, generator=g).to(dt)
+    online = torch.randn(W, wk, H, generator=g).to(dt)
+    resid = torch.randn(n, H, generator=g).to(dt) if with_residual else None
+    T = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    out = torch.empty(n, H, dtype=dt, device=dev)
+    vd, od, cd = T(values), T(online), T(computed)
+    N.call("tm_slot_combine", N.TM_DT_BF16, n, k, H, T(w).data_ptr(), k, N.as_u8(T(compute)).data_ptr(),
+           cd.data_ptr(), cd.stride(0), cd.stride(1), N.as_u8(T(off_hit)).data_ptr(), T(off_idx).data_ptr(),
+           T(sel).data_ptr(), k, N.as_u8(T(vis)).data_ptr(), vd.data_ptr(), E, K, vd.stride(0), vd.stride(1),
+           vd.stride(2), N.as_u8(T(on_hit)).data_ptr(), T(on_idx).data_ptr(), T(on_slot).data_ptr(), od.data_ptr(), W,
+           wk, od.stride(0), od.stride(1), N.TM_TARGET_ONE if target == "one" else N.TM_TARGET_ORIG_SUM,
+           None if resid is None else T(resid).data_ptr(), H, out.data_ptr(), H, N.stream(dev))
+    torch.cuda.synchronize()
+    # the collected buffer of the reference (cached_layers.py:439-461), built on the host
+    coll = np.zeros((n, k, H))
+    m = np.where(vis.numpy(), 0, 1)
+    cn, vn, onn = np64(computed), np64(values), np64(online)
+    for b in range(n):
+        for s in range(k):
+            if compute[b, s]:
+                coll[b, s] = cn[b, s]
+            if on_hit[b, s]:
+                coll[b, s] = onn[on_idx[b], on_slot[b, s]]
+            if off_hit[b, s]:
+                coll[b, s] = vn[sel[b, s], m[b], off_idx[b, s]]
+    surv = (compute | on_hit | off_hit).numpy()
+    want, _ = O.slot_combine(coll, np64(w), surv, O.BF16, target_mode=target,
+                             residual=None if resid is None else np64(resid))
+    got = np64(out)
+    np.testing.assert_allclose(got, want, atol=1e-2, rtol=2e-3)
+    assert (got[:2] == (0 if resid is None else np64(resid)[:2])).all()
+
+
+# ---------------------------------------------- mode R engine (drop-in API)
+def _mode_r_manager(dev, E=16, H=512, d=64, K=256, seed=121, dtype=torch.bfloat16):
+    from table_moe.cache_engine import CacheConfig, HybridStorageManager
+
+    g = _gen(seed)
+    saved = {k: getattr(CacheConfig, k) for k in ("FIXED_K", "COMPRESSED_DIM", "MODEL_DTYPE", "ONLINE_CACHE_SIZE",
+                                                  "ONLINE_TOP_K")}
+    CacheConfig.FIXED_K, CacheConfig.COMPRESSED_DIM, CacheConfig.MODEL_DTYPE = K, d, dtype
+    CacheConfig.ONLINE_CACHE_SIZE, CacheConfig.ONLINE_TOP_K = 64, 8
+    try:
+        mgr = HybridStorageManager(2, E, H, dev)
+    finally:
+        for k_, v in saved.items():
+            setattr(CacheConfig, k_, v)
+    for mod in ("vision", "text"):
+        p = torch.linalg.qr(torch.randn(H, d, generator=g, dtype=torch.float64))[0].to(dtype)
+        mgr.pca[mod] = {"proj": p.to(dev), "bias": (torch.randn(d, generator=g) * 0.05).to(dtype).to(dev)}
+    for e in range(E):
+        for m in range(2):
+            mgr.load_table_entry(e, m, torch.randn(K, d, generator=g), torch.randn(K, H, generator=g))
+    return mgr, g
+
+
+def test_engine_prefill_offline_end_to_end(hip_device):
+    from table_moe.cache_engine import CacheConfig, VectorSearchEngine
+
+    dev = hip_device
+    mgr, g = _mode_r_manager(dev)
+    eng = VectorSearchEngine(mgr)
+    n, k = 700, 8
+    x = torch.randn(n, 512, generator=g).to(torch.bfloat16)
+    pvn = mgr.pca["vision"]["proj"].cpu()
+    c = mgr.keys_buffer.cpu()[torch.randint(0, 16, (n,), generator=g), 0, torch.randint(0, 256, (n,), generator=g)]
+    x[: n // 2] = (x[: n // 2].float() * 0.3 + (c[: n // 2].float() @ pvn.float().T) * 3).to(torch.bfloat16)
+    sel = torch.stack([torch.randperm(16, generator=g)[:k] for _ in range(n)])
+    vis = torch.rand(n, generator=g) < 0.7
+    reuse = torch.rand(n, k, generator=g) < 0.5
+    hit, idx = eng.search_prefill_offline(0, x.to(dev), sel.to(dev), vis.to(dev), reuse.to(dev))
+    torch.cuda.synchronize()
+    assert hit.dtype == torch.bool and idx.dtype == torch.long and hit.shape == (n, k)
+    # stage 1: the engine's projected + normalised queries
+    q = np64(eng.prefill_query_workspace[:n])
+    pca = mgr.pca
+    ref_q = O.project_queries(np64(x), vis.numpy(), (np64(pca["vision"]["proj"]), np64(pca["vision"]["bias"])),
+                              (np64(pca["text"]["proj"]), np64(pca["text"]["bias"])), True, O.BF16)
+    assert_within_ulps(q, ref_q, torch.bfloat16, n_ulp=1, min_exact=0.9)
+    # stage 2: cosine search on those queries
+    thr_v, thr_t = CacheConfig.OFFLINE_COSINE_THRESHOLD_VISION, CacheConfig.OFFLINE_COSINE_THRESHOLD_TEXT
+    wh, wi, mx, scores = O.search_gated(q, np64(mgr.keys_buffer), sel.numpy(), vis.numpy(), reuse.numpy(), thr_v,
+                                        thr_t, O.CMP_GE)
+    gh, gi = np64(hit), np64(idx)
+    assert 0 < gh.sum() < reuse.sum()
+    for b, s in zip(*np.nonzero(reuse.numpy())):
+        thr = float(np.float32(thr_v if vis[b] else thr_t))
+        assert O.threshold_ok(mx[b, s], thr, gh[b, s], wh[b, s])
+        if gh[b, s]:
+            check_pick(scores[b, s], gi[b, s], int(np.argmax(scores[b, s])), True)
+    assert not gh[~reuse.numpy()].any()
+
+
+def test_engine_decode_hybrid_with_window(hip_device):
+    from table_moe.cache_engine import VectorSearchEngine
+
+    dev = hip_device
+    mgr, g = _mode_r_manager(dev, seed=131)
+    eng = VectorSearchEngine(mgr)
+    H, k = 512, 8
+    hist = torch.randn(40, H, generator=g).to(torch.bfloat16)
+    hist_ids = torch.stack([torch.randperm(16, generator=g)[:k] for _ in range(40)])
+    mgr.update_online_cache(hist.to(dev), hist_ids.to(dev), torch.randn(40, k, H, generator=g).to(torch.bfloat16).to(dev))
+    n = 6
+    x = (hist[torch.tensor([3, 9, 30, 31, 0, 5])].float() + 0.3 * torch.randn(n, H, generator=g)).to(torch.bfloat16)
+    sel = hist_ids[torch.tensor([3, 9, 30, 31, 0, 5])].clone()
+    sel[:, ::2] = torch.randint(0, 16, (n, 4), generator=g)
+    vis = torch.zeros(n, dtype=torch.bool)
+    on_hit, on_idx, off_hit, off_idx, on_slot = eng.search_decode_hybrid(0, x.to(dev), sel.to(dev), vis.to(dev), 4)
+    torch.cuda.synchronize()
+    assert on_hit.data_ptr() == eng.workspace["on_hit"].data_ptr()  # workspace views, as the reference
+    ref = O.search_hybrid(np64(x), vis.numpy(), (np64(mgr.pca["vision"]["proj"]), np64(mgr.pca["vision"]["bias"])),
+                          (np64(mgr.pca["text"]["proj"]), np64(mgr.pca["text"]["bias"])), O.BF16,
+                          np64(mgr.keys_buffer), sel.numpy(), 4, np64(mgr.online_keys), np64(mgr.online_expert_ids),
+                          40)
+    np.testing.assert_array_equal(np64(on_idx), ref["on_idx"])
+    np.testing.assert_array_equal(np64(on_hit), ref["on_hit"])
+    np.testing.assert_array_equal(np64(on_slot), ref["on_slot"])
+    assert np64(on_hit).any()
+    # bs1 entry writes the caller's buffers
+    bufs = [torch.empty(k, dtype=torch.bool, device=dev), torch.empty(1, dtype=torch.long, device=dev),
+            torch.empty(k, dtype=torch.bool, device=dev), torch.empty(k, dtype=torch.long, device=dev),
+            torch.empty(k, dtype=torch.long, device=dev)]
+    eng.search_decode_hybrid_bs1_into(x[1].to(dev), sel[1].to(dev), vis[1].to(dev), 4, *bufs)
+    torch.cuda.synchronize()
+    assert int(bufs[1].item()) == int(on_idx[1].item())
+    assert torch.equal(bufs[0], on_hit[1]) and torch.equal(bufs[4], on_slot[1])
+    assert torch.equal(bufs[2], off_hit[1]) and torch.equal(bufs[3], off_idx[1])
+
+
+def test_engine_rejects_host_tensors():
+    """No CPU fallback: host tensors raise instead of silently running elsewhere."""
+    from table_moe.skip import renormalize_surviving_weights
+
+    with pytest.raises(RuntimeError, match="HIP device"):
+        renormalize_surviving_weights(torch.rand(2, 4), torch.ones(2, 4, dtype=torch.bool))
+
+
+# ------------------------------------------------ mode G: gather + combine
+@pytest.mark.parametrize("nn,hidden,with_residual", [(1, 2048, True), (4, 2048, True), (4, 1004, False)])
+def test_gather_combine_vs_oracle(hip_device, nn, hidden, with_residual):
+    from table_moe.cache_engine import GlobalTable
+
+    g = _gen(141)
+    dev = hip_device
+    n, k, C, d = 257, 8, 500, 64
+    dt = torch.bfloat16
+    values = torch.randn(C, hidden, generator=g).to(dt)
+    slot_out = torch.randn(n, k, hidden, generator=g).to(dt)
+    w = torch.rand(n, k, generator=g) + 0.01
+    idx = torch.randint(0, C, (n, nn), generator=g)
+    dist = torch.rand(n, nn, generator=g) * 10
+    dist[:, 0] = 0.0  # exact hit of a centroid
+    keep = torch.rand(n, generator=g) < 0.6
+    resid = torch.randn(n, hidden, generator=g).to(dt) if with_residual else None
+    tbl = GlobalTable(torch.zeros(C, d, dtype=dt, device=dev), values.to(dev),
+                      (torch.zeros(hidden, d, dtype=dt, device=dev), torch.zeros(d, dtype=dt, device=dev)))
+    out = tbl.gather_combine(keep.to(dev), slot_out.to(dev), w.to(dev), idx.to(dev), dist.to(dev),
+                             None if resid is None else resid.to(dev))
+    torch.cuda.synchronize()
+    r = np.zeros((n, hidden)) if resid is None else np64(resid)
+    want = O.gather_combine(keep.numpy(), np64(slot_out), np64(w), np64(values), idx.numpy(), np64(dist), r, O.BF16)
+    exact = O.gather_combine(keep.numpy(), np64(slot_out), np64(w), np64(values), idx.numpy(), np64(dist), r, O.F32)
+    got = np64(out)
+    np.testing.assert_allclose(got, want, atol=1e-2, rtol=2e-3)
+    assert_within_ulps(got, exact, dt, n_ulp=1, min_exact=0.0)
+
+
+# ------------------------------------------ mode G: full layer at config 2
+def test_layer_forward_config2_end_to_end(hip_device):
+    from table_moe.cache_engine import GlobalTable
+    from table_moe.synth import make_workload
+
+    wl = make_workload(2)
+    dev = hip_device
+    d = wl.to(dev)
+    tbl = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
+    res = tbl.layer_forward(d.x, d.is_vision, d.logits, d.slot_out, d.residual, router_top_k=8, n_nearest=1,
+                            keep_rate=0.6)
+    torch.cuda.synchronize()
+    # router
+    ww, wids, p = O.topk_softmax(np64(wl.logits), 8)
+    check_topk_rows(p, np64(res["ids"]), wids, True, "router")
+    # projection
+    q = np64(res["q"])
+    ref_q = O.project_queries(np64(wl.x), wl.is_vision.numpy(), (np64(wl.proj_vis), np64(wl.bias_vis)),
+                              (np64(wl.proj_txt), np64(wl.bias_txt)), False, O.BF16)
+    assert_within_ulps(q, ref_q, torch.bfloat16, n_ulp=1, min_exact=0.97)
+    # search on the device's queries
+    vals, want_idx, exact = O.global_search(q, np64(wl.centroids), 1)
+    gi = np64(res["idx"])
+    n_mis = check_topk_rows(exact, gi, want_idx, False, "search")
+    assert n_mis <= 3
+    near = wl.cluster_of.numpy() >= 0
+    assert np.mean(gi[near, 0] == wl.cluster_of.numpy()[near]) > 0.99
+    # keep selection: bit-exact on the device's distances
+    gd = np64(res["dist"])
+    keep = np64(res["keep"])
+    assert keep.sum() == O.keep_count(4096, 0.6) == 2457
+    np.testing.assert_array_equal(keep, O.keep_select(gd[:, 0].astype(np.float32).astype(np.float64), 2457))
+    # combine on the device's selections
+    want = O.gather_combine(keep, np64(wl.slot_out), np64(res["weights"]), np64(wl.values), gi, gd, np64(wl.residual),
+                            O.BF16)
+    np.testing.assert_allclose(np64(res["out"]), want, atol=1e-2, rtol=2e-3)

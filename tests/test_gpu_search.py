@@ -1,0 +1,328 @@
+"""GPU parity of the search kernels against the CPU oracle.
+
+Projection (tm_project), gated per-(expert, modality) search
+(tm_search_gated), decode hybrid search (tm_search_hybrid), global-table
+search (tm_search_global) and keep-rate selection (tm_keep_select).  Searches
+are checked stage-wise: the oracle scores the device's own projected queries,
+so a one-ulp difference in a query cannot be mistaken for a search error.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tm_oracle as O
+from parity_util import ODT, assert_within_ulps, check_pick, check_topk_rows, np64
+from table_moe import _native as N
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _rand_proj(g, hidden, dim):
+    return torch.linalg.qr(torch.randn(hidden, dim, generator=g, dtype=torch.float64))[0].float()
+
+
+# ------------------------------------------------------------------ projection
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dim", [16, 64, 128, 256])
+@pytest.mark.parametrize("layout", ["kmajor", "rowmajor"])
+@pytest.mark.parametrize("normalize", [0, 1])
+def test_project_mfma_vs_oracle(hip_device, dtype, dim, layout, normalize):
+    g = _gen(100 + dim)
+    n, hidden = 133, 512
+    x = torch.randn(n, hidden, generator=g).to(dtype)
+    pv, pt = _rand_proj(g, hidden, dim).to(dtype), _rand_proj(g, hidden, dim).to(dtype)
+    bv, bt = (torch.randn(dim, generator=g) * 0.1).to(dtype), (torch.randn(dim, generator=g) * 0.1).to(dtype)
+    vis = torch.rand(n, generator=g) < 0.5
+    dev = hip_device
+    xd, visd = x.to(dev), vis.to(dev)
+    if layout == "kmajor":
+        Pv, Pt, ps_h, ps_d = pv.t().contiguous().to(dev), pt.t().contiguous().to(dev), 1, hidden
+    else:
+        Pv, Pt, ps_h, ps_d = pv.contiguous().to(dev), pt.contiguous().to(dev), dim, 1
+    bvd, btd = bv.to(dev), bt.to(dev)
+    q = torch.empty(n, dim, dtype=dtype, device=dev)
+    qn = torch.empty(n, dtype=torch.float32, device=dev)
+    N.call("tm_project", N.dtype_tag(dtype), xd.data_ptr(), n, hidden, hidden, N.as_u8(visd).data_ptr(),
+           Pv.data_ptr(), bvd.data_ptr(), Pt.data_ptr(), btd.data_ptr(), ps_h, ps_d, dim, normalize, 1e-6,
+           q.data_ptr(), dim, qn.data_ptr(), N.stream(dev))
+    torch.cuda.synchronize()
+    ref = O.project_queries(np64(x), vis.numpy(), (np64(pv), np64(bv)), (np64(pt), np64(bt)), bool(normalize),
+                            ODT[dtype])
+    got = np64(q)
+    assert_within_ulps(got, ref, dtype, n_ulp=1, min_exact=0.95 if normalize else 0.97)
+    np.testing.assert_allclose(np64(qn), (got * got).sum(1), rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype,dim", [(torch.float32, 2), (torch.float32, 64), (torch.bfloat16, 48)])
+def test_project_scalar_path_vs_oracle(hip_device, dtype, dim):
+    g = _gen(7)
+    n, hidden = 37, 96
+    x = torch.randn(n, hidden, generator=g).to(dtype)
+    p = _rand_proj(g, hidden, dim).to(dtype)
+    b = (torch.randn(dim, generator=g) * 0.1).to(dtype)
+    dev = hip_device
+    xd, pd, bd = x.to(dev), p.to(dev), b.to(dev)
+    q = torch.empty(n, dim, dtype=dtype, device=dev)
+    qn = torch.empty(n, dtype=torch.float32, device=dev)
+    N.call("tm_project", N.dtype_tag(dtype), xd.data_ptr(), n, hidden, hidden, None, pd.data_ptr(), bd.data_ptr(),
+           None, None, dim, 1, dim, 1, 1e-6, q.data_ptr(), dim, qn.data_ptr(), N.stream(dev))
+    torch.cuda.synchronize()
+    ref = O.project_queries(np64(x), np.ones(n, bool), (np64(p), np64(b)), None, True, ODT[dtype])
+    if dtype == torch.float32:
+        np.testing.assert_allclose(np64(q), ref, rtol=2e-5, atol=2e-6)
+    else:
+        assert_within_ulps(np64(q), ref, dtype, n_ulp=1, min_exact=0.95)
+    np.testing.assert_allclose(np64(qn), (np64(q) ** 2).sum(1), rtol=2e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------- gated search
+def _norm_rows(t):
+    return t / t.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("cmp", [N.TM_CMP_GE, N.TM_CMP_GT])
+@pytest.mark.parametrize("col_offset", [0, 3])
+def test_search_gated_vs_oracle(hip_device, dtype, cmp, col_offset):
+    g = _gen(11)
+    E, K, d, n, k = 16, 256, 64, 300, 8
+    keys = _norm_rows(torch.randn(E, 2, K, d, generator=g)).to(dtype)
+    q = _norm_rows(torch.randn(n, d, generator=g)).to(dtype)
+    sel = torch.randint(0, E, (n, k), generator=g)
+    bad = torch.rand(n, k, generator=g) < 0.03
+    sel[bad] = torch.where(torch.rand(int(bad.sum()), generator=g) < 0.5, -1, E)  # out-of-range ids: never searched
+    vis = torch.rand(n, generator=g) < 0.6
+    reuse = torch.rand(n, k, generator=g) < 0.6
+    thr_v, thr_t = 0.33, 0.36
+    dev = hip_device
+    qd, kd, seld, visd, rsd = q.to(dev), keys.to(dev), sel.to(dev), vis.to(dev), reuse.to(dev)
+    big_hit = torch.full((n, k + 3), 7, dtype=torch.uint8, device=dev)
+    big_idx = torch.full((n, k + 3), -7, dtype=torch.long, device=dev)
+    hit, idx = big_hit[:, :k], big_idx[:, :k]  # strided outputs
+    N.call("tm_search_gated", N.dtype_tag(dtype), qd.data_ptr(), n, d, kd.data_ptr(), E, K, d, kd.stride(0),
+           kd.stride(1), kd.stride(2), seld.data_ptr(), k, k, 1, N.as_u8(visd).data_ptr(), N.as_u8(rsd).data_ptr(),
+           k, 1, col_offset, thr_v, thr_t, cmp, hit.data_ptr(), idx.data_ptr(), k + 3, 1, N.stream(dev))
+    torch.cuda.synchronize()
+    assert (big_hit[:, k:] == 7).all() and (big_idx[:, k:] == -7).all()
+    want_hit, want_idx, mx, scores = O.search_gated(np64(q), np64(keys), sel.numpy(), vis.numpy(), reuse.numpy(),
+                                                    thr_v, thr_t, cmp, col_offset=col_offset)
+    got_hit, got_idx = np64(hit).astype(bool), np64(idx)
+    assert np.isin(np64(hit), [0, 1]).all()
+    n_hits = 0
+    for b in range(n):
+        thr = float(np.float32(thr_v if vis[b] else thr_t))
+        for s in range(k):
+            if np.isnan(mx[b, s]):
+                assert not got_hit[b, s] and got_idx[b, s] == 0
+                continue
+            assert O.threshold_ok(mx[b, s], thr, got_hit[b, s], want_hit[b, s]), (b, s, mx[b, s])
+            if got_hit[b, s]:
+                n_hits += 1
+                best = int(np.argmax(scores[b, s]))
+                check_pick(scores[b, s], got_idx[b, s], best, True, f"token {b} slot {s}")
+            else:
+                assert got_idx[b, s] == 0
+    assert n_hits > 50  # the thresholds produce both hits and misses
+
+
+def test_engine_reference_kat_dot(hip_device):
+    """table_moe/cache_engine/test_search.py:48-89 on the device: fp32 identity
+    PCA, raw keys {[1,0],[-1,0]} and {[0,0],[-1,0]}, query [1,0]."""
+    from table_moe.cache_engine import CacheConfig, VectorSearchEngine
+
+    class DummyManager:
+        def __init__(self, dev):
+            self.device = dev
+            self.keys_buffer = torch.zeros((2, 2, 2, 2), dtype=torch.float32, device=dev)
+            self.raw_keys_buffer = torch.zeros((2, 2, 2, 2), dtype=torch.float32, device=dev)
+            eye = {"proj": torch.eye(2, device=dev), "bias": torch.zeros(2, device=dev)}
+            self.pca = {"vision": dict(eye), "text": dict(eye)}
+            self.online_expert_ids = None
+
+    dev = hip_device
+    m = DummyManager(dev)
+    m.raw_keys_buffer[0, 0] = torch.tensor([[1.0, 0.0], [-1.0, 0.0]], device=dev)
+    m.raw_keys_buffer[1, 0] = torch.tensor([[0.0, 0.0], [-1.0, 0.0]], device=dev)
+    old = float(CacheConfig.OFFLINE_DOT_THRESHOLD)
+    CacheConfig.OFFLINE_DOT_THRESHOLD = 0.0
+    try:
+        eng = VectorSearchEngine(m)
+        args = dict(layer_idx=0, hidden_states=torch.tensor([[1.0, 0.0], [1.0, 0.0]], device=dev),
+                    selected_experts=torch.tensor([[0], [1]], device=dev),
+                    is_vision_mask=torch.tensor([True, True], device=dev),
+                    reuse_mask=torch.tensor([[True], [True]], device=dev))
+        for fn in (eng.search_prefill_offline_dot, eng.search_decode_offline_dot):
+            hit, idx = fn(**args)
+            assert bool(hit[0, 0].item()) and int(idx[0, 0].item()) == 0
+            assert not bool(hit[1, 0].item())
+    finally:
+        CacheConfig.OFFLINE_DOT_THRESHOLD = old
+
+
+# --------------------------------------------------------------- hybrid search
+@pytest.mark.parametrize("n_valid", [0, 5, 64])
+@pytest.mark.parametrize("keep_k", [0, 4, 8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_search_hybrid_vs_oracle(hip_device, n_valid, keep_k, dtype):
+    g = _gen(21 + n_valid + keep_k)
+    E, K, d, H, n, k, W, wk = 24, 256, 64, 512, 20, 8, 64, 8
+    keys = _norm_rows(torch.randn(E, 2, K, d, generator=g)).to(dtype)
+    pv, pt = _rand_proj(g, H, d).to(dtype), _rand_proj(g, H, d).to(dtype)
+    bv, bt = (torch.randn(d, generator=g) * 0.05).to(dtype), (torch.randn(d, generator=g) * 0.05).to(dtype)
+    on_keys = torch.randn(W, H, generator=g).to(dtype)
+    x = (0.7 * on_keys[torch.randint(0, max(n_valid, 1), (n,), generator=g)].float()
+         + torch.randn(n, H, generator=g)).to(dtype)
+    x[::5] = -x[::5]  # some tokens with no positive online score
+    sel = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(n)])
+    on_ids = torch.randint(0, E, (W, wk), generator=g)
+    on_ids[torch.rand(W, wk, generator=g) < 0.2] = -1
+    vis = torch.rand(n, generator=g) < 0.5
+    dev = hip_device
+    T = lambda t: t.to(dev)  # noqa: E731
+    xd, kd, visd, seld, okd, oid = T(x), T(keys), T(vis), T(sel), T(on_keys), T(on_ids)
+    pvt, ptt, bvd, btd = T(pv.t().contiguous()), T(pt.t().contiguous()), T(bv), T(bt)
+    on_hit = torch.full((n, k), 9, dtype=torch.uint8, device=dev)
+    off_hit = torch.full((n, k), 9, dtype=torch.uint8, device=dev)
+    on_idx = torch.full((n,), -9, dtype=torch.long, device=dev)
+    off_idx = torch.full((n, k), -9, dtype=torch.long, device=dev)
+    on_slot = torch.full((n, k), -9, dtype=torch.long, device=dev)
+    ws = torch.zeros(n, d, dtype=dtype, device=dev)
+    N.call("tm_search_hybrid", N.dtype_tag(dtype), xd.data_ptr(), n, H, H, N.as_u8(visd).data_ptr(), pvt.data_ptr(),
+           bvd.data_ptr(), ptt.data_ptr(), btd.data_ptr(), 1, H, d, okd.data_ptr() if n_valid else None, H, n_valid,
+           oid.data_ptr() if n_valid else None, wk, wk, kd.data_ptr(), E, K, kd.stride(0), kd.stride(1), kd.stride(2),
+           seld.data_ptr(), k, k, 1, keep_k, on_hit.data_ptr(), on_idx.data_ptr(), off_hit.data_ptr(),
+           off_idx.data_ptr(), on_slot.data_ptr(), k, 1, ws.data_ptr(), ws.numel() * ws.element_size(), N.stream(dev))
+    torch.cuda.synchronize()
+    ref = O.search_hybrid(np64(x), vis.numpy(), (np64(pv), np64(bv)), (np64(pt), np64(bt)), ODT[dtype], np64(keys),
+                          sel.numpy(), keep_k, np64(on_keys) if n_valid else None, on_ids.numpy() if n_valid else None,
+                          n_valid)
+    g_on_hit, g_on_idx, g_off_hit = np64(on_hit), np64(on_idx), np64(off_hit)
+    g_off_idx, g_on_slot = np64(off_idx), np64(on_slot)
+    assert np.isin(g_on_hit, [0, 1]).all() and np.isin(g_off_hit, [0, 1]).all()
+    assert (g_on_hit[:, :keep_k] == 0).all() and (g_off_hit[:, :keep_k] == 0).all()
+    # online stage
+    if n_valid and keep_k < k:
+        for b in range(n):
+            sc = ref["on_scores"][b]
+            best = int(np.argmax(sc))
+            if g_on_idx[b] >= 0:
+                check_pick(sc, g_on_idx[b], best, True, f"online token {b}")
+            assert O.threshold_ok(ref["on_max"][b], 0.0, g_on_idx[b] >= 0, ref["on_idx"][b] >= 0)
+        same_online = g_on_idx == ref["on_idx"]
+        np.testing.assert_array_equal(g_on_hit[same_online].astype(bool), ref["on_hit"][same_online])
+        np.testing.assert_array_equal(g_on_slot[same_online], ref["on_slot"][same_online])
+    else:
+        assert (g_on_idx == -1).all() and (g_on_hit == 0).all()
+    # offline stage, scored on the device's own projected queries
+    if keep_k < k:
+        rows = np.nonzero(((g_on_hit == 0)[:, keep_k:]).any(1))[0]
+        qg = np64(ws)
+        assert_within_ulps(qg[rows], ref["q_low"][rows], dtype, n_ulp=1, min_exact=0.9)
+        reuse = np.zeros((n, k), bool)
+        reuse[:, keep_k:] = g_on_hit[:, keep_k:] == 0
+        h, i, mx, scores = O.search_gated(qg, np64(keys), sel.numpy(), vis.numpy(), reuse, 0.0, 0.0, O.CMP_GE)
+        for b in range(n):
+            for s in range(k):
+                if not reuse[b, s]:
+                    assert g_off_hit[b, s] == 0 and g_off_idx[b, s] == 0
+                    continue
+                assert O.threshold_ok(mx[b, s], 0.0, g_off_hit[b, s], h[b, s])
+                if g_off_hit[b, s]:
+                    check_pick(scores[b, s], g_off_idx[b, s], int(np.argmax(scores[b, s])), True, f"off {b},{s}")
+                else:
+                    assert g_off_idx[b, s] == 0
+
+
+# ---------------------------------------------------------- global-table search
+GLOBAL_CASES = [
+    # n, C, dim, top_k, metric, dtype
+    (4096, 8192, 128, 1, "l2", torch.bfloat16),  # config 2 shape
+    (1, 16384, 128, 4, "l2", torch.bfloat16),    # config 3 decode shapes
+    (8, 16384, 128, 4, "l2", torch.bfloat16),
+    (32, 16384, 128, 4, "l2", torch.bfloat16),
+    (256, 1024, 64, 1, "l2", torch.bfloat16),    # config 1 shape (bf16 storage)
+    (300, 1000, 64, 8, "l2", torch.float16),
+    (77, 5000, 256, 2, "dot", torch.bfloat16),
+    (33, 129, 128, 3, "l2", torch.float16),
+    (130, 77, 128, 1, "dot", torch.float16),
+]
+
+
+@pytest.mark.parametrize("n,c,dim,top_k,metric,dtype", GLOBAL_CASES)
+def test_search_global_vs_oracle(hip_device, n, c, dim, top_k, metric, dtype):
+    g = _gen(31 + n + c)
+    cents = torch.randn(c, dim, generator=g)
+    near = cents[torch.randint(0, c, (n,), generator=g)] + 0.2 * torch.randn(n, dim, generator=g)
+    q = torch.where((torch.rand(n, 1, generator=g) < 0.7), near, torch.randn(n, dim, generator=g) * 1.2).to(dtype)
+    cents = cents.to(dtype)
+    dev = hip_device
+    qd, cd = q.to(dev), cents.to(dev)
+    from table_moe.cache_engine.global_table import GlobalTable
+
+    H = 16
+    tbl = GlobalTable(cd, torch.zeros(c, H, dtype=dtype, device=dev),
+                      (torch.zeros(H, dim, dtype=dtype, device=dev), torch.zeros(dim, dtype=dtype, device=dev)),
+                      metric=metric)
+    dist, idx = tbl.search(qd, top_k)
+    torch.cuda.synchronize()
+    vals, want_idx, exact = O.global_search(np64(q), np64(cents), top_k, metric)
+    got_idx = np64(idx)
+    check_topk_rows(exact, got_idx, want_idx, larger_is_better=(metric == "dot"), what=f"global {metric}")
+    got_exact = np.take_along_axis(exact, got_idx, axis=1)
+    scale = np.abs(np64(q) ** 2).sum(1, keepdims=True) + (np64(cents) ** 2).sum(1).max()
+    np.testing.assert_allclose(np64(dist), got_exact, rtol=0, atol=float(scale.max()) * 2e-6 + 1e-5)
+    np.testing.assert_allclose(np64(tbl.c_sqnorm), (np64(cents) ** 2).sum(1), rtol=2e-6)
+
+
+def test_search_global_precomputed_qnorm_and_repeat(hip_device):
+    """The q_sqnorm argument changes nothing; a second call reuses the workspace."""
+    from table_moe.cache_engine.global_table import GlobalTable
+
+    g = _gen(41)
+    dev = hip_device
+    c, dim, H = 3000, 128, 64
+    cents = torch.randn(c, dim, generator=g).to(torch.bfloat16).to(dev)
+    x = torch.randn(500, H, generator=g).to(torch.bfloat16).to(dev)
+    p = _rand_proj(g, H, dim).to(torch.bfloat16).to(dev)
+    tbl = GlobalTable(cents, torch.zeros(c, H, dtype=torch.bfloat16, device=dev),
+                      (p, torch.zeros(dim, dtype=torch.bfloat16, device=dev)))
+    q, qn = tbl.project(x)
+    d1, i1 = [t.clone() for t in tbl.search(q, 1, qn)]
+    d2, i2 = [t.clone() for t in tbl.search(q, 1)]
+    q2, _ = tbl.project(x[:100])
+    d3, i3 = [t.clone() for t in tbl.search(q2, 1)]
+    torch.cuda.synchronize()
+    assert torch.equal(i1, i2) and torch.equal(i1[:100], i3)
+    torch.testing.assert_close(d1, d2, rtol=0, atol=1e-3)
+
+
+# ------------------------------------------------------------- keep selection
+@pytest.mark.parametrize("n", [1, 2, 5, 1023, 1024, 1025, 4096, 5000, 70000])
+@pytest.mark.parametrize("pattern", ["random", "ties", "constant", "signed"])
+def test_keep_select_exact(hip_device, n, pattern):
+    g = _gen(51 + n)
+    if pattern == "random":
+        s = torch.rand(n, generator=g) * 300
+    elif pattern == "ties":
+        s = torch.randint(0, 7, (n,), generator=g).float() * 0.5
+    elif pattern == "constant":
+        s = torch.full((n,), 3.25)
+    else:
+        s = torch.randn(n, generator=g) * 1e3
+        s[: n // 3] = -0.0
+    dev = hip_device
+    col = torch.zeros(n, 4)
+    col[:, 0] = s
+    sd = col.to(dev)[:, 0]  # strided score column
+    keep = torch.empty(n, dtype=torch.bool, device=dev)
+    for n_keep in sorted({0, 1, n // 3, O.keep_count(n, 0.6), n - 1, n}):
+        keep.fill_(False)
+        N.call("tm_keep_select", sd.data_ptr(), n, 4, n_keep, N.as_u8(keep).data_ptr(), None, 0, N.stream(dev))
+        torch.cuda.synchronize()
+        want = O.keep_select(np64(s), n_keep)
+        np.testing.assert_array_equal(np64(keep), want, err_msg=f"n={n} n_keep={n_keep}")
