@@ -80,35 +80,61 @@ def run_layer_bench(cfg_id, steps, warmup, n=None):
 
     def step(i, ev=None):
         r, t, o = reps[i % N_REPLICAS], tables[i % N_REPLICAS], outs[i % N_REPLICAS]
-        if ev is not None:
-            ev[0].record()
-        w, _ = t.route(r.logits, topk)
-        if ev is not None:
-            ev[1].record()
-        q, qn = t.project(r.x, r.is_vision)
-        if ev is not None:
-            ev[2].record()
-        dist, idx = t.search(q, nn, qn)
-        if ev is not None:
-            ev[3].record()
-        keep = t.keep_select(dist[:, 0], t.keep_count(N, kr))
-        if ev is not None:
-            ev[4].record()
-        t.gather_combine(keep, r.slot_out, w, idx, dist, r.residual, o)
-        if ev is not None:
-            ev[5].record()
-        return keep
+        return t.layer_forward(r.x, r.is_vision, r.logits, r.slot_out, r.residual, router_top_k=topk,
+                               n_nearest=nn, keep_rate=kr, out=o, stage_events=ev)["keep"]
 
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
+    # 1) timed region: K layers back to back, no instrumentation inside
+    ev_all = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize()
     t_start = time.perf_counter()
+    ev_all[0].record()
+    for i in range(steps):
+        step(i)
+    ev_all[1].record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    device_us = 1000.0 * ev_all[0].elapsed_time(ev_all[1]) / steps
+    # 1b) the same K layers replayed from HIP graphs (one captured layer per
+    #     replica): identical kernels and work, without host launch cost
+    graphs = []
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(N_REPLICAS):
+            step(i)
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(N_REPLICAS):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(i)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        graphs[i % N_REPLICAS].replay()
+    torch.cuda.synchronize()
+    g_ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    t_g = time.perf_counter()
+    g_ev[0].record()
+    for i in range(steps):
+        graphs[i % N_REPLICAS].replay()
+    g_ev[1].record()
+    torch.cuda.synchronize()
+    graph_elapsed = time.perf_counter() - t_g
+    graph_device_us = 1000.0 * g_ev[0].elapsed_time(g_ev[1]) / steps
+    del graphs
+    # 2) instrumented pass over the same steps: HIP events between the stages
+    #    (an event record adds a few microseconds of its own between stages)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
+    for e in evs:  # create the underlying HIP events first
+        for x in e:
+            x.record()
+    torch.cuda.synchronize()
     for i in range(steps):
         step(i, evs[i])
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t_start
     stage_ms = {s: 0.0 for s in stage_names}
     for e in evs:
         for j, s in enumerate(stage_names):
@@ -117,8 +143,9 @@ def run_layer_bench(cfg_id, steps, warmup, n=None):
     keep = step(0)
     torch.cuda.synchronize()
     n_keep = int(keep.sum().item())
-    return dict(cfg=cfg, wl=wl, elapsed=elapsed, ms_per_step=1000.0 * elapsed / steps, stage_us=stage_us,
-                n_keep=n_keep, bytes=_stage_bytes(cfg, N, n_keep, nn, topk))
+    return dict(cfg=cfg, wl=wl, elapsed=elapsed, eager_ms_per_step=1000.0 * elapsed / steps,
+                ms_per_step=1000.0 * graph_elapsed / steps, graph_device_us=graph_device_us, stage_us=stage_us,
+                device_us=device_us, n_keep=n_keep, bytes=_stage_bytes(cfg, N, n_keep, nn, topk))
 
 
 def cpu_baseline(wl, budget_s=12.0):
@@ -191,9 +218,11 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_name(0)}")
 
     pre = run_layer_bench(2, args.steps, args.warmup)
-    log(f"prefill: {pre['ms_per_step'] * 1000:.1f} us/layer, stages {json.dumps(pre['stage_us'])}")
+    log(f"prefill: {pre['ms_per_step'] * 1000:.1f} us/layer (graph), {pre['eager_ms_per_step'] * 1000:.1f} eager, "
+        f"stages {json.dumps(pre['stage_us'])}")
     dec = run_layer_bench(3, args.steps, args.warmup, n=32)
-    log(f"decode N=32: {dec['ms_per_step'] * 1000:.1f} us/layer, stages {json.dumps(dec['stage_us'])}")
+    log(f"decode N=32: {dec['ms_per_step'] * 1000:.1f} us/layer (graph), {dec['eager_ms_per_step'] * 1000:.1f} eager, "
+        f"stages {json.dumps(dec['stage_us'])}")
 
     cfg = pre["cfg"]
     N, C, d = cfg["n"], cfg["n_cent"], cfg["dim"]
@@ -237,6 +266,11 @@ def main() -> int:
             "replicas": N_REPLICAS,
         },
         "stages_us": {k: round(v, 2) for k, v in st.items()},
+        "timing": "ms_per_step: layers replayed from HIP graphs (one captured tm_table_forward per "
+                  "replica); eager_ms_per_step: one tm_table_forward call per layer from Python",
+        "eager_ms_per_step": pre["eager_ms_per_step"],
+        "eager_tokens_per_s": N / (pre["eager_ms_per_step"] * 1e-3),
+        "layer_device_us": pre["graph_device_us"],
         "layer_hbm_GBps": total_bytes / (sum(st.values()) * 1e-6) / 1e9,
         "search_mfma_tflops": search_tflops,
         "search_mfma_frac": search_tflops / BF16_PEAK_TFLOPS,
@@ -245,6 +279,8 @@ def main() -> int:
             "workload": "config 3: N=32 text tokens, C=16384 x 128 bf16, cached outputs 16384x2048, top-4 "
                         "inverse-distance blend, keep_rate 0.6",
             "us_per_layer": dec["ms_per_step"] * 1000.0,
+            "eager_us_per_layer": dec["eager_ms_per_step"] * 1000.0,
+            "layer_device_us": dec["graph_device_us"],
             "tokens_per_s": 32 / (dec["ms_per_step"] * 1e-3),
             "stages_us": {k: round(v, 2) for k, v in ds.items()},
             "search_hbm_GBps": dec["bytes"]["search"] / (ds["search"] * 1e-6) / 1e9,

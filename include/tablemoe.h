@@ -94,16 +94,36 @@ int tm_topk_softmax(const float *logits, int64_t n_tokens, int32_t n_experts, in
  * ||q|| <= eps become 0.  x [n, hidden] (row stride ld_x), bias_m [dim],
  * P_m element (h, j) at P_m[h*ps_h + j*ps_d] with ps_d == 1 (the reference's
  * row-major [hidden, dim]) or ps_h == 1 (a k-contiguous transposed copy),
- * q_out [n, dim] (row stride ld_q).  q_sqnorm (nullable) receives
+ * or ps_h == ps_d == 0: P_m in the packed layout written by tm_project_pack
+ * (F16/BF16, the fast path: every matrix-core operand is one contiguous
+ * load).  q_out [n, dim] (row stride ld_q).  q_sqnorm (nullable) receives
  * sum_j q[b,j]^2 in fp32 of the stored (rounded) q.
+ * workspace (nullable): >= tm_project_workspace_size(n, hidden, dim) bytes
+ * lets the strided layouts split `hidden` over workgroups (fp32 partials
+ * summed in a fixed order, so results do not depend on it); without it one
+ * workgroup walks all of `hidden` for its rows.  The packed layout needs no
+ * workspace.
  * Limits: dim <= 256; hidden % 8 == 0 and dim in {16, 32, 64, 128, 256} for
- * F16/BF16 (MFMA path).
+ * F16/BF16 (MFMA path; required for the packed layout, whose bias pointers
+ * must also be 16-byte aligned).
  * ====================================================================== */
+size_t tm_project_workspace_size(int64_t n_tokens, int32_t hidden, int32_t dim);
+
+/* Packed projection layout (no reference counterpart: an on-device re-layout
+ * of the reference's [hidden, dim] PCA matrix, made once when a table is
+ * loaded).  For k-step t < ceil(hidden/32), column block c < dim/16 and lane
+ * l < 64, the 8 elements at 16-byte chunk (t*(dim/16) + c)*64 + l are
+ * P[32t + 8(l/16) + e][16c + l%16], e = 0..7, zero where the row index
+ * reaches `hidden`.  Source element (h, j) at src[h*ps_h + j*ps_d] (any
+ * strides).  Limits: F16/BF16, dim in {16, 32, 64, 128, 256}. */
+size_t tm_project_packed_size(int32_t hidden, int32_t dim, int32_t dtype);
+int tm_project_pack(int32_t dtype, const void *src, int32_t hidden, int32_t dim, int64_t ps_h, int64_t ps_d,
+                    void *packed, size_t packed_bytes, tm_stream_t stream);
 int tm_project(int32_t dtype, const void *x, int64_t n_tokens, int32_t hidden, int64_t ld_x,
                const uint8_t *is_vision, const void *proj_vis, const void *bias_vis,
                const void *proj_txt, const void *bias_txt, int64_t ps_h, int64_t ps_d,
                int32_t dim, int32_t normalize, float eps, void *q_out, int64_t ld_q, float *q_sqnorm,
-               tm_stream_t stream);
+               void *workspace, size_t workspace_bytes, tm_stream_t stream);
 
 /* ======================================================================
  * a5/a6/a7 -- gated search of each reused (token, slot) in the table of its
@@ -295,6 +315,70 @@ int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden, const uin
                       int64_t ld_v, const int64_t *idx, const float *dist, int64_t ld_idx,
                       int32_t n_nearest, const void *residual, int64_t ld_r, void *out,
                       int64_t ld_o, tm_stream_t stream);
+
+/* ======================================================================
+ * Mode G -- one MoE layer of the table path in ONE call.
+ * Enqueues, back to back on `stream`: tm_topk_softmax (router) ->
+ * tm_project -> tm_search_global -> tm_keep_select (n_keep =
+ * tm_keep_count(n, keep_rate)) -> tm_gather_combine, with the semantics of
+ * each of those entry points.  One FFI call per layer keeps host overhead
+ * out of the layer time.  The table descriptor is fixed per layer; the I/O
+ * descriptor names the token batch, the caller's output and intermediate
+ * buffers.  `stage_events` (nullable) is an array of 6 hipEvent_t recorded
+ * before the router and after each stage (timing hook).
+ * ====================================================================== */
+typedef struct tm_table_layer {
+  int32_t dtype;            /* TM_DT_BF16 or TM_DT_F16                     */
+  int32_t metric;           /* TM_METRIC_L2 or TM_METRIC_DOT               */
+  int32_t dim;              /* PCA dimension (64, 128 or 256)              */
+  int32_t hidden;           /* model hidden size                           */
+  int64_t n_cent;           /* centroids                                   */
+  const void *cents;        /* [n_cent, dim], row stride ld_c              */
+  int64_t ld_c;
+  const float *c_sqnorm;    /* [n_cent] (tm_centroid_sqnorms)              */
+  const void *values;       /* cached outputs [n_cent, hidden], ld_v       */
+  int64_t ld_v;
+  const void *proj_vis;     /* P_m as in tm_project (ps_h, ps_d)           */
+  const void *bias_vis;
+  const void *proj_txt;     /* nullable: shared with vision                */
+  const void *bias_txt;
+  int64_t ps_h, ps_d;
+} tm_table_layer;
+
+typedef struct tm_layer_io {
+  int64_t n_tokens;
+  const void *x;            /* [n, hidden], row stride ld_x                */
+  int64_t ld_x;
+  const uint8_t *is_vision; /* [n] nullable (all vision)                   */
+  const float *router_logits; /* [n, n_experts] fp32, row stride ld_logits */
+  int64_t ld_logits;
+  int32_t n_experts;
+  int32_t router_top_k;
+  int32_t n_nearest;        /* 1..8                                        */
+  int32_t reserved;
+  double keep_rate;
+  const void *slot_out;     /* [n, router_top_k, hidden] strides so_b, so_s */
+  int64_t so_b, so_s;
+  const void *residual;     /* [n, hidden] nullable, row stride ld_r       */
+  int64_t ld_r;
+  void *out;                /* [n, hidden], row stride ld_o                */
+  int64_t ld_o;
+  /* intermediates, caller buffers (contiguous): */
+  float *weights;           /* [n, router_top_k]                           */
+  int64_t *expert_ids;      /* [n, router_top_k]                           */
+  void *q;                  /* [n, dim]                                    */
+  float *q_sqnorm;          /* [n]                                         */
+  float *dist;              /* [n, n_nearest]                              */
+  int64_t *idx;             /* [n, n_nearest]                              */
+  uint8_t *keep;            /* [n]                                         */
+} tm_layer_io;
+
+/* sizeof(tm_table_layer) for which == 0, sizeof(tm_layer_io) for which == 1
+ * (lets a binding check its mirror of the two structs). */
+size_t tm_struct_size(int32_t which);
+size_t tm_table_forward_workspace_size(const tm_table_layer *table, int64_t n_tokens, int32_t n_nearest);
+int tm_table_forward(const tm_table_layer *table, const tm_layer_io *io, void *workspace,
+                     size_t workspace_bytes, void *const *stage_events, tm_stream_t stream);
 
 #ifdef __cplusplus
 }

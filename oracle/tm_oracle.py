@@ -429,7 +429,8 @@ def online_update(state, hidden, ids, outputs, valid_mask=None):
 # ---------------------------------------------------------------------------
 # a11: slot combine (reference semantics)
 # ---------------------------------------------------------------------------
-def slot_combine(collected, routing_weights, survivor, dt: str, target_mode: str = "one", residual=None):
+def slot_combine(collected, routing_weights, survivor, dt: str, target_mode: str = "one", residual=None,
+                 out_dt: str | None = None):
     """Combine of surviving slots.
 
     target_mode "one": Qwen path, w~ = renormalize(w, survivor).to(dtype),
@@ -438,6 +439,9 @@ def slot_combine(collected, routing_weights, survivor, dt: str, target_mode: str
     target_mode "orig_sum": DeepSeek path, w~ rescaled to sum(w), product and
     sum in the weights' fp32, then rounded
     (table_moe/models/deepseek_vl2/deepseek_layers.py:715-729).
+    ``dt`` is the model dtype (the weights' rounding in the Qwen path); the
+    output is rounded to ``out_dt`` (default ``dt``; F32 gives the value
+    before the final rounding).
     """
     c = np.asarray(collected, dtype=np.float64)
     w = np.asarray(routing_weights, dtype=np.float64)
@@ -449,7 +453,7 @@ def slot_combine(collected, routing_weights, survivor, dt: str, target_mode: str
         y = np.einsum("bs,bsh->bh", wt, c)
     if residual is not None:
         y = y + np.asarray(residual, dtype=np.float64)
-    return round_to(y, dt), wt
+    return round_to(y, dt if out_dt is None else out_dt), wt
 
 
 # ---------------------------------------------------------------------------

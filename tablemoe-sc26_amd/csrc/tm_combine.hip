@@ -69,7 +69,122 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
 
 // ---------------------------------------------------------------------------
 // (4) mode G: out[b] = residual[b] + (keep ? sum_s w~ E[b,s] : sum_j beta V[idx])
+//
+// One workgroup per token row.  The row's sources and coefficients depend on
+// the row only, so every wave derives them itself from wave-uniform loads (no
+// LDS hand-off, no barrier).  Fast path: at most 8 sources; all 16-byte loads
+// of a chunk are issued before the FMAs so they are in flight together.
 // ---------------------------------------------------------------------------
+constexpr int kFastSrc = 8;
+constexpr int kRowsPerGroup = 1;  // rows per workgroup of the fast kernel (more in flight per CU with 1)
+
+// Sources and coefficients of one row (wave-uniform).
+template <int DT>
+struct RowPlan {
+  const typename Elem<DT>::T *src[kFastSrc];
+  float coef[kFastSrc];
+  bool use[kFastSrc];
+};
+
+template <int DT>
+__device__ __forceinline__ void plan_row(RowPlan<DT> &p, int64_t b, const uint8_t *keep,
+                                         const typename Elem<DT>::T *slot_out, int64_t so_b, int64_t so_s,
+                                         const float *w, int64_t ld_w, int top_k,
+                                         const typename Elem<DT>::T *values, int64_t n_cent, int64_t ld_v,
+                                         const int64_t *idx, const float *dist, int64_t ld_idx, int nn) {
+  // every metadata load of the row is issued before any is used
+  float wv[kFastSrc], dv[kFastSrc];
+  int64_t cv[kFastSrc];
+  const bool kept = keep[b] != 0;
+#pragma unroll
+  for (int j = 0; j < kFastSrc; ++j) {
+    wv[j] = (j < top_k) ? w[b * ld_w + j] : 0.f;
+    cv[j] = (j < nn) ? idx[b * ld_idx + j] : -1;
+    dv[j] = (j < nn && nn > 1) ? dist[b * ld_idx + j] : 0.f;
+  }
+  if (kept) {
+    float sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < kFastSrc; ++s) sum += wv[s];
+#pragma unroll
+    for (int s = 0; s < kFastSrc; ++s) {
+      p.use[s] = s < top_k && sum > 0.f;
+      p.coef[s] = p.use[s] ? wv[s] / sum : 0.f;
+      p.src[s] = slot_out + b * so_b + (int64_t)s * so_s;
+    }
+  } else {
+    float inv_sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < kFastSrc; ++j) {
+      p.use[j] = cv[j] >= 0 && cv[j] < n_cent;
+      p.src[j] = values + (p.use[j] ? cv[j] : 0) * ld_v;
+      p.coef[j] = (p.use[j] && nn > 1) ? 1.f / (dv[j] + 1e-6f) : (p.use[j] ? 1.f : 0.f);
+      inv_sum += p.coef[j];
+    }
+    if (nn > 1) {
+#pragma unroll
+      for (int j = 0; j < kFastSrc; ++j) p.coef[j] = p.use[j] ? p.coef[j] / inv_sum : 0.f;
+    }
+  }
+}
+
+// One workgroup streams kRowsPerGroup rows; the next row's plan (metadata
+// loads) is formed before the current row's data is combined, and all 16-byte
+// loads of a chunk are issued before the FMAs.
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kThreads) void gather_combine_fast_kernel(
+    int64_t n, int hidden, const uint8_t *__restrict__ keep, const typename Elem<DT>::T *__restrict__ slot_out,
+    int64_t so_b, int64_t so_s, const float *__restrict__ w, int64_t ld_w, int top_k,
+    const typename Elem<DT>::T *__restrict__ values, int64_t n_cent, int64_t ld_v,
+    const int64_t *__restrict__ idx, const float *__restrict__ dist, int64_t ld_idx, int nn,
+    const typename Elem<DT>::T *__restrict__ residual, int64_t ld_r,
+    typename Elem<DT>::T *__restrict__ out, int64_t ld_o) {
+  using T = typename Elem<DT>::T;
+  const int64_t b0 = (int64_t)blockIdx.x * kRowsPerGroup;
+  const int64_t b1 = (b0 + kRowsPerGroup < n) ? b0 + kRowsPerGroup : n;
+  RowPlan<DT> cur, nxt;
+  plan_row<DT>(cur, b0, keep, slot_out, so_b, so_s, w, ld_w, top_k, values, n_cent, ld_v, idx, dist, ld_idx, nn);
+  for (int64_t b = b0; b < b1; ++b) {
+    if (b + 1 < b1)
+      plan_row<DT>(nxt, b + 1, keep, slot_out, so_b, so_s, w, ld_w, top_k, values, n_cent, ld_v, idx, dist,
+                   ld_idx, nn);
+    const T *res_row = residual ? residual + b * ld_r : nullptr;
+    T *dst = out + b * ld_o;
+    if constexpr (VEC) {
+      for (int h0 = threadIdx.x * 8; h0 < hidden; h0 += kThreads * 8) {
+        float v[kFastSrc][8];
+#pragma unroll
+        for (int j = 0; j < kFastSrc; ++j)
+          if (cur.use[j]) tm_load8<DT>(cur.src[j] + h0, v[j]);
+        float acc[8];
+        if (res_row) {
+          tm_load8<DT>(res_row + h0, acc);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < kFastSrc; ++j)
+          if (cur.use[j]) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = fmaf(cur.coef[j], v[j][i], acc[i]);
+          }
+        tm_store8<DT>(dst + h0, acc);
+      }
+    } else {
+      for (int h = threadIdx.x; h < hidden; h += kThreads) {
+        float acc = res_row ? Elem<DT>::to_f(res_row[h]) : 0.f;
+#pragma unroll
+        for (int j = 0; j < kFastSrc; ++j)
+          if (cur.use[j]) acc = fmaf(cur.coef[j], Elem<DT>::to_f(cur.src[j][h]), acc);
+        dst[h] = Elem<DT>::from_f(acc);
+      }
+    }
+    cur = nxt;
+  }
+}
+
+// General path (more than 8 sources): sources staged through LDS.
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void gather_combine_kernel(
     int hidden, const uint8_t *__restrict__ keep, const typename Elem<DT>::T *__restrict__ slot_out,
@@ -95,24 +210,17 @@ __global__ __launch_bounds__(kThreads) void gather_combine_kernel(
           ++ns;
         }
       }
-    } else if (nn == 1) {
-      const int64_t c = idx[b * ld_idx];
-      if (c >= 0 && c < n_cent) {
-        s_src[0] = values + c * ld_v;
-        s_coef[0] = 1.f;
-        ns = 1;
-      }
     } else {
       float inv_sum = 0.f;
       for (int j = 0; j < nn; ++j) {
         const int64_t c = idx[b * ld_idx + j];
-        if (c >= 0 && c < n_cent) inv_sum += 1.f / (dist[b * ld_idx + j] + 1e-6f);
+        if (c >= 0 && c < n_cent) inv_sum += (nn > 1) ? 1.f / (dist[b * ld_idx + j] + 1e-6f) : 1.f;
       }
       for (int j = 0; j < nn; ++j) {
         const int64_t c = idx[b * ld_idx + j];
         if (c >= 0 && c < n_cent) {
           s_src[ns] = values + c * ld_v;
-          s_coef[ns] = (1.f / (dist[b * ld_idx + j] + 1e-6f)) / inv_sum;
+          s_coef[ns] = (nn > 1) ? (1.f / (dist[b * ld_idx + j] + 1e-6f)) / inv_sum : 1.f;
           ++ns;
         }
       }
@@ -276,13 +384,22 @@ extern "C" int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden
     const bool vec = hidden % 8 == 0 && tm_aligned16(slot_out) && (so_b * E) % 16 == 0 &&
                      (so_s * E) % 16 == 0 && rows_aligned(values, ld_v, E) &&
                      rows_aligned(residual, ld_r, E) && rows_aligned(out, ld_o, E);
+    const bool fast = top_k <= kFastSrc && n_nearest <= kFastSrc;
     auto launch = [&](auto vec_tag) {
       constexpr bool VEC = decltype(vec_tag)::value;
-      hipLaunchKernelGGL((gather_combine_kernel<DT, VEC>), dim3((unsigned)n_tokens), dim3(kThreads), 0,
-                         tm_hip_stream(stream), hidden, keep, static_cast<const T *>(slot_out), so_b,
-                         so_s, weights, ld_w, top_k, static_cast<const T *>(values), n_cent, ld_v, idx,
-                         dist, ld_idx, n_nearest, static_cast<const T *>(residual), ld_r,
-                         static_cast<T *>(out), ld_o);
+      if (fast)
+        hipLaunchKernelGGL((gather_combine_fast_kernel<DT, VEC>), dim3((unsigned)tm_cdiv(n_tokens, kRowsPerGroup)),
+                           dim3(kThreads), 0, tm_hip_stream(stream), n_tokens, hidden, keep,
+                           static_cast<const T *>(slot_out), so_b,
+                           so_s, weights, ld_w, top_k, static_cast<const T *>(values), n_cent, ld_v, idx,
+                           dist, ld_idx, n_nearest, static_cast<const T *>(residual), ld_r,
+                           static_cast<T *>(out), ld_o);
+      else
+        hipLaunchKernelGGL((gather_combine_kernel<DT, VEC>), dim3((unsigned)n_tokens), dim3(kThreads), 0,
+                           tm_hip_stream(stream), hidden, keep, static_cast<const T *>(slot_out), so_b,
+                           so_s, weights, ld_w, top_k, static_cast<const T *>(values), n_cent, ld_v, idx,
+                           dist, ld_idx, n_nearest, static_cast<const T *>(residual), ld_r,
+                           static_cast<T *>(out), ld_o);
     };
     if (vec) launch(std::true_type{});
     else launch(std::false_type{});

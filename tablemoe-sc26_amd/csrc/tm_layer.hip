@@ -1,0 +1,82 @@
+// One MoE layer of the global-table path in one call: the stage entry points
+// enqueued back to back on one stream, the workspace split between them.
+#include "tm_common.h"
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct WsLayout {
+  size_t project, search, keep, total;
+};
+
+WsLayout layout(const tm_table_layer *t, int64_t n, int32_t nn) {
+  WsLayout w;
+  w.project = align_up(tm_project_workspace_size(n, t->hidden, t->dim));
+  w.search = align_up(tm_search_global_workspace_size(n, t->n_cent, t->dim, nn));
+  w.keep = align_up(tm_keep_select_workspace_size(n));
+  w.total = w.project + w.search + w.keep;
+  return w;
+}
+
+int record(void *const *events, int i, hipStream_t s) {
+  if (events == nullptr || events[i] == nullptr) return TM_OK;
+  const hipError_t e = hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), s);
+  if (e != hipSuccess) return tm_fail(TM_EHIP, "tm_table_forward: hipEventRecord: %s", hipGetErrorString(e));
+  return TM_OK;
+}
+
+}  // namespace
+
+extern "C" size_t tm_struct_size(int32_t which) {
+  return which == 0 ? sizeof(tm_table_layer) : (which == 1 ? sizeof(tm_layer_io) : 0);
+}
+
+extern "C" size_t tm_table_forward_workspace_size(const tm_table_layer *table, int64_t n_tokens, int32_t n_nearest) {
+  if (table == nullptr || n_tokens <= 0) return 0;
+  return layout(table, n_tokens, n_nearest).total;
+}
+
+extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, void *workspace,
+                                size_t workspace_bytes, void *const *stage_events, tm_stream_t stream) {
+  TM_REQUIRE(t && io, TM_EINVAL_ARG, "tm_table_forward: null descriptor");
+  const int64_t n = io->n_tokens;
+  TM_REQUIRE(n >= 0, TM_EINVAL_SHAPE, "tm_table_forward: negative token count");
+  if (n == 0) return TM_OK;
+  TM_REQUIRE(io->weights && io->expert_ids && io->q && io->q_sqnorm && io->dist && io->idx && io->keep,
+             TM_EINVAL_ARG, "tm_table_forward: intermediate buffers missing");
+  const WsLayout w = layout(t, n, io->n_nearest);
+  TM_REQUIRE(workspace != nullptr || w.total == 0, TM_EWORKSPACE, "tm_table_forward: workspace missing");
+  TM_REQUIRE(workspace_bytes >= w.total, TM_EWORKSPACE, "tm_table_forward: workspace %zu bytes < %zu",
+             workspace_bytes, w.total);
+  char *ws = static_cast<char *>(workspace);
+  hipStream_t s = tm_hip_stream(stream);
+  int st;
+  if ((st = record(stage_events, 0, s)) != TM_OK) return st;
+  if ((st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k, 0,
+                            io->weights, io->expert_ids, stream)) != TM_OK)
+    return st;
+  if ((st = record(stage_events, 1, s)) != TM_OK) return st;
+  if ((st = tm_project(t->dtype, io->x, n, t->hidden, io->ld_x, io->is_vision, t->proj_vis, t->bias_vis,
+                       t->proj_txt, t->bias_txt, t->ps_h, t->ps_d, t->dim, 0, 1e-6f, io->q, t->dim,
+                       io->q_sqnorm, w.project ? ws : nullptr, w.project, stream)) != TM_OK)
+    return st;
+  if ((st = record(stage_events, 2, s)) != TM_OK) return st;
+  if ((st = tm_search_global(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c,
+                             t->c_sqnorm, t->dim, io->n_nearest, t->metric, io->dist, io->idx,
+                             ws + w.project, w.search, stream)) != TM_OK)
+    return st;
+  if ((st = record(stage_events, 3, s)) != TM_OK) return st;
+  if ((st = tm_keep_select(io->dist, n, io->n_nearest, tm_keep_count(n, io->keep_rate), io->keep,
+                           w.keep ? ws + w.project + w.search : nullptr, w.keep, stream)) != TM_OK)
+    return st;
+  if ((st = record(stage_events, 4, s)) != TM_OK) return st;
+  if ((st = tm_gather_combine(t->dtype, n, t->hidden, io->keep, io->slot_out, io->so_b, io->so_s, io->weights,
+                              io->router_top_k, io->router_top_k, t->values, t->n_cent, t->ld_v, io->idx,
+                              io->dist, io->n_nearest, io->n_nearest, io->residual, io->ld_r, io->out, io->ld_o,
+                              stream)) != TM_OK)
+    return st;
+  return record(stage_events, 5, s);
+}

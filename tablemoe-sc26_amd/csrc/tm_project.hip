@@ -6,11 +6,23 @@
 // rounded to dtype, the quotient is an fp32 division rounded to dtype, and
 // rows with norm <= eps become zero.
 //
-// MFMA path (F16/BF16): a workgroup owns 32 token rows and all `DIM` output
-// columns.  Hidden is walked in 64-wide stages: the x tile is staged in LDS
-// row-major, the P tile transposed (k-contiguous per output column) so both
-// MFMA operands are 16-byte LDS reads.  Tiles that mix modalities run one
-// pass per modality and keep each row's own result.
+// F16/BF16 with P stored k-contiguous (ps_h == 1, the layout the table path
+// keeps): project_direct_kernel below, MFMA operands loaded straight from
+// global memory, no workspace.
+//
+// Other P layouts (LDS-staged MFMA path): a workgroup owns 32 token rows, all
+// `DIM` output columns and one slice of `hidden` (the k split).  The slice is walked in
+// 64-wide stages through double-buffered LDS: the next stage's x and P tiles
+// are fetched into registers while the current stage's MFMAs run, so global
+// latency overlaps compute and each stage needs one barrier.  The x tile is
+// stored row-major, the P tile k-contiguous per output column, so both MFMA
+// operands are 16-byte LDS reads.  Tiles that mix modalities run one pass per
+// modality and keep each row's own result.
+//
+// With a k split, workgroups write fp32 partial sums [split][n][DIM] and
+// project_epilogue_kernel adds them in split order (deterministic), adds the
+// bias, rounds, normalises and stores q.  Without one, the same epilogue runs
+// inside the workgroup.
 #include "tm_mfma.h"
 
 namespace {
@@ -20,19 +32,266 @@ constexpr int kBK = 64;
 constexpr int kPad = 8;
 constexpr int kThreads = 256;
 
-template <int DT, int DIM, bool PK>
+struct ProjPlan {
+  int64_t row_blocks;
+  int nsplit;
+  int k_chunk;  // multiple of kBK
+};
+
+ProjPlan plan_project(int64_t n, int hidden) {
+  ProjPlan p;
+  p.row_blocks = tm_cdiv(n, kBM);
+  const int ksteps = (int)tm_cdiv(hidden, kBK);
+  int64_t want = tm_cdiv(512, p.row_blocks);  // fill the chip: ~2 workgroups per CU
+  if (want > 8) want = 8;                      // bounds the partial traffic of small batches
+  if (want > ksteps) want = ksteps;
+  if (want < 1) want = 1;
+  p.k_chunk = (int)tm_cdiv(ksteps, want) * kBK;
+  p.nsplit = (int)tm_cdiv(hidden, p.k_chunk);
+  return p;
+}
+
+// Row epilogue shared by the fused kernel and the split epilogue: one row is
+// handled by TPR consecutive lanes, 8 columns each.  v[] holds the rounded
+// pre-normalisation values.
+template <int DT, int TPR>
+__device__ __forceinline__ void finish_row(float (&v)[8], int normalize, float eps,
+                                           typename Elem<DT>::T *dst, float *sq_dst) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+#pragma unroll
+  for (int o = 1; o < TPR; o <<= 1) ss += __shfl_xor(ss, o, 64);
+  if (normalize) {
+    const float norm = tm_round<DT>(sqrtf(ss));
+    const float eps_dt = tm_round<DT>(eps);
+    const bool zero_row = !(norm > eps_dt);
+    const float den = fmaxf(norm, eps_dt);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = zero_row ? 0.f : tm_round<DT>(v[i] / den);
+  }
+  float so = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) so = fmaf(v[i], v[i], so);
+#pragma unroll
+  for (int o = 1; o < TPR; o <<= 1) so += __shfl_xor(so, o, 64);
+  if (dst) tm_store8<DT>(dst, v);
+  if (sq_dst) *sq_dst = so;
+}
+
+// Packed path (P in the layout of tm_project_pack).
+//
+// A workgroup owns 16 token rows and all DIM output columns; its KW waves
+// split `hidden` into KW contiguous slices.  Every MFMA operand is one 16-byte
+// load straight from global memory: A = x[row][k..k+7] and B = one lane's
+// chunk of a packed 1 KiB fragment, so each B load of a wave is a contiguous
+// 1 KiB and the k loop has no LDS staging and no barrier.  Each wave keeps
+// kDepth k-steps of loads in flight in a register ring and issues the MFMAs
+// of the oldest.  The KW partial tiles are then added in wave order through
+// LDS (deterministic), the bias is added and the row epilogue runs in the
+// same workgroup.  A tile whose rows mix modalities runs the k loop once per
+// modality present and keeps each row's own result.
+template <int DIM>
+struct DirectCfg {
+  static constexpr int NCB = DIM / 16;             // 16-column MFMA blocks
+  static constexpr int kDepthX = 8;                // k-steps of x (HBM) loads in flight per wave
+  static constexpr int kDepthP = DIM <= 128 ? 4 : 2;  // k-steps of P (L2-resident) loads in flight
+};
+
+template <int DT, int DIM, int KW>
+__global__ __launch_bounds__(64 * KW) void project_direct_kernel(
+    const typename Elem<DT>::T *__restrict__ x, int64_t n, int hidden, int64_t ld_x,
+    const uint8_t *__restrict__ is_vision, const typename Elem<DT>::T *__restrict__ pv,
+    const typename Elem<DT>::T *__restrict__ bv, const typename Elem<DT>::T *__restrict__ pt,
+    const typename Elem<DT>::T *__restrict__ bt, int normalize, float eps,
+    typename Elem<DT>::T *__restrict__ q, int64_t ld_q, float *__restrict__ q_sqnorm) {
+  using T = typename Elem<DT>::T;
+  constexpr int NCB = DirectCfg<DIM>::NCB;
+  constexpr int DX = DirectCfg<DIM>::kDepthX;
+  constexpr int DP = DirectCfg<DIM>::kDepthP;
+  static_assert(DX % DP == 0, "x ring must be a multiple of the P ring");
+  constexpr int kRowPad = DIM + 4;
+  __shared__ float red[KW][16][kRowPad];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t row0 = (int64_t)blockIdx.x * 16;
+  const int64_t arow = row0 + (lane & 15);  // the row this lane loads (lanes l and l+16k share it)
+  const bool arow_ok = arow < n;
+  const T *xrow = x + (arow_ok ? arow : 0) * ld_x;
+
+  const int nks = (hidden + 31) / 32;
+  const int per = (nks + KW - 1) / KW;
+  const int ks_begin = wave * per;
+  const int ks_end = (ks_begin + per < nks) ? ks_begin + per : nks;
+  const int klast = ks_end - 1;  // >= 0: clamp target of every load past this wave's slice
+  const int kq = 8 * (lane >> 4);  // this lane's 8-wide k chunk within a 32-wide k-step
+
+  // Loads are unconditional (addresses clamped into the operands) so the
+  // compiler can count them and keep both rings in flight; rows past n read
+  // row 0 (their results are dropped) and x chunks past `hidden` in a partial
+  // last k-step are zeroed when consumed (the packed P is zero there too).
+  uint4 ar[DX];
+  bool kin[DX];
+  uint4 br[DP][NCB];
+  auto fetch_x = [&](int slot, int ks) {
+    const int kc = ks < klast ? ks : klast;
+    const int kraw = kc * 32 + kq;
+    kin[slot] = kraw < hidden;
+    const int k = kraw < hidden - 8 ? kraw : hidden - 8;  // a valid 16-byte chunk
+    ar[slot] = *reinterpret_cast<const uint4 *>(xrow + k);
+  };
+  // Issue order: the row's modality byte, then the first pass's x ring, then
+  // the bias; loads complete in order, so the modality ballot below waits only
+  // for the first load while the x loads stay in flight.
+  // (unconditional load: without is_vision it reads a byte of x and ignores it)
+  const uint8_t *vsrc = is_vision ? is_vision + (arow_ok ? arow : 0) : reinterpret_cast<const uint8_t *>(x);
+  const uint8_t vis_byte = *vsrc;
+#pragma unroll
+  for (int s = 0; s < DX; ++s) fetch_x(s, ks_begin + s);
+
+  const int amod = !arow_ok ? 2 : ((is_vision == nullptr || vis_byte) ? 0 : 1);
+  const uint32_t vis_bits = (uint32_t)(__ballot(amod == 0) & 0xFFFFull);  // bit r: row r uses P_vis
+  const uint32_t txt_bits = (uint32_t)(__ballot(amod == 1) & 0xFFFFull);
+
+  // Epilogue mapping (TPR threads per row, 8 columns each); both modalities'
+  // bias chunks are loaded now so their latency hides behind the k loop.
+  constexpr int TPR = DIM / 8;
+  constexpr int RPP = 64 * KW / TPR;  // rows per pass
+  constexpr int NPASS = (16 + RPP - 1) / RPP;
+  const int part = tid % TPR;
+  float bias_v[8], bias_t[8];
+  tm_load8<DT>(bv + part * 8, bias_v);
+  tm_load8<DT>(bt + part * 8, bias_t);
+
+  tm_f32x4 fin[NCB];
+#pragma unroll
+  for (int c = 0; c < NCB; ++c) fin[c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto run_pass = [&](const T *P, uint32_t rows_of_pass, bool refetch_x) {
+    tm_f32x4 acc[NCB];
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) acc[c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint4 *pf = reinterpret_cast<const uint4 *>(P) + lane;
+    auto fetch_p = [&](int slot, int ks) {
+      const int kc = ks < klast ? ks : klast;
+#pragma unroll
+      for (int c = 0; c < NCB; ++c) br[slot][c] = pf[((int64_t)kc * NCB + c) * 64];
+    };
+    auto consume = [&](int xs, int ps) {
+      const uint4 a = kin[xs] ? ar[xs] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int c = 0; c < NCB; ++c) acc[c] = tm_mfma16x16x32<DT>(a, br[ps][c], acc[c]);
+    };
+    if (refetch_x) {
+#pragma unroll
+      for (int s = 0; s < DX; ++s) fetch_x(s, ks_begin + s);
+    }
+#pragma unroll
+    for (int s = 0; s < DP; ++s) fetch_p(s, ks_begin + s);
+    int ks0 = ks_begin;
+    for (; ks0 + DX <= ks_end; ks0 += DX) {  // full rings: no guards
+#pragma unroll
+      for (int j = 0; j < DX; ++j) {
+        consume(j, j % DP);
+        fetch_p(j % DP, ks0 + j + DP);
+        fetch_x(j, ks0 + j + DX);
+      }
+    }
+    if (ks0 < ks_end) {  // remainder: x already in the ring, P still streamed
+#pragma unroll
+      for (int j = 0; j < DX; ++j) {
+        if (ks0 + j < ks_end) consume(j, j % DP);
+        fetch_p(j % DP, ks0 + j + DP);
+      }
+    }
+    // keep the rows of this pass: D row of acc[c][i] is 4*(lane>>4)+i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool mine = (rows_of_pass >> (4 * (lane >> 4) + i)) & 1u;
+#pragma unroll
+      for (int c = 0; c < NCB; ++c)
+        if (mine) fin[c][i] = acc[c][i];
+    }
+  };
+  if (vis_bits) run_pass(pv, vis_bits, false);  // uniform branches
+  if (txt_bits) run_pass(pt, txt_bits, vis_bits != 0);
+
+#pragma unroll
+  for (int c = 0; c < NCB; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][4 * (lane >> 4) + i][c * 16 + (lane & 15)] = fin[c][i];
+  __syncthreads();
+
+  // Row epilogue: the wave partials are added in wave order.
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int row = ps * RPP + tid / TPR;
+    const bool in_tile = row < 16;
+    const int64_t gr = row0 + row;
+    const bool ok = in_tile && gr < n;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.f;
+    if (ok) {
+#pragma unroll
+      for (int w = 0; w < KW; ++w) {
+        const float4 a = *reinterpret_cast<const float4 *>(&red[w][row][part * 8]);
+        const float4 b = *reinterpret_cast<const float4 *>(&red[w][row][part * 8 + 4]);
+        v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+        v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+      }
+      const bool vis = (vis_bits >> row) & 1u;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = tm_round<DT>(v[i] + (vis ? bias_v[i] : bias_t[i]));
+    }
+    finish_row<DT, TPR>(v, normalize, eps, ok ? q + gr * ld_q + part * 8 : nullptr,
+                        (ok && part == 0 && q_sqnorm) ? q_sqnorm + gr : nullptr);
+  }
+}
+
+// tm_project_pack: one thread per 16-byte chunk of the packed layout.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void project_pack_kernel(const typename Elem<DT>::T *__restrict__ src,
+                                                                int hidden, int dim, int64_t ps_h, int64_t ps_d,
+                                                                int64_t n_chunks, uint4 *__restrict__ out) {
+  using T = typename Elem<DT>::T;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n_chunks) return;
+  const int ncb = dim / 16;
+  const int lane = (int)(i & 63);
+  const int64_t frag = i >> 6;
+  const int c = (int)(frag % ncb);
+  const int64_t t = frag / ncb;
+  const int col = 16 * c + (lane & 15);
+  const int64_t k0 = 32 * t + 8 * (lane >> 4);
+  T e[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t h = k0 + j;
+    e[j] = (h < hidden) ? src[h * ps_h + (int64_t)col * ps_d] : Elem<DT>::from_f(0.f);
+  }
+  uint4 v;
+  __builtin_memcpy(&v, e, sizeof(v));
+  out[i] = v;
+}
+
+template <int DT, int DIM, bool PK, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void project_mfma_kernel(
     const typename Elem<DT>::T *__restrict__ x, int64_t n, int hidden, int64_t ld_x,
     const uint8_t *__restrict__ is_vision, const typename Elem<DT>::T *__restrict__ pv,
     const typename Elem<DT>::T *__restrict__ bv, const typename Elem<DT>::T *__restrict__ pt,
     const typename Elem<DT>::T *__restrict__ bt, int64_t ps_h, int64_t ps_d, int normalize,
-    float eps, typename Elem<DT>::T *__restrict__ q, int64_t ld_q, float *__restrict__ q_sqnorm) {
+    float eps, typename Elem<DT>::T *__restrict__ q, int64_t ld_q, float *__restrict__ q_sqnorm,
+    int k_chunk, float *__restrict__ partial) {
   using T = typename Elem<DT>::T;
-  constexpr int NBLK = (kBM / 16) * (DIM / 16);          // 16x16 output blocks
+  constexpr int NBLK = (kBM / 16) * (DIM / 16);  // 16x16 output blocks
   constexpr int PER_WAVE = (NBLK + 3) / 4;
-  __shared__ __attribute__((aligned(16))) T xs[kBM][kBK + kPad];
-  __shared__ __attribute__((aligned(16))) T ps[DIM][kBK + kPad];
-  __shared__ float qs[kBM][DIM + 1];
+  constexpr int PCH = (DIM * kBK / 8 + kThreads - 1) / kThreads;  // P chunks per thread per stage
+  __shared__ __attribute__((aligned(16))) T xs[2][kBM][kBK + kPad];
+  __shared__ __attribute__((aligned(16))) T ps[2][DIM][kBK + kPad];
+  __shared__ float qs[SPLIT ? 1 : kBM][SPLIT ? 1 : DIM + 1];
   __shared__ uint8_t row_mod[kBM];
   __shared__ int mod_present[2];
 
@@ -40,11 +299,15 @@ __global__ __launch_bounds__(kThreads) void project_mfma_kernel(
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int64_t row0 = (int64_t)blockIdx.x * kBM;
+  const int split = blockIdx.y;
+  const int k_begin = split * k_chunk;
+  const int k_end = (k_begin + k_chunk < hidden) ? k_begin + k_chunk : hidden;
+  const int nstage = (k_end - k_begin + kBK - 1) / kBK;
 
   if (tid < 2) mod_present[tid] = 0;
   __syncthreads();
   if (tid < kBM) {
-    int64_t r = row0 + tid;
+    const int64_t r = row0 + tid;
     uint8_t m = 0;
     if (r < n) {
       m = (is_vision == nullptr || is_vision[r]) ? 0 : 1;
@@ -57,41 +320,63 @@ __global__ __launch_bounds__(kThreads) void project_mfma_kernel(
   for (int m = 0; m < 2; ++m) {
     if (!mod_present[m]) continue;  // uniform across the workgroup
     const T *P = (m == 0) ? pv : pt;
-    const T *bias = (m == 0) ? bv : bt;
 
     tm_f32x4 acc[PER_WAVE];
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) acc[i] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int k0 = 0; k0 < hidden; k0 += kBK) {
-      // x tile: 32 rows x 64 elements = 256 chunks of 8.
+    uint4 xr;
+    uint4 pr[PCH];
+    auto fetch = [&](int k0) {
       {
         const int r = tid >> 3, c8 = (tid & 7) * 8;
         const int64_t gr = row0 + r;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (gr < n && k0 + c8 < hidden)
-          v = *reinterpret_cast<const uint4 *>(x + gr * ld_x + k0 + c8);
-        *reinterpret_cast<uint4 *>(&xs[r][c8]) = v;
+        xr = make_uint4(0, 0, 0, 0);
+        if (gr < n && k0 + c8 < k_end) xr = *reinterpret_cast<const uint4 *>(x + gr * ld_x + k0 + c8);
       }
-      // P tile, transposed into ps[j][h].
-      if constexpr (PK) {
-        for (int ci = tid; ci < DIM * (kBK / 8); ci += kThreads) {
-          const int j = ci / (kBK / 8), h0 = (ci % (kBK / 8)) * 8;
-          uint4 v = make_uint4(0, 0, 0, 0);
-          if (k0 + h0 < hidden) v = *reinterpret_cast<const uint4 *>(P + (int64_t)j * ps_d + k0 + h0);
-          *reinterpret_cast<uint4 *>(&ps[j][h0]) = v;
-        }
-      } else {
-        for (int ci = tid; ci < kBK * (DIM / 8); ci += kThreads) {
-          const int h = ci / (DIM / 8), j0 = (ci % (DIM / 8)) * 8;
-          uint4 v = make_uint4(0, 0, 0, 0);
-          if (k0 + h < hidden) v = *reinterpret_cast<const uint4 *>(P + (int64_t)(k0 + h) * ps_h + j0);
-          const T *e = reinterpret_cast<const T *>(&v);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) ps[j0 + i][h] = e[i];
+      for (int u = 0; u < PCH; ++u) {
+        const int ci = tid + u * kThreads;
+        pr[u] = make_uint4(0, 0, 0, 0);
+        if (ci < DIM * (kBK / 8)) {
+          if constexpr (PK) {
+            const int j = ci / (kBK / 8), h0 = (ci % (kBK / 8)) * 8;
+            if (k0 + h0 < k_end) pr[u] = *reinterpret_cast<const uint4 *>(P + (int64_t)j * ps_d + k0 + h0);
+          } else {
+            const int h = ci / (DIM / 8), j0 = (ci % (DIM / 8)) * 8;
+            if (k0 + h < k_end) pr[u] = *reinterpret_cast<const uint4 *>(P + (int64_t)(k0 + h) * ps_h + j0);
+          }
         }
       }
+    };
+    auto stash = [&](int buf) {
+      {
+        const int r = tid >> 3, c8 = (tid & 7) * 8;
+        *reinterpret_cast<uint4 *>(&xs[buf][r][c8]) = xr;
+      }
+#pragma unroll
+      for (int u = 0; u < PCH; ++u) {
+        const int ci = tid + u * kThreads;
+        if (ci < DIM * (kBK / 8)) {
+          if constexpr (PK) {
+            const int j = ci / (kBK / 8), h0 = (ci % (kBK / 8)) * 8;
+            *reinterpret_cast<uint4 *>(&ps[buf][j][h0]) = pr[u];
+          } else {
+            const int h = ci / (DIM / 8), j0 = (ci % (DIM / 8)) * 8;
+            const T *e = reinterpret_cast<const T *>(&pr[u]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ps[buf][j0 + i][h] = e[i];
+          }
+        }
+      }
+    };
+
+    fetch(k_begin);
+    for (int st = 0; st < nstage; ++st) {
+      const int buf = st & 1;
+      stash(buf);
       __syncthreads();
+      if (st + 1 < nstage) fetch(k_begin + (st + 1) * kBK);
 #pragma unroll
       for (int ks = 0; ks < kBK / 32; ++ks) {
         const int kk = ks * 32 + 8 * (lane >> 4);
@@ -100,70 +385,99 @@ __global__ __launch_bounds__(kThreads) void project_mfma_kernel(
           const int b = wave + 4 * i;
           if (b < NBLK) {
             const int rb = b % (kBM / 16), cb = b / (kBM / 16);
-            uint4 a = *reinterpret_cast<const uint4 *>(&xs[rb * 16 + (lane & 15)][kk]);
-            uint4 bb = *reinterpret_cast<const uint4 *>(&ps[cb * 16 + (lane & 15)][kk]);
+            const uint4 a = *reinterpret_cast<const uint4 *>(&xs[buf][rb * 16 + (lane & 15)][kk]);
+            const uint4 bb = *reinterpret_cast<const uint4 *>(&ps[buf][cb * 16 + (lane & 15)][kk]);
             acc[i] = tm_mfma16x16x32<DT>(a, bb, acc[i]);
           }
         }
       }
-      __syncthreads();
     }
-    // bias + rounding; keep the rows of this modality.
+    __syncthreads();  // every wave is done with both LDS buffers before the next pass refills them
+
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
       const int b = wave + 4 * i;
       if (b < NBLK) {
         const int rb = b % (kBM / 16), cb = b / (kBM / 16);
         const int col = cb * 16 + (lane & 15);
-        const float bcol = Elem<DT>::to_f(bias[col]);
+        if constexpr (SPLIT) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = rb * 16 + 4 * (lane >> 4) + r;
-          if (row_mod[row] == m) qs[row][col] = tm_round<DT>(acc[i][r] + bcol);
+          for (int r = 0; r < 4; ++r) {
+            const int row = rb * 16 + 4 * (lane >> 4) + r;
+            const int64_t gr = row0 + row;
+            if (gr < n && row_mod[row] == m) partial[((int64_t)split * n + gr) * DIM + col] = acc[i][r];
+          }
+        } else {
+          const float bcol = Elem<DT>::to_f(((m == 0) ? bv : bt)[col]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = rb * 16 + 4 * (lane >> 4) + r;
+            if (row_mod[row] == m) qs[row][col] = tm_round<DT>(acc[i][r] + bcol);
+          }
         }
       }
     }
+  }
+  if constexpr (!SPLIT) {
     __syncthreads();
-  }
-
-  // Row epilogue: 8 threads per row, DIM/8 columns each.
-  constexpr int CPT = DIM / 8;
-  const int row = tid >> 3, part = tid & 7;
-  const int64_t gr = row0 + row;
-  float ss = 0.f;
+    // Row epilogue: DIM/8 threads per row, 8 columns each (DIM >= 16 -> 2..32 threads).
+    constexpr int TPR = DIM / 8;
+    constexpr int RPP = kThreads / TPR;  // rows per pass
+    for (int r0 = 0; r0 < kBM; r0 += RPP) {
+      const int row = r0 + tid / TPR, part = tid % TPR;
+      const int64_t gr = row0 + row;
+      float v[8];
 #pragma unroll
-  for (int c = 0; c < CPT; ++c) {
-    float v = qs[row][part * CPT + c];
-    ss = fmaf(v, v, ss);
-  }
-  ss += __shfl_xor(ss, 1, 64);
-  ss += __shfl_xor(ss, 2, 64);
-  ss += __shfl_xor(ss, 4, 64);
-  float scale_den = 1.f;
-  bool zero_row = false;
-  if (normalize) {
-    const float norm = tm_round<DT>(sqrtf(ss));
-    const float eps_dt = tm_round<DT>(eps);
-    zero_row = !(norm > eps_dt);
-    scale_den = fmaxf(norm, eps_dt);
-  }
-  float ss_out = 0.f;
-  if (gr < n) {
-    T *dst = q + gr * ld_q + part * CPT;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      float v = qs[row][part * CPT + c];
-      if (normalize) v = zero_row ? 0.f : tm_round<DT>(v / scale_den);
-      ss_out = fmaf(v, v, ss_out);
-      dst[c] = Elem<DT>::from_f(v);
+      for (int i = 0; i < 8; ++i) v[i] = (row < kBM) ? qs[row < kBM ? row : 0][part * 8 + i] : 0.f;
+      const bool ok = row < kBM && gr < n;
+      finish_row<DT, TPR>(v, normalize, eps, ok ? q + gr * ld_q + part * 8 : nullptr,
+                          (ok && part == 0 && q_sqnorm) ? q_sqnorm + gr : nullptr);
     }
   }
-  if (q_sqnorm != nullptr) {
-    ss_out += __shfl_xor(ss_out, 1, 64);
-    ss_out += __shfl_xor(ss_out, 2, 64);
-    ss_out += __shfl_xor(ss_out, 4, 64);
-    if (part == 0 && gr < n) q_sqnorm[gr] = ss_out;
+}
+
+// Split epilogue: q[r] = finish(dtype(sum_s partial[s][r] + bias_m)).
+template <int DT, int DIM>
+__global__ __launch_bounds__(kThreads) void project_epilogue_kernel(
+    const float *__restrict__ partial, int nsplit, int64_t n, const uint8_t *__restrict__ is_vision,
+    const typename Elem<DT>::T *__restrict__ bv, const typename Elem<DT>::T *__restrict__ bt, int normalize,
+    float eps, typename Elem<DT>::T *__restrict__ q, int64_t ld_q, float *__restrict__ q_sqnorm) {
+  constexpr int TPR = DIM / 8;
+  constexpr int RPB = kThreads / TPR;
+  const int tid = threadIdx.x;
+  const int64_t r = (int64_t)blockIdx.x * RPB + tid / TPR;
+  const int part = tid % TPR;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  const bool ok = r < n;
+  if (ok) {
+    // splits summed in order; loads of up to 8 splits issued before the adds
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+      float4 a[8], b[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (s0 + u < nsplit) {
+          const float4 *src = reinterpret_cast<const float4 *>(partial + ((int64_t)(s0 + u) * n + r) * DIM + part * 8);
+          a[u] = src[0];
+          b[u] = src[1];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (s0 + u < nsplit) {
+          v[0] += a[u].x; v[1] += a[u].y; v[2] += a[u].z; v[3] += a[u].w;
+          v[4] += b[u].x; v[5] += b[u].y; v[6] += b[u].z; v[7] += b[u].w;
+        }
+      }
+    }
+    const bool vis = is_vision == nullptr || is_vision[r];
+    const typename Elem<DT>::T *bias = (vis ? bv : bt) + part * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = tm_round<DT>(v[i] + Elem<DT>::to_f(bias[i]));
   }
+  finish_row<DT, TPR>(v, normalize, eps, ok ? q + r * ld_q + part * 8 : nullptr,
+                      (ok && part == 0 && q_sqnorm) ? q_sqnorm + r : nullptr);
 }
 
 // Generic path (any dtype, dim <= 256): one thread per output element,
@@ -219,45 +533,102 @@ __global__ __launch_bounds__(kThreads) void project_scalar_kernel(
   }
 }
 
+template <int DT, int DIM>
+int launch_mfma(const ProjPlan &pl, bool split, bool pk, const typename Elem<DT>::T *X, int64_t n, int hidden,
+                int64_t ld_x, const uint8_t *is_vision, const typename Elem<DT>::T *PV,
+                const typename Elem<DT>::T *BV, const typename Elem<DT>::T *PT, const typename Elem<DT>::T *BT,
+                int64_t ps_h, int64_t ps_d, int normalize, float eps, typename Elem<DT>::T *Q, int64_t ld_q,
+                float *q_sqnorm, float *partial, hipStream_t stream) {
+  const int nsplit = split ? pl.nsplit : 1;
+  const int k_chunk = split ? pl.k_chunk : (int)tm_cdiv(hidden, kBK) * kBK;
+  dim3 grid((unsigned)pl.row_blocks, (unsigned)nsplit), block(kThreads);
+  if (split) {
+    if (pk)
+      hipLaunchKernelGGL((project_mfma_kernel<DT, DIM, true, true>), grid, block, 0, stream, X, n, hidden, ld_x,
+                         is_vision, PV, BV, PT, BT, ps_h, ps_d, normalize, eps, Q, ld_q, q_sqnorm, k_chunk, partial);
+    else
+      hipLaunchKernelGGL((project_mfma_kernel<DT, DIM, false, true>), grid, block, 0, stream, X, n, hidden, ld_x,
+                         is_vision, PV, BV, PT, BT, ps_h, ps_d, normalize, eps, Q, ld_q, q_sqnorm, k_chunk, partial);
+    TM_LAUNCH_CHECK("tm_project");
+    constexpr int RPB = kThreads / (DIM / 8);
+    hipLaunchKernelGGL((project_epilogue_kernel<DT, DIM>), dim3((unsigned)tm_cdiv(n, RPB)), block, 0, stream,
+                       partial, nsplit, n, is_vision, BV, BT, normalize, eps, Q, ld_q, q_sqnorm);
+    TM_LAUNCH_CHECK("tm_project(epilogue)");
+    return TM_OK;
+  }
+  if (pk)
+    hipLaunchKernelGGL((project_mfma_kernel<DT, DIM, true, false>), grid, block, 0, stream, X, n, hidden, ld_x,
+                       is_vision, PV, BV, PT, BT, ps_h, ps_d, normalize, eps, Q, ld_q, q_sqnorm, k_chunk, nullptr);
+  else
+    hipLaunchKernelGGL((project_mfma_kernel<DT, DIM, false, false>), grid, block, 0, stream, X, n, hidden, ld_x,
+                       is_vision, PV, BV, PT, BT, ps_h, ps_d, normalize, eps, Q, ld_q, q_sqnorm, k_chunk, nullptr);
+  TM_LAUNCH_CHECK("tm_project");
+  return TM_OK;
+}
+
 template <int DT>
 int launch_project(const void *x, int64_t n, int hidden, int64_t ld_x, const uint8_t *is_vision,
                    const void *pv, const void *bv, const void *pt, const void *bt, int64_t ps_h,
                    int64_t ps_d, int dim, int normalize, float eps, void *q, int64_t ld_q,
-                   float *q_sqnorm, hipStream_t stream) {
+                   float *q_sqnorm, void *workspace, size_t workspace_bytes, hipStream_t stream) {
   using T = typename Elem<DT>::T;
   const T *X = static_cast<const T *>(x);
   const T *PV = static_cast<const T *>(pv), *BV = static_cast<const T *>(bv);
   const T *PT = static_cast<const T *>(pt ? pt : pv), *BT = static_cast<const T *>(pt ? bt : bv);
   T *Q = static_cast<T *>(q);
+  const bool packed = ps_h == 0 && ps_d == 0;
   const bool pk = (ps_h == 1);
+  const int E = Elem<DT>::kBytes;
   bool mfma_ok = DT != TM_DT_F32 && (hidden % 8 == 0) && (dim == 16 || dim == 32 || dim == 64 ||
                                                            dim == 128 || dim == 256);
-  if (mfma_ok) {
-    const int E = Elem<DT>::kBytes;
+  if (mfma_ok)
     mfma_ok = tm_aligned16(x) && ((ld_x * E) % 16 == 0) && tm_aligned16(pv) && tm_aligned16(PT) &&
-              (pk ? ((ps_d * E) % 16 == 0) : ((ps_h * E) % 16 == 0));
+              (pk ? ((ps_d * E) % 16 == 0) : ((ps_h * E) % 16 == 0)) && tm_aligned16(q) && ((ld_q * E) % 16 == 0);
+  if (packed) {
+    TM_REQUIRE(mfma_ok && tm_aligned16(BV) && tm_aligned16(BT), TM_EINVAL_ARG,
+               "tm_project: the packed layout needs F16/BF16, hidden %% 8 == 0, dim in {16..256} and "
+               "16-byte aligned x/q rows and bias");
+  }
+  if constexpr (DT != TM_DT_F32) {
+  if (packed) {
+    // 16 rows per workgroup, 4 waves splitting hidden
+    const dim3 grid((unsigned)tm_cdiv(n, 16));
+    switch (dim) {
+#define TM_PROJ_PACKED(D)                                                                                    \
+  case D:                                                                                                  \
+    hipLaunchKernelGGL((project_direct_kernel<DT, D, 4>), grid, dim3(256), 0, stream, X, n, hidden, ld_x,     \
+                       is_vision, PV, BV, PT, BT, normalize, eps, Q, ld_q, q_sqnorm);                       \
+    TM_LAUNCH_CHECK("tm_project");                                                                         \
+    return TM_OK;
+      TM_PROJ_PACKED(16)
+      TM_PROJ_PACKED(32)
+      TM_PROJ_PACKED(64)
+      TM_PROJ_PACKED(128)
+      TM_PROJ_PACKED(256)
+#undef TM_PROJ_PACKED
+      default: break;
+    }
   }
   if (mfma_ok) {
-    dim3 grid((unsigned)tm_cdiv(n, kBM)), block(kThreads);
-#define TM_PROJ_LAUNCH(D)                                                                        \
-  if (dim == D) {                                                                                \
-    if (pk)                                                                                      \
-      hipLaunchKernelGGL((project_mfma_kernel<DT, D, true>), grid, block, 0, stream, X, n, hidden, \
-                         ld_x, is_vision, PV, BV, PT, BT, ps_h, ps_d, normalize, eps, Q, ld_q,   \
-                         q_sqnorm);                                                              \
-    else                                                                                         \
-      hipLaunchKernelGGL((project_mfma_kernel<DT, D, false>), grid, block, 0, stream, X, n,      \
-                         hidden, ld_x, is_vision, PV, BV, PT, BT, ps_h, ps_d, normalize, eps, Q,  \
-                         ld_q, q_sqnorm);                                                        \
+    const ProjPlan pl = plan_project(n, hidden);
+    const size_t need = (size_t)pl.nsplit * (size_t)n * (size_t)dim * sizeof(float);
+    const bool split = pl.nsplit > 1 && workspace != nullptr && workspace_bytes >= need &&
+                       tm_aligned16(workspace);
+    float *partial = static_cast<float *>(workspace);
+    switch (dim) {
+#define TM_PROJ_CASE(D)                                                                                     \
+  case D:                                                                                                  \
+    return launch_mfma<DT, D>(pl, split, pk, X, n, hidden, ld_x, is_vision, PV, BV, PT, BT, ps_h, ps_d,     \
+                              normalize, eps, Q, ld_q, q_sqnorm, partial, stream);
+      TM_PROJ_CASE(16)
+      TM_PROJ_CASE(32)
+      TM_PROJ_CASE(64)
+      TM_PROJ_CASE(128)
+      TM_PROJ_CASE(256)
+#undef TM_PROJ_CASE
+      default: break;
+    }
   }
-    TM_PROJ_LAUNCH(16)
-    TM_PROJ_LAUNCH(32)
-    TM_PROJ_LAUNCH(64)
-    TM_PROJ_LAUNCH(128)
-    TM_PROJ_LAUNCH(256)
-#undef TM_PROJ_LAUNCH
-    TM_LAUNCH_CHECK("tm_project");
-    return TM_OK;
   }
   const int rows_per_block = kThreads / dim;
   dim3 grid((unsigned)tm_cdiv(n, rows_per_block)), block(kThreads);
@@ -269,24 +640,60 @@ int launch_project(const void *x, int64_t n, int hidden, int64_t ld_x, const uin
 
 }  // namespace
 
+extern "C" size_t tm_project_workspace_size(int64_t n_tokens, int32_t hidden, int32_t dim) {
+  if (n_tokens <= 0 || hidden <= 0 || dim <= 0) return 0;
+  const ProjPlan pl = plan_project(n_tokens, hidden);
+  if (pl.nsplit <= 1) return 0;
+  return (size_t)pl.nsplit * (size_t)n_tokens * (size_t)dim * sizeof(float);
+}
+
 extern "C" int tm_project(int32_t dtype, const void *x, int64_t n_tokens, int32_t hidden,
                           int64_t ld_x, const uint8_t *is_vision, const void *proj_vis,
                           const void *bias_vis, const void *proj_txt, const void *bias_txt,
                           int64_t ps_h, int64_t ps_d, int32_t dim, int32_t normalize, float eps,
-                          void *q_out, int64_t ld_q, float *q_sqnorm, tm_stream_t stream) {
+                          void *q_out, int64_t ld_q, float *q_sqnorm, void *workspace,
+                          size_t workspace_bytes, tm_stream_t stream) {
   TM_REQUIRE(n_tokens >= 0 && hidden > 0 && dim > 0 && dim <= 256, TM_EINVAL_SHAPE,
              "tm_project: bad sizes n=%lld hidden=%d dim=%d", (long long)n_tokens, hidden, dim);
   TM_REQUIRE(ld_x >= hidden && ld_q >= dim, TM_EINVAL_SHAPE, "tm_project: bad row strides");
-  TM_REQUIRE(ps_h == 1 || ps_d == 1, TM_EINVAL_SHAPE,
-             "tm_project: projection needs a unit stride along hidden or dim");
+  TM_REQUIRE(ps_h == 1 || ps_d == 1 || (ps_h == 0 && ps_d == 0), TM_EINVAL_SHAPE,
+             "tm_project: projection needs a unit stride along hidden or dim, or the packed layout");
   TM_REQUIRE(proj_vis && bias_vis && q_out && (n_tokens == 0 || x), TM_EINVAL_ARG,
              "tm_project: null pointer");
   TM_REQUIRE((proj_txt == nullptr) == (bias_txt == nullptr), TM_EINVAL_ARG,
              "tm_project: proj_txt and bias_txt must both be set or both be NULL");
+  TM_REQUIRE(n_tokens < ((int64_t)1 << 31) / 32, TM_EINVAL_SHAPE, "tm_project: too many tokens");
   if (n_tokens == 0) return TM_OK;
   return TM_DISPATCH_DTYPE(dtype, DT, [&] {
     return launch_project<DT>(x, n_tokens, hidden, ld_x, is_vision, proj_vis, bias_vis, proj_txt,
                               bias_txt, ps_h, ps_d, dim, normalize, eps, q_out, ld_q, q_sqnorm,
-                              tm_hip_stream(stream));
+                              workspace, workspace_bytes, tm_hip_stream(stream));
+  });
+}
+
+extern "C" size_t tm_project_packed_size(int32_t hidden, int32_t dim, int32_t dtype) {
+  if (hidden <= 0 || (dim != 16 && dim != 32 && dim != 64 && dim != 128 && dim != 256) ||
+      (dtype != TM_DT_BF16 && dtype != TM_DT_F16))
+    return 0;
+  return (size_t)tm_cdiv(hidden, 32) * 32 * (size_t)dim * 2;
+}
+
+extern "C" int tm_project_pack(int32_t dtype, const void *src, int32_t hidden, int32_t dim, int64_t ps_h,
+                               int64_t ps_d, void *packed, size_t packed_bytes, tm_stream_t stream) {
+  const size_t need = tm_project_packed_size(hidden, dim, dtype);
+  TM_REQUIRE(dtype == TM_DT_BF16 || dtype == TM_DT_F16, TM_EINVAL_DTYPE, "tm_project_pack: dtype %d", dtype);
+  TM_REQUIRE(need > 0, TM_EINVAL_SHAPE, "tm_project_pack: bad sizes hidden=%d dim=%d", hidden, dim);
+  TM_REQUIRE(src && packed && tm_aligned16(packed), TM_EINVAL_ARG, "tm_project_pack: null or unaligned pointer");
+  TM_REQUIRE(packed_bytes >= need, TM_EWORKSPACE, "tm_project_pack: %zu bytes given, %zu needed", packed_bytes,
+             need);
+  const int64_t n_chunks = (int64_t)(need / 16);
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    if constexpr (DT != TM_DT_F32) {
+      hipLaunchKernelGGL((project_pack_kernel<DT>), dim3((unsigned)tm_cdiv(n_chunks, kThreads)), dim3(kThreads), 0,
+                         tm_hip_stream(stream), static_cast<const typename Elem<DT>::T *>(src), hidden, dim, ps_h,
+                         ps_d, n_chunks, static_cast<uint4 *>(packed));
+      TM_LAUNCH_CHECK("tm_project_pack");
+    }
+    return TM_OK;
   });
 }

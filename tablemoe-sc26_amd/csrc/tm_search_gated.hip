@@ -265,6 +265,8 @@ extern "C" int tm_search_hybrid(int32_t dtype, const void *x, int64_t n_tokens, 
   TM_REQUIRE(n_tokens < (int64_t)0x7fffffff, TM_EINVAL_SHAPE, "tm_search_hybrid: too many tokens");
   if (keep_k < 0) keep_k = 0;
   if (keep_k > top_k) keep_k = top_k;
+  // nothing searched: outputs are only cleared (on_idx = -1), no window lookup
+  if (keep_k == top_k) n_online_valid = 0;
   return TM_DISPATCH_DTYPE(dtype, DT, [&] {
     using T = typename Elem<DT>::T;
     const int E = Elem<DT>::kBytes;

@@ -5,37 +5,60 @@
 // query) and the n x C score matrix is never written.
 //
 // Layout of the contraction: D^T = C . Q^T with v_mfma_f32_32x32x16.  The A
-// operand is a 32-centroid slab read from LDS, the B operand is the wave's 32
-// queries held in registers for the whole kernel (DIM/16 k-steps).  In the
-// result each lane owns ONE query (column l%32) and 16 centroids, so the
-// running top-k is a per-lane register list and needs no cross-lane traffic
-// until the very end.
+// operand is a 32-centroid slab, the B operand is one slab of 32 queries held
+// in registers for the whole kernel (DIM/16 k-steps).  In the result each
+// lane owns ONE query (column l%32) and 16 centroids, so the running top-k is
+// a per-lane register list with no cross-lane traffic until the end.
 //
-// Grid = (row blocks) x (centroid splits).  Each workgroup writes its top-k
-// per query as packed keys (orderable(d') << 32 | c) into the workspace;
-// tm_merge_kernel reduces the splits.  Packed keys make the order total:
-// smaller distance first, then lower centroid index.
+// Two launch shapes:
+//  - tile kernel (n > 64): a workgroup owns 256 queries (4 waves x 2 slabs of
+//    32, so each A fragment read from LDS feeds two MFMAs) and one chunk of
+//    centroids, staged 64 at a time through double-buffered LDS with the next
+//    stage prefetched into registers while the current one is multiplied;
+//  - stream kernel (n <= 64, decode): the workgroup's waves share the queries
+//    and each wave streams its own 32-centroid blocks straight from global
+//    memory (next block prefetched), so a small batch still reads the table
+//    across the whole chip.
+// Invalid centroid positions (past the end of the chunk) carry an infinite
+// penalty instead of a branch.
+//
+// Each workgroup writes its top-k per query as packed keys
+// (orderable(d') << 32 | c) into the workspace; merge_kernel reduces the
+// splits.  Packed keys make the order total: smaller distance first, then
+// lower centroid index.
 #include "tm_mfma.h"
 
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kStage = 128;  // centroids per LDS stage (4 slabs of 32)
+constexpr int kStage = 64;  // centroids per LDS stage of the tile kernel
 constexpr int kPad = 8;
+constexpr int kQS = 2;      // query slabs per wave in the tile kernel
+constexpr int kTileRows = 4 * kQS * 32;
+constexpr int kStreamBlocksPerWave = 2;
 
 struct SplitPlan {
-  int rw;        // query slabs (of 32) per workgroup: 4, or 1 for small n
+  bool stream;  // small-n shape
+  int qs;       // query slabs per wave
   int64_t row_blocks;
   int64_t nsplit;
-  int64_t chunk;  // centroids per split (multiple of kStage)
+  int64_t chunk;  // centroids per split
 };
 
 SplitPlan plan_split(int64_t n, int64_t c) {
   SplitPlan p;
-  p.rw = (n <= 32) ? 1 : 4;
-  p.row_blocks = tm_cdiv(n, 32 * p.rw);
+  p.stream = n <= 64;
+  if (p.stream) {
+    p.qs = n <= 32 ? 1 : 2;
+    p.row_blocks = 1;
+    p.chunk = 4 * 32 * kStreamBlocksPerWave;  // each wave: kStreamBlocksPerWave blocks of 32
+    p.nsplit = tm_cdiv(c, p.chunk);
+    return p;
+  }
+  p.qs = kQS;
+  p.row_blocks = tm_cdiv(n, kTileRows);
   const int64_t max_split = tm_cdiv(c, kStage);
-  int64_t want = tm_cdiv(1024, p.row_blocks);  // aim at ~1024 workgroups (4 per CU)
+  int64_t want = tm_cdiv(512, p.row_blocks);  // ~2 workgroups per CU
   if (want < 1) want = 1;
   if (want > max_split) want = max_split;
   p.chunk = tm_cdiv(tm_cdiv(c, want), kStage) * kStage;
@@ -62,119 +85,261 @@ __device__ __forceinline__ void list_insert(uint64_t (&l)[K], uint64_t x) {
   }
 }
 
-template <int DT, int DIM, int K, int RW, int METRIC>
-__global__ __launch_bounds__(kThreads) void search_global_kernel(
+// Running best of one lane: top-1 as (value, index) registers, top-k as a
+// packed-key list.
+template <int K>
+struct Best {
+  float d;
+  int i;
+  uint64_t l[K];
+  __device__ __forceinline__ void init() {
+    d = __builtin_huge_valf();
+    i = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < K; ++j) l[j] = ~0ull;
+  }
+  // candidates arrive in increasing centroid order within a lane
+  __device__ __forceinline__ void push(float dp, int c) {
+    if constexpr (K == 1) {
+      if (dp < d) { d = dp; i = c; }
+    } else {
+      const uint64_t key = make_key(dp, c);
+      if (key < l[K - 1]) list_insert<K>(l, key);
+    }
+  }
+  __device__ __forceinline__ void finalize() {
+    if constexpr (K == 1) l[0] = (i == 0x7fffffff || d == __builtin_huge_valf()) ? ~0ull : make_key(d, i);
+  }
+  // merge with the lane `o` lanes away (same query, other centroids)
+  __device__ __forceinline__ void merge_xor(int o) {
+    uint64_t other[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) other[j] = __shfl_xor(l[j], o, 64);
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+      if (other[j] < l[K - 1]) list_insert<K>(l, other[j]);
+  }
+};
+
+// Epilogue of one 32x32 block: lane owns query (l%32) and the 16 centroids
+// m = 8*(i/4) + 4*(l/32) + (i%4) of the block.  pen[i] = ||c||^2 (L2) or
+// 0 (dot) for valid centroids, +inf past the end.
+template <int K, int METRIC>
+__device__ __forceinline__ void block_epilogue(const tm_f32x16 &acc, const float (&pen)[16], int cbase,
+                                               int lane, Best<K> &best) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = cbase + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    const float dp = (METRIC == TM_METRIC_L2) ? fmaf(-2.f, acc[i], pen[i]) : (pen[i] - acc[i]);
+    best.push(dp, c);
+  }
+}
+
+template <int DT, int DIM, int K, int METRIC>
+__global__ __launch_bounds__(kThreads) void search_tile_kernel(
     const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
     const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
     const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws) {
   using T = typename Elem<DT>::T;
-  constexpr int KS = DIM / 16;  // k-steps of the 32x32x16 MFMA
-  __shared__ __attribute__((aligned(16))) T cs[kStage][DIM + kPad];
-  __shared__ float cn[kStage];
-  __shared__ uint64_t merge_buf[(RW == 1) ? 4 * 32 * K : 1];
+  constexpr int KS = DIM / 16;             // k-steps of the 32x32x16 MFMA
+  constexpr int CH = DIM / 8;              // 16-byte chunks per centroid row
+  constexpr int PF = kStage * CH / kThreads;  // prefetch chunks per thread per stage
+  static_assert(kStage * CH % kThreads == 0, "stage must split evenly");
+  __shared__ __attribute__((aligned(16))) T cs[2][kStage][DIM + kPad];
+  __shared__ __attribute__((aligned(16))) float pen_s[2][kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int slab = (RW == 4) ? wave : 0;
   const int64_t split = blockIdx.y;
-  const int64_t row_base = (int64_t)blockIdx.x * (32 * RW) + slab * 32;
+  const int64_t row_base = (int64_t)blockIdx.x * kTileRows + wave * (kQS * 32);
+  const int64_t c_begin = split * chunk;
+  const int64_t c_end = (c_begin + chunk < n_cent) ? c_begin + chunk : n_cent;
+  const int nstage = (int)((c_end - c_begin + kStage - 1) / kStage);
+
+  // B operands: kQS slabs of 32 queries, all k-steps, in registers.
+  uint4 qf[kQS][KS];
+#pragma unroll
+  for (int sl = 0; sl < kQS; ++sl) {
+    const int64_t r = row_base + sl * 32 + (lane & 31);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[sl][ks] = make_uint4(0, 0, 0, 0);
+      if (r < n) qf[sl][ks] = *reinterpret_cast<const uint4 *>(q + r * ld_q + ks * 16 + 8 * (lane >> 5));
+    }
+  }
+
+  Best<K> best[kQS];
+#pragma unroll
+  for (int sl = 0; sl < kQS; ++sl) best[sl].init();
+
+  uint4 pf[PF];
+  float pf_pen = 0.f;
+  auto fetch = [&](int64_t s0) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int ci = tid + u * kThreads;
+      const int r = ci / CH, c8 = (ci % CH) * 8;
+      pf[u] = make_uint4(0, 0, 0, 0);
+      if (s0 + r < c_end) pf[u] = *reinterpret_cast<const uint4 *>(cents + (s0 + r) * ld_c + c8);
+    }
+    if (tid < kStage) {
+      const int64_t c = s0 + tid;
+      pf_pen = (c < c_end) ? ((METRIC == TM_METRIC_L2) ? c_sqnorm[c] : 0.f) : __builtin_huge_valf();
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int ci = tid + u * kThreads;
+      const int r = ci / CH, c8 = (ci % CH) * 8;
+      *reinterpret_cast<uint4 *>(&cs[buf][r][c8]) = pf[u];
+    }
+    if (tid < kStage) pen_s[buf][tid] = pf_pen;
+  };
+
+  fetch(c_begin);
+  for (int st = 0; st < nstage; ++st) {
+    const int buf = st & 1;
+    const int64_t s0 = c_begin + (int64_t)st * kStage;
+    stash(buf);
+    __syncthreads();
+    if (st + 1 < nstage) fetch(s0 + kStage);
+    // Both 32-centroid blocks' MFMAs are issued before either epilogue, so
+    // the VALU epilogue of one block overlaps the matrix unit on the other.
+    constexpr int NSUB = kStage / 32;
+    tm_f32x16 acc[NSUB][kQS];
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) {
+#pragma unroll
+      for (int sl = 0; sl < kQS; ++sl) acc[sub][sl] = tm_f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(&cs[buf][sub * 32 + (lane & 31)][ks * 16 + 8 * (lane >> 5)]);
+#pragma unroll
+        for (int sl = 0; sl < kQS; ++sl) acc[sub][sl] = tm_mfma32x32x16<DT>(a, qf[sl][ks], acc[sub][sl]);
+      }
+    }
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) {
+      float pen[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 p4 = *reinterpret_cast<const float4 *>(&pen_s[buf][sub * 32 + 8 * g + 4 * (lane >> 5)]);
+        pen[4 * g + 0] = p4.x; pen[4 * g + 1] = p4.y; pen[4 * g + 2] = p4.z; pen[4 * g + 3] = p4.w;
+      }
+      const int cbase = (int)(s0 + sub * 32);
+#pragma unroll
+      for (int sl = 0; sl < kQS; ++sl) block_epilogue<K, METRIC>(acc[sub][sl], pen, cbase, lane, best[sl]);
+    }
+  }
+
+#pragma unroll
+  for (int sl = 0; sl < kQS; ++sl) {
+    best[sl].finalize();
+    best[sl].merge_xor(32);  // the two half-waves saw disjoint centroids of the same query
+    const int64_t r = row_base + sl * 32 + (lane & 31);
+    if (lane < 32 && r < n) {
+      uint64_t *dst = ws + (split * n + r) * K;
+#pragma unroll
+      for (int j = 0; j < K; ++j) dst[j] = best[sl].l[j];
+    }
+  }
+}
+
+template <int DT, int DIM, int K, int QS, int METRIC>
+__global__ __launch_bounds__(kThreads) void search_stream_kernel(
+    const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
+    const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
+    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws) {
+  constexpr int KS = DIM / 16;
+  __shared__ uint64_t merge_buf[4][QS * 32][K];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t split = blockIdx.x;
   const int64_t c_begin = split * chunk;
   const int64_t c_end = (c_begin + chunk < n_cent) ? c_begin + chunk : n_cent;
 
-  // B operand: this wave's 32 queries, all k-steps, in registers.
-  uint4 qf[KS];
-  {
-    const int64_t r = row_base + (lane & 31);
+  uint4 qf[QS][KS];
+#pragma unroll
+  for (int sl = 0; sl < QS; ++sl) {
+    const int64_t r = sl * 32 + (lane & 31);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qf[ks] = make_uint4(0, 0, 0, 0);
-      if (r < n) qf[ks] = *reinterpret_cast<const uint4 *>(q + r * ld_q + ks * 16 + 8 * (lane >> 5));
+      qf[sl][ks] = make_uint4(0, 0, 0, 0);
+      if (r < n) qf[sl][ks] = *reinterpret_cast<const uint4 *>(q + r * ld_q + ks * 16 + 8 * (lane >> 5));
     }
   }
-
-  float best_d = __builtin_huge_valf();
-  int best_i = 0x7fffffff;
-  uint64_t lst[K];
+  Best<K> best[QS];
 #pragma unroll
-  for (int j = 0; j < K; ++j) lst[j] = ~0ull;
+  for (int sl = 0; sl < QS; ++sl) best[sl].init();
 
-  for (int64_t s0 = c_begin; s0 < c_end; s0 += kStage) {
-    // Stage kStage centroids (rows beyond c_end are zero and skipped later).
-    constexpr int CH = DIM / 8;  // 16-byte chunks per centroid row
-    for (int ci = tid; ci < kStage * CH; ci += kThreads) {
-      const int r = ci / CH, c8 = (ci % CH) * 8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (s0 + r < c_end) v = *reinterpret_cast<const uint4 *>(cents + (s0 + r) * ld_c + c8);
-      *reinterpret_cast<uint4 *>(&cs[r][c8]) = v;
+  // this wave's 32-centroid blocks: c_begin + 32*(wave + 4*j)
+  uint4 af[KS];
+  float pen[16];
+  auto fetch = [&](int64_t c0) {
+    const int64_t c = c0 + (lane & 31);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      af[ks] = make_uint4(0, 0, 0, 0);
+      if (c < c_end) af[ks] = *reinterpret_cast<const uint4 *>(cents + c * ld_c + ks * 16 + 8 * (lane >> 5));
     }
-    if (tid < kStage) cn[tid] = (METRIC == TM_METRIC_L2 && s0 + tid < c_end) ? c_sqnorm[s0 + tid] : 0.f;
-    __syncthreads();
-
 #pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-      if (RW == 1 && sub != wave) continue;
-      tm_f32x16 acc = {};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint4 a = *reinterpret_cast<const uint4 *>(&cs[sub * 32 + (lane & 31)][ks * 16 + 8 * (lane >> 5)]);
-        acc = tm_mfma32x32x16<DT>(a, qf[ks], acc);
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = sub * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        const int64_t c = s0 + m;
-        const float dp = (METRIC == TM_METRIC_L2) ? fmaf(-2.f, acc[i], cn[m]) : -acc[i];
-        if (c < c_end) {
-          if constexpr (K == 1) {
-            if (dp < best_d) { best_d = dp; best_i = (int)c; }
-          } else {
-            const uint64_t key = make_key(dp, (int)c);
-            if (key < lst[K - 1]) list_insert<K>(lst, key);
-          }
-        }
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int64_t cm = c0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      pen[i] = (cm < c_end) ? ((METRIC == TM_METRIC_L2) ? c_sqnorm[cm] : 0.f) : __builtin_huge_valf();
     }
-    __syncthreads();
-  }
-
-  if constexpr (K == 1) lst[0] = (best_i == 0x7fffffff) ? ~0ull : make_key(best_d, best_i);
-
-  // Merge the two half-waves (same query column, disjoint centroids).
-  {
-    uint64_t other[K];
+  };
+  int64_t c0 = c_begin + 32 * wave;
+  if (c0 < c_end) fetch(c0);
+  while (c0 < c_end) {
+    uint4 a[KS];
+    float p[16];
 #pragma unroll
-    for (int j = 0; j < K; ++j) other[j] = __shfl_xor(lst[j], 32, 64);
+    for (int ks = 0; ks < KS; ++ks) a[ks] = af[ks];
 #pragma unroll
-    for (int j = 0; j < K; ++j)
-      if (other[j] < lst[K - 1]) list_insert<K>(lst, other[j]);
+    for (int i = 0; i < 16; ++i) p[i] = pen[i];
+    const int64_t next = c0 + 128;
+    if (next < c_end) fetch(next);
+    tm_f32x16 acc[QS];
+#pragma unroll
+    for (int sl = 0; sl < QS; ++sl) acc[sl] = tm_f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int sl = 0; sl < QS; ++sl) acc[sl] = tm_mfma32x32x16<DT>(a[ks], qf[sl][ks], acc[sl]);
+#pragma unroll
+    for (int sl = 0; sl < QS; ++sl) block_epilogue<K, METRIC>(acc[sl], p, (int)c0, lane, best[sl]);
+    c0 = next;
   }
-
-  if constexpr (RW == 1) {
-    // Waves share the queries but saw disjoint centroid slabs: merge via LDS.
+#pragma unroll
+  for (int sl = 0; sl < QS; ++sl) {
+    best[sl].finalize();
+    best[sl].merge_xor(32);
     if (lane < 32) {
 #pragma unroll
-      for (int j = 0; j < K; ++j) merge_buf[(wave * 32 + lane) * K + j] = lst[j];
-    }
-    __syncthreads();
-    if (wave == 0 && lane < 32) {
-      for (int w = 1; w < 4; ++w) {
-#pragma unroll
-        for (int j = 0; j < K; ++j) {
-          const uint64_t o = merge_buf[(w * 32 + lane) * K + j];
-          if (o < lst[K - 1]) list_insert<K>(lst, o);
-        }
-      }
-    } else {
-      return;
+      for (int j = 0; j < K; ++j) merge_buf[wave][sl * 32 + lane][j] = best[sl].l[j];
     }
   }
-
-  const int64_t r = row_base + (lane & 31);
-  if (lane < 32 && r < n) {
-    uint64_t *dst = ws + (split * n + r) * K;
+  __syncthreads();
+  // waves saw disjoint centroid blocks of the same queries: merge through LDS
+  if (tid < QS * 32) {
+    const int r = tid;
+    uint64_t l[K];
 #pragma unroll
-    for (int j = 0; j < K; ++j) dst[j] = lst[j];
+    for (int j = 0; j < K; ++j) l[j] = merge_buf[0][r][j];
+    for (int w = 1; w < 4; ++w)
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        const uint64_t o = merge_buf[w][r][j];
+        if (o < l[K - 1]) list_insert<K>(l, o);
+      }
+    if (r < n) {
+      uint64_t *dst = ws + (split * n + r) * K;
+#pragma unroll
+      for (int j = 0; j < K; ++j) dst[j] = l[j];
+    }
   }
 }
 
@@ -254,19 +419,23 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
                   float *out_dist, int64_t *out_idx, uint64_t *ws, hipStream_t stream) {
   using T = typename Elem<DT>::T;
   const SplitPlan p = plan_split(n, n_cent);
-  dim3 grid((unsigned)p.row_blocks, (unsigned)p.nsplit), block(kThreads);
-  if (p.rw == 4)
-    hipLaunchKernelGGL((search_global_kernel<DT, DIM, K, 4, METRIC>), grid, block, 0, stream,
-                       static_cast<const T *>(q), n, ld_q, static_cast<const T *>(cents), n_cent,
-                       ld_c, c_sqnorm, p.chunk, ws);
-  else
-    hipLaunchKernelGGL((search_global_kernel<DT, DIM, K, 1, METRIC>), grid, block, 0, stream,
-                       static_cast<const T *>(q), n, ld_q, static_cast<const T *>(cents), n_cent,
-                       ld_c, c_sqnorm, p.chunk, ws);
+  const T *Q = static_cast<const T *>(q);
+  const T *C = static_cast<const T *>(cents);
+  dim3 block(kThreads);
+  if (p.stream) {
+    if (p.qs == 1)
+      hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 1, METRIC>), dim3((unsigned)p.nsplit), block, 0, stream,
+                         Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
+    else
+      hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 2, METRIC>), dim3((unsigned)p.nsplit), block, 0, stream,
+                         Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
+  } else {
+    hipLaunchKernelGGL((search_tile_kernel<DT, DIM, K, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
+                       block, 0, stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
+  }
   TM_LAUNCH_CHECK("tm_search_global");
   hipLaunchKernelGGL((merge_kernel<DT, K, METRIC>), dim3((unsigned)tm_cdiv(n, kThreads / 64)),
-                     block, 0, stream, ws, n, p.nsplit, static_cast<const T *>(q), ld_q, DIM,
-                     q_sqnorm, top_k, out_dist, out_idx);
+                     block, 0, stream, ws, n, p.nsplit, Q, ld_q, DIM, q_sqnorm, top_k, out_dist, out_idx);
   TM_LAUNCH_CHECK("tm_search_global(merge)");
   return TM_OK;
 }
@@ -323,7 +492,7 @@ extern "C" int tm_search_global(int32_t dtype, const void *q, int64_t n_tokens, 
                                 int64_t ld_c, const float *c_sqnorm, int32_t dim, int32_t top_k,
                                 int32_t metric, float *out_dist, int64_t *out_idx, void *workspace,
                                 size_t workspace_bytes, tm_stream_t stream) {
-  TM_REQUIRE(n_tokens >= 0 && n_cent > 0 && n_cent < (int64_t)0x7fffffff, TM_EINVAL_SHAPE,
+  TM_REQUIRE(n_tokens >= 0 && n_tokens < ((int64_t)1 << 31) && n_cent > 0 && n_cent < (int64_t)0x7fffffff, TM_EINVAL_SHAPE,
              "tm_search_global: bad sizes n=%lld C=%lld", (long long)n_tokens, (long long)n_cent);
   TM_REQUIRE(ld_q >= dim && ld_c >= dim, TM_EINVAL_SHAPE, "tm_search_global: bad row strides");
   TM_REQUIRE(top_k >= 1 && top_k <= 8, TM_EINVAL_SHAPE, "tm_search_global: top_k %d not in [1, 8]", top_k);

@@ -35,62 +35,113 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *w
 
 // ---------------------------------------------------------------------------
 // (3) keep the n_keep largest scores; ties -> lower token index.
-// One workgroup.  Four 8-bit radix passes over order-preserving uint32 keys
-// find the boundary key T and how many copies of T are kept; a scan over the
-// tokens in index order then keeps the first of the tied ones.
+// One workgroup; thread t owns the contiguous token range [t*per, (t+1)*per)
+// and caches its order-preserving uint32 keys in registers (n <= 16384).
+// Four 8-bit radix passes find the boundary key T and how many copies of T
+// are kept: each pass builds a 256-bin histogram of the keys still matching
+// the known high bits (one private histogram per wave, so nearby distances
+// sharing their high digits only contend within a wave), the wave histograms
+// are summed bin-parallel, and wave 0 locates the bin holding the n_keep-th largest key
+// with a reverse prefix sum (4 bins per lane).  A block scan over the tokens
+// in index order keeps the first of the tied ones.
 // ---------------------------------------------------------------------------
 constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kSelRegs = 16;
 
 __global__ __launch_bounds__(kSelThreads) void keep_select_kernel(const float *__restrict__ score,
                                                                   int64_t n, int64_t ld,
                                                                   int64_t n_keep,
                                                                   uint8_t *__restrict__ out) {
+  __shared__ uint32_t whist[kSelWaves][256];  // per-wave private histograms
   __shared__ uint32_t hist[256];
   __shared__ uint32_t s_prefix, s_mask;
   __shared__ int64_t s_remaining;
-  __shared__ uint32_t wave_tot[kSelThreads / 64 + 1];
-  const int tid = threadIdx.x;
+  __shared__ uint32_t wave_tot[kSelWaves + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t per = (n + kSelThreads - 1) / kSelThreads;
   const int64_t lo = tid * per;
   const int64_t hi = (lo + per < n) ? lo + per : n;
+  const int cnt = (int)(hi > lo ? hi - lo : 0);
 
   if (n_keep <= 0 || n_keep >= n) {
     const uint8_t v = n_keep > 0 ? 1 : 0;
     for (int64_t i = lo; i < hi; ++i) out[i] = v;
     return;
   }
+  const bool cached = per <= kSelRegs;  // uniform
+  uint32_t keys[kSelRegs];
+  if (cached) {
+#pragma unroll
+    for (int j = 0; j < kSelRegs; ++j) keys[j] = (j < cnt) ? tm_orderable(score[(lo + j) * ld]) : 0u;
+  }
+  auto key_at = [&](int j) -> uint32_t {
+    if (cached) {
+      uint32_t k = 0;
+#pragma unroll
+      for (int u = 0; u < kSelRegs; ++u)
+        if (u == j) k = keys[u];
+      return k;
+    }
+    return tm_orderable(score[(lo + j) * ld]);
+  };
+
   if (tid == 0) { s_prefix = 0; s_mask = 0; s_remaining = n_keep; }
-  __syncthreads();
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = tid; b < 256; b += kSelThreads) hist[b] = 0;
+    for (int b = lane; b < 256; b += 64) whist[wave][b] = 0;
     __syncthreads();
     const uint32_t prefix = s_prefix, mask = s_mask;
-    for (int64_t i = lo; i < hi; ++i) {
-      const uint32_t key = tm_orderable(score[i * ld]);
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    if (cached) {
+#pragma unroll
+      for (int j = 0; j < kSelRegs; ++j)
+        if (j < cnt && (keys[j] & mask) == prefix) atomicAdd(&whist[wave][(keys[j] >> shift) & 255u], 1u);
+    } else {
+      for (int j = 0; j < cnt; ++j) {
+        const uint32_t k = key_at(j);
+        if ((k & mask) == prefix) atomicAdd(&whist[wave][(k >> shift) & 255u], 1u);
+      }
     }
     __syncthreads();
-    if (tid == 0) {
-      int64_t above = 0;
-      int b = 255;
-      for (; b > 0; --b) {
-        if (above + hist[b] >= s_remaining) break;
-        above += hist[b];
+    if (tid < 256) {  // thread t sums bin t over the waves
+      uint32_t acc = 0;
+#pragma unroll
+      for (int w = 0; w < kSelWaves; ++w) acc += whist[w][tid];
+      hist[tid] = acc;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      uint32_t hb[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) hb[b] = hist[4 * lane + b];
+      const uint32_t t = hb[0] + hb[1] + hb[2] + hb[3];
+      uint32_t incl = t;  // sum over lanes >= this lane (bins >= 4*lane)
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_down(incl, o, 64);
+        if (lane + o < 64) incl += v;
       }
-      s_remaining -= above;
-      s_prefix = prefix | ((uint32_t)b << shift);
-      s_mask = mask | (255u << shift);
+      const int64_t rem = s_remaining;
+      int64_t above = (int64_t)(incl - t);
+#pragma unroll
+      for (int b = 3; b >= 0; --b) {
+        if (above < rem && rem <= above + (int64_t)hb[b]) {
+          s_prefix = prefix | ((uint32_t)(4 * lane + b) << shift);
+          s_mask = mask | (255u << shift);
+          s_remaining = rem - above;
+        }
+        above += hb[b];
+      }
     }
     __syncthreads();
   }
   const uint32_t T = s_prefix;
   const int64_t keep_eq = s_remaining;  // copies of T to keep, >= 1
-  uint32_t cnt = 0;
-  for (int64_t i = lo; i < hi; ++i) cnt += (tm_orderable(score[i * ld]) == T);
+  uint32_t eq = 0;
+  for (int j = 0; j < cnt; ++j) eq += (key_at(j) == T);
   uint32_t total;
-  uint32_t rank = block_exclusive_scan<kSelThreads>(cnt, wave_tot, total);
-  for (int64_t i = lo; i < hi; ++i) {
-    const uint32_t key = tm_orderable(score[i * ld]);
+  uint32_t rank = block_exclusive_scan<kSelThreads>(eq, wave_tot, total);
+  for (int j = 0; j < cnt; ++j) {
+    const uint32_t key = key_at(j);
     uint8_t k = 0;
     if (key > T) {
       k = 1;
@@ -98,7 +149,7 @@ __global__ __launch_bounds__(kSelThreads) void keep_select_kernel(const float *_
       k = ((int64_t)rank < keep_eq) ? 1 : 0;
       ++rank;
     }
-    out[i] = k;
+    out[lo + j] = k;
   }
 }
 

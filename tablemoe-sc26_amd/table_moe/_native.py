@@ -27,13 +27,37 @@ _DTYPE_TAG = {torch.float32: TM_DT_F32, torch.float16: TM_DT_F16, torch.bfloat16
 
 i32, i64, f32, f64, vp, sz = C.c_int32, C.c_int64, C.c_float, C.c_double, C.c_void_p, C.c_size_t
 
+
+
+class TableLayer(C.Structure):
+    """Mirror of tm_table_layer (include/tablemoe.h)."""
+
+    _fields_ = [("dtype", i32), ("metric", i32), ("dim", i32), ("hidden", i32), ("n_cent", i64), ("cents", vp),
+                ("ld_c", i64), ("c_sqnorm", vp), ("values", vp), ("ld_v", i64), ("proj_vis", vp), ("bias_vis", vp),
+                ("proj_txt", vp), ("bias_txt", vp), ("ps_h", i64), ("ps_d", i64)]
+
+
+class LayerIO(C.Structure):
+    """Mirror of tm_layer_io (include/tablemoe.h)."""
+
+    _fields_ = [("n_tokens", i64), ("x", vp), ("ld_x", i64), ("is_vision", vp), ("router_logits", vp),
+                ("ld_logits", i64), ("n_experts", i32), ("router_top_k", i32), ("n_nearest", i32),
+                ("reserved", i32), ("keep_rate", f64), ("slot_out", vp), ("so_b", i64), ("so_s", i64),
+                ("residual", vp), ("ld_r", i64), ("out", vp), ("ld_o", i64), ("weights", vp), ("expert_ids", vp),
+                ("q", vp), ("q_sqnorm", vp), ("dist", vp), ("idx", vp), ("keep", vp)]
+
+
 # name -> (restype, argtypes); mirrors include/tablemoe.h
 PROTOTYPES = {
     "tm_version": (C.c_int, []),
     "tm_status_string": (C.c_char_p, [C.c_int]),
     "tm_last_error": (C.c_char_p, []),
     "tm_topk_softmax": (C.c_int, [vp, i64, i32, i64, i32, i32, vp, vp, vp]),
-    "tm_project": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, vp, vp, i64, i64, i32, i32, f32, vp, i64, vp, vp]),
+    "tm_project_workspace_size": (sz, [i64, i32, i32]),
+    "tm_project_packed_size": (sz, [i32, i32, i32]),
+    "tm_project_pack": (C.c_int, [i32, vp, i32, i32, i64, i64, vp, sz, vp]),
+    "tm_project": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, vp, vp, i64, i64, i32, i32, f32, vp, i64, vp, vp, sz,
+                             vp]),
     "tm_search_gated": (C.c_int, [i32, vp, i64, i64, vp, i64, i64, i32, i64, i64, i64, vp, i32, i64, i64, vp, vp,
                                   i64, i64, i32, f32, f32, i32, vp, vp, i64, i64, vp]),
     "tm_search_hybrid": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, vp, vp, i64, i64, i32, vp, i64, i32, vp, i32,
@@ -56,6 +80,9 @@ PROTOTYPES = {
     "tm_keep_select": (C.c_int, [vp, i64, i64, i64, vp, vp, sz, vp]),
     "tm_gather_combine": (C.c_int, [i32, i64, i32, vp, vp, i64, i64, vp, i64, i32, vp, i64, i64, vp, vp, i64, i32,
                                     vp, i64, vp, i64, vp]),
+    "tm_struct_size": (sz, [i32]),
+    "tm_table_forward_workspace_size": (sz, [C.POINTER(TableLayer), i64, i32]),
+    "tm_table_forward": (C.c_int, [C.POINTER(TableLayer), C.POINTER(LayerIO), vp, sz, vp, vp]),
 }
 
 _lock = threading.Lock()
@@ -82,6 +109,10 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
+        for which, struct in ((0, TableLayer), (1, LayerIO)):
+            if lib.tm_struct_size(which) != C.sizeof(struct):
+                raise RuntimeError(f"{struct.__name__} mirror ({C.sizeof(struct)} bytes) does not match the library "
+                                   f"({lib.tm_struct_size(which)} bytes)")
         _lib = lib
         return lib
 
@@ -147,6 +178,22 @@ def as_u8(mask: torch.Tensor) -> torch.Tensor:
     if mask.dtype == torch.uint8:
         return mask
     return (mask != 0).to(torch.uint8)
+
+
+def pack_projection(proj: torch.Tensor, bias: torch.Tensor) -> torch.Tensor | None:
+    """The packed device layout of a [hidden, dim] projection (tm_project_pack),
+    or None when the packed fast path does not apply (fp32, unsupported dim or
+    hidden, unaligned bias); callers then keep a strided layout."""
+    require_hip(proj, bias)
+    hidden, dim = proj.shape
+    tag = dtype_tag(proj.dtype)
+    nbytes = lib().tm_project_packed_size(hidden, dim, tag)
+    if nbytes == 0 or hidden % 8 != 0 or bias.data_ptr() % 16 != 0:
+        return None
+    out = torch.empty(nbytes, dtype=torch.uint8, device=proj.device)
+    call("tm_project_pack", tag, ptr(proj), hidden, dim, proj.stride(0), proj.stride(1), ptr(out), nbytes,
+         stream(proj.device))
+    return out
 
 
 def exported_symbols() -> list[str]:

@@ -18,6 +18,8 @@ The reference counterparts it generalises: the projection
 
 from __future__ import annotations
 
+import ctypes as C
+
 import torch
 
 from .. import _native as N
@@ -45,15 +47,26 @@ class GlobalTable:
             raise ValueError("values must have one row per centroid")
         pca_txt = pca_vis if pca_txt is None else pca_txt
         self.proj = (pca_vis[0], pca_txt[0])
-        self.proj_t = tuple(p.t().contiguous() for p in self.proj)  # [d, H], k-contiguous
         self.bias = tuple(b.contiguous() for b in (pca_vis[1], pca_txt[1]))
         for p in self.proj:
             if p.shape != (self.hidden, self.dim) or p.dtype != self.dtype:
                 raise ValueError(f"projection must be [{self.hidden}, {self.dim}] {self.dtype}")
+        # packed layout for the matrix cores when it applies, else a k-contiguous copy
+        packed = tuple(N.pack_projection(p, b) for p, b in zip(self.proj, self.bias))
+        if all(p is not None for p in packed):
+            self.proj_dev, self.ps = packed, (0, 0)
+        else:
+            self.proj_dev, self.ps = tuple(p.t().contiguous() for p in self.proj), (1, self.hidden)
         self.c_sqnorm = torch.empty(self.n_cent, dtype=torch.float32, device=dev)
         N.call("tm_centroid_sqnorms", N.dtype_tag(self.dtype), N.ptr(self.centroids), self.n_cent, self.dim,
                self.centroids.stride(0), N.ptr(self.c_sqnorm), N.stream(dev))
         self._bufs: dict = {}
+        self._desc = N.TableLayer(
+            dtype=N.dtype_tag(self.dtype), metric=_METRICS[metric], dim=self.dim, hidden=self.hidden,
+            n_cent=self.n_cent, cents=N.ptr(self.centroids), ld_c=self.centroids.stride(0),
+            c_sqnorm=N.ptr(self.c_sqnorm), values=N.ptr(self.values), ld_v=self.values.stride(0),
+            proj_vis=N.ptr(self.proj_dev[0]), bias_vis=N.ptr(self.bias[0]), proj_txt=N.ptr(self.proj_dev[1]),
+            bias_txt=N.ptr(self.bias[1]), ps_h=self.ps[0], ps_d=self.ps[1])
 
     # --------------------------------------------------------------- buffers
     def _buf(self, name, shape, dtype):
@@ -77,9 +90,12 @@ class GlobalTable:
         q = self._buf("q", (n, self.dim), self.dtype)
         qn = self._buf("qn", (n,), torch.float32)
         isv = None if is_vision is None else N.as_u8(is_vision.reshape(-1).to(dtype=torch.bool))
+        nbytes = N.lib().tm_project_workspace_size(n, self.hidden, self.dim)
+        ws = self._buf("project_ws", (max(nbytes, 1),), torch.uint8)
         N.call("tm_project", N.dtype_tag(self.dtype), N.ptr(x), n, self.hidden, x.stride(0), N.ptr(isv),
-               N.ptr(self.proj_t[0]), N.ptr(self.bias[0]), N.ptr(self.proj_t[1]), N.ptr(self.bias[1]), 1,
-               self.hidden, self.dim, 0, 1e-6, N.ptr(q), q.stride(0), N.ptr(qn), N.stream(self.device))
+               N.ptr(self.proj_dev[0]), N.ptr(self.bias[0]), N.ptr(self.proj_dev[1]), N.ptr(self.bias[1]),
+               self.ps[0], self.ps[1], self.dim, 0, 1e-6, N.ptr(q), q.stride(0), N.ptr(qn), N.ptr(ws), ws.numel(),
+               N.stream(self.device))
         return q, qn
 
     def search(self, q: torch.Tensor, top_k: int = 1, q_sqnorm: torch.Tensor | None = None):
@@ -131,12 +147,53 @@ class GlobalTable:
                N.ptr(ids), N.stream(self.device))
         return w, ids
 
-    def layer_forward(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k: int = 8,
-                      n_nearest: int = 1, keep_rate: float = 0.6, out=None):
-        """One MoE layer of the table path; returns a dict of every stage's output."""
+    def layer_forward_staged(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k: int = 8,
+                             n_nearest: int = 1, keep_rate: float = 0.6, out=None):
+        """The layer as five separate C-ABI calls (one per stage)."""
         w, ids = self.route(router_logits, router_top_k)
         q, qn = self.project(hidden, is_vision)
         dist, idx = self.search(q, n_nearest, qn)
         keep = self.keep_select(dist[:, 0], self.keep_count(hidden.shape[0], keep_rate))
         y = self.gather_combine(keep, slot_out, w, idx, dist, residual, out)
         return {"weights": w, "ids": ids, "q": q, "qn": qn, "dist": dist, "idx": idx, "keep": keep, "out": y}
+
+    def layer_forward(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k: int = 8,
+                      n_nearest: int = 1, keep_rate: float = 0.6, out=None, stage_events=None):
+        """One MoE layer of the table path in one C-ABI call (tm_table_forward);
+        returns a dict of every stage's output.  ``stage_events``: optional six
+        torch.cuda.Event recorded around the stages."""
+        N.require_hip(hidden, router_logits, slot_out)
+        if hidden.dtype != self.dtype or slot_out.dtype != self.dtype:
+            raise RuntimeError(f"hidden/slot_out dtype must be the table dtype {self.dtype}")
+        x = hidden if hidden.stride(-1) == 1 else hidden.contiguous()
+        logits = router_logits.float()
+        if logits.stride(-1) != 1:
+            logits = logits.contiguous()
+        if slot_out.stride(-1) != 1:
+            slot_out = slot_out.contiguous()
+        n = x.shape[0]
+        if out is None:
+            out = self._buf("out", (n, self.hidden), self.dtype)
+        w = self._buf("route_w", (n, router_top_k), torch.float32)
+        ids = self._buf("route_ids", (n, router_top_k), torch.long)
+        q = self._buf("q", (n, self.dim), self.dtype)
+        qn = self._buf("qn", (n,), torch.float32)
+        dist = self._buf("dist", (n, n_nearest), torch.float32)
+        idx = self._buf("idx", (n, n_nearest), torch.long)
+        keep = self._buf("keep", (n,), torch.bool)
+        isv = None if is_vision is None else N.as_u8(is_vision.reshape(-1).to(dtype=torch.bool))
+        io = N.LayerIO(
+            n_tokens=n, x=N.ptr(x), ld_x=x.stride(0), is_vision=N.ptr(isv), router_logits=N.ptr(logits),
+            ld_logits=logits.stride(0), n_experts=logits.shape[1], router_top_k=router_top_k, n_nearest=n_nearest,
+            keep_rate=float(keep_rate), slot_out=N.ptr(slot_out), so_b=slot_out.stride(0), so_s=slot_out.stride(1),
+            residual=N.ptr(residual), ld_r=0 if residual is None else residual.stride(0), out=N.ptr(out),
+            ld_o=out.stride(0), weights=N.ptr(w), expert_ids=N.ptr(ids), q=N.ptr(q), q_sqnorm=N.ptr(qn),
+            dist=N.ptr(dist), idx=N.ptr(idx), keep=N.ptr(N.as_u8(keep)))
+        nbytes = N.lib().tm_table_forward_workspace_size(C.byref(self._desc), n, n_nearest)
+        ws = self._buf("layer_ws", (max(nbytes, 1),), torch.uint8)
+        evs = None
+        if stage_events is not None:
+            evs = (C.c_void_p * 6)(*[e.cuda_event for e in stage_events])
+        N.check(N.lib().tm_table_forward(C.byref(self._desc), C.byref(io), N.ptr(ws), ws.numel(), evs,
+                                         N.stream(self.device)), "tm_table_forward")
+        return {"weights": w, "ids": ids, "q": q, "qn": qn, "dist": dist, "idx": idx, "keep": keep, "out": out}

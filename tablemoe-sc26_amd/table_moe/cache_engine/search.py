@@ -69,14 +69,21 @@ class VectorSearchEngine:
             "compressed_dim": compressed_dim,
             "fixed_k": int(self.manager.keys_buffer.shape[2]),
             "online_topk": online_topk,
-            # k-contiguous copies of the projections for the MFMA projection
+            # k-contiguous copies of the projections (fused decode projection)
             "proj_t": (self._transposed(pca_vis["proj"]), self._transposed(pca_txt["proj"])),
+            # packed layouts for tm_project (None: the strided copies are used)
+            "proj_pk": self._packed(pca_vis, pca_txt),
         }
         return self.search_dims_cache
 
     @staticmethod
     def _transposed(proj: torch.Tensor) -> torch.Tensor:
         return proj.t().contiguous()  # [dim, hidden]
+
+    @staticmethod
+    def _packed(pca_vis, pca_txt):
+        pk = (N.pack_projection(pca_vis["proj"], pca_vis["bias"]), N.pack_projection(pca_txt["proj"], pca_txt["bias"]))
+        return None if any(p is None for p in pk) else pk
 
     def _ensure_workspace(self, batch_size, top_k):
         if batch_size > self.workspace_capacity or top_k != self._workspace_top_k:
@@ -129,13 +136,32 @@ class VectorSearchEngine:
         pv, pt = search_dims["pca_vis"], search_dims["pca_txt"]
         tv, tt = search_dims["proj_t"]
         isv = N.as_u8(is_vision_mask.reshape(-1).to(device=dev, dtype=torch.bool))
+        d = search_dims["compressed_dim"]
+        pk = search_dims["proj_pk"]
+        if pk is not None and x.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0 and query_low.data_ptr() % 16 == 0 \
+                and query_low.stride(0) % 8 == 0:
+            (tv, tt), ps_h, ps_d, ws = pk, 0, 0, None  # packed layout, no workspace
+        else:
+            ps_h, ps_d = 1, hidden
+            ws = self._scratch("project", N.lib().tm_project_workspace_size(n, hidden, d))
         N.call(
             "tm_project", N.dtype_tag(dtype), N.ptr(x), n, hidden, x.stride(0), N.ptr(isv),
-            N.ptr(tv), N.ptr(pv["bias"]), N.ptr(tt), N.ptr(pt["bias"]), 1, hidden,
-            search_dims["compressed_dim"], 1 if normalize else 0, float(CacheConfig.OFFLINE_COSINE_EPS),
-            N.ptr(query_low), query_low.stride(0), None, N.stream(dev),
+            N.ptr(tv), N.ptr(pv["bias"]), N.ptr(tt), N.ptr(pt["bias"]), ps_h, ps_d, d,
+            1 if normalize else 0, float(CacheConfig.OFFLINE_COSINE_EPS), N.ptr(query_low), query_low.stride(0),
+            None, N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(dev),
         )
         return query_low
+
+    def _scratch(self, name, nbytes):
+        """Reusable device workspace of at least ``nbytes`` (None for 0)."""
+        if nbytes <= 0:
+            return None
+        cache = self.__dict__.setdefault("_scratch_bufs", {})
+        buf = cache.get(name)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            cache[name] = buf
+        return buf
 
     def _build_prefill_queries(self, hidden_states, is_vision_mask, search_dims):
         q = self._ensure_prefill_query_workspace(hidden_states.shape[0], search_dims["compressed_dim"])

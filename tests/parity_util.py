@@ -49,3 +49,38 @@ def check_topk_rows(exact, got_idx, want_idx, larger_is_better, what=""):
                 n_mis += 1
                 check_pick(exact[r], g[j], w[j], larger_is_better, f"{what} row {r} pos {j}")
     return n_mis
+
+
+def assert_projection_close(got, ref, abssum, dtype, min_exact=0.95):
+    """q from an fp32-accumulated contraction vs the exactly-rounded oracle:
+    within 1 ulp of the reference plus the fp32 accumulation bound on the
+    absolute sum of the terms (cancellation can leave tiny results whose ulp
+    is below the accumulation error)."""
+    got, ref = np.asarray(got), np.asarray(ref)
+    tol = ulp(ref, dtype) + 2.0**-18 * np.asarray(abssum)
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), f"{bad.sum()} values off, e.g. got {got[bad][:4]} want {ref[bad][:4]}"
+    frac = float(np.mean(got == ref)) if got.size else 1.0
+    assert frac >= min_exact, f"only {frac:.4f} bit-exact"
+
+
+def proj_abssum(x, is_vision, pv, pt, normalized_ref=None):
+    """sum_h |x_h P_hj| per output (scaled by 1/||q|| for normalised outputs)."""
+    x = np.abs(np.asarray(x, dtype=np.float64))
+    vis = np.asarray(is_vision, dtype=bool)
+    out = np.where(vis[:, None], x @ np.abs(pv), x @ np.abs(pt))
+    return out
+
+
+def assert_bf16_output(got, exact, abssum, dtype=torch.bfloat16, atol=1e-2, rtol=2e-3):
+    """A combined output stored in a 16-bit type against the unrounded exact
+    value: within one ulp of it (plus the fp32 accumulation bound over the
+    absolute terms), and within (atol, rtol) wherever that tolerance exceeds
+    the type's own half-ulp (|v| < 8 for bf16; beyond, one rounding alone can
+    exceed 2e-3 relative)."""
+    got, exact = np.asarray(got), np.asarray(exact)
+    tol = ulp(exact, dtype) + 2.0**-20 * np.asarray(abssum)
+    bad = np.abs(got - exact) > tol
+    assert not bad.any(), f"{bad.sum()} values off, e.g. got {got[bad][:4]} want {exact[bad][:4]}"
+    small = np.abs(exact) < 8.0
+    np.testing.assert_allclose(got[small], exact[small], atol=atol, rtol=rtol)

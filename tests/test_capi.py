@@ -72,7 +72,8 @@ def test_argument_validation_without_device(lib):
     # empty inputs are no-ops
     assert lib.tm_keep_select(None, 0, 1, 0, None, None, 0, None) == N.TM_OK
     assert lib.tm_project(N.TM_DT_BF16, None, 0, 2048, 2048, None, C.c_void_p(16), C.c_void_p(16), None, None,
-                          1, 2048, 128, 0, 1e-6, C.c_void_p(16), 128, None, None) == N.TM_OK
+                          1, 2048, 128, 0, 1e-6, C.c_void_p(16), 128, None, None, 0, None) == N.TM_OK
+    assert lib.tm_project_workspace_size(4096, 2048, 128) == 4 * 4096 * 128 * 4  # 4-way split of hidden
     # bad sizes / enums / dtypes are rejected before any launch
     assert lib.tm_search_global(N.TM_DT_BF16, None, 10, 128, None, None, 100, 128, None, 128, 9, 0, None, None,
                                 None, 0, None) == N.TM_EINVAL_SHAPE
@@ -97,3 +98,12 @@ def test_argument_validation_without_device(lib):
                                 C.c_void_p(16), 128, 1, 0, C.c_void_p(16), C.c_void_p(16), C.c_void_p(16),
                                 need - 1, None) == N.TM_EWORKSPACE
     assert lib.tm_expert_keep_mask_workspace_size(4096, 128) > 0
+    # packed projection layout: ceil(hidden/32)*32 rows of dim 2-byte elements
+    assert lib.tm_project_packed_size(2048, 128, N.TM_DT_BF16) == 2048 * 128 * 2
+    assert lib.tm_project_packed_size(1000, 64, N.TM_DT_F16) == 1024 * 64 * 2
+    assert lib.tm_project_packed_size(2048, 48, N.TM_DT_BF16) == 0
+    assert lib.tm_project_packed_size(2048, 128, N.TM_DT_F32) == 0
+    assert lib.tm_project_pack(N.TM_DT_BF16, C.c_void_p(16), 2048, 128, 128, 1, C.c_void_p(16), 100,
+                               None) == N.TM_EWORKSPACE
+    assert lib.tm_project_pack(N.TM_DT_F32, C.c_void_p(16), 2048, 128, 128, 1, C.c_void_p(16), 1 << 20,
+                               None) == N.TM_EINVAL_DTYPE
