@@ -12,9 +12,9 @@
 //
 // Two launch shapes:
 //  - tile kernel (n > 64): a workgroup owns 256 queries (4 waves x 2 slabs of
-//    32, so each A fragment read from LDS feeds two MFMAs) and one chunk of
-//    centroids, staged 64 at a time through double-buffered LDS with the next
-//    stage prefetched into registers while the current one is multiplied;
+//    32, so each A fragment read from LDS feeds two MFMAs) and one range of
+//    centroids, streamed in 16 KiB stages through a 4-slot LDS ring filled by
+//    direct global->LDS loads, three stages in flight;
 //  - stream kernel (n <= 64, decode): the workgroup's waves share the queries
 //    and each wave streams its own 32-centroid blocks straight from global
 //    memory (next block prefetched), so a small batch still reads the table
@@ -31,8 +31,6 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kStage = 64;  // centroids per LDS stage of the tile kernel
-constexpr int kPad = 8;
 constexpr int kQS = 2;      // query slabs per wave in the tile kernel
 constexpr int kTileRows = 4 * kQS * 32;
 constexpr int kStreamBlocksPerWave = 2;
@@ -45,7 +43,10 @@ struct SplitPlan {
   int64_t chunk;  // centroids per split
 };
 
-SplitPlan plan_split(int64_t n, int64_t c) {
+// Centroid rows per pipelined stage of the tile kernel (16 KiB stages).
+static inline int64_t dma_rows(int dim) { return 16384 / (dim * 2); }
+
+SplitPlan plan_split(int64_t n, int64_t c, int dim) {
   SplitPlan p;
   p.stream = n <= 64;
   if (p.stream) {
@@ -57,11 +58,14 @@ SplitPlan plan_split(int64_t n, int64_t c) {
   }
   p.qs = kQS;
   p.row_blocks = tm_cdiv(n, kTileRows);
-  const int64_t max_split = tm_cdiv(c, kStage);
+  const int64_t rows = dma_rows(dim);
+  const int64_t max_split = tm_cdiv(c, rows);
   int64_t want = tm_cdiv(512, p.row_blocks);  // ~2 workgroups per CU
+  const int64_t min_split = tm_cdiv(c, 2048);  // the penalty array holds 2048 centroids
+  if (want < min_split) want = min_split;
   if (want < 1) want = 1;
   if (want > max_split) want = max_split;
-  p.chunk = tm_cdiv(tm_cdiv(c, want), kStage) * kStage;
+  p.chunk = tm_cdiv(tm_cdiv(c, want), rows) * rows;
   p.nsplit = tm_cdiv(c, p.chunk);
   return p;
 }
@@ -135,18 +139,67 @@ __device__ __forceinline__ void block_epilogue(const tm_f32x16 &acc, const float
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined tile kernel: centroid stages arrive through direct global->LDS
+// loads (global_load_lds_dwordx4: lane l of a wave writes LDS bytes
+// [M0 + 16 l, M0 + 16 l + 16)), kDmaBufs stages in a ring, kDmaBufs - 1 of
+// them in flight while one is multiplied.  Each ring slot is its own LDS
+// array and the loop is unrolled over the ring, so the compiler can tell the
+// loads of one slot from the reads of another and the only waits are the
+// explicit ones below (one per stage, before the stage's barrier).
+//
+// A stage holds kDmaRows centroid rows as 16-byte chunks.  Chunk j of row r
+// is stored at slot r*CH + (j ^ (r % CH)) (CH = chunks per row): the
+// matrix-core operand reads (32 rows at one chunk) then fall in distinct
+// banks.  The lane that fills slot p loads the chunk that belongs there.
+// The penalty ||c||^2 of the workgroup's whole centroid range is staged in
+// LDS once, +inf past the end of the range (rows past the end are loaded
+// from the last valid row and lose on their infinite penalty).
+// ---------------------------------------------------------------------------
+constexpr int kDmaBufs = 4;
+constexpr int kDmaStageBytes = 16384;
+constexpr int kDmaMaxChunk = 2048;  // centroids per workgroup (penalty array in LDS)
+
+// One wave-wide 16-byte-per-lane direct load into LDS at `lds_base` (wave
+// uniform) + 16 * lane.  Issued from inline asm so the compiler's own wait
+// insertion does not treat it as an LDS store (it would drain every in-flight
+// stage before each LDS read); the loads are waited for explicitly.  M0 is
+// saved and restored around the load.
+__device__ __forceinline__ void tm_dma16(const void *gaddr, const void *lds_base) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_base);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gaddr), "s"(base)
+      : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void tm_wait_vm_lgkm0() {
+  // s_waitcnt vmcnt(N) lgkmcnt(0), expcnt left at its maximum
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
 template <int DT, int DIM, int K, int METRIC>
-__global__ __launch_bounds__(kThreads) void search_tile_kernel(
+__global__ __launch_bounds__(kThreads, 2) void search_dma_kernel(
     const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
     const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
     const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws) {
   using T = typename Elem<DT>::T;
-  constexpr int KS = DIM / 16;             // k-steps of the 32x32x16 MFMA
-  constexpr int CH = DIM / 8;              // 16-byte chunks per centroid row
-  constexpr int PF = kStage * CH / kThreads;  // prefetch chunks per thread per stage
-  static_assert(kStage * CH % kThreads == 0, "stage must split evenly");
-  __shared__ __attribute__((aligned(16))) T cs[2][kStage][DIM + kPad];
-  __shared__ __attribute__((aligned(16))) float pen_s[2][kStage];
+  constexpr int KS = DIM / 16;                       // k-steps of the 32x32x16 MFMA
+  constexpr int CH = DIM / 8;                        // 16-byte chunks per centroid row
+  constexpr int ROWS = kDmaStageBytes / (DIM * 2);   // centroid rows per stage
+  constexpr int NSUB = ROWS / 32;                    // 32-row MFMA blocks per stage
+  constexpr int SLOTS = ROWS * CH;                   // 16-byte chunks per stage
+  constexpr int NDMA = SLOTS / kThreads;             // loads per thread (= per wave instruction count) per stage
+  static_assert(SLOTS % kThreads == 0 && NSUB >= 1, "stage shape");
+  __shared__ uint4 st0[SLOTS], st1[SLOTS], st2[SLOTS], st3[SLOTS];
+  __shared__ float pen_s[kDmaMaxChunk];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -155,84 +208,101 @@ __global__ __launch_bounds__(kThreads) void search_tile_kernel(
   const int64_t row_base = (int64_t)blockIdx.x * kTileRows + wave * (kQS * 32);
   const int64_t c_begin = split * chunk;
   const int64_t c_end = (c_begin + chunk < n_cent) ? c_begin + chunk : n_cent;
-  const int nstage = (int)((c_end - c_begin + kStage - 1) / kStage);
+  const int64_t c_last = c_end - 1;
+  const int nstage = (int)((c_end - c_begin + ROWS - 1) / ROWS);
+  const T *q_rows[kQS];
+#pragma unroll
+  for (int sl = 0; sl < kQS; ++sl) {
+    const int64_t r = row_base + sl * 32 + (lane & 31);
+    q_rows[sl] = (r < n) ? q + r * ld_q : nullptr;
+  }
+
+  // ring fill: slot p = tid + 256 u of stage `s` (clamped to the last stage,
+  // so every wave issues the same number of loads per step)
+  auto issue = [&](uint4 *buf, int s) {
+    const int sc = s < nstage - 1 ? s : nstage - 1;
+    const int64_t r0 = c_begin + (int64_t)sc * ROWS;
+#pragma unroll
+    for (int u = 0; u < NDMA; ++u) {
+      const int p = tid + u * kThreads;
+      const int r = p / CH;
+      const int j = (p % CH) ^ (r % CH);
+      const int64_t row = (r0 + r < c_last) ? r0 + r : c_last;
+      tm_dma16(cents + row * ld_c + j * 8, &buf[p - lane]);
+    }
+  };
+  // Issue order: penalties, the first ring stages, the queries; the penalty
+  // stores to LDS then wait only for the penalty loads.
+  constexpr int PEN_PER_THREAD = kDmaMaxChunk / kThreads;
+  float pen_v[PEN_PER_THREAD];
+#pragma unroll
+  for (int u = 0; u < PEN_PER_THREAD; ++u) {
+    const int64_t c = c_begin + tid + u * kThreads;
+    const float v = (METRIC == TM_METRIC_L2) ? c_sqnorm[c < c_last ? c : c_last] : 0.f;
+    pen_v[u] = (c < c_end) ? v : __builtin_huge_valf();
+  }
+  issue(st0, 0);
+  issue(st1, 1);
+  issue(st2, 2);
 
   // B operands: kQS slabs of 32 queries, all k-steps, in registers.
   uint4 qf[kQS][KS];
 #pragma unroll
-  for (int sl = 0; sl < kQS; ++sl) {
-    const int64_t r = row_base + sl * 32 + (lane & 31);
+  for (int sl = 0; sl < kQS; ++sl)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qf[sl][ks] = make_uint4(0, 0, 0, 0);
-      if (r < n) qf[sl][ks] = *reinterpret_cast<const uint4 *>(q + r * ld_q + ks * 16 + 8 * (lane >> 5));
-    }
-  }
+    for (int ks = 0; ks < KS; ++ks)
+      qf[sl][ks] = q_rows[sl] ? *reinterpret_cast<const uint4 *>(q_rows[sl] + ks * 16 + 8 * (lane >> 5))
+                              : make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int u = 0; u < PEN_PER_THREAD; ++u) pen_s[tid + u * kThreads] = pen_v[u];
 
   Best<K> best[kQS];
 #pragma unroll
   for (int sl = 0; sl < kQS; ++sl) best[sl].init();
 
-  uint4 pf[PF];
-  float pf_pen = 0.f;
-  auto fetch = [&](int64_t s0) {
-#pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int ci = tid + u * kThreads;
-      const int r = ci / CH, c8 = (ci % CH) * 8;
-      pf[u] = make_uint4(0, 0, 0, 0);
-      if (s0 + r < c_end) pf[u] = *reinterpret_cast<const uint4 *>(cents + (s0 + r) * ld_c + c8);
-    }
-    if (tid < kStage) {
-      const int64_t c = s0 + tid;
-      pf_pen = (c < c_end) ? ((METRIC == TM_METRIC_L2) ? c_sqnorm[c] : 0.f) : __builtin_huge_valf();
-    }
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int ci = tid + u * kThreads;
-      const int r = ci / CH, c8 = (ci % CH) * 8;
-      *reinterpret_cast<uint4 *>(&cs[buf][r][c8]) = pf[u];
-    }
-    if (tid < kStage) pen_s[buf][tid] = pf_pen;
-  };
-
-  fetch(c_begin);
-  for (int st = 0; st < nstage; ++st) {
-    const int buf = st & 1;
-    const int64_t s0 = c_begin + (int64_t)st * kStage;
-    stash(buf);
-    __syncthreads();
-    if (st + 1 < nstage) fetch(s0 + kStage);
-    // Both 32-centroid blocks' MFMAs are issued before either epilogue, so
-    // the VALU epilogue of one block overlaps the matrix unit on the other.
-    constexpr int NSUB = kStage / 32;
-    tm_f32x16 acc[NSUB][kQS];
+  auto step = [&](const uint4 *cur, uint4 *refill, int s) {
+    tm_wait_vm_lgkm0<2 * NDMA>();  // this stage's loads are done (two younger stages may be in flight)
+    __builtin_amdgcn_s_barrier();  // ... and every wave's, and the slot refilled below is free
+    issue(refill, s + kDmaBufs - 1);
+    const int64_t s0 = c_begin + (int64_t)s * ROWS;
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
+      const int row = sub * 32 + (lane & 31);
+      tm_f32x16 acc[kQS];
 #pragma unroll
-      for (int sl = 0; sl < kQS; ++sl) acc[sub][sl] = tm_f32x16{};
+      for (int sl = 0; sl < kQS; ++sl) acc[sl] = tm_f32x16{};
+      constexpr int AB = KS < 8 ? KS : 8;  // A fragments read ahead of their MFMAs
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint4 a = *reinterpret_cast<const uint4 *>(&cs[buf][sub * 32 + (lane & 31)][ks * 16 + 8 * (lane >> 5)]);
+      for (int k0 = 0; k0 < KS; k0 += AB) {
+        uint4 a[AB];
 #pragma unroll
-        for (int sl = 0; sl < kQS; ++sl) acc[sub][sl] = tm_mfma32x32x16<DT>(a, qf[sl][ks], acc[sub][sl]);
+        for (int u = 0; u < AB; ++u) {
+          const int j = 2 * (k0 + u) + (lane >> 5);
+          a[u] = cur[row * CH + (j ^ (row % CH))];
+        }
+#pragma unroll
+        for (int u = 0; u < AB; ++u)
+#pragma unroll
+          for (int sl = 0; sl < kQS; ++sl) acc[sl] = tm_mfma32x32x16<DT>(a[u], qf[sl][k0 + u], acc[sl]);
       }
-    }
-#pragma unroll
-    for (int sub = 0; sub < NSUB; ++sub) {
       float pen[16];
+      const int pb = s * ROWS + sub * 32 + 4 * (lane >> 5);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const float4 p4 = *reinterpret_cast<const float4 *>(&pen_s[buf][sub * 32 + 8 * g + 4 * (lane >> 5)]);
+        const float4 p4 = *reinterpret_cast<const float4 *>(&pen_s[pb + 8 * g]);
         pen[4 * g + 0] = p4.x; pen[4 * g + 1] = p4.y; pen[4 * g + 2] = p4.z; pen[4 * g + 3] = p4.w;
       }
-      const int cbase = (int)(s0 + sub * 32);
 #pragma unroll
-      for (int sl = 0; sl < kQS; ++sl) block_epilogue<K, METRIC>(acc[sub][sl], pen, cbase, lane, best[sl]);
+      for (int sl = 0; sl < kQS; ++sl) block_epilogue<K, METRIC>(acc[sl], pen, (int)(s0 + sub * 32), lane, best[sl]);
     }
+  };
+  for (int s = 0; s < nstage; s += kDmaBufs) {
+    step(st0, st3, s);
+    if (s + 1 < nstage) step(st1, st0, s + 1);  // uniform
+    if (s + 2 < nstage) step(st2, st1, s + 2);
+    if (s + 3 < nstage) step(st3, st2, s + 3);
   }
+  tm_wait_vm_lgkm0<0>();  // no load may still target this workgroup's LDS when it exits
 
 #pragma unroll
   for (int sl = 0; sl < kQS; ++sl) {
@@ -418,7 +488,7 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
                   const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm,
                   float *out_dist, int64_t *out_idx, uint64_t *ws, hipStream_t stream) {
   using T = typename Elem<DT>::T;
-  const SplitPlan p = plan_split(n, n_cent);
+  const SplitPlan p = plan_split(n, n_cent, DIM);
   const T *Q = static_cast<const T *>(q);
   const T *C = static_cast<const T *>(cents);
   dim3 block(kThreads);
@@ -430,7 +500,7 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
       hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 2, METRIC>), dim3((unsigned)p.nsplit), block, 0, stream,
                          Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
   } else {
-    hipLaunchKernelGGL((search_tile_kernel<DT, DIM, K, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
+    hipLaunchKernelGGL((search_dma_kernel<DT, DIM, K, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
                        block, 0, stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
   }
   TM_LAUNCH_CHECK("tm_search_global");
@@ -481,9 +551,8 @@ extern "C" int tm_centroid_sqnorms(int32_t dtype, const void *cents, int64_t n_c
 
 extern "C" size_t tm_search_global_workspace_size(int64_t n_tokens, int64_t n_cent, int32_t dim,
                                                   int32_t top_k) {
-  (void)dim;
-  if (n_tokens <= 0 || n_cent <= 0 || top_k <= 0) return 0;
-  const SplitPlan p = plan_split(n_tokens, n_cent);
+  if (n_tokens <= 0 || n_cent <= 0 || top_k <= 0 || (dim != 64 && dim != 128 && dim != 256)) return 0;
+  const SplitPlan p = plan_split(n_tokens, n_cent, dim);
   return (size_t)p.nsplit * (size_t)n_tokens * (size_t)list_len(top_k) * sizeof(uint64_t);
 }
 
