@@ -11,10 +11,13 @@ selection -> gather + combine + residual.  Inputs are resident in HBM before
 timing; steps rotate over replicas of the workload totalling > 2x the 256 MB
 Infinity Cache so reads come from HBM.
 
-Prints ONE JSON line: tokens/s per MoE layer (value), per-stage device times
-from HIP events recorded on the stream the kernels run on, the roofline of the
-dominant kernel, the decode (N=32, C=16384, top-4) layer, and the reference
-path restated on the host CPU (oracle, numpy fp32) as the CPU baseline.
+Prints ONE JSON line: tokens/s per MoE layer (value, from HIP-graph replays of
+one tm_table_forward call per layer), per-stage device times, the average
+device time of each stage's C-ABI call (graphs of 32 back-to-back calls timed
+with HIP events on the stream the kernels run on), the roofline of the
+dominant call (HBM bytes from the committed rocprofv3 PMC summary when
+present), the decode (N=32, C=16384, top-4) layer, and the reference path
+restated on the host CPU (oracle, numpy fp32) as the CPU baseline.
 """
 
 from __future__ import annotations
@@ -143,9 +146,94 @@ def run_layer_bench(cfg_id, steps, warmup, n=None):
     keep = step(0)
     torch.cuda.synchronize()
     n_keep = int(keep.sum().item())
+    kernel_us = stage_kernel_times(reps, tables, outs, topk, nn, kr)
     return dict(cfg=cfg, wl=wl, elapsed=elapsed, eager_ms_per_step=1000.0 * elapsed / steps,
                 ms_per_step=1000.0 * graph_elapsed / steps, graph_device_us=graph_device_us, stage_us=stage_us,
-                device_us=device_us, n_keep=n_keep, bytes=_stage_bytes(cfg, N, n_keep, nn, topk))
+                kernel_us=kernel_us, device_us=device_us, n_keep=n_keep,
+                bytes=_stage_bytes(cfg, N, n_keep, nn, topk))
+
+
+def stage_kernel_times(reps, tables, outs, topk, nn, kr, launches=32, replays=3):
+    """Average device time of each stage's C-ABI call: `launches` back-to-back
+    calls (rotating over the table replicas, so reads stay HBM-cold) captured
+    in one HIP graph, replayed `replays` times between two HIP events recorded
+    on the stream the kernels run on."""
+    import torch
+
+    def calls(name, i):
+        r, t, o = reps[i % len(reps)], tables[i % len(tables)], outs[i % len(outs)]
+        b = t._bufs
+        n = r.x.shape[0]
+        if name == "router":
+            t.route(r.logits, topk)
+        elif name == "project":
+            t.project(r.x, r.is_vision)
+        elif name == "search":
+            t.search(b["q"][: n * t.dim].view(n, t.dim), nn, b["qn"][:n])
+        elif name == "keep":
+            t.keep_select(b["dist"][: n * nn].view(n, nn)[:, 0], t.keep_count(n, kr))
+        else:
+            t.gather_combine(b["keep"][:n], r.slot_out, b["route_w"][: n * topk].view(n, topk),
+                             b["idx"][: n * nn].view(n, nn), b["dist"][: n * nn].view(n, nn), r.residual, o)
+
+    out = {}
+    for name in ("router", "project", "search", "keep", "combine"):
+        for i in range(len(tables)):  # allocate the stage's own buffers outside capture
+            calls(name, i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(launches):
+                calls(name, i)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = 1000.0 * e0.elapsed_time(e1) / (replays * launches)
+        del g
+    return out
+
+
+COPY_CAL_BYTES = 256 << 20  # bytes read (and written) by the calibration copy
+
+
+def copy_calibration(reps=3):
+    """A plain device copy pass over COPY_CAL_BYTES, launched `reps` times: under
+    `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` its counters give the scale
+    from counter KiB to bytes moved (profiles/gather_combine_config2_traffic.txt)."""
+    import torch
+
+    a = torch.empty(COPY_CAL_BYTES // 2, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        torch.neg(a, out=b)  # one elementwise pass: reads and writes COPY_CAL_BYTES (a distinct kernel name)
+    torch.cuda.synchronize()
+    del a, b
+
+
+def traffic_from_profile(kernel_prefix):
+    """HBM bytes per launch of `kernel_prefix` from the committed PMC summary
+    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by the same
+    counter's reading for the calibration copy), or None without a summary."""
+    path = REPO / "profiles" / "gather_combine_config2_traffic.txt"
+    if not path.exists():
+        return None
+    vals = {}
+    for line in path.read_text().splitlines():
+        if "=" in line and not line.lstrip().startswith("#"):
+            k, v = line.split("=", 1)
+            vals[k.strip()] = v.strip()
+    try:
+        fetch = float(vals[f"{kernel_prefix}.FETCH_SIZE_KiB"]) * 1024.0 * float(vals["copy.fetch_scale"])
+        write = float(vals[f"{kernel_prefix}.WRITE_SIZE_KiB"]) * 1024.0 * float(vals["copy.write_scale"])
+    except (KeyError, ValueError):
+        return None
+    return fetch + write
 
 
 def cpu_baseline(wl, budget_s=12.0):
@@ -226,25 +314,29 @@ def main() -> int:
 
     cfg = pre["cfg"]
     N, C, d = cfg["n"], cfg["n_cent"], cfg["dim"]
-    st, by = pre["stage_us"], pre["bytes"]
-    # dominant kernel and its roofline
-    dom = max(st, key=st.get)
+    st, by, ku = pre["stage_us"], pre["bytes"], pre["kernel_us"]
+    log(f"prefill per-call device times (graph of 32 calls): {json.dumps({k: round(v, 2) for k, v in ku.items()})}")
+    # dominant kernel (longest average call) and its roofline
+    dom = max(ku, key=ku.get)
+    entry = {"combine": "tm_gather_combine", "project": "tm_project", "router": "tm_topk_softmax",
+             "keep": "tm_keep_select", "search": "tm_search_global"}[dom]
     if dom == "search":
         flops = 2.0 * N * C * d
-        achieved = flops / (st[dom] * 1e-6) / 1e12
-        roof = {"kernel": "tm_search_global (search + merge launches)", "bound": "mfma", "achieved": achieved,
-                "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None}
+        achieved = flops / (ku[dom] * 1e-6) / 1e12
+        roof = {"kernel": entry, "bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None,
+                "algorithmic_per_launch": flops}
     else:
-        achieved = by[dom] / (st[dom] * 1e-6) / 1e9
-        roof = {"kernel": {"combine": "tm_gather_combine", "project": "tm_project", "router": "tm_topk_softmax",
-                           "keep": "tm_keep_select"}[dom], "bound": "hbm", "achieved": achieved,
-                "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": None}
-    roof["algorithmic_per_launch"] = by[dom] if roof["bound"] == "hbm" else 2.0 * N * C * d
-    roof["avg_launch_us"] = st[dom]
+        achieved = by[dom] / (ku[dom] * 1e-6) / 1e9
+        roof = {"kernel": entry, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBPS,
+                "traffic": traffic_from_profile("gather_combine") if dom == "combine" else None,
+                "algorithmic_per_launch": by[dom]}
+    roof["avg_launch_us"] = ku[dom]
 
     total_bytes = sum(by.values())
     ds = dec["stage_us"]
-    search_tflops = 2.0 * N * C * d / (st["search"] * 1e-6) / 1e12
+    search_tflops = 2.0 * N * C * d / (ku["search"] * 1e-6) / 1e12
     result = {
         "metric": METRIC,
         "value": N / (pre["ms_per_step"] * 1e-3),
@@ -266,12 +358,13 @@ def main() -> int:
             "replicas": N_REPLICAS,
         },
         "stages_us": {k: round(v, 2) for k, v in st.items()},
+        "calls_us": {k: round(v, 2) for k, v in ku.items()},
         "timing": "ms_per_step: layers replayed from HIP graphs (one captured tm_table_forward per "
                   "replica); eager_ms_per_step: one tm_table_forward call per layer from Python",
         "eager_ms_per_step": pre["eager_ms_per_step"],
         "eager_tokens_per_s": N / (pre["eager_ms_per_step"] * 1e-3),
         "layer_device_us": pre["graph_device_us"],
-        "layer_hbm_GBps": total_bytes / (sum(st.values()) * 1e-6) / 1e9,
+        "layer_hbm_GBps": total_bytes / (pre["graph_device_us"] * 1e-6) / 1e9,
         "search_mfma_tflops": search_tflops,
         "search_mfma_frac": search_tflops / BF16_PEAK_TFLOPS,
         "roofline": roof,
@@ -283,10 +376,12 @@ def main() -> int:
             "layer_device_us": dec["graph_device_us"],
             "tokens_per_s": 32 / (dec["ms_per_step"] * 1e-3),
             "stages_us": {k: round(v, 2) for k, v in ds.items()},
-            "search_hbm_GBps": dec["bytes"]["search"] / (ds["search"] * 1e-6) / 1e9,
-            "layer_hbm_GBps": sum(dec["bytes"].values()) / (sum(ds.values()) * 1e-6) / 1e9,
+            "calls_us": {k: round(v, 2) for k, v in dec["kernel_us"].items()},
+            "search_hbm_GBps": dec["bytes"]["search"] / (dec["kernel_us"]["search"] * 1e-6) / 1e9,
+            "layer_hbm_GBps": sum(dec["bytes"].values()) / (dec["graph_device_us"] * 1e-6) / 1e9,
         },
     }
+    copy_calibration()
     if not args.no_cpu:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(pre["wl"])
