@@ -184,6 +184,97 @@ __global__ __launch_bounds__(kThreads) void gather_combine_fast_kernel(
   }
 }
 
+// Shape-specialised path (top_k = TK recomputed slots, NN nearest centroids,
+// 2-byte types, 16-byte aligned rows): the keep flag selects one of two
+// wave-uniform branches, and inside each every source load is unconditional,
+// so all of a chunk's loads are in flight together (a load behind a per-source
+// branch makes the compiler wait for everything outstanding at the join).
+// Slot outputs, the residual and the output are streamed once: non-temporal
+// accesses; gathered value rows use ordinary loads (centroids repeat).
+// Same arithmetic as gather_combine_fast_kernel: fp32 accumulation starting
+// from the residual, sources added in order with fmaf, one rounding.
+template <int DT, int TK, int NN>
+__global__ __launch_bounds__(kThreads) void gather_combine_tk_kernel(
+    int hidden, const uint8_t *__restrict__ keep, const typename Elem<DT>::T *__restrict__ slot_out, int64_t so_b,
+    int64_t so_s, const float *__restrict__ w, int64_t ld_w, const typename Elem<DT>::T *__restrict__ values,
+    int64_t n_cent, int64_t ld_v, const int64_t *__restrict__ idx, const float *__restrict__ dist, int64_t ld_idx,
+    const typename Elem<DT>::T *__restrict__ residual, int64_t ld_r, typename Elem<DT>::T *__restrict__ out,
+    int64_t ld_o) {
+  using T = typename Elem<DT>::T;
+  const int64_t b = blockIdx.x;
+  const T *res_row = residual ? residual + b * ld_r : nullptr;
+  T *dst = out + b * ld_o;
+  if (keep[b]) {  // uniform
+    float coef[TK];
+    float sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < TK; ++s) {
+      coef[s] = w[b * ld_w + s];
+      sum += coef[s];
+    }
+    const bool any = sum > 0.f;  // rows whose weights sum to 0 contribute nothing
+#pragma unroll
+    for (int s = 0; s < TK; ++s) coef[s] = coef[s] / sum;
+    const T *src = slot_out + b * so_b;
+    for (int h0 = threadIdx.x * 8; h0 < hidden; h0 += kThreads * 8) {
+      float acc[8];
+      if (res_row) {
+        tm_load8_nt<DT>(res_row + h0, acc);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+      }
+      if (any) {
+        float v[TK][8];
+#pragma unroll
+        for (int s = 0; s < TK; ++s) tm_load8_nt<DT>(src + (int64_t)s * so_s + h0, v[s]);
+#pragma unroll
+        for (int s = 0; s < TK; ++s)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], v[s][i], acc[i]);
+      }
+      tm_store8_nt<DT>(dst + h0, acc);
+    }
+  } else {
+    const T *src[NN];
+    float coef[NN];
+    bool ok[NN];
+    float inv_sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < NN; ++j) {
+      const int64_t c = idx[b * ld_idx + j];
+      ok[j] = c >= 0 && c < n_cent;
+      src[j] = values + (ok[j] ? c : 0) * ld_v;
+      coef[j] = ok[j] ? ((NN > 1) ? 1.f / (dist[b * ld_idx + j] + 1e-6f) : 1.f) : 0.f;
+      inv_sum += coef[j];
+    }
+    if (NN > 1) {
+#pragma unroll
+      for (int j = 0; j < NN; ++j) coef[j] = ok[j] ? coef[j] / inv_sum : 0.f;
+    }
+    for (int h0 = threadIdx.x * 8; h0 < hidden; h0 += kThreads * 8) {
+      float acc[8];
+      if (res_row) {
+        tm_load8_nt<DT>(res_row + h0, acc);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+      }
+      float v[NN][8];
+#pragma unroll
+      for (int j = 0; j < NN; ++j) tm_load8<DT>(src[j] + h0, v[j]);
+#pragma unroll
+      for (int j = 0; j < NN; ++j) {
+        if (ok[j]) {  // uniform; the loads above are already issued
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[j], v[j][i], acc[i]);
+        }
+      }
+      tm_store8_nt<DT>(dst + h0, acc);
+    }
+  }
+}
+
 // General path (more than 8 sources): sources staged through LDS.
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void gather_combine_kernel(
@@ -364,6 +455,17 @@ extern "C" int tm_gather_rows(int32_t dtype, const void *values, int64_t n_exper
   });
 }
 
+// Launch of the shape-specialised combine when (top_k, n_nearest) matches.
+#define TM_GC_TK(TK_, NN_)                                                                                     \
+  if (top_k == TK_ && n_nearest == NN_) {                                                                      \
+    hipLaunchKernelGGL((gather_combine_tk_kernel<DT, TK_, NN_>), grid, block, 0, s, hidden, keep,              \
+                       static_cast<const T *>(slot_out), so_b, so_s, weights, ld_w, static_cast<const T *>(values), \
+                       n_cent, ld_v, idx, dist, ld_idx, static_cast<const T *>(residual), ld_r, static_cast<T *>(out), \
+                       ld_o);                                                                                  \
+    TM_LAUNCH_CHECK("tm_gather_combine");                                                                      \
+    return TM_OK;                                                                                              \
+  }
+
 extern "C" int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden, const uint8_t *keep,
                                  const void *slot_out, int64_t so_b, int64_t so_s, const float *weights,
                                  int64_t ld_w, int32_t top_k, const void *values, int64_t n_cent,
@@ -385,6 +487,16 @@ extern "C" int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden
                      (so_s * E) % 16 == 0 && rows_aligned(values, ld_v, E) &&
                      rows_aligned(residual, ld_r, E) && rows_aligned(out, ld_o, E);
     const bool fast = top_k <= kFastSrc && n_nearest <= kFastSrc;
+    if constexpr (Elem<DT>::kBytes == 2) {
+      if (vec) {
+        const dim3 grid((unsigned)n_tokens), block(kThreads);
+        hipStream_t s = tm_hip_stream(stream);
+        TM_GC_TK(8, 1)
+        TM_GC_TK(8, 4)
+        TM_GC_TK(6, 1)
+        TM_GC_TK(6, 4)
+      }
+    }
     auto launch = [&](auto vec_tag) {
       constexpr bool VEC = decltype(vec_tag)::value;
       if (fast)
@@ -407,6 +519,8 @@ extern "C" int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden
     return TM_OK;
   });
 }
+
+#undef TM_GC_TK
 
 extern "C" int tm_slot_combine(int32_t dtype, int64_t n_tokens, int32_t top_k, int32_t hidden,
                                const float *weights, int64_t ld_w, const uint8_t *compute_mask,

@@ -105,6 +105,29 @@ __device__ __forceinline__ void tm_store8(typename Elem<DT>::T *p, const float (
   }
 }
 
+// Streaming variants for 2-byte types: non-temporal 16-byte accesses for data
+// read or written once (kept out of the caches' working set).
+typedef unsigned int tm_u32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ void tm_load8_nt(const typename Elem<DT>::T *p, float (&v)[8]) {
+  static_assert(Elem<DT>::kBytes == 2, "2-byte types only");
+  const tm_u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const tm_u32x4 *>(p));
+  const typename Elem<DT>::T *e = reinterpret_cast<const typename Elem<DT>::T *>(&r);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = Elem<DT>::to_f(e[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void tm_store8_nt(typename Elem<DT>::T *p, const float (&v)[8]) {
+  static_assert(Elem<DT>::kBytes == 2, "2-byte types only");
+  tm_u32x4 r;
+  typename Elem<DT>::T *e = reinterpret_cast<typename Elem<DT>::T *>(&r);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) e[i] = Elem<DT>::from_f(v[i]);
+  __builtin_nontemporal_store(r, reinterpret_cast<tm_u32x4 *>(p));
+}
+
 // True when a pointer is aligned for tm_load8/tm_store8 of this type.
 static inline bool tm_aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

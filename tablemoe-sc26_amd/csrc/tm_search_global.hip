@@ -33,7 +33,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kQS = 2;      // query slabs per wave in the tile kernel
 constexpr int kTileRows = 4 * kQS * 32;
-constexpr int kStreamBlocksPerWave = 2;
+constexpr int kStreamBlocksPerWave = 1;
 
 struct SplitPlan {
   bool stream;  // small-n shape

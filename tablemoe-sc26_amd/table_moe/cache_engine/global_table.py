@@ -75,7 +75,8 @@ class GlobalTable:
         for s in shape:
             numel *= s
         if t is None or t.dtype != dtype or t.numel() < numel:
-            t = torch.empty(max(numel, 1), dtype=dtype, device=self.device)
+            # zero-filled: the search workspace starts with counters that must be zero
+            t = torch.zeros(max(numel, 1), dtype=dtype, device=self.device)
             self._bufs[name] = t
         return t[:numel].view(shape)
 

@@ -349,13 +349,18 @@ def test_engine_rejects_host_tensors():
 
 
 # ------------------------------------------------ mode G: gather + combine
-@pytest.mark.parametrize("nn,hidden,with_residual", [(1, 2048, True), (4, 2048, True), (4, 1004, False)])
-def test_gather_combine_vs_oracle(hip_device, nn, hidden, with_residual):
+@pytest.mark.parametrize("k,nn,hidden,with_residual", [(8, 1, 2048, True), (8, 4, 2048, True), (8, 4, 1004, False),
+                                                        (6, 1, 2560, True), (6, 4, 2560, False), (5, 2, 2048, True),
+                                                        (8, 1, 4096, False)])
+def test_gather_combine_vs_oracle(hip_device, k, nn, hidden, with_residual):
+    """Shape-specialised kernels (top-8/top-6 x 1/4 nearest, 16-byte rows),
+    hidden sizes that take several or partial 2048-wide chunks, and the
+    general kernels (other shapes, unaligned rows)."""
     from table_moe.cache_engine import GlobalTable
 
-    g = _gen(141)
+    g = _gen(141 + k + nn + hidden)
     dev = hip_device
-    n, k, C, d = 257, 8, 500, 64
+    n, C, d = 257, 500, 64
     dt = torch.bfloat16
     values = torch.randn(C, hidden, generator=g).to(dt)
     slot_out = torch.randn(n, k, hidden, generator=g).to(dt)
