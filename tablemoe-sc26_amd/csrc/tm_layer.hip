@@ -1,6 +1,6 @@
 // One MoE layer of the global-table path in one call: the stage entry points
 // enqueued back to back on one stream, the workspace split between them.
-#include "tm_common.h"
+#include "tm_internal.h"
 
 namespace {
 
@@ -54,8 +54,14 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
   char *ws = static_cast<char *>(workspace);
   hipStream_t s = tm_hip_stream(stream);
   int st;
+  // The router's results are only consumed by the combine: without stage
+  // events it rides in the keep-selection launch (whose single selecting
+  // workgroup leaves the chip idle), and its own stage interval is empty.
+  const bool route_with_keep = stage_events == nullptr && io->router_top_k <= 8 &&
+                               (io->n_experts == 64 || io->n_experts == 128);
   if ((st = record(stage_events, 0, s)) != TM_OK) return st;
-  if ((st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k, 0,
+  if (!route_with_keep &&
+      (st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k, 0,
                             io->weights, io->expert_ids, stream)) != TM_OK)
     return st;
   if ((st = record(stage_events, 1, s)) != TM_OK) return st;
@@ -69,9 +75,23 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
                              ws + w.project, w.search, stream)) != TM_OK)
     return st;
   if ((st = record(stage_events, 3, s)) != TM_OK) return st;
-  if ((st = tm_keep_select(io->dist, n, io->n_nearest, tm_keep_count(n, io->keep_rate), io->keep,
-                           w.keep ? ws + w.project + w.search : nullptr, w.keep, stream)) != TM_OK)
-    return st;
+  const int64_t n_keep = tm_keep_count(n, io->keep_rate);
+  int fused = TM_NOT_FUSED;
+  if (route_with_keep) {
+    TM_REQUIRE(io->router_logits && n_keep >= 0, TM_EINVAL_ARG, "tm_table_forward: router logits missing");
+    fused = tm_internal_keep_route(io->dist, n, io->n_nearest, n_keep, io->keep, io->router_logits, io->ld_logits,
+                                   io->n_experts, io->router_top_k, io->weights, io->expert_ids, s);
+    if (fused != TM_OK && fused != TM_NOT_FUSED) return fused;
+  }
+  if (fused == TM_NOT_FUSED) {
+    if (route_with_keep &&
+        (st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k, 0,
+                              io->weights, io->expert_ids, stream)) != TM_OK)
+      return st;
+    if ((st = tm_keep_select(io->dist, n, io->n_nearest, n_keep, io->keep,
+                             w.keep ? ws + w.project + w.search : nullptr, w.keep, stream)) != TM_OK)
+      return st;
+  }
   if ((st = record(stage_events, 4, s)) != TM_OK) return st;
   if ((st = tm_gather_combine(t->dtype, n, t->hidden, io->keep, io->slot_out, io->so_b, io->so_s, io->weights,
                               io->router_top_k, io->router_top_k, t->values, t->n_cent, t->ld_v, io->idx,

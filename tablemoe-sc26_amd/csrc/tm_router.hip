@@ -4,7 +4,7 @@
 // fp32 softmax (max, exp, sum, divide), then top_k rounds of an arg-max whose
 // ties go to the lower expert id; the winner is masked out after each round.
 // Rows of up to 256 experts use 8 lanes per token; wider rows one wave.
-#include "tm_common.h"
+#include "tm_route_dev.h"
 
 namespace {
 
@@ -142,6 +142,17 @@ __global__ __launch_bounds__(kThreads) void topk_softmax_group_kernel(const floa
   }
 }
 
+// Rows of 64, 128 or 256 experts with 16-byte aligned rows: tm_route_token,
+// 8 tokens per 64-thread workgroup.
+template <int VPL, int KM>
+__global__ __launch_bounds__(64) void topk_softmax_vec_kernel(const float *__restrict__ logits, int64_t n, int64_t ld,
+                                                             int top_k, int renorm, float *__restrict__ out_w,
+                                                             int64_t *__restrict__ out_ids) {
+  const int lane = threadIdx.x & 63;
+  tm_route_token<VPL, KM>(logits, n, ld, top_k, renorm, out_w, out_ids, (int64_t)blockIdx.x * 8 + (lane >> 3),
+                          lane & 7);
+}
+
 }  // namespace
 
 extern "C" int tm_topk_softmax(const float *logits, int64_t n_tokens, int32_t n_experts,
@@ -157,6 +168,22 @@ extern "C" int tm_topk_softmax(const float *logits, int64_t n_tokens, int32_t n_
   hipStream_t s = tm_hip_stream(stream);
   // one wave (8 tokens) per workgroup: spreads small batches over more CUs
   const dim3 ggrid((unsigned)tm_cdiv(n_tokens, 8)), gblock(64);
+  const bool vec4 = tm_aligned16(logits) && ld_logits % 4 == 0;
+#define TM_ROUTER_VEC(E_, VPL_)                                                                                \
+  if (vec4 && n_experts == E_) {                                                                              \
+    if (top_k <= 8)                                                                                           \
+      hipLaunchKernelGGL((topk_softmax_vec_kernel<VPL_, 8>), ggrid, gblock, 0, s, logits, n_tokens, ld_logits,  \
+                         top_k, renormalize, out_weights, out_ids);                                          \
+    else                                                                                                      \
+      hipLaunchKernelGGL((topk_softmax_vec_kernel<VPL_, 32>), ggrid, gblock, 0, s, logits, n_tokens, ld_logits, \
+                         top_k, renormalize, out_weights, out_ids);                                          \
+    TM_LAUNCH_CHECK("tm_topk_softmax");                                                                       \
+    return TM_OK;                                                                                             \
+  }
+  TM_ROUTER_VEC(64, 8)
+  TM_ROUTER_VEC(128, 16)
+  TM_ROUTER_VEC(256, 32)
+#undef TM_ROUTER_VEC
   if (n_experts <= 64)
     hipLaunchKernelGGL(topk_softmax_group_kernel<8>, ggrid, gblock, 0, s, logits, n_tokens, n_experts, ld_logits, top_k, renormalize, out_weights, out_ids);
   else if (n_experts <= 128)

@@ -1,7 +1,8 @@
 // Selection kernels: keep-rate radix select (north-star kernel (3)), the
 // reference's keep masks (table_moe/skip/pruning.py) and surviving-weight
 // renormalisation.
-#include "tm_common.h"
+#include "tm_internal.h"
+#include "tm_route_dev.h"
 
 namespace {
 
@@ -49,10 +50,30 @@ constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kSelRegs = 16;
 
+// Router work carried by the keep launch (the fused layer call): the
+// selection uses one workgroup and leaves the rest of the chip idle, and the
+// routing results are only needed by the combine that follows.  Workgroups
+// 1.. route kSelThreads / 8 tokens each (8 lanes per token).
+struct SelRoute {
+  const float *logits;
+  int64_t ld;
+  int top_k;
+  float *out_w;
+  int64_t *out_ids;
+};
+
+template <int RVPL>
 __global__ __launch_bounds__(kSelThreads) void keep_select_kernel(const float *__restrict__ score,
                                                                   int64_t n, int64_t ld,
                                                                   int64_t n_keep,
-                                                                  uint8_t *__restrict__ out) {
+                                                                  uint8_t *__restrict__ out, SelRoute ra) {
+  if constexpr (RVPL > 0) {
+    if (blockIdx.x > 0) {  // uniform: a routing workgroup (no barrier)
+      const int64_t tok = (int64_t)(blockIdx.x - 1) * (kSelThreads / 8) + (threadIdx.x >> 3);
+      tm_route_token<RVPL, 8>(ra.logits, n, ra.ld, ra.top_k, 0, ra.out_w, ra.out_ids, tok, threadIdx.x & 7);
+      return;
+    }
+  }
   __shared__ uint32_t whist[kSelWaves][256];  // per-wave private histograms
   __shared__ uint32_t hist[256];
   __shared__ uint32_t s_prefix, s_mask;
@@ -307,9 +328,28 @@ extern "C" int tm_keep_select(const float *score, int64_t n, int64_t ld_score, i
              "tm_keep_select: bad sizes n=%lld", (long long)n);
   if (n == 0) return TM_OK;
   TM_REQUIRE(score && out_keep, TM_EINVAL_ARG, "tm_keep_select: null pointer");
-  hipLaunchKernelGGL(keep_select_kernel, dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
-                     score, n, ld_score, n_keep, out_keep);
+  hipLaunchKernelGGL((keep_select_kernel<0>), dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
+                     score, n, ld_score, n_keep, out_keep, SelRoute{});
   TM_LAUNCH_CHECK("tm_keep_select");
+  return TM_OK;
+}
+
+int tm_internal_keep_route(const float *score, int64_t n, int64_t ld_score, int64_t n_keep, uint8_t *out_keep,
+                           const float *logits, int64_t ld_logits, int32_t n_experts, int32_t top_k, float *out_w,
+                           int64_t *out_ids, hipStream_t stream) {
+  if (n <= 0 || n >= ((int64_t)1 << 31) || ld_score < 1 || !score || !out_keep || !logits || !out_w || !out_ids ||
+      top_k < 1 || top_k > 8 || (n_experts != 64 && n_experts != 128) || ld_logits < n_experts ||
+      !tm_aligned16(logits) || ld_logits % 4 != 0)
+    return TM_NOT_FUSED;
+  const SelRoute ra{logits, ld_logits, top_k, out_w, out_ids};
+  const dim3 grid((unsigned)(1 + tm_cdiv(n, kSelThreads / 8)));
+  if (n_experts == 64)
+    hipLaunchKernelGGL((keep_select_kernel<8>), grid, dim3(kSelThreads), 0, stream, score, n, ld_score, n_keep,
+                       out_keep, ra);
+  else
+    hipLaunchKernelGGL((keep_select_kernel<16>), grid, dim3(kSelThreads), 0, stream, score, n, ld_score, n_keep,
+                       out_keep, ra);
+  TM_LAUNCH_CHECK("tm_table_forward(keep+route)");
   return TM_OK;
 }
 

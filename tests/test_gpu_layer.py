@@ -32,7 +32,8 @@ def test_single_hip_runtime_in_process(hip_device):
 
 # ---------------------------------------------------------------- a1 router
 @pytest.mark.parametrize("n,e,k,renorm", [(4096, 128, 8, False), (300, 64, 6, True), (77, 300, 5, False),
-                                          (5, 2048, 32, False), (1, 8, 8, True)])
+                                          (5, 2048, 32, False), (1, 8, 8, True), (1001, 256, 12, True),
+                                          (13, 128, 1, False), (9, 100, 8, False)])
 def test_topk_softmax_vs_oracle(hip_device, n, e, k, renorm):
     from table_moe.ops import qwen_topk_softmax
 
@@ -424,12 +425,15 @@ def test_layer_forward_config2_end_to_end(hip_device):
 
 
 def test_layer_forward_one_call_matches_staged(hip_device):
-    """tm_table_forward (one call) and the five stage calls give identical bits."""
+    """tm_table_forward (one call, router fused into the projection launch for
+    64/128 experts) and the five stage calls give identical bits; config 5
+    shapes (64 experts, top-6, hidden 2560) at a token count that leaves a
+    partial routing workgroup."""
     from table_moe.cache_engine import GlobalTable
     from table_moe.synth import make_workload
 
     dev = hip_device
-    for cfg, n, nn in ((2, 1000, 1), (3, 32, 4)):
+    for cfg, n, nn in ((2, 1000, 1), (3, 32, 4), (5, 77, 1)):
         d = make_workload(cfg, n=n).to(dev)
         a = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
         b = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
