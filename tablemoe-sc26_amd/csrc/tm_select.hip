@@ -175,6 +175,138 @@ __global__ __launch_bounds__(kSelThreads) void keep_select_kernel(const float *_
 }
 
 // ---------------------------------------------------------------------------
+// (3), fast form for n <= kSelThreads * kSelRegs: same result as above.
+// A block min/max first finds the highest bit in which the keys differ (the
+// bits above it are common: for distances, the sign and most of the
+// exponent), then radix passes of up to 12 bits walk down from there over
+// one shared 4096-bin histogram (usually two passes).  The boundary bin is
+// found with one block scan over the bins in descending order (thread t
+// owns the 4 bins of rank 1023 - t).  Ties at the boundary: lower token
+// index first, as above.
+// ---------------------------------------------------------------------------
+constexpr int kFastBins = 4096;
+constexpr int kFastDigit = 12;
+
+template <int RVPL>
+__global__ __launch_bounds__(kSelThreads) void keep_select_fast_kernel(const float *__restrict__ score, int64_t n,
+                                                                       int64_t ld, int64_t n_keep,
+                                                                       uint8_t *__restrict__ out, SelRoute ra) {
+  if constexpr (RVPL > 0) {
+    if (blockIdx.x > 0) {  // uniform: a routing workgroup (no barrier)
+      const int64_t tok = (int64_t)(blockIdx.x - 1) * (kSelThreads / 8) + (threadIdx.x >> 3);
+      tm_route_token<RVPL, 8>(ra.logits, n, ra.ld, ra.top_k, 0, ra.out_w, ra.out_ids, tok, threadIdx.x & 7);
+      return;
+    }
+  }
+  __shared__ uint32_t hist[kFastBins];
+  __shared__ uint32_t wave_tot[kSelWaves + 1];
+  __shared__ uint32_t s_min[kSelWaves], s_max[kSelWaves];
+  __shared__ uint32_t s_prefix;
+  __shared__ int64_t s_remaining;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (int)((n + kSelThreads - 1) / kSelThreads);
+  const int64_t lo = (int64_t)tid * per;
+  const int64_t hi = (lo + per < n) ? lo + per : n;
+  const int cnt = (int)(hi > lo ? hi - lo : 0);
+
+  if (n_keep <= 0 || n_keep >= n) {
+    const uint8_t v = n_keep > 0 ? 1 : 0;
+    for (int64_t i = lo; i < hi; ++i) out[i] = v;
+    return;
+  }
+  uint32_t keys[kSelRegs];
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+  for (int j = 0; j < kSelRegs; ++j) {
+    keys[j] = (j < cnt) ? tm_orderable(score[(lo + j) * ld]) : 0u;
+    if (j < cnt) {
+      kmin = keys[j] < kmin ? keys[j] : kmin;
+      kmax = keys[j] > kmax ? keys[j] : kmax;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t a = __shfl_xor(kmin, o, 64), b = __shfl_xor(kmax, o, 64);
+    kmin = a < kmin ? a : kmin;
+    kmax = b > kmax ? b : kmax;
+  }
+  if (lane == 0) { s_min[wave] = kmin; s_max[wave] = kmax; }
+  if (tid == 0) s_remaining = n_keep;
+  __syncthreads();
+  kmin = s_min[0];
+  kmax = s_max[0];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) {
+    kmin = s_min[w] < kmin ? s_min[w] : kmin;
+    kmax = s_max[w] > kmax ? s_max[w] : kmax;
+  }
+  uint32_t prefix = kmin & kmax, mask = 0u;  // common high bits
+  int top = -1;
+  if (kmin != kmax) {
+    top = 31 - __builtin_clz(kmin ^ kmax);  // highest differing bit
+    mask = (top == 31) ? 0u : (0xffffffffu << (top + 1));
+    prefix &= mask;
+  } else {
+    mask = 0xffffffffu;
+    prefix = kmin;
+  }
+  for (int hi_bit = top; hi_bit >= 0; hi_bit -= kFastDigit) {  // uniform trip count
+    const int w = hi_bit + 1 < kFastDigit ? hi_bit + 1 : kFastDigit;
+    const int shift = hi_bit + 1 - w;
+    const uint32_t dmask = (1u << w) - 1u;
+#pragma unroll
+    for (int b = 0; b < kFastBins / kSelThreads; ++b) hist[tid + b * kSelThreads] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSelRegs; ++j)
+      if (j < cnt && (keys[j] & mask) == prefix) atomicAdd(&hist[(keys[j] >> shift) & dmask], 1u);
+    __syncthreads();
+    // thread t owns bins 4r .. 4r+3 of rank r = 1023 - t (descending bin order across threads)
+    const int r = kSelThreads - 1 - tid;
+    uint32_t hb[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) hb[b] = hist[4 * r + b];
+    const uint32_t tsum = hb[0] + hb[1] + hb[2] + hb[3];
+    const int64_t rem = s_remaining;  // read before the scan's barriers: the update below follows them
+    uint32_t total;
+    const uint32_t above0 = block_exclusive_scan<kSelThreads>(tsum, wave_tot, total);  // keys in higher bins
+    int64_t above = above0;
+#pragma unroll
+    for (int b = 3; b >= 0; --b) {
+      if (above < rem && rem <= above + (int64_t)hb[b]) {
+        s_prefix = prefix | ((uint32_t)(4 * r + b) << shift);
+        s_remaining = rem - above;
+      }
+      above += hb[b];
+    }
+    __syncthreads();
+    prefix = s_prefix;
+    mask |= dmask << shift;
+    __syncthreads();  // every thread has read s_prefix / s_remaining / wave_tot before the next pass
+  }
+  const uint32_t T = prefix;
+  const int64_t keep_eq = s_remaining;  // copies of T to keep, >= 1
+  uint32_t eq = 0;
+#pragma unroll
+  for (int j = 0; j < kSelRegs; ++j) eq += (j < cnt && keys[j] == T) ? 1u : 0u;
+  uint32_t total;
+  uint32_t rank = block_exclusive_scan<kSelThreads>(eq, wave_tot, total);
+#pragma unroll
+  for (int j = 0; j < kSelRegs; ++j) {
+    if (j < cnt) {
+      uint8_t k = 0;
+      if (keys[j] > T) {
+        k = 1;
+      } else if (keys[j] == T) {
+        k = ((int64_t)rank < keep_eq) ? 1 : 0;
+        ++rank;
+      }
+      out[lo + j] = k;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // a3: build_fixed_keep_mask (pruning.py:4-15)
 // ---------------------------------------------------------------------------
 __global__ void fixed_keep_kernel(int64_t total, int top_k, int keep_k, uint8_t *out) {
@@ -328,8 +460,12 @@ extern "C" int tm_keep_select(const float *score, int64_t n, int64_t ld_score, i
              "tm_keep_select: bad sizes n=%lld", (long long)n);
   if (n == 0) return TM_OK;
   TM_REQUIRE(score && out_keep, TM_EINVAL_ARG, "tm_keep_select: null pointer");
-  hipLaunchKernelGGL((keep_select_kernel<0>), dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
-                     score, n, ld_score, n_keep, out_keep, SelRoute{});
+  if (n <= (int64_t)kSelThreads * kSelRegs)
+    hipLaunchKernelGGL((keep_select_fast_kernel<0>), dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
+                       score, n, ld_score, n_keep, out_keep, SelRoute{});
+  else
+    hipLaunchKernelGGL((keep_select_kernel<0>), dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
+                       score, n, ld_score, n_keep, out_keep, SelRoute{});
   TM_LAUNCH_CHECK("tm_keep_select");
   return TM_OK;
 }
@@ -343,7 +479,14 @@ int tm_internal_keep_route(const float *score, int64_t n, int64_t ld_score, int6
     return TM_NOT_FUSED;
   const SelRoute ra{logits, ld_logits, top_k, out_w, out_ids};
   const dim3 grid((unsigned)(1 + tm_cdiv(n, kSelThreads / 8)));
-  if (n_experts == 64)
+  const bool fast = n <= (int64_t)kSelThreads * kSelRegs;
+  if (n_experts == 64 && fast)
+    hipLaunchKernelGGL((keep_select_fast_kernel<8>), grid, dim3(kSelThreads), 0, stream, score, n, ld_score, n_keep,
+                       out_keep, ra);
+  else if (fast)
+    hipLaunchKernelGGL((keep_select_fast_kernel<16>), grid, dim3(kSelThreads), 0, stream, score, n, ld_score,
+                       n_keep, out_keep, ra);
+  else if (n_experts == 64)
     hipLaunchKernelGGL((keep_select_kernel<8>), grid, dim3(kSelThreads), 0, stream, score, n, ld_score, n_keep,
                        out_keep, ra);
   else

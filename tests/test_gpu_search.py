@@ -396,8 +396,8 @@ def test_search_global_precomputed_qnorm_and_repeat(hip_device):
 
 
 # ------------------------------------------------------------- keep selection
-@pytest.mark.parametrize("n", [1, 2, 5, 1023, 1024, 1025, 4096, 5000, 70000])
-@pytest.mark.parametrize("pattern", ["random", "ties", "constant", "signed"])
+@pytest.mark.parametrize("n", [1, 2, 5, 1023, 1024, 1025, 4096, 5000, 16384, 16385, 70000])
+@pytest.mark.parametrize("pattern", ["random", "ties", "constant", "signed", "clustered"])
 def test_keep_select_exact(hip_device, n, pattern):
     g = _gen(51 + n)
     if pattern == "random":
@@ -406,6 +406,8 @@ def test_keep_select_exact(hip_device, n, pattern):
         s = torch.randint(0, 7, (n,), generator=g).float() * 0.5
     elif pattern == "constant":
         s = torch.full((n,), 3.25)
+    elif pattern == "clustered":  # one exponent, keys differing only in low mantissa bits
+        s = 100.0 + torch.randint(0, 50, (n,), generator=g).float() * 2.0 ** -16
     else:
         s = torch.randn(n, generator=g) * 1e3
         s[: n // 3] = -0.0
