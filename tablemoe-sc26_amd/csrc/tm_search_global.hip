@@ -46,7 +46,12 @@ struct SplitPlan {
 // Centroid rows per pipelined stage of the tile kernel (16 KiB stages).
 static inline int64_t dma_rows(int dim) { return 16384 / (dim * 2); }
 
-SplitPlan plan_split(int64_t n, int64_t c, int dim) {
+// Top-1 searches with d <= 128 run search_top1_kernel (or, for very wide
+// centroid strides, search_dma_kernel); its loop covers whole rounds of the
+// four-stage ring, so their chunks are a multiple of four stages.
+static inline bool top1_tile(int dim, int top_k) { return top_k <= 1 && dim <= 128; }
+
+SplitPlan plan_split(int64_t n, int64_t c, int dim, int top_k) {
   SplitPlan p;
   p.stream = n <= 64;
   if (p.stream) {
@@ -65,7 +70,8 @@ SplitPlan plan_split(int64_t n, int64_t c, int dim) {
   if (want < min_split) want = min_split;
   if (want < 1) want = 1;
   if (want > max_split) want = max_split;
-  p.chunk = tm_cdiv(tm_cdiv(c, want), rows) * rows;
+  const int64_t unit = top1_tile(dim, top_k) ? 4 * rows : rows;  // 2048 is a multiple of either
+  p.chunk = tm_cdiv(tm_cdiv(c, want), unit) * unit;
   p.nsplit = tm_cdiv(c, p.chunk);
   return p;
 }
@@ -175,6 +181,34 @@ __device__ __forceinline__ void tm_dma16(const void *gaddr, const void *lds_base
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
       : "v"(gaddr), "s"(base)
+      : "memory");
+}
+
+// The same direct-to-LDS load through a buffer resource (4 SGPRs: base,
+// stride 0, size in bytes, raw 32-bit format): lanes whose byte offset is at
+// or past the size are range-checked by the hardware and read nothing, so a
+// stage that runs past the end of the table needs no clamping.
+typedef uint32_t tm_rsrc_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ tm_rsrc_t tm_make_rsrc(const void *base, uint64_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  tm_rsrc_t r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);  // stride 0
+  r.z = __builtin_amdgcn_readfirstlane((uint32_t)(bytes < 0xffffffffull ? bytes : 0xffffffffull));
+  r.w = 0x00020000u;  // raw buffer, 32-bit data format
+  return r;
+}
+
+__device__ __forceinline__ void tm_dma16_buf(tm_rsrc_t rsrc, uint32_t voff, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(rsrc), "s"(lds_base)
       : "memory");
 }
 
@@ -314,6 +348,286 @@ __global__ __launch_bounds__(kThreads, 2) void search_dma_kernel(
 #pragma unroll
       for (int j = 0; j < K; ++j) dst[j] = best[sl].l[j];
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Top-1 tile kernel (the prefill shape): the stage layout of search_dma_kernel
+// (256 queries x one centroid range per workgroup, 16 KiB stages of swizzled
+// centroid rows in a 4-slot LDS ring), with the work software-pipelined
+// inside each wave: while the matrix cores multiply block b (32 centroids x
+// 2 query slabs), the same wave runs block b-1's epilogue and reads block
+// b+1's operands, so neither sits between two blocks' MFMAs.  Blocks
+// alternate between two accumulator sets; sched_group_barrier pins the
+// interleave (per k-step: 2 MFMAs, a share of the epilogue, one LDS read).
+//
+// Epilogue: the accumulator of a block starts from -||c||^2/2 (L2) or 0
+// (dot), -inf past the end of the range, and so ends at -d'/2 or -d': the
+// nearest centroid holds the LARGEST value.  Per block only the block
+// maximum is computed (a max3 tree); where it beats the lane's running
+// maximum, the block's 16 values and its first centroid are kept (selects,
+// no branch).  At the end the first kept position holding the maximum names
+// the centroid.  Strict comparisons keep the earliest block, and within a
+// lane position order is centroid order, so ties go to the lower index.
+//
+// Ring: stages are loaded by buffer loads straight into LDS, two stages
+// ahead.  The barrier before the last block of stage t waits for stage t+1
+// and refills the slot of stage t-1 (read by no wave any more) with stage
+// t+3.  The stage count is padded to whole rounds of the ring so the loop
+// body has no branch; padded stages meet -inf start values.
+// ---------------------------------------------------------------------------
+// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void tm_static_for(F &&f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    tm_static_for<N, I + 1>(f);
+  }
+}
+
+struct Top1Lane {
+  float r;      // running maximum
+  int cb;       // first centroid of the block it came from (-1: none)
+  float s[16];  // that block's values
+};
+
+__device__ __forceinline__ void top1_init(Top1Lane &t) {
+  t.r = -__builtin_huge_valf();
+  t.cb = -1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) t.s[i] = t.r;
+}
+
+// ~10 (max tree) + 1 + 18 (selects) VALU ops, no branch.
+__device__ __forceinline__ void top1_update(Top1Lane &t, const tm_f32x16 &acc, int cbase) {
+  const float m0 = fmaxf(fmaxf(acc[0], acc[1]), acc[2]);
+  const float m1 = fmaxf(fmaxf(acc[3], acc[4]), acc[5]);
+  const float m2 = fmaxf(fmaxf(acc[6], acc[7]), acc[8]);
+  const float m3 = fmaxf(fmaxf(acc[9], acc[10]), acc[11]);
+  const float m4 = fmaxf(fmaxf(acc[12], acc[13]), acc[14]);
+  const float m = fmaxf(fmaxf(fmaxf(m0, m1), m2), fmaxf(fmaxf(m3, m4), acc[15]));
+  const bool gt = m > t.r;
+  t.r = gt ? m : t.r;
+  t.cb = gt ? cbase : t.cb;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) t.s[i] = gt ? acc[i] : t.s[i];
+}
+
+// The first kept position holding the maximum names the centroid.
+template <int METRIC>
+__device__ __forceinline__ void top1_to_best(const Top1Lane &t, int lane, Best<1> &b) {
+  int pos = 15;
+#pragma unroll
+  for (int i = 14; i >= 0; --i)
+    if (t.s[i] == t.r) pos = i;
+  if (t.cb >= 0) {
+    b.d = (METRIC == TM_METRIC_L2) ? -2.f * t.r : -t.r;
+    b.i = t.cb + 8 * (pos >> 2) + 4 * (lane >> 5) + (pos & 3);
+  }
+}
+
+template <int DT, int DIM, int METRIC>
+__global__ __launch_bounds__(kThreads, 2) void search_top1_kernel(
+    const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
+    const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
+    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws) {
+  using T = typename Elem<DT>::T;
+  constexpr int KS = DIM / 16;
+  constexpr int CH = DIM / 8;
+  constexpr int ROWS = kDmaStageBytes / (DIM * 2);
+  constexpr int NSUB = ROWS / 32;
+  constexpr int SLOTS = ROWS * CH;
+  constexpr int NDMA = SLOTS / kThreads;
+  static_assert(SLOTS % kThreads == 0 && NSUB >= 1, "stage shape");
+  __shared__ uint4 st0[SLOTS], st1[SLOTS], st2[SLOTS], st3[SLOTS];
+  __shared__ float init_s[kDmaMaxChunk];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t split = blockIdx.y;
+  const int64_t row_base = (int64_t)blockIdx.x * kTileRows + wave * (kQS * 32);
+  const int64_t c_begin = split * chunk;
+  const int64_t c_end = (c_begin + chunk < n_cent) ? c_begin + chunk : n_cent;
+  const int64_t c_last = c_end - 1;
+  const int nstage = (int)((c_end - c_begin + ROWS - 1) / ROWS);
+  const int nstage4 = (nstage + kDmaBufs - 1) / kDmaBufs * kDmaBufs;  // <= kDmaMaxChunk / ROWS
+  const T *q_rows[kQS];
+#pragma unroll
+  for (int sl = 0; sl < kQS; ++sl) {
+    const int64_t r = row_base + sl * 32 + (lane & 31);
+    q_rows[sl] = (r < n) ? q + r * ld_q : nullptr;
+  }
+
+  // Ring fill of stage `s`: a buffer over the table from the stage's first row
+  // on, so rows past the end of the table read nothing (the range's rows past
+  // c_end are read but carry a -inf start value).  Thread t's chunk u sits at
+  // a fixed byte offset from the stage's first row: chunk 0's plus
+  // u * (256 / CH) rows (the swizzle repeats every CH rows).  The host keeps
+  // ROWS * ld_c * sizeof(T) below 2^31.
+  static_assert(CH <= 16, "one swizzle period per 256 chunks");
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint64_t ldb = (uint64_t)ld_c * sizeof(T);
+  constexpr int kRowsPerU = kThreads / CH;
+  uint32_t voff[NDMA];
+#pragma unroll
+  for (int u = 0; u < NDMA; ++u) {
+    const int r = tid / CH + u * kRowsPerU;
+    const int j = (tid % CH) ^ (r % CH);
+    voff[u] = (uint32_t)r * (uint32_t)ldb + (uint32_t)j * 16u;
+  }
+  auto issue = [&](uint4 *buf, int s) {
+    const uint32_t lds0 = (uint32_t)(uintptr_t)buf + (uint32_t)wave_u * 1024u;
+    const int64_t row0 = __builtin_elementwise_min(c_begin + (int64_t)s * ROWS, n_cent);
+    const tm_rsrc_t rs = tm_make_rsrc(cents + row0 * ld_c, (uint64_t)(n_cent - row0) * ldb);
+#pragma unroll
+    for (int u = 0; u < NDMA; ++u) tm_dma16_buf(rs, voff[u], lds0 + (uint32_t)(u * kThreads * 16));
+  };
+  constexpr int INIT_PER_THREAD = kDmaMaxChunk / kThreads;
+  float init_v[INIT_PER_THREAD];
+#pragma unroll
+  for (int u = 0; u < INIT_PER_THREAD; ++u) {
+    const int64_t c = c_begin + tid + u * kThreads;
+    const float v = (METRIC == TM_METRIC_L2) ? -0.5f * c_sqnorm[c < c_last ? c : c_last] : 0.f;
+    init_v[u] = (c < c_end) ? v : -__builtin_huge_valf();
+  }
+  issue(st0, 0);
+  issue(st1, 1);
+  uint4 qf[kQS][KS];
+#pragma unroll
+  for (int sl = 0; sl < kQS; ++sl)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[sl][ks] = q_rows[sl] ? *reinterpret_cast<const uint4 *>(q_rows[sl] + ks * 16 + 8 * (lane >> 5))
+                              : make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int u = 0; u < INIT_PER_THREAD; ++u) init_s[tid + u * kThreads] = init_v[u];
+
+  static_assert(NSUB % 2 == 0, "blocks alternate between two accumulator sets");
+  Top1Lane top[kQS];
+  // Accumulators of even and odd blocks: block b fills set b&1 while the
+  // epilogue of block b-1 reads set (b-1)&1 (no copy between them).
+  tm_f32x16 accs[2][kQS];
+  int cbs[2] = {0, 0};  // first centroid of the block in each set
+#pragma unroll
+  for (int sl = 0; sl < kQS; ++sl) {
+    top1_init(top[sl]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) accs[1][sl][i] = -__builtin_huge_valf();
+  }
+
+  // Lane byte offsets of A operand k within a 32-row block (the same for
+  // every block, slot and stage).  Made opaque to the compiler so that the
+  // slot and block offsets stay additive immediates of the LDS reads.
+  uint32_t a_off[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    const int row = lane & 31;
+    const int j = 2 * k + (lane >> 5);
+    a_off[k] = (uint32_t)(row * CH + (j ^ (row % CH))) * 16u;
+    asm volatile("" : "+v"(a_off[k]));
+  }
+  uint32_t i_off = (uint32_t)(16 * (lane >> 5));
+  asm volatile("" : "+v"(i_off));
+  // A operands are read kAhead k-steps before their MFMAs (a sliding window
+  // that runs into the next block), start values near the end of the block
+  // before; only kAhead + 1 operand registers are live at a time.
+  constexpr int kAhead = KS >= 8 ? 3 : 2;
+  static_assert(KS >= 4 && kAhead < KS, "window shorter than a block");
+  uint4 fa[KS];
+  float fi[16];
+  auto read_a = [&](const uint4 *buf, int sub, int k) {
+    fa[k] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const char *>(buf) + sub * 32 * CH * 16 + a_off[k]);
+  };
+  auto read_start = [&](int s, int sub) {
+    const int sc = s < nstage4 ? s : nstage4 - 1;  // the read past the last stage: any in-range values
+    const char *ib = reinterpret_cast<const char *>(init_s) + (sc * ROWS + sub * 32) * 4 + i_off;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 p4 = *reinterpret_cast<const float4 *>(ib + 32 * g);
+      fi[4 * g + 0] = p4.x; fi[4 * g + 1] = p4.y; fi[4 * g + 2] = p4.z; fi[4 * g + 3] = p4.w;
+    }
+  };
+
+  // Two stages in flight: the barrier before the last block of stage t waits
+  // for stage t+1 (stage t+2 may still be loading) and refills the slot of
+  // stage t-1, which every wave has finished reading, with stage t+3.
+  tm_wait_vm_lgkm0<0>();  // stages 0, 1 and the query operands landed; init_s written
+  __builtin_amdgcn_s_barrier();
+  issue(st2, 2);
+  read_start(0, 0);
+#pragma unroll
+  for (int k = 0; k < kAhead; ++k) read_a(st0, 0, k);
+
+  // stage s: slot `cur`; stage s+1: `nxt`; `old` (stage s-1's) is refilled with stage s+3
+  auto step = [&](const uint4 *cur, const uint4 *nxt, uint4 *old, int s) {
+    const int64_t s0 = c_begin + (int64_t)s * ROWS;
+    tm_static_for<NSUB>([&](auto sub_c) {
+      constexpr int sub = decltype(sub_c)::value;
+      constexpr int PA = sub & 1;  // this block's accumulator set
+      if (sub == NSUB - 1) {
+        tm_wait_vm_lgkm0<NDMA>();      // stage s+1 landed (stage s+2 may be in flight)
+        __builtin_amdgcn_s_barrier();  // ... in every wave; stage s-1's slot is no longer read
+        issue(old, s + 3);
+      }
+      tm_f32x16 (&acc)[kQS] = accs[PA];
+      tm_f32x16 start;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) start[i] = fi[i];
+      tm_static_for<KS>([&](auto k_c) {
+        constexpr int k = decltype(k_c)::value;
+#pragma unroll
+        for (int sl = 0; sl < kQS; ++sl) acc[sl] = tm_mfma32x32x16<DT>(fa[k], qf[sl][k], k == 0 ? start : acc[sl]);
+        constexpr int kk = k + kAhead;  // operand read this step
+        if constexpr (kk < KS)
+          read_a(cur, sub, kk);
+        else if constexpr (sub + 1 < NSUB)
+          read_a(cur, sub + 1, kk - KS);
+        else
+          read_a(nxt, 0, kk - KS);
+        if constexpr (k == KS - 3) {
+          if constexpr (sub + 1 < NSUB)
+            read_start(s, sub + 1);
+          else
+            read_start(s + 1, 0);
+        }
+      });
+#pragma unroll
+      for (int sl = 0; sl < kQS; ++sl) top1_update(top[sl], accs[PA ^ 1][sl], cbs[PA ^ 1]);
+      cbs[PA] = (int)(s0 + sub * 32);
+      // per k-step: its MFMAs, a share of the previous block's epilogue, a read
+      constexpr int kValu = (30 * kQS + KS - 1) / KS;
+      tm_static_for<KS>([&](auto k_c) {
+        constexpr int k = decltype(k_c)::value;
+        __builtin_amdgcn_sched_group_barrier(0x008, kQS, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x100, k == KS - 3 ? 5 : 1, 0);  // DS read
+      });
+      __builtin_amdgcn_sched_barrier(0);  // blocks are scheduled one at a time
+    });
+  };
+  // Whole rounds of the ring: stages past the range only meet -inf start
+  // values (and rows past the table read nothing), so padding nstage to a
+  // multiple of the ring keeps the loop body free of branches.
+  for (int s = 0; s < nstage4; s += kDmaBufs) {
+    step(st0, st1, st3, s);
+    step(st1, st2, st0, s + 1);
+    step(st2, st3, st1, s + 2);
+    step(st3, st0, st2, s + 3);
+  }
+#pragma unroll
+  for (int sl = 0; sl < kQS; ++sl) top1_update(top[sl], accs[1][sl], cbs[1]);  // the last block is odd
+  tm_wait_vm_lgkm0<0>();  // no load may still target this workgroup's LDS when it exits
+
+#pragma unroll
+  for (int sl = 0; sl < kQS; ++sl) {
+    Best<1> best;
+    best.init();
+    top1_to_best<METRIC>(top[sl], lane, best);
+    best.finalize();
+    best.merge_xor(32);  // the two half-waves saw disjoint centroids of the same query
+    const int64_t r = row_base + sl * 32 + (lane & 31);
+    if (lane < 32 && r < n) ws[split * n + r] = best.l[0];
   }
 }
 
@@ -488,7 +802,7 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
                   const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm,
                   float *out_dist, int64_t *out_idx, uint64_t *ws, hipStream_t stream) {
   using T = typename Elem<DT>::T;
-  const SplitPlan p = plan_split(n, n_cent, DIM);
+  const SplitPlan p = plan_split(n, n_cent, DIM, top_k);
   const T *Q = static_cast<const T *>(q);
   const T *C = static_cast<const T *>(cents);
   dim3 block(kThreads);
@@ -499,6 +813,10 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
     else
       hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 2, METRIC>), dim3((unsigned)p.nsplit), block, 0, stream,
                          Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
+  } else if (K == 1 && DIM <= 128 && ld_c * dma_rows(DIM) * (int64_t)sizeof(T) < ((int64_t)1 << 31)) {
+    // (d = 256 would not fit two waves per SIMD; the stage byte offsets must fit 31 bits)
+    hipLaunchKernelGGL((search_top1_kernel<DT, DIM < 256 ? DIM : 128, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
+                       block, 0, stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
   } else {
     hipLaunchKernelGGL((search_dma_kernel<DT, DIM, K, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
                        block, 0, stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
@@ -552,7 +870,7 @@ extern "C" int tm_centroid_sqnorms(int32_t dtype, const void *cents, int64_t n_c
 extern "C" size_t tm_search_global_workspace_size(int64_t n_tokens, int64_t n_cent, int32_t dim,
                                                   int32_t top_k) {
   if (n_tokens <= 0 || n_cent <= 0 || top_k <= 0 || (dim != 64 && dim != 128 && dim != 256)) return 0;
-  const SplitPlan p = plan_split(n_tokens, n_cent, dim);
+  const SplitPlan p = plan_split(n_tokens, n_cent, dim, top_k);
   return (size_t)p.nsplit * (size_t)n_tokens * (size_t)list_len(top_k) * sizeof(uint64_t);
 }
 

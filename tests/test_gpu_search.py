@@ -373,6 +373,55 @@ def test_search_global_vs_oracle(hip_device, n, c, dim, top_k, metric, dtype):
     np.testing.assert_allclose(np64(tbl.c_sqnorm), (np64(cents) ** 2).sum(1), rtol=2e-6)
 
 
+@pytest.mark.parametrize("n,c,dim,top_k,metric", [
+    (777, 3000, 128, 1, "l2"),    # tile kernel, several splits and a partial last stage
+    (300, 2100, 64, 1, "l2"),
+    (513, 1500, 128, 1, "dot"),
+    (300, 1000, 128, 4, "l2"),    # top-k tile kernel
+    (40, 3000, 128, 1, "l2"),     # decode-sized stream kernel
+    (40, 3000, 128, 4, "l2"),
+])
+def test_search_global_exact_ties(hip_device, n, c, dim, top_k, metric):
+    """Centroid rows repeat (row i equals row i % 97), so every distance is tied
+    with at least one other centroid bit for bit: each kernel path must return
+    the lowest index among the tied centroids, as the reference's first-minimum
+    rule does (search.py argmin / topk order)."""
+    g = _gen(53 + n + c + top_k)
+    base = torch.randn(97, dim, generator=g).to(torch.bfloat16)
+    cents = base[torch.arange(c) % 97]
+    q = (base[torch.randint(0, 97, (n,), generator=g)].float() + 0.3 * torch.randn(n, dim, generator=g)).to(torch.bfloat16)
+    dev = hip_device
+    from table_moe.cache_engine.global_table import GlobalTable
+
+    H = 16
+    tbl = GlobalTable(cents.to(dev), torch.zeros(c, H, dtype=torch.bfloat16, device=dev),
+                      (torch.zeros(H, dim, dtype=torch.bfloat16, device=dev),
+                       torch.zeros(dim, dtype=torch.bfloat16, device=dev)), metric=metric)
+    dist, idx = tbl.search(q.to(dev), top_k)
+    torch.cuda.synchronize()
+    got = np64(idx)
+    # distances of the 97 distinct rows; the true answer lists, per distinct
+    # row in rank order, its first occurrences (index r, then r + 97, ...)
+    _, want_base, exact_base = O.global_search(np64(q), np64(base), 97, metric)
+    assert got.min() >= 0 and got.max() < c
+    # every returned index must be one of the lowest-indexed copies of a
+    # best-ranked distinct row: for top-1, exactly the first copy of the best row
+    for r in range(n):
+        row_rank = want_base[r]
+        if top_k == 1:
+            b0 = int(row_rank[0])
+            if exact_base[r, b0] == exact_base[r, int(row_rank[1])]:
+                continue  # two distinct rows at the same distance: not this test's concern
+            assert got[r, 0] == b0, f"row {r}: got {got[r, 0]} want {b0}"
+        else:
+            # the best distinct row has c // 97 (+1) copies; the top_k list must be
+            # its lowest-indexed copies in increasing index order
+            b0 = int(row_rank[0])
+            copies = np.arange(b0, c, 97)[:top_k]
+            if len(copies) == top_k:
+                np.testing.assert_array_equal(got[r], copies, err_msg=f"row {r}")
+
+
 def test_search_global_precomputed_qnorm_and_repeat(hip_device):
     """The q_sqnorm argument changes nothing; a second call reuses the workspace."""
     from table_moe.cache_engine.global_table import GlobalTable
