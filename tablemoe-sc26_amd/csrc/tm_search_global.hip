@@ -727,7 +727,88 @@ __global__ __launch_bounds__(kThreads) void search_stream_kernel(
   }
 }
 
-// One wave per query: reduce nsplit partial lists to the final top-k.
+// The K smallest of two ascending K-lists, ascending: min(a[i], b[K-1-i]) is
+// bitonic and holds exactly the K smallest; a half-cleaner cascade sorts it.
+template <int K>
+__device__ __forceinline__ void merge_min(uint64_t (&a)[K], const uint64_t (&b)[K]) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) a[i] = a[i] < b[K - 1 - i] ? a[i] : b[K - 1 - i];
+#pragma unroll
+  for (int d = K / 2; d > 0; d >>= 1)
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      if ((i & d) == 0) {
+        const uint64_t lo = a[i] < a[i + d] ? a[i] : a[i + d];
+        const uint64_t hi = a[i] < a[i + d] ? a[i + d] : a[i];
+        a[i] = lo;
+        a[i + d] = hi;
+      }
+}
+
+// Output of one query: key ~0 (no candidate) -> index -1 and the worst distance.
+template <int METRIC>
+__device__ __forceinline__ void write_hit(uint64_t key, float qn, float *dist, int64_t *idx) {
+  if (key == ~0ull) {
+    *idx = -1;
+    *dist = (METRIC == TM_METRIC_L2) ? __builtin_huge_valf() : -__builtin_huge_valf();
+  } else {
+    const float dp = tm_from_orderable((uint32_t)(key >> 32));
+    *idx = (int64_t)(uint32_t)key;
+    *dist = (METRIC == TM_METRIC_L2) ? fmaxf(qn + dp, 0.f) : -dp;
+  }
+}
+
+// 64-bit value of the lane `x` lanes away within a quad (x = 1 or 2), by DPP.
+template <int X>
+__device__ __forceinline__ uint64_t quad_xor(uint64_t v) {
+  constexpr int ctrl = X == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, ctrl, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), ctrl, 0xF, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+template <int X>
+__device__ __forceinline__ float quad_xor_f(float v) {
+  constexpr int ctrl = X == 1 ? 0xB1 : 0x4E;
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+
+// Top-1 merge: a quad of lanes per query; lane j takes splits j, j+4, ... (8
+// loads in flight per lane), then two DPP steps give every lane of the quad
+// the smallest key.  Every lane of a partial last quad reads a valid query.
+template <int DT, int METRIC>
+__global__ __launch_bounds__(kThreads) void merge_top1_kernel(
+    const uint64_t *__restrict__ ws, int64_t n, int64_t nsplit, const typename Elem<DT>::T *__restrict__ q,
+    int64_t ld_q, int dim, const float *__restrict__ q_sqnorm, float *__restrict__ out_dist,
+    int64_t *__restrict__ out_idx) {
+  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t r = t >> 2;
+  const int j = threadIdx.x & 3;
+  const int64_t rr = r < n ? r : n - 1;
+  float qn = 0.f;
+  if (METRIC == TM_METRIC_L2 && q_sqnorm != nullptr) qn = q_sqnorm[rr];
+  uint64_t best = ~0ull;
+#pragma unroll 8
+  for (int64_t s = j; s < nsplit; s += 4) {
+    const uint64_t v = ws[s * n + rr];
+    best = v < best ? v : best;
+  }
+  uint64_t o = quad_xor<1>(best);
+  best = o < best ? o : best;
+  o = quad_xor<2>(best);
+  best = o < best ? o : best;
+  if (METRIC == TM_METRIC_L2 && q_sqnorm == nullptr) {
+    for (int i = j; i < dim; i += 4) {
+      const float v = Elem<DT>::to_f(q[rr * ld_q + i]);
+      qn = fmaf(v, v, qn);
+    }
+    qn += quad_xor_f<1>(qn);
+    qn += quad_xor_f<2>(qn);
+  }
+  if (r < n && j == 0) write_hit<METRIC>(best, qn, out_dist + r, out_idx + r);
+}
+
+// Top-k merge (k = 4 or 8): one wave per query; lane l merges the sorted lists
+// of splits l, l+64, ...; then six xor-shuffle steps merge the lanes' lists.
 template <int DT, int K, int METRIC>
 __global__ __launch_bounds__(kThreads) void merge_kernel(
     const uint64_t *__restrict__ ws, int64_t n, int64_t nsplit, const typename Elem<DT>::T *__restrict__ q,
@@ -736,52 +817,37 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
   if (r >= n) return;  // whole wave exits together
+  float qn = 0.f;
+  if (METRIC == TM_METRIC_L2 && q_sqnorm != nullptr) qn = q_sqnorm[r];
   uint64_t lst[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) lst[j] = ~0ull;
   for (int64_t s = lane; s < nsplit; s += 64) {
     const uint64_t *src = ws + (s * n + r) * K;
+    uint64_t b[K];
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-      const uint64_t v = src[j];
-      if (v < lst[K - 1]) list_insert<K>(lst, v);
-    }
+    for (int j = 0; j < K; ++j) b[j] = src[j];
+    merge_min<K>(lst, b);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
+    if (o >= nsplit) continue;  // (uniform) lanes o.. hold no list
     uint64_t other[K];
 #pragma unroll
     for (int j = 0; j < K; ++j) other[j] = __shfl_xor(lst[j], o, 64);
-#pragma unroll
-    for (int j = 0; j < K; ++j)
-      if (other[j] < lst[K - 1]) list_insert<K>(lst, other[j]);
+    merge_min<K>(lst, other);
   }
-  float qn = 0.f;
-  if (METRIC == TM_METRIC_L2) {
-    if (q_sqnorm != nullptr) {
-      qn = q_sqnorm[r];
-    } else {
-      for (int j = lane; j < dim; j += 64) {
-        const float v = Elem<DT>::to_f(q[r * ld_q + j]);
-        qn = fmaf(v, v, qn);
-      }
-      qn = tm_wave_sum(qn);
+  if (METRIC == TM_METRIC_L2 && q_sqnorm == nullptr) {
+    for (int j = lane; j < dim; j += 64) {
+      const float v = Elem<DT>::to_f(q[r * ld_q + j]);
+      qn = fmaf(v, v, qn);
     }
+    qn = tm_wave_sum(qn);
   }
   if (lane == 0) {
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-      if (j >= top_k) break;
-      const uint64_t key = lst[j];
-      if (key == ~0ull) {
-        out_idx[r * top_k + j] = -1;
-        out_dist[r * top_k + j] = (METRIC == TM_METRIC_L2) ? __builtin_huge_valf() : -__builtin_huge_valf();
-      } else {
-        const float dp = tm_from_orderable((uint32_t)(key >> 32));
-        out_idx[r * top_k + j] = (int64_t)(uint32_t)key;
-        out_dist[r * top_k + j] = (METRIC == TM_METRIC_L2) ? fmaxf(qn + dp, 0.f) : -dp;
-      }
-    }
+    for (int j = 0; j < K; ++j)
+      if (j < top_k) write_hit<METRIC>(lst[j], qn, out_dist + r * top_k + j, out_idx + r * top_k + j);
   }
 }
 
@@ -822,8 +888,12 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
                        block, 0, stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
   }
   TM_LAUNCH_CHECK("tm_search_global");
-  hipLaunchKernelGGL((merge_kernel<DT, K, METRIC>), dim3((unsigned)tm_cdiv(n, kThreads / 64)),
-                     block, 0, stream, ws, n, p.nsplit, Q, ld_q, DIM, q_sqnorm, top_k, out_dist, out_idx);
+  if constexpr (K == 1)
+    hipLaunchKernelGGL((merge_top1_kernel<DT, METRIC>), dim3((unsigned)tm_cdiv(n, kThreads / 4)),
+                       block, 0, stream, ws, n, p.nsplit, Q, ld_q, DIM, q_sqnorm, out_dist, out_idx);
+  else
+    hipLaunchKernelGGL((merge_kernel<DT, K, METRIC>), dim3((unsigned)tm_cdiv(n, kThreads / 64)),
+                       block, 0, stream, ws, n, p.nsplit, Q, ld_q, DIM, q_sqnorm, top_k, out_dist, out_idx);
   TM_LAUNCH_CHECK("tm_search_global(merge)");
   return TM_OK;
 }
