@@ -11,8 +11,8 @@ selection -> gather + combine + residual.  Inputs are resident in HBM before
 timing; steps rotate over replicas of the workload totalling > 2x the 256 MB
 Infinity Cache so reads come from HBM.
 
-Prints ONE JSON line: tokens/s per MoE layer (value, from HIP-graph replays of
-one tm_table_forward call per layer), per-stage device times, the average
+Prints ONE JSON line: tokens/s per MoE layer (value, from replays of one HIP
+graph holding four consecutive layers, one tm_table_forward call each), per-stage device times, the average
 device time of each stage's C-ABI call (graphs of 32 back-to-back calls timed
 with HIP events on the stream the kernels run on), the roofline of the
 dominant call (HBM bytes from the committed rocprofv3 PMC summary when
@@ -100,34 +100,42 @@ def run_layer_bench(cfg_id, steps, warmup, n=None):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
     device_us = 1000.0 * ev_all[0].elapsed_time(ev_all[1]) / steps
-    # 1b) the same K layers replayed from HIP graphs (one captured layer per
-    #     replica): identical kernels and work, without host launch cost
-    graphs = []
+    # 1b) the same layers replayed from one HIP graph holding N_REPLICAS
+    #     consecutive layers (one per replica, as a model runs its layers):
+    #     identical kernels and work, without host launch cost
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for i in range(N_REPLICAS):
             step(i)
     torch.cuda.current_stream().wait_stream(side)
-    for i in range(N_REPLICAS):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(N_REPLICAS):
             step(i)
-        graphs.append(g)
+    tail = None  # the last steps % N_REPLICAS layers, so exactly `steps` layers are timed
+    if steps % N_REPLICAS:
+        tail = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(tail):
+            for i in range(steps % N_REPLICAS):
+                step(i)
     torch.cuda.synchronize()
-    for i in range(warmup):
-        graphs[i % N_REPLICAS].replay()
+    for _ in range(max(1, warmup // N_REPLICAS)):
+        graph.replay()
     torch.cuda.synchronize()
+    g_steps = steps
     g_ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     t_g = time.perf_counter()
     g_ev[0].record()
-    for i in range(steps):
-        graphs[i % N_REPLICAS].replay()
+    for _ in range(steps // N_REPLICAS):
+        graph.replay()
+    if tail is not None:
+        tail.replay()
     g_ev[1].record()
     torch.cuda.synchronize()
     graph_elapsed = time.perf_counter() - t_g
-    graph_device_us = 1000.0 * g_ev[0].elapsed_time(g_ev[1]) / steps
-    del graphs
+    graph_device_us = 1000.0 * g_ev[0].elapsed_time(g_ev[1]) / g_steps
+    del graph, tail
     # 2) instrumented pass over the same steps: HIP events between the stages
     #    (an event record adds a few microseconds of its own between stages)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
@@ -148,7 +156,7 @@ def run_layer_bench(cfg_id, steps, warmup, n=None):
     n_keep = int(keep.sum().item())
     kernel_us = stage_kernel_times(reps, tables, outs, topk, nn, kr)
     return dict(cfg=cfg, wl=wl, elapsed=elapsed, eager_ms_per_step=1000.0 * elapsed / steps,
-                ms_per_step=1000.0 * graph_elapsed / steps, graph_device_us=graph_device_us, stage_us=stage_us,
+                ms_per_step=1000.0 * graph_elapsed / g_steps, graph_device_us=graph_device_us, stage_us=stage_us,
                 kernel_us=kernel_us, device_us=device_us, n_keep=n_keep,
                 bytes=_stage_bytes(cfg, N, n_keep, nn, topk))
 
@@ -359,8 +367,9 @@ def main() -> int:
         },
         "stages_us": {k: round(v, 2) for k, v in st.items()},
         "calls_us": {k: round(v, 2) for k, v in ku.items()},
-        "timing": "ms_per_step: layers replayed from HIP graphs (one captured tm_table_forward per "
-                  "replica); eager_ms_per_step: one tm_table_forward call per layer from Python",
+        "timing": "ms_per_step: layers replayed from one HIP graph of four consecutive layers (one "
+                  "tm_table_forward per replica); eager_ms_per_step: one tm_table_forward call per layer "
+                  "from Python",
         "eager_ms_per_step": pre["eager_ms_per_step"],
         "eager_tokens_per_s": N / (pre["eager_ms_per_step"] * 1e-3),
         "layer_device_us": pre["graph_device_us"],

@@ -157,6 +157,42 @@ __device__ __forceinline__ float tm_from_orderable(uint32_t k) {
 // ---------------------------------------------------------------------------
 // wave64 reductions
 // ---------------------------------------------------------------------------
+// DPP (data-parallel primitives, gfx9): row_shr:n reads lane i-n of the same
+// 16-lane row, row_bcast:15 / row_bcast:31 read lane 15 / 31 of the previous
+// row(s).  Lanes whose source is outside the row keep `old`.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t tm_dpp(uint32_t old, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, ROW_MASK, 0xF, false);
+}
+// Inclusive prefix sum over the wave (11 VALU ops, no LDS).
+__device__ __forceinline__ uint32_t tm_wave_incl_scan(uint32_t v) {
+  v += tm_dpp<0x111>(0u, v);        // row_shr:1
+  v += tm_dpp<0x112>(0u, v);        // row_shr:2
+  v += tm_dpp<0x114>(0u, v);        // row_shr:4
+  v += tm_dpp<0x118>(0u, v);        // row_shr:8
+  v += tm_dpp<0x142, 0xA>(0u, v);   // row_bcast:15 into rows 1, 3
+  v += tm_dpp<0x143, 0xC>(0u, v);   // row_bcast:31 into rows 2, 3
+  return v;
+}
+// Minimum / maximum over the wave, returned in every lane.
+__device__ __forceinline__ uint32_t tm_wave_min_u32(uint32_t v) {
+  v = min(v, tm_dpp<0x111>(v, v));
+  v = min(v, tm_dpp<0x112>(v, v));
+  v = min(v, tm_dpp<0x114>(v, v));
+  v = min(v, tm_dpp<0x118>(v, v));
+  v = min(v, tm_dpp<0x142, 0xA>(v, v));
+  v = min(v, tm_dpp<0x143, 0xC>(v, v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ uint32_t tm_wave_max_u32(uint32_t v) {
+  v = max(v, tm_dpp<0x111>(v, v));
+  v = max(v, tm_dpp<0x112>(v, v));
+  v = max(v, tm_dpp<0x114>(v, v));
+  v = max(v, tm_dpp<0x118>(v, v));
+  v = max(v, tm_dpp<0x142, 0xA>(v, v));
+  v = max(v, tm_dpp<0x143, 0xC>(v, v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
 __device__ __forceinline__ float tm_wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

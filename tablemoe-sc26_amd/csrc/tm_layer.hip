@@ -55,12 +55,13 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
   hipStream_t s = tm_hip_stream(stream);
   int st;
   // The router's results are only consumed by the combine: without stage
-  // events it rides in the keep-selection launch (whose single selecting
-  // workgroup leaves the chip idle), and its own stage interval is empty.
-  const bool route_with_keep = stage_events == nullptr && io->router_top_k <= 8 &&
-                               (io->n_experts == 64 || io->n_experts == 128);
+  // events it rides in the search's split-merge launch (a few latency-bound
+  // workgroups that leave the chip idle) and its own stage interval is empty.
+  const tm_route_args ra{io->router_logits, io->ld_logits, io->n_experts, io->router_top_k, io->weights,
+                         io->expert_ids};
+  const bool route_in_search = stage_events == nullptr && tm_internal_route_fusable(&ra);
   if ((st = record(stage_events, 0, s)) != TM_OK) return st;
-  if (!route_with_keep &&
+  if (!route_in_search &&
       (st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k, 0,
                             io->weights, io->expert_ids, stream)) != TM_OK)
     return st;
@@ -70,28 +71,19 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
                        io->q_sqnorm, w.project ? ws : nullptr, w.project, stream)) != TM_OK)
     return st;
   if ((st = record(stage_events, 2, s)) != TM_OK) return st;
-  if ((st = tm_search_global(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c,
-                             t->c_sqnorm, t->dim, io->n_nearest, t->metric, io->dist, io->idx,
-                             ws + w.project, w.search, stream)) != TM_OK)
-    return st;
+  if (route_in_search)
+    st = tm_internal_search_route(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c,
+                                  t->c_sqnorm, t->dim, io->n_nearest, t->metric, io->dist, io->idx,
+                                  ws + w.project, w.search, &ra, s);
+  else
+    st = tm_search_global(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c, t->c_sqnorm,
+                          t->dim, io->n_nearest, t->metric, io->dist, io->idx, ws + w.project, w.search, stream);
+  if (st != TM_OK) return st;
   if ((st = record(stage_events, 3, s)) != TM_OK) return st;
   const int64_t n_keep = tm_keep_count(n, io->keep_rate);
-  int fused = TM_NOT_FUSED;
-  if (route_with_keep) {
-    TM_REQUIRE(io->router_logits && n_keep >= 0, TM_EINVAL_ARG, "tm_table_forward: router logits missing");
-    fused = tm_internal_keep_route(io->dist, n, io->n_nearest, n_keep, io->keep, io->router_logits, io->ld_logits,
-                                   io->n_experts, io->router_top_k, io->weights, io->expert_ids, s);
-    if (fused != TM_OK && fused != TM_NOT_FUSED) return fused;
-  }
-  if (fused == TM_NOT_FUSED) {
-    if (route_with_keep &&
-        (st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k, 0,
-                              io->weights, io->expert_ids, stream)) != TM_OK)
-      return st;
-    if ((st = tm_keep_select(io->dist, n, io->n_nearest, n_keep, io->keep,
-                             w.keep ? ws + w.project + w.search : nullptr, w.keep, stream)) != TM_OK)
-      return st;
-  }
+  if ((st = tm_keep_select(io->dist, n, io->n_nearest, n_keep, io->keep,
+                           w.keep ? ws + w.project + w.search : nullptr, w.keep, stream)) != TM_OK)
+    return st;
   if ((st = record(stage_events, 4, s)) != TM_OK) return st;
   if ((st = tm_gather_combine(t->dtype, n, t->hidden, io->keep, io->slot_out, io->so_b, io->so_s, io->weights,
                               io->router_top_k, io->router_top_k, t->values, t->n_cent, t->ld_v, io->idx,

@@ -4,6 +4,19 @@
 
 #include "tm_common.h"
 
+// Exchange within 8-lane groups by DPP (VALU, no LDS round trip): quad_perm
+// [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror (lane i <-> 7-i).  After the
+// three steps of a symmetric reduction every lane of the group holds the result.
+template <int CTRL>
+__device__ __forceinline__ float tm_g8f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int tm_g8i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kG8Steps[3] = {0xB1, 0x4E, 0x141};
+
 // Rows of 8*VPL experts (VPL % 4 == 0): lane `sub` (0..7) of the token's
 // group holds the contiguous experts [sub*VPL, sub*VPL + VPL), loaded as
 // VPL/4 unconditional 16-byte loads (the group reads the row as one
@@ -11,7 +24,7 @@
 // fp32 softmax (max, exp, sum, divide), then top_k rounds of an arg-max whose
 // ties go to the lower expert id; the winner is masked out after each round.
 // The group's lane 0 keeps the winners (top_k <= KM) and writes them once.
-// Every lane of the wave must call this (the reductions are 8-lane shuffles).
+// Every lane of the wave must call this (the reductions are 8-lane DPP exchanges).
 template <int VPL, int KM>
 __device__ __forceinline__ void tm_route_token(const float *__restrict__ logits, int64_t n, int64_t ld, int top_k,
                                                int renorm, float *__restrict__ out_w,
@@ -28,16 +41,18 @@ __device__ __forceinline__ void tm_route_token(const float *__restrict__ logits,
   float mx = v[0];
 #pragma unroll
   for (int j = 1; j < VPL; ++j) mx = fmaxf(mx, v[j]);
-#pragma unroll
-  for (int o = 1; o < 8; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  mx = fmaxf(mx, tm_g8f<kG8Steps[0]>(mx));
+  mx = fmaxf(mx, tm_g8f<kG8Steps[1]>(mx));
+  mx = fmaxf(mx, tm_g8f<kG8Steps[2]>(mx));
   float sum = 0.f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     v[j] = expf(v[j] - mx);
     sum += v[j];
   }
-#pragma unroll
-  for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o, 64);
+  sum += tm_g8f<kG8Steps[0]>(sum);
+  sum += tm_g8f<kG8Steps[1]>(sum);
+  sum += tm_g8f<kG8Steps[2]>(sum);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) v[j] = v[j] / sum;
   float kw[KM];
@@ -50,10 +65,15 @@ __device__ __forceinline__ void tm_route_token(const float *__restrict__ logits,
     for (int j = 0; j < VPL; ++j) {
       if (v[j] > bv) { bv = v[j]; bi = sub * VPL + j; }
     }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
+    {
+      float ov = tm_g8f<kG8Steps[0]>(bv);
+      int oi = tm_g8i<kG8Steps[0]>(bi);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      ov = tm_g8f<kG8Steps[1]>(bv);
+      oi = tm_g8i<kG8Steps[1]>(bi);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      ov = tm_g8f<kG8Steps[2]>(bv);
+      oi = tm_g8i<kG8Steps[2]>(bi);
       if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
     }
     if (bi / VPL == sub) {

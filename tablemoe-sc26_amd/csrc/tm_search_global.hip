@@ -26,7 +26,9 @@
 // (orderable(d') << 32 | c) into the workspace; merge_kernel reduces the
 // splits.  Packed keys make the order total: smaller distance first, then
 // lower centroid index.
+#include "tm_internal.h"
 #include "tm_mfma.h"
+#include "tm_route_dev.h"
 
 namespace {
 
@@ -772,14 +774,34 @@ __device__ __forceinline__ float quad_xor_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
 }
 
+// A merge launch may carry the router: workgroups from `first` on route
+// kThreads / 8 tokens each (8 lanes per token).
+struct MergeRoute {
+  tm_route_args a;
+  int64_t first;
+};
+
+template <int RVPL>
+__device__ __forceinline__ bool merge_route_role(const MergeRoute &mr, int64_t n) {
+  if constexpr (RVPL > 0) {
+    if ((int64_t)blockIdx.x >= mr.first) {  // uniform
+      const int64_t tok = ((int64_t)blockIdx.x - mr.first) * (kThreads / 8) + (threadIdx.x >> 3);
+      tm_route_token<RVPL, 8>(mr.a.logits, n, mr.a.ld, mr.a.top_k, 0, mr.a.out_w, mr.a.out_ids, tok, threadIdx.x & 7);
+      return true;
+    }
+  }
+  return false;
+}
+
 // Top-1 merge: a quad of lanes per query; lane j takes splits j, j+4, ... (8
 // loads in flight per lane), then two DPP steps give every lane of the quad
 // the smallest key.  Every lane of a partial last quad reads a valid query.
-template <int DT, int METRIC>
+template <int DT, int METRIC, int RVPL>
 __global__ __launch_bounds__(kThreads) void merge_top1_kernel(
     const uint64_t *__restrict__ ws, int64_t n, int64_t nsplit, const typename Elem<DT>::T *__restrict__ q,
     int64_t ld_q, int dim, const float *__restrict__ q_sqnorm, float *__restrict__ out_dist,
-    int64_t *__restrict__ out_idx) {
+    int64_t *__restrict__ out_idx, MergeRoute mr) {
+  if (merge_route_role<RVPL>(mr, n)) return;
   const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   const int64_t r = t >> 2;
   const int j = threadIdx.x & 3;
@@ -809,11 +831,12 @@ __global__ __launch_bounds__(kThreads) void merge_top1_kernel(
 
 // Top-k merge (k = 4 or 8): one wave per query; lane l merges the sorted lists
 // of splits l, l+64, ...; then six xor-shuffle steps merge the lanes' lists.
-template <int DT, int K, int METRIC>
+template <int DT, int K, int METRIC, int RVPL>
 __global__ __launch_bounds__(kThreads) void merge_kernel(
     const uint64_t *__restrict__ ws, int64_t n, int64_t nsplit, const typename Elem<DT>::T *__restrict__ q,
     int64_t ld_q, int dim, const float *__restrict__ q_sqnorm, int top_k, float *__restrict__ out_dist,
-    int64_t *__restrict__ out_idx) {
+    int64_t *__restrict__ out_idx, MergeRoute mr) {
+  if (merge_route_role<RVPL>(mr, n)) return;
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
   if (r >= n) return;  // whole wave exits together
@@ -863,10 +886,30 @@ __global__ void sqnorm_kernel(const typename Elem<DT>::T *c, int64_t n, int dim,
   out[i] = s;
 }
 
+template <int DT, int K, int METRIC, int RVPL>
+void launch_merge(const SplitPlan &p, int top_k, const typename Elem<DT>::T *Q, int64_t n, int64_t ld_q, int dim,
+                  const float *q_sqnorm, float *out_dist, int64_t *out_idx, const uint64_t *ws,
+                  const tm_route_args *ra, hipStream_t stream) {
+  const int64_t mblocks = K == 1 ? tm_cdiv(n, kThreads / 4) : tm_cdiv(n, kThreads / 64);
+  MergeRoute mr{};
+  int64_t blocks = mblocks;
+  if (RVPL > 0) {
+    mr.a = *ra;
+    mr.first = mblocks;
+    blocks += tm_cdiv(n, kThreads / 8);
+  }
+  if constexpr (K == 1)
+    hipLaunchKernelGGL((merge_top1_kernel<DT, METRIC, RVPL>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, ws,
+                       n, p.nsplit, Q, ld_q, dim, q_sqnorm, out_dist, out_idx, mr);
+  else
+    hipLaunchKernelGGL((merge_kernel<DT, K, METRIC, RVPL>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, ws,
+                       n, p.nsplit, Q, ld_q, dim, q_sqnorm, top_k, out_dist, out_idx, mr);
+}
+
 template <int DT, int DIM, int K, int METRIC>
 int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float *q_sqnorm,
                   const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm,
-                  float *out_dist, int64_t *out_idx, uint64_t *ws, hipStream_t stream) {
+                  float *out_dist, int64_t *out_idx, uint64_t *ws, const tm_route_args *ra, hipStream_t stream) {
   using T = typename Elem<DT>::T;
   const SplitPlan p = plan_split(n, n_cent, DIM, top_k);
   const T *Q = static_cast<const T *>(q);
@@ -888,12 +931,12 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
                        block, 0, stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
   }
   TM_LAUNCH_CHECK("tm_search_global");
-  if constexpr (K == 1)
-    hipLaunchKernelGGL((merge_top1_kernel<DT, METRIC>), dim3((unsigned)tm_cdiv(n, kThreads / 4)),
-                       block, 0, stream, ws, n, p.nsplit, Q, ld_q, DIM, q_sqnorm, out_dist, out_idx);
+  if (ra == nullptr)
+    launch_merge<DT, K, METRIC, 0>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, ra, stream);
+  else if (ra->n_experts == 64)
+    launch_merge<DT, K, METRIC, 8>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, ra, stream);
   else
-    hipLaunchKernelGGL((merge_kernel<DT, K, METRIC>), dim3((unsigned)tm_cdiv(n, kThreads / 64)),
-                       block, 0, stream, ws, n, p.nsplit, Q, ld_q, DIM, q_sqnorm, top_k, out_dist, out_idx);
+    launch_merge<DT, K, METRIC, 16>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, ra, stream);
   TM_LAUNCH_CHECK("tm_search_global(merge)");
   return TM_OK;
 }
@@ -901,22 +944,22 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
 template <int DT, int DIM, int METRIC>
 int dispatch_k(int top_k, const void *q, int64_t n, int64_t ld_q, const float *q_sqnorm,
                const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm,
-               float *out_dist, int64_t *out_idx, uint64_t *ws, hipStream_t stream) {
+               float *out_dist, int64_t *out_idx, uint64_t *ws, const tm_route_args *ra, hipStream_t stream) {
   switch (list_len(top_k)) {
-    case 1: return launch_search<DT, DIM, 1, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
-    case 4: return launch_search<DT, DIM, 4, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
-    default: return launch_search<DT, DIM, 8, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
+    case 1: return launch_search<DT, DIM, 1, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, stream);
+    case 4: return launch_search<DT, DIM, 4, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, stream);
+    default: return launch_search<DT, DIM, 8, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, stream);
   }
 }
 
 template <int DT, int METRIC>
 int dispatch_dim(int dim, int top_k, const void *q, int64_t n, int64_t ld_q, const float *q_sqnorm,
                  const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm,
-                 float *out_dist, int64_t *out_idx, uint64_t *ws, hipStream_t stream) {
+                 float *out_dist, int64_t *out_idx, uint64_t *ws, const tm_route_args *ra, hipStream_t stream) {
   switch (dim) {
-    case 64: return dispatch_k<DT, 64, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
-    case 128: return dispatch_k<DT, 128, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
-    case 256: return dispatch_k<DT, 256, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, stream);
+    case 64: return dispatch_k<DT, 64, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, stream);
+    case 128: return dispatch_k<DT, 128, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, stream);
+    case 256: return dispatch_k<DT, 256, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, stream);
     default: return tm_fail(TM_EINVAL_SHAPE, "tm_search_global: dim %d not in {64, 128, 256}", dim);
   }
 }
@@ -944,11 +987,10 @@ extern "C" size_t tm_search_global_workspace_size(int64_t n_tokens, int64_t n_ce
   return (size_t)p.nsplit * (size_t)n_tokens * (size_t)list_len(top_k) * sizeof(uint64_t);
 }
 
-extern "C" int tm_search_global(int32_t dtype, const void *q, int64_t n_tokens, int64_t ld_q,
-                                const float *q_sqnorm, const void *cents, int64_t n_cent,
-                                int64_t ld_c, const float *c_sqnorm, int32_t dim, int32_t top_k,
-                                int32_t metric, float *out_dist, int64_t *out_idx, void *workspace,
-                                size_t workspace_bytes, tm_stream_t stream) {
+static int search_impl(int32_t dtype, const void *q, int64_t n_tokens, int64_t ld_q, const float *q_sqnorm,
+                       const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm, int32_t dim,
+                       int32_t top_k, int32_t metric, float *out_dist, int64_t *out_idx, void *workspace,
+                       size_t workspace_bytes, const tm_route_args *ra, hipStream_t s) {
   TM_REQUIRE(n_tokens >= 0 && n_tokens < ((int64_t)1 << 31) && n_cent > 0 && n_cent < (int64_t)0x7fffffff, TM_EINVAL_SHAPE,
              "tm_search_global: bad sizes n=%lld C=%lld", (long long)n_tokens, (long long)n_cent);
   TM_REQUIRE(ld_q >= dim && ld_c >= dim, TM_EINVAL_SHAPE, "tm_search_global: bad row strides");
@@ -965,13 +1007,36 @@ extern "C" int tm_search_global(int32_t dtype, const void *q, int64_t n_tokens, 
   TM_REQUIRE(workspace != nullptr && workspace_bytes >= need, TM_EWORKSPACE,
              "tm_search_global: workspace %zu bytes < %zu", workspace_bytes, need);
   uint64_t *ws = static_cast<uint64_t *>(workspace);
-  hipStream_t s = tm_hip_stream(stream);
   if (dtype == TM_DT_BF16) {
     if (metric == TM_METRIC_L2)
-      return dispatch_dim<TM_DT_BF16, TM_METRIC_L2>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, s);
-    return dispatch_dim<TM_DT_BF16, TM_METRIC_DOT>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, s);
+      return dispatch_dim<TM_DT_BF16, TM_METRIC_L2>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, s);
+    return dispatch_dim<TM_DT_BF16, TM_METRIC_DOT>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, s);
   }
   if (metric == TM_METRIC_L2)
-    return dispatch_dim<TM_DT_F16, TM_METRIC_L2>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, s);
-  return dispatch_dim<TM_DT_F16, TM_METRIC_DOT>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, s);
+    return dispatch_dim<TM_DT_F16, TM_METRIC_L2>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, s);
+  return dispatch_dim<TM_DT_F16, TM_METRIC_DOT>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, s);
+}
+
+bool tm_internal_route_fusable(const tm_route_args *ra) {
+  return ra != nullptr && ra->logits != nullptr && ra->out_w != nullptr && ra->out_ids != nullptr &&
+         ra->top_k >= 1 && ra->top_k <= 8 && (ra->n_experts == 64 || ra->n_experts == 128) &&
+         ra->ld >= ra->n_experts && ra->ld % 4 == 0 && tm_aligned16(ra->logits);
+}
+
+int tm_internal_search_route(int32_t dtype, const void *q, int64_t n_tokens, int64_t ld_q, const float *q_sqnorm,
+                             const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm, int32_t dim,
+                             int32_t top_k, int32_t metric, float *out_dist, int64_t *out_idx, void *workspace,
+                             size_t workspace_bytes, const tm_route_args *ra, hipStream_t stream) {
+  TM_REQUIRE(tm_internal_route_fusable(ra), TM_EINVAL_ARG, "tm_table_forward: router shape cannot be fused");
+  return search_impl(dtype, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, dim, top_k, metric,
+                     out_dist, out_idx, workspace, workspace_bytes, ra, stream);
+}
+
+extern "C" int tm_search_global(int32_t dtype, const void *q, int64_t n_tokens, int64_t ld_q,
+                                const float *q_sqnorm, const void *cents, int64_t n_cent,
+                                int64_t ld_c, const float *c_sqnorm, int32_t dim, int32_t top_k,
+                                int32_t metric, float *out_dist, int64_t *out_idx, void *workspace,
+                                size_t workspace_bytes, tm_stream_t stream) {
+  return search_impl(dtype, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, dim, top_k, metric,
+                     out_dist, out_idx, workspace, workspace_bytes, nullptr, tm_hip_stream(stream));
 }

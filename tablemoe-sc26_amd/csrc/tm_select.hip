@@ -1,8 +1,7 @@
 // Selection kernels: keep-rate radix select (north-star kernel (3)), the
 // reference's keep masks (table_moe/skip/pruning.py) and surviving-weight
 // renormalisation.
-#include "tm_internal.h"
-#include "tm_route_dev.h"
+#include "tm_common.h"
 
 namespace {
 
@@ -11,27 +10,27 @@ namespace {
 // ---------------------------------------------------------------------------
 template <int NT>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *wave_tot, uint32_t &total) {
+  constexpr int NW = NT / 64;
+  static_assert(NW % 4 == 0, "wave totals are read four at a time");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t t = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += t;
-  }
+  const uint32_t inc = tm_wave_incl_scan(v);
   if (lane == 63) wave_tot[wave] = inc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t run = 0;
-    for (int w = 0; w < NT / 64; ++w) {
-      const uint32_t t = wave_tot[w];
-      wave_tot[w] = run;
-      run += t;
+  // every thread adds up the totals of the waves before its own (no second
+  // barrier; the callers do not write wave_tot again before their next barrier)
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < NW; w += 4) {
+    const uint4 t = *reinterpret_cast<const uint4 *>(&wave_tot[w]);
+    const uint32_t tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      all += tv[e];
+      before += (w + e < wave) ? tv[e] : 0u;
     }
-    wave_tot[NT / 64] = run;
   }
-  __syncthreads();
-  total = wave_tot[NT / 64];
-  return wave_tot[wave] + inc - v;
+  total = all;
+  return before + inc - v;
 }
 
 // ---------------------------------------------------------------------------
@@ -50,35 +49,15 @@ constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kSelRegs = 16;
 
-// Router work carried by the keep launch (the fused layer call): the
-// selection uses one workgroup and leaves the rest of the chip idle, and the
-// routing results are only needed by the combine that follows.  Workgroups
-// 1.. route kSelThreads / 8 tokens each (8 lanes per token).
-struct SelRoute {
-  const float *logits;
-  int64_t ld;
-  int top_k;
-  float *out_w;
-  int64_t *out_ids;
-};
-
-template <int RVPL>
 __global__ __launch_bounds__(kSelThreads) void keep_select_kernel(const float *__restrict__ score,
                                                                   int64_t n, int64_t ld,
                                                                   int64_t n_keep,
-                                                                  uint8_t *__restrict__ out, SelRoute ra) {
-  if constexpr (RVPL > 0) {
-    if (blockIdx.x > 0) {  // uniform: a routing workgroup (no barrier)
-      const int64_t tok = (int64_t)(blockIdx.x - 1) * (kSelThreads / 8) + (threadIdx.x >> 3);
-      tm_route_token<RVPL, 8>(ra.logits, n, ra.ld, ra.top_k, 0, ra.out_w, ra.out_ids, tok, threadIdx.x & 7);
-      return;
-    }
-  }
+                                                                  uint8_t *__restrict__ out) {
   __shared__ uint32_t whist[kSelWaves][256];  // per-wave private histograms
   __shared__ uint32_t hist[256];
   __shared__ uint32_t s_prefix, s_mask;
   __shared__ int64_t s_remaining;
-  __shared__ uint32_t wave_tot[kSelWaves + 1];
+  __shared__ __align__(16) uint32_t wave_tot[kSelWaves + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t per = (n + kSelThreads - 1) / kSelThreads;
   const int64_t lo = tid * per;
@@ -186,23 +165,24 @@ __global__ __launch_bounds__(kSelThreads) void keep_select_kernel(const float *_
 // ---------------------------------------------------------------------------
 constexpr int kFastBins = 4096;
 constexpr int kFastDigit = 12;
+constexpr int kFastPasses = 3;  // 32-bit keys: at most three 12-bit digits
 
-template <int RVPL>
+// Sum over the wave of `v` for lanes below `nl` (one LDS read per wave when
+// `v` comes from shared memory, then DPP; no all-lane broadcast reads).
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)tm_wave_incl_scan(v), 63);
+}
+
 __global__ __launch_bounds__(kSelThreads) void keep_select_fast_kernel(const float *__restrict__ score, int64_t n,
                                                                        int64_t ld, int64_t n_keep,
-                                                                       uint8_t *__restrict__ out, SelRoute ra) {
-  if constexpr (RVPL > 0) {
-    if (blockIdx.x > 0) {  // uniform: a routing workgroup (no barrier)
-      const int64_t tok = (int64_t)(blockIdx.x - 1) * (kSelThreads / 8) + (threadIdx.x >> 3);
-      tm_route_token<RVPL, 8>(ra.logits, n, ra.ld, ra.top_k, 0, ra.out_w, ra.out_ids, tok, threadIdx.x & 7);
-      return;
-    }
-  }
-  __shared__ uint32_t hist[kFastBins];
-  __shared__ uint32_t wave_tot[kSelWaves + 1];
+                                                                       uint8_t *__restrict__ out) {
+  // One histogram per pass, all cleared up front while the keys load; every
+  // LDS value that all threads need is read by one lane per wave and spread
+  // with DPP (LDS instruction issue, not bandwidth, bounds this kernel).
+  __shared__ __align__(16) uint32_t hist[kFastPasses][kFastBins];
+  __shared__ uint32_t wave_tot[kSelWaves];
   __shared__ uint32_t s_min[kSelWaves], s_max[kSelWaves];
-  __shared__ uint32_t s_prefix;
-  __shared__ int64_t s_remaining;
+  __shared__ uint2 s_sel;  // (boundary prefix, keys still to keep at it)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (int)((n + kSelThreads - 1) / kSelThreads);
   const int64_t lo = (int64_t)tid * per;
@@ -214,32 +194,47 @@ __global__ __launch_bounds__(kSelThreads) void keep_select_fast_kernel(const flo
     for (int64_t i = lo; i < hi; ++i) out[i] = v;
     return;
   }
+  if (n <= 64) {  // uniform: one wave ranks the keys directly (no LDS, no barrier)
+    if (wave == 0) {
+      const uint32_t key = lane < n ? tm_orderable(score[(int64_t)lane * ld]) : 0u;
+      uint32_t rank = 0;  // keys ahead of this one: larger, or equal at a lower index
+      for (int j = 0; j < (int)n; ++j) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)key, j);
+        rank += (kj > key || (kj == key && j < lane)) ? 1u : 0u;
+      }
+      if (lane < n) out[lane] = rank < (uint32_t)n_keep ? 1 : 0;
+    }
+    return;
+  }
+  {
+    uint4 *h4 = reinterpret_cast<uint4 *>(&hist[0][0]);
+#pragma unroll
+    for (int i = 0; i < kFastPasses * kFastBins / 4 / kSelThreads; ++i) h4[tid + i * kSelThreads] = make_uint4(0, 0, 0, 0);
+  }
   uint32_t keys[kSelRegs];
+  const bool vec4 = per == 4 && ld == 1 && (reinterpret_cast<uintptr_t>(score) & 15) == 0;  // uniform
+  if (vec4 && cnt == 4) {
+    const float4 f = *reinterpret_cast<const float4 *>(score + lo);
+    keys[0] = tm_orderable(f.x); keys[1] = tm_orderable(f.y); keys[2] = tm_orderable(f.z); keys[3] = tm_orderable(f.w);
+#pragma unroll
+    for (int j = 4; j < kSelRegs; ++j) keys[j] = 0u;
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSelRegs; ++j) keys[j] = (j < cnt) ? tm_orderable(score[(lo + j) * ld]) : 0u;
+  }
   uint32_t kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
-  for (int j = 0; j < kSelRegs; ++j) {
-    keys[j] = (j < cnt) ? tm_orderable(score[(lo + j) * ld]) : 0u;
+  for (int j = 0; j < kSelRegs; ++j)
     if (j < cnt) {
       kmin = keys[j] < kmin ? keys[j] : kmin;
       kmax = keys[j] > kmax ? keys[j] : kmax;
     }
-  }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t a = __shfl_xor(kmin, o, 64), b = __shfl_xor(kmax, o, 64);
-    kmin = a < kmin ? a : kmin;
-    kmax = b > kmax ? b : kmax;
-  }
+  kmin = tm_wave_min_u32(kmin);
+  kmax = tm_wave_max_u32(kmax);
   if (lane == 0) { s_min[wave] = kmin; s_max[wave] = kmax; }
-  if (tid == 0) s_remaining = n_keep;
   __syncthreads();
-  kmin = s_min[0];
-  kmax = s_max[0];
-#pragma unroll
-  for (int w = 1; w < kSelWaves; ++w) {
-    kmin = s_min[w] < kmin ? s_min[w] : kmin;
-    kmax = s_max[w] > kmax ? s_max[w] : kmax;
-  }
+  kmin = tm_wave_min_u32(lane < kSelWaves ? s_min[lane] : 0xffffffffu);
+  kmax = tm_wave_max_u32(lane < kSelWaves ? s_max[lane] : 0u);
   uint32_t prefix = kmin & kmax, mask = 0u;  // common high bits
   int top = -1;
   if (kmin != kmax) {
@@ -250,60 +245,65 @@ __global__ __launch_bounds__(kSelThreads) void keep_select_fast_kernel(const flo
     mask = 0xffffffffu;
     prefix = kmin;
   }
-  for (int hi_bit = top; hi_bit >= 0; hi_bit -= kFastDigit) {  // uniform trip count
+  uint32_t rem = (uint32_t)n_keep;  // keys still to keep among those matching `prefix`
+  int pass = 0;
+  for (int hi_bit = top; hi_bit >= 0; hi_bit -= kFastDigit, ++pass) {  // uniform trip count (<= 3)
     const int w = hi_bit + 1 < kFastDigit ? hi_bit + 1 : kFastDigit;
     const int shift = hi_bit + 1 - w;
     const uint32_t dmask = (1u << w) - 1u;
-#pragma unroll
-    for (int b = 0; b < kFastBins / kSelThreads; ++b) hist[tid + b * kSelThreads] = 0u;
-    __syncthreads();
+    uint32_t *h = hist[pass];
 #pragma unroll
     for (int j = 0; j < kSelRegs; ++j)
-      if (j < cnt && (keys[j] & mask) == prefix) atomicAdd(&hist[(keys[j] >> shift) & dmask], 1u);
+      if (j < cnt && (keys[j] & mask) == prefix) atomicAdd(&h[(keys[j] >> shift) & dmask], 1u);
     __syncthreads();
     // thread t owns bins 4r .. 4r+3 of rank r = 1023 - t (descending bin order across threads)
     const int r = kSelThreads - 1 - tid;
-    uint32_t hb[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) hb[b] = hist[4 * r + b];
+    const uint4 hb4 = *reinterpret_cast<const uint4 *>(&h[4 * r]);
+    const uint32_t hb[4] = {hb4.x, hb4.y, hb4.z, hb4.w};
     const uint32_t tsum = hb[0] + hb[1] + hb[2] + hb[3];
-    const int64_t rem = s_remaining;  // read before the scan's barriers: the update below follows them
-    uint32_t total;
-    const uint32_t above0 = block_exclusive_scan<kSelThreads>(tsum, wave_tot, total);  // keys in higher bins
-    int64_t above = above0;
+    const uint32_t inc = tm_wave_incl_scan(tsum);
+    if (lane == 63) wave_tot[wave] = inc;
+    __syncthreads();
+    uint32_t above = wave_sum_u32(lane < wave ? wave_tot[lane] : 0u) + inc - tsum;  // keys in higher bins
 #pragma unroll
     for (int b = 3; b >= 0; --b) {
-      if (above < rem && rem <= above + (int64_t)hb[b]) {
-        s_prefix = prefix | ((uint32_t)(4 * r + b) << shift);
-        s_remaining = rem - above;
-      }
+      if (above < rem && rem <= above + hb[b]) s_sel = make_uint2(prefix | ((uint32_t)(4 * r + b) << shift), rem - above);
       above += hb[b];
     }
     __syncthreads();
-    prefix = s_prefix;
+    // (the next pass writes wave_tot and s_sel only after its first barrier)
+    const uint2 sel = s_sel;
+    prefix = sel.x;
+    rem = sel.y;
     mask |= dmask << shift;
-    __syncthreads();  // every thread has read s_prefix / s_remaining / wave_tot before the next pass
   }
-  const uint32_t T = prefix;
-  const int64_t keep_eq = s_remaining;  // copies of T to keep, >= 1
+  const uint32_t T = prefix;  // the boundary key; `rem` copies of it are kept (>= 1)
   uint32_t eq = 0;
 #pragma unroll
   for (int j = 0; j < kSelRegs; ++j) eq += (j < cnt && keys[j] == T) ? 1u : 0u;
-  uint32_t total;
-  uint32_t rank = block_exclusive_scan<kSelThreads>(eq, wave_tot, total);
+  const uint32_t inc = tm_wave_incl_scan(eq);
+  if (lane == 63) wave_tot[wave] = inc;
+  __syncthreads();
+  uint32_t rank = wave_sum_u32(lane < wave ? wave_tot[lane] : 0u) + inc - eq;  // copies of T at lower indices
+  uint32_t packed = 0;
 #pragma unroll
   for (int j = 0; j < kSelRegs; ++j) {
+    uint32_t k = 0;
     if (j < cnt) {
-      uint8_t k = 0;
       if (keys[j] > T) {
         k = 1;
       } else if (keys[j] == T) {
-        k = ((int64_t)rank < keep_eq) ? 1 : 0;
+        k = rank < rem ? 1u : 0u;
         ++rank;
       }
-      out[lo + j] = k;
     }
+    if (j < 4) packed |= k << (8 * j);
+    if (!(vec4 && cnt == 4) && j < cnt) out[lo + j] = (uint8_t)k;
   }
+  if (vec4 && cnt == 4 && (reinterpret_cast<uintptr_t>(out) & 3) == 0)
+    *reinterpret_cast<uint32_t *>(out + lo) = packed;
+  else if (vec4 && cnt == 4)
+    for (int j = 0; j < 4; ++j) out[lo + j] = (uint8_t)((packed >> (8 * j)) & 1u);
 }
 
 // ---------------------------------------------------------------------------
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(kRankThreads) void expert_rank_kernel(
   __shared__ float score[kMaxExperts];
   __shared__ uint8_t active[kMaxExperts];
   __shared__ uint8_t kept[kMaxExperts];
-  __shared__ uint32_t wave_tot[kRankThreads / 64 + 1];
+  __shared__ __align__(16) uint32_t wave_tot[kRankThreads / 64 + 1];
   const int tid = threadIdx.x;
   uint32_t my_active = 0;
   for (int e = tid; e < n_experts; e += kRankThreads) {
@@ -461,38 +461,12 @@ extern "C" int tm_keep_select(const float *score, int64_t n, int64_t ld_score, i
   if (n == 0) return TM_OK;
   TM_REQUIRE(score && out_keep, TM_EINVAL_ARG, "tm_keep_select: null pointer");
   if (n <= (int64_t)kSelThreads * kSelRegs)
-    hipLaunchKernelGGL((keep_select_fast_kernel<0>), dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
-                       score, n, ld_score, n_keep, out_keep, SelRoute{});
+    hipLaunchKernelGGL(keep_select_fast_kernel, dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
+                       score, n, ld_score, n_keep, out_keep);
   else
-    hipLaunchKernelGGL((keep_select_kernel<0>), dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
-                       score, n, ld_score, n_keep, out_keep, SelRoute{});
+    hipLaunchKernelGGL(keep_select_kernel, dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
+                       score, n, ld_score, n_keep, out_keep);
   TM_LAUNCH_CHECK("tm_keep_select");
-  return TM_OK;
-}
-
-int tm_internal_keep_route(const float *score, int64_t n, int64_t ld_score, int64_t n_keep, uint8_t *out_keep,
-                           const float *logits, int64_t ld_logits, int32_t n_experts, int32_t top_k, float *out_w,
-                           int64_t *out_ids, hipStream_t stream) {
-  if (n <= 0 || n >= ((int64_t)1 << 31) || ld_score < 1 || !score || !out_keep || !logits || !out_w || !out_ids ||
-      top_k < 1 || top_k > 8 || (n_experts != 64 && n_experts != 128) || ld_logits < n_experts ||
-      !tm_aligned16(logits) || ld_logits % 4 != 0)
-    return TM_NOT_FUSED;
-  const SelRoute ra{logits, ld_logits, top_k, out_w, out_ids};
-  const dim3 grid((unsigned)(1 + tm_cdiv(n, kSelThreads / 8)));
-  const bool fast = n <= (int64_t)kSelThreads * kSelRegs;
-  if (n_experts == 64 && fast)
-    hipLaunchKernelGGL((keep_select_fast_kernel<8>), grid, dim3(kSelThreads), 0, stream, score, n, ld_score, n_keep,
-                       out_keep, ra);
-  else if (fast)
-    hipLaunchKernelGGL((keep_select_fast_kernel<16>), grid, dim3(kSelThreads), 0, stream, score, n, ld_score,
-                       n_keep, out_keep, ra);
-  else if (n_experts == 64)
-    hipLaunchKernelGGL((keep_select_kernel<8>), grid, dim3(kSelThreads), 0, stream, score, n, ld_score, n_keep,
-                       out_keep, ra);
-  else
-    hipLaunchKernelGGL((keep_select_kernel<16>), grid, dim3(kSelThreads), 0, stream, score, n, ld_score, n_keep,
-                       out_keep, ra);
-  TM_LAUNCH_CHECK("tm_table_forward(keep+route)");
   return TM_OK;
 }
 
