@@ -154,6 +154,20 @@ __device__ __forceinline__ float tm_from_orderable(uint32_t k) {
   return __uint_as_float(u);
 }
 
+// A packed search key (orderable(dp) << 32 | centroid) of one query turned
+// into its output: dp = -2 * (q.c - |c|^2 / 2) for L2 (distance |q|^2 + dp,
+// clamped at 0), dp = -q.c for DOT (score -dp).  Key ~0 (no candidate) gives
+// index -1 and the worst distance.
+__device__ __forceinline__ float tm_key_to_dist(uint64_t key, float qn, bool l2, int64_t &idx) {
+  if (key == ~0ull) {
+    idx = -1;
+    return l2 ? __builtin_huge_valf() : -__builtin_huge_valf();
+  }
+  const float dp = tm_from_orderable((uint32_t)(key >> 32));
+  idx = (int64_t)(uint32_t)key;
+  return l2 ? fmaxf(qn + dp, 0.f) : -dp;
+}
+
 // ---------------------------------------------------------------------------
 // wave64 reductions
 // ---------------------------------------------------------------------------

@@ -25,3 +25,37 @@ __attribute__((visibility("hidden"))) int tm_internal_search_route(
     int64_t n_cent, int64_t ld_c, const float *c_sqnorm, int32_t dim, int32_t top_k, int32_t metric,
     float *out_dist, int64_t *out_idx, void *workspace, size_t workspace_bytes, const tm_route_args *ra,
     hipStream_t stream);
+
+// Column-split projection of packed P (no normalisation): q rows plus the
+// partial squared norms qn_part[g][row] of column group g (dim / 64 groups,
+// added in group order by the consumer).  With `keys` set, also resets the
+// rows' packed top-1 search keys to ~0; with `ra` set, the launch also routes
+// the n tokens (`ra` must be fusable).
+__attribute__((visibility("hidden"))) bool tm_internal_project_cols_ok(
+    int32_t dtype, const void *x, int64_t n, int32_t hidden, int64_t ld_x, const void *pv, const void *bv,
+    const void *pt, const void *bt, int64_t ps_h, int64_t ps_d, int32_t dim, const void *q, int64_t ld_q);
+__attribute__((visibility("hidden"))) size_t tm_internal_project_cols_parts(int32_t dim);
+__attribute__((visibility("hidden"))) int tm_internal_project_cols(
+    int32_t dtype, const void *x, int64_t n, int32_t hidden, int64_t ld_x, const uint8_t *is_vision,
+    const void *pv, const void *bv, const void *pt, const void *bt, int64_t ps_h, int64_t ps_d, int32_t dim,
+    void *q, int64_t ld_q, float *qn_part, uint64_t *keys, const tm_route_args *ra, hipStream_t stream);
+
+// Top-1 global search that merges its centroid ranges by an atomic minimum of
+// packed keys (orderable(dp) << 32 | centroid) into keys[n] (reset to ~0
+// beforehand): no split-merge launch.  Only the shapes that run the pipelined
+// top-1 kernel qualify.
+__attribute__((visibility("hidden"))) bool tm_internal_search_keys_ok(int32_t dtype, int64_t n, int64_t n_cent,
+                                                                      int64_t ld_c, int32_t dim, int32_t top_k);
+__attribute__((visibility("hidden"))) int tm_internal_search_keys(
+    int32_t dtype, const void *q, int64_t n, int64_t ld_q, const void *cents, int64_t n_cent, int64_t ld_c,
+    const float *c_sqnorm, int32_t dim, int32_t metric, uint64_t *keys, hipStream_t stream);
+
+// tm_keep_select over the distances the packed keys give (|q|^2 = the sum of
+// `parts` partial norms qn_part[p][i]); also writes dist[i], idx[i] and
+// q_sqnorm[i].  n <= 16384.
+__attribute__((visibility("hidden"))) bool tm_internal_keep_keys_ok(int64_t n);
+__attribute__((visibility("hidden"))) int tm_internal_keep_keys(const uint64_t *keys, const float *qn_part,
+                                                                int32_t parts, int32_t metric, int64_t n,
+                                                                int64_t n_keep, float *out_dist,
+                                                                int64_t *out_idx, float *out_qn,
+                                                                uint8_t *out_keep, hipStream_t stream);

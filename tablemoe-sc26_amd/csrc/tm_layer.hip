@@ -8,8 +8,13 @@ constexpr size_t kAlign = 256;
 
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
+// Two plans share one workspace layout: the general one (tm_project,
+// tm_search_global, tm_keep_select as exported) and the fused top-1 one
+// (packed keys and partial query norms: column-split projection carrying the
+// router and the key reset, search merging by atomic minimum, keep select
+// decoding the keys), which needs no split-merge launch.
 struct WsLayout {
-  size_t project, search, keep, total;
+  size_t project, search, keep, keys, qn_part, total;
 };
 
 WsLayout layout(const tm_table_layer *t, int64_t n, int32_t nn) {
@@ -17,8 +22,18 @@ WsLayout layout(const tm_table_layer *t, int64_t n, int32_t nn) {
   w.project = align_up(tm_project_workspace_size(n, t->hidden, t->dim));
   w.search = align_up(tm_search_global_workspace_size(n, t->n_cent, t->dim, nn));
   w.keep = align_up(tm_keep_select_workspace_size(n));
-  w.total = w.project + w.search + w.keep;
+  w.keys = align_up((size_t)n * sizeof(uint64_t));
+  w.qn_part = align_up((size_t)n * 4 * sizeof(float));
+  w.total = w.project + w.search + w.keep + w.keys + w.qn_part;
   return w;
+}
+
+bool fused_top1_ok(const tm_table_layer *t, const tm_layer_io *io) {
+  const int64_t n = io->n_tokens;
+  return io->n_nearest == 1 &&
+         tm_internal_project_cols_ok(t->dtype, io->x, n, t->hidden, io->ld_x, t->proj_vis, t->bias_vis,
+                                     t->proj_txt, t->bias_txt, t->ps_h, t->ps_d, t->dim, io->q, t->dim) &&
+         tm_internal_search_keys_ok(t->dtype, n, t->n_cent, t->ld_c, t->dim, 1) && tm_internal_keep_keys_ok(n);
 }
 
 int record(void *const *events, int i, hipStream_t s) {
@@ -26,6 +41,61 @@ int record(void *const *events, int i, hipStream_t s) {
   const hipError_t e = hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), s);
   if (e != hipSuccess) return tm_fail(TM_EHIP, "tm_table_forward: hipEventRecord: %s", hipGetErrorString(e));
   return TM_OK;
+}
+
+// Stages 0-4 of the fused top-1 plan (events 0..4 bracket router, projection,
+// search, keep select).
+int fused_top1_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout &w, char *ws,
+                      const tm_route_args &ra, bool route_fused, int64_t n_keep, void *const *ev, hipStream_t s) {
+  const int64_t n = io->n_tokens;
+  uint64_t *keys = reinterpret_cast<uint64_t *>(ws + w.project + w.search + w.keep);
+  float *qn_part = reinterpret_cast<float *>(ws + w.project + w.search + w.keep + w.keys);
+  int st;
+  if ((st = record(ev, 0, s)) != TM_OK) return st;
+  if (!route_fused && (st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k,
+                                            0, io->weights, io->expert_ids, s)) != TM_OK)
+    return st;
+  if ((st = record(ev, 1, s)) != TM_OK) return st;
+  if ((st = tm_internal_project_cols(t->dtype, io->x, n, t->hidden, io->ld_x, io->is_vision, t->proj_vis,
+                                     t->bias_vis, t->proj_txt, t->bias_txt, t->ps_h, t->ps_d, t->dim, io->q, t->dim,
+                                     qn_part, keys, route_fused ? &ra : nullptr, s)) != TM_OK)
+    return st;
+  if ((st = record(ev, 2, s)) != TM_OK) return st;
+  if ((st = tm_internal_search_keys(t->dtype, io->q, n, t->dim, t->cents, t->n_cent, t->ld_c, t->c_sqnorm, t->dim,
+                                    t->metric, keys, s)) != TM_OK)
+    return st;
+  if ((st = record(ev, 3, s)) != TM_OK) return st;
+  return tm_internal_keep_keys(keys, qn_part, (int32_t)tm_internal_project_cols_parts(t->dim), t->metric, n, n_keep,
+                               io->dist, io->idx, io->q_sqnorm, io->keep, s);
+}
+
+// Stages 0-4 of the general plan: the exported entry points; the router rides
+// in the search's split-merge launch when it can.
+int general_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout &w, char *ws,
+                   const tm_route_args &ra, bool route_fused, int64_t n_keep, void *const *ev, hipStream_t s) {
+  const int64_t n = io->n_tokens;
+  int st;
+  if ((st = record(ev, 0, s)) != TM_OK) return st;
+  if (!route_fused && (st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k,
+                                            0, io->weights, io->expert_ids, s)) != TM_OK)
+    return st;
+  if ((st = record(ev, 1, s)) != TM_OK) return st;
+  if ((st = tm_project(t->dtype, io->x, n, t->hidden, io->ld_x, io->is_vision, t->proj_vis, t->bias_vis,
+                       t->proj_txt, t->bias_txt, t->ps_h, t->ps_d, t->dim, 0, 1e-6f, io->q, t->dim, io->q_sqnorm,
+                       w.project ? ws : nullptr, w.project, s)) != TM_OK)
+    return st;
+  if ((st = record(ev, 2, s)) != TM_OK) return st;
+  if (route_fused)
+    st = tm_internal_search_route(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c,
+                                  t->c_sqnorm, t->dim, io->n_nearest, t->metric, io->dist, io->idx, ws + w.project,
+                                  w.search, &ra, s);
+  else
+    st = tm_search_global(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c, t->c_sqnorm,
+                          t->dim, io->n_nearest, t->metric, io->dist, io->idx, ws + w.project, w.search, s);
+  if (st != TM_OK) return st;
+  if ((st = record(ev, 3, s)) != TM_OK) return st;
+  return tm_keep_select(io->dist, n, io->n_nearest, n_keep, io->keep, w.keep ? ws + w.project + w.search : nullptr,
+                        w.keep, s);
 }
 
 }  // namespace
@@ -53,37 +123,17 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
              workspace_bytes, w.total);
   char *ws = static_cast<char *>(workspace);
   hipStream_t s = tm_hip_stream(stream);
-  int st;
   // The router's results are only consumed by the combine: without stage
-  // events it rides in the search's split-merge launch (a few latency-bound
-  // workgroups that leave the chip idle) and its own stage interval is empty.
+  // events it rides in another launch (its own launch would be a few
+  // latency-bound workgroups that leave the chip idle) and its stage interval
+  // is empty.
   const tm_route_args ra{io->router_logits, io->ld_logits, io->n_experts, io->router_top_k, io->weights,
                          io->expert_ids};
-  const bool route_in_search = stage_events == nullptr && tm_internal_route_fusable(&ra);
-  if ((st = record(stage_events, 0, s)) != TM_OK) return st;
-  if (!route_in_search &&
-      (st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k, 0,
-                            io->weights, io->expert_ids, stream)) != TM_OK)
-    return st;
-  if ((st = record(stage_events, 1, s)) != TM_OK) return st;
-  if ((st = tm_project(t->dtype, io->x, n, t->hidden, io->ld_x, io->is_vision, t->proj_vis, t->bias_vis,
-                       t->proj_txt, t->bias_txt, t->ps_h, t->ps_d, t->dim, 0, 1e-6f, io->q, t->dim,
-                       io->q_sqnorm, w.project ? ws : nullptr, w.project, stream)) != TM_OK)
-    return st;
-  if ((st = record(stage_events, 2, s)) != TM_OK) return st;
-  if (route_in_search)
-    st = tm_internal_search_route(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c,
-                                  t->c_sqnorm, t->dim, io->n_nearest, t->metric, io->dist, io->idx,
-                                  ws + w.project, w.search, &ra, s);
-  else
-    st = tm_search_global(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c, t->c_sqnorm,
-                          t->dim, io->n_nearest, t->metric, io->dist, io->idx, ws + w.project, w.search, stream);
-  if (st != TM_OK) return st;
-  if ((st = record(stage_events, 3, s)) != TM_OK) return st;
+  const bool route_fused = stage_events == nullptr && tm_internal_route_fusable(&ra);
   const int64_t n_keep = tm_keep_count(n, io->keep_rate);
-  if ((st = tm_keep_select(io->dist, n, io->n_nearest, n_keep, io->keep,
-                           w.keep ? ws + w.project + w.search : nullptr, w.keep, stream)) != TM_OK)
-    return st;
+  int st = fused_top1_ok(t, io) ? fused_top1_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s)
+                                : general_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s);
+  if (st != TM_OK) return st;
   if ((st = record(stage_events, 4, s)) != TM_OK) return st;
   if ((st = tm_gather_combine(t->dtype, n, t->hidden, io->keep, io->slot_out, io->so_b, io->so_s, io->weights,
                               io->router_top_k, io->router_top_k, t->values, t->n_cent, t->ld_v, io->idx,

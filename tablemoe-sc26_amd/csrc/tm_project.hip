@@ -23,7 +23,9 @@
 // project_epilogue_kernel adds them in split order (deterministic), adds the
 // bias, rounds, normalises and stores q.  Without one, the same epilogue runs
 // inside the workgroup.
+#include "tm_internal.h"
 #include "tm_mfma.h"
+#include "tm_route_dev.h"
 
 namespace {
 
@@ -248,6 +250,242 @@ __global__ __launch_bounds__(64 * KW) void project_direct_kernel(
     }
     finish_row<DT, TPR>(v, normalize, eps, ok ? q + gr * ld_q + part * 8 : nullptr,
                         (ok && part == 0 && q_sqnorm) ? q_sqnorm + gr : nullptr);
+  }
+}
+
+// Column-split packed path (internal, used by the layer call).
+//
+// Every CU that owns all DIM columns of its rows streams all of P (hidden *
+// DIM * 2 bytes) from L2, and the per-CU fetch rate bounds that.  Here a
+// workgroup owns 32 token rows and 64 of the DIM columns, so a CU fetches
+// (32 + 64) * hidden * 2 bytes (the smallest sum for 32 * 64 outputs), and
+// its 4 waves split `hidden` so no two waves load the same bytes.  Each wave
+// computes a 32 x 64 partial tile (2 x 4 MFMA blocks per 32-wide k-step); the
+// wave partials are added in wave order through LDS.  The row epilogue adds
+// the bias, rounds once and writes the 64 columns and the partial |q|^2 of
+// those columns, qn_part[g][row] (the consumer adds the DIM / 64 parts in
+// order).  No normalisation (the rows' norm needs all columns).
+//
+// Operands: B (packed P) fragments are contiguous 1 KiB per wave and are
+// loaded straight into a register ring.  A (x) fragments span 16 rows x 64
+// bytes, a gather that halves the fetch rate, so x travels in chunks of 4
+// k-steps instead: one load covers 4 rows x 256 contiguous bytes (whole cache
+// lines), the chunk is written to the wave's own LDS tile and the fragments
+// are read back from it.  Slot s (16 bytes) of tile row r holds the row's
+// chunk s ^ (r % 16), so the 16 rows of a fragment read fall in distinct
+// banks.  The values and the order of every fp32 operation are those of
+// project_direct_kernel with 4 waves (same k slices, same MFMA sequence).
+//
+// Placement: the DIM / 64 column groups of a row tile get block ids 8 apart,
+// so the dispatcher's round-robin over the 8 XCDs puts them on one XCD and
+// they share its L2 copy of the x rows.  The same launch may carry the
+// router (workgroups after the projection ones) and, when `keys` is set,
+// resets the tile's packed top-1 search keys to ~0 (no candidate yet).
+template <int DIM>
+struct ColsCfg {
+  static constexpr int G = DIM / 64;    // column groups
+  static constexpr int NCB = DIM / 16;  // 16-column blocks of the packed layout
+  static constexpr int XC = 1;          // x chunks (4 k-steps each) in flight per wave
+  static constexpr int DP = 4;          // k-steps of P in flight per wave (= k-steps per x chunk)
+};
+
+struct ColsRoute {
+  tm_route_args a;
+  int64_t first;  // first router workgroup
+};
+
+template <int DT, int DIM, int RVPL>
+__global__ __launch_bounds__(256, 2) void project_cols_kernel(
+    const typename Elem<DT>::T *__restrict__ x, int64_t n, int hidden, int64_t ld_x,
+    const uint8_t *__restrict__ is_vision, const typename Elem<DT>::T *__restrict__ pv,
+    const typename Elem<DT>::T *__restrict__ bv, const typename Elem<DT>::T *__restrict__ pt,
+    const typename Elem<DT>::T *__restrict__ bt, typename Elem<DT>::T *__restrict__ q, int64_t ld_q,
+    float *__restrict__ qn_part, uint64_t *__restrict__ keys, int64_t n_tiles, ColsRoute cr) {
+  using T = typename Elem<DT>::T;
+  constexpr int G = ColsCfg<DIM>::G;
+  constexpr int NCB = ColsCfg<DIM>::NCB;
+  constexpr int XC = ColsCfg<DIM>::XC;
+  constexpr int DP = ColsCfg<DIM>::DP;
+  static_assert(DP == 4 && G >= 1, "one P ring round per x chunk");
+  constexpr int kRowPad = 64 + 4;
+  __shared__ float red[4][32][kRowPad];
+  __shared__ uint4 xs[4][32 * 16];  // per wave: 32 rows x 16 slots (one 4-k-step chunk)
+
+  const int tid = threadIdx.x;
+  if constexpr (RVPL > 0) {
+    if ((int64_t)blockIdx.x >= cr.first) {  // uniform: router workgroup, 32 tokens
+      const int64_t tok = ((int64_t)blockIdx.x - cr.first) * 32 + (tid >> 3);
+      tm_route_token<RVPL, 8>(cr.a.logits, n, cr.a.ld, cr.a.top_k, 0, cr.a.out_w, cr.a.out_ids, tok, tid & 7);
+      return;
+    }
+  }
+  const int64_t b = blockIdx.x;
+  const int64_t tile = (b / (8 * G)) * 8 + (b % 8);
+  const int g = (int)((b / 8) % G);
+  if (tile >= n_tiles) return;  // uniform (the grid is padded to whole groups of 8 tiles)
+
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t row0 = tile * 32;
+
+  const int nks = (hidden + 31) / 32;
+  const int per = (nks + 3) / 4;
+  const int ks_begin = wave * per;
+  const int ks_end = (ks_begin + per < nks) ? ks_begin + per : nks;
+  const int klast = ks_end - 1 >= 0 ? ks_end - 1 : 0;  // clamp target of every P load past this wave's slice
+  const int nchunk = ks_end > ks_begin ? (ks_end - ks_begin + 3) / 4 : 0;
+
+  // x chunk loads: load i (0..7) of a chunk brings tile rows 4i + lane/16, this
+  // lane's 16 bytes being the row's chunk slot (lane % 16) ^ (row % 16).
+  // Unconditional with clamped addresses (rows past n read the last row and
+  // are dropped; chunks past `hidden` are zeroed when written to LDS).
+  // (addresses are recomputed per load: a pointer per load slot would cost
+  // more registers than the ring itself)
+  const int xslot = lane & 15;
+  const int xr0 = lane >> 4;
+  const int64_t rows_left = n - 1 - row0;  // rows past n read the last row
+  auto x_src = [&](int i, int c) {
+    const int r = 4 * i + xr0;
+    const int kk = (ks_begin + 4 * c) * 32 + 8 * (xslot ^ (r & 15));
+    return x + (row0 + (r < rows_left ? r : rows_left)) * ld_x + (kk < hidden ? kk : hidden - 8);
+  };
+  uint4 xr[XC][8];
+  auto load_x = [&](int u, int c) {  // chunk c of this wave's slice into register set u
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xr[u][i] = *reinterpret_cast<const uint4 *>(x_src(i, c));
+  };
+  uint4 *xw = &xs[wave][0];
+  auto store_x = [&](int u, int c) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 4 * i + xr0;
+      const int kk = (ks_begin + 4 * c) * 32 + 8 * (xslot ^ (r & 15));
+      xw[r * 16 + xslot] = kk < hidden ? xr[u][i] : make_uint4(0, 0, 0, 0);
+    }
+  };
+  // A fragment of k-step t of the chunk in LDS, rows 16*rb + lane%16
+  auto read_a = [&](int rb, int t) {
+    const int r = 16 * rb + (lane & 15);
+    return xw[r * 16 + ((4 * t + (lane >> 4)) ^ (r & 15))];
+  };
+
+  // modality byte of row (lane & 31) first: loads complete in order
+  const int64_t vr = row0 + (lane & 31);
+  const bool vr_ok = vr < n;
+  const uint8_t *vsrc = is_vision ? is_vision + (vr_ok ? vr : 0) : reinterpret_cast<const uint8_t *>(x);
+  const uint8_t vis_byte = *vsrc;
+#pragma unroll
+  for (int u = 0; u < XC; ++u) load_x(u, u);
+  const int amod = !vr_ok ? 2 : ((is_vision == nullptr || vis_byte) ? 0 : 1);
+  const uint32_t vis_bits = (uint32_t)(__ballot(amod == 0) & 0xFFFFFFFFull);  // bit r: tile row r uses P_vis
+  const uint32_t txt_bits = (uint32_t)(__ballot(amod == 1) & 0xFFFFFFFFull);
+
+  // epilogue mapping: 8 threads per row, 8 columns each
+  const int erow = tid >> 3;
+  const int part = tid & 7;
+  const int col = 64 * g + 8 * part;
+  const uint4 braw_v = *reinterpret_cast<const uint4 *>(bv + col);  // raw: 4 registers each
+  const uint4 braw_t = *reinterpret_cast<const uint4 *>(bt + col);
+
+  uint4 br[DP][4];
+  auto run_pass = [&](const T *P, uint32_t rows_of_pass, bool refetch_x) {
+    tm_f32x4 acc[2][4];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[rb][c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint4 *pf = reinterpret_cast<const uint4 *>(P) + (int64_t)(4 * g) * 64 + lane;
+    auto fetch_p = [&](int slot, int ks) {
+      const int kc = ks < klast ? ks : klast;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) br[slot][c] = pf[((int64_t)kc * NCB + c) * 64];
+    };
+    auto consume = [&](int t) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const uint4 a = read_a(rb, t);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[rb][c] = tm_mfma16x16x32<DT>(a, br[t][c], acc[rb][c]);
+      }
+    };
+    if (refetch_x) {
+#pragma unroll
+      for (int u = 0; u < XC; ++u) load_x(u, u);
+    }
+#pragma unroll
+    for (int t = 0; t < DP; ++t) fetch_p(t, ks_begin + t);
+    int c0 = 0;
+    for (; c0 + XC <= nchunk; c0 += XC) {  // whole rounds of the x ring: no guards
+#pragma unroll
+      for (int u = 0; u < XC; ++u) {
+        const int c = c0 + u;
+        store_x(u, c);
+        load_x(u, c + XC);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int ks = ks_begin + 4 * c + t;
+          if (ks < ks_end) consume(t);  // (only a partial last chunk skips)
+          fetch_p(t, ks + DP);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < XC; ++u) {  // remainder: fewer than XC chunks, already in registers
+      const int c = c0 + u;
+      if (c < nchunk) {  // uniform
+        store_x(u, c);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int ks = ks_begin + 4 * c + t;
+          if (ks < ks_end) consume(t);
+          fetch_p(t, ks + DP);
+        }
+      }
+    }
+    // this pass's rows go to the wave's LDS tile (D row of acc[rb][c][i] is
+    // 16*rb + 4*(lane>>4) + i); the passes own disjoint rows
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * rb + 4 * (lane >> 4) + i;
+        if ((rows_of_pass >> r) & 1u) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) red[wave][r][16 * c + (lane & 15)] = acc[rb][c][i];
+        }
+      }
+  };
+  if (vis_bits) run_pass(pv, vis_bits, false);  // uniform branches
+  if (txt_bits) run_pass(pt, txt_bits, vis_bits != 0);
+  __syncthreads();
+
+  const int64_t gr = row0 + erow;
+  const bool ok = gr < n;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {  // wave order: deterministic
+    const float4 a = *reinterpret_cast<const float4 *>(&red[w][erow][8 * part]);
+    const float4 c = *reinterpret_cast<const float4 *>(&red[w][erow][8 * part + 4]);
+    v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+    v[4] += c.x; v[5] += c.y; v[6] += c.z; v[7] += c.w;
+  }
+  const bool vis = (vis_bits >> erow) & 1u;
+  const uint4 braw = vis ? braw_v : braw_t;
+  const T *be = reinterpret_cast<const T *>(&braw);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = tm_round<DT>(v[i] + Elem<DT>::to_f(be[i]));
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+  ss += __shfl_xor(ss, 1, 64);
+  ss += __shfl_xor(ss, 2, 64);
+  ss += __shfl_xor(ss, 4, 64);
+  if (ok) {
+    tm_store8<DT>(q + gr * ld_q + col, v);
+    if (part == 0) qn_part[(int64_t)g * n + gr] = ss;
+    if (keys != nullptr && g == 0 && part == 1) keys[gr] = ~0ull;
   }
 }
 
@@ -693,6 +931,76 @@ extern "C" int tm_project_pack(int32_t dtype, const void *src, int32_t hidden, i
                          tm_hip_stream(stream), static_cast<const typename Elem<DT>::T *>(src), hidden, dim, ps_h,
                          ps_d, n_chunks, static_cast<uint4 *>(packed));
       TM_LAUNCH_CHECK("tm_project_pack");
+    }
+    return TM_OK;
+  });
+}
+
+namespace {
+
+template <int DT, int DIM, int RVPL>
+void launch_cols(const void *x, int64_t n, int hidden, int64_t ld_x, const uint8_t *is_vision, const void *pv,
+                 const void *bv, const void *pt, const void *bt, void *q, int64_t ld_q, float *qn_part,
+                 uint64_t *keys, const tm_route_args *ra, hipStream_t stream) {
+  using T = typename Elem<DT>::T;
+  const int64_t n_tiles = tm_cdiv(n, 32);
+  ColsRoute cr{};
+  int64_t blocks = tm_cdiv(n_tiles, 8) * 8 * ColsCfg<DIM>::G;
+  if (RVPL > 0) {
+    cr.a = *ra;
+    cr.first = blocks;
+    blocks += tm_cdiv(n, 32);
+  }
+  hipLaunchKernelGGL((project_cols_kernel<DT, DIM, RVPL>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const T *>(x), n, hidden, ld_x, is_vision, static_cast<const T *>(pv),
+                     static_cast<const T *>(bv), static_cast<const T *>(pt ? pt : pv),
+                     static_cast<const T *>(pt ? bt : bv), static_cast<T *>(q), ld_q, qn_part, keys, n_tiles, cr);
+}
+
+template <int DT, int DIM>
+void launch_cols_route(const void *x, int64_t n, int hidden, int64_t ld_x, const uint8_t *is_vision,
+                       const void *pv, const void *bv, const void *pt, const void *bt, void *q, int64_t ld_q,
+                       float *qn_part, uint64_t *keys, const tm_route_args *ra, hipStream_t stream) {
+  if (ra == nullptr)
+    launch_cols<DT, DIM, 0>(x, n, hidden, ld_x, is_vision, pv, bv, pt, bt, q, ld_q, qn_part, keys, ra, stream);
+  else if (ra->n_experts == 64)
+    launch_cols<DT, DIM, 8>(x, n, hidden, ld_x, is_vision, pv, bv, pt, bt, q, ld_q, qn_part, keys, ra, stream);
+  else
+    launch_cols<DT, DIM, 16>(x, n, hidden, ld_x, is_vision, pv, bv, pt, bt, q, ld_q, qn_part, keys, ra, stream);
+}
+
+}  // namespace
+
+bool tm_internal_project_cols_ok(int32_t dtype, const void *x, int64_t n, int32_t hidden, int64_t ld_x,
+                                 const void *pv, const void *bv, const void *pt, const void *bt, int64_t ps_h,
+                                 int64_t ps_d, int32_t dim, const void *q, int64_t ld_q) {
+  const bool packed = ps_h == 0 && ps_d == 0;
+  return (dtype == TM_DT_BF16 || dtype == TM_DT_F16) && packed && (dim == 64 || dim == 128 || dim == 256) &&
+         n > 0 && n < ((int64_t)1 << 31) / 32 && hidden >= 8 && hidden % 8 == 0 && ld_x >= hidden &&
+         ld_q >= dim && x && pv && bv && q && (pt == nullptr) == (bt == nullptr) && tm_aligned16(x) &&
+         (ld_x * 2) % 16 == 0 && tm_aligned16(pv) && tm_aligned16(bv) && (pt == nullptr || tm_aligned16(pt)) &&
+         (bt == nullptr || tm_aligned16(bt)) && tm_aligned16(q) && (ld_q * 2) % 16 == 0;
+}
+
+size_t tm_internal_project_cols_parts(int32_t dim) { return dim >= 64 ? (size_t)dim / 64 : 0; }
+
+int tm_internal_project_cols(int32_t dtype, const void *x, int64_t n, int32_t hidden, int64_t ld_x,
+                             const uint8_t *is_vision, const void *pv, const void *bv, const void *pt,
+                             const void *bt, int64_t ps_h, int64_t ps_d, int32_t dim, void *q, int64_t ld_q,
+                             float *qn_part, uint64_t *keys, const tm_route_args *ra, hipStream_t stream) {
+  TM_REQUIRE(tm_internal_project_cols_ok(dtype, x, n, hidden, ld_x, pv, bv, pt, bt, ps_h, ps_d, dim, q, ld_q) &&
+                 qn_part != nullptr,
+             TM_EINVAL_ARG, "tm_table_forward: projection shape not supported by the column-split kernel");
+  TM_REQUIRE(ra == nullptr || tm_internal_route_fusable(ra), TM_EINVAL_ARG,
+             "tm_table_forward: router shape cannot be fused");
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    if constexpr (DT != TM_DT_F32) {
+      switch (dim) {
+        case 64: launch_cols_route<DT, 64>(x, n, hidden, ld_x, is_vision, pv, bv, pt, bt, q, ld_q, qn_part, keys, ra, stream); break;
+        case 128: launch_cols_route<DT, 128>(x, n, hidden, ld_x, is_vision, pv, bv, pt, bt, q, ld_q, qn_part, keys, ra, stream); break;
+        default: launch_cols_route<DT, 256>(x, n, hidden, ld_x, is_vision, pv, bv, pt, bt, q, ld_q, qn_part, keys, ra, stream); break;
+      }
+      TM_LAUNCH_CHECK("tm_table_forward(project)");
     }
     return TM_OK;
   });

@@ -432,7 +432,7 @@ template <int DT, int DIM, int METRIC>
 __global__ __launch_bounds__(kThreads, 2) void search_top1_kernel(
     const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
     const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
-    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws) {
+    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws, uint64_t *__restrict__ keys) {
   using T = typename Elem<DT>::T;
   constexpr int KS = DIM / 16;
   constexpr int CH = DIM / 8;
@@ -629,7 +629,12 @@ __global__ __launch_bounds__(kThreads, 2) void search_top1_kernel(
     best.finalize();
     best.merge_xor(32);  // the two half-waves saw disjoint centroids of the same query
     const int64_t r = row_base + sl * 32 + (lane & 31);
-    if (lane < 32 && r < n) ws[split * n + r] = best.l[0];
+    if (lane < 32 && r < n) {
+      if (keys == nullptr)
+        ws[split * n + r] = best.l[0];
+      else if (best.l[0] != ~0ull)
+        atomicMin(reinterpret_cast<unsigned long long *>(keys + r), (unsigned long long)best.l[0]);
+    }
   }
 }
 
@@ -750,14 +755,9 @@ __device__ __forceinline__ void merge_min(uint64_t (&a)[K], const uint64_t (&b)[
 // Output of one query: key ~0 (no candidate) -> index -1 and the worst distance.
 template <int METRIC>
 __device__ __forceinline__ void write_hit(uint64_t key, float qn, float *dist, int64_t *idx) {
-  if (key == ~0ull) {
-    *idx = -1;
-    *dist = (METRIC == TM_METRIC_L2) ? __builtin_huge_valf() : -__builtin_huge_valf();
-  } else {
-    const float dp = tm_from_orderable((uint32_t)(key >> 32));
-    *idx = (int64_t)(uint32_t)key;
-    *dist = (METRIC == TM_METRIC_L2) ? fmaxf(qn + dp, 0.f) : -dp;
-  }
+  int64_t i;
+  *dist = tm_key_to_dist(key, qn, METRIC == TM_METRIC_L2, i);
+  *idx = i;
 }
 
 // 64-bit value of the lane `x` lanes away within a quad (x = 1 or 2), by DPP.
@@ -925,7 +925,7 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
   } else if (K == 1 && DIM <= 128 && ld_c * dma_rows(DIM) * (int64_t)sizeof(T) < ((int64_t)1 << 31)) {
     // (d = 256 would not fit two waves per SIMD; the stage byte offsets must fit 31 bits)
     hipLaunchKernelGGL((search_top1_kernel<DT, DIM < 256 ? DIM : 128, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
-                       block, 0, stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
+                       block, 0, stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws, nullptr);
   } else {
     hipLaunchKernelGGL((search_dma_kernel<DT, DIM, K, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
                        block, 0, stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
@@ -1039,4 +1039,60 @@ extern "C" int tm_search_global(int32_t dtype, const void *q, int64_t n_tokens, 
                                 size_t workspace_bytes, tm_stream_t stream) {
   return search_impl(dtype, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, dim, top_k, metric,
                      out_dist, out_idx, workspace, workspace_bytes, nullptr, tm_hip_stream(stream));
+}
+
+namespace {
+
+template <int DT, int DIM, int METRIC>
+void launch_search_keys(const void *q, int64_t n, int64_t ld_q, const void *cents, int64_t n_cent, int64_t ld_c,
+                        const float *c_sqnorm, uint64_t *keys, hipStream_t stream) {
+  using T = typename Elem<DT>::T;
+  const SplitPlan p = plan_split(n, n_cent, DIM, 1);
+  hipLaunchKernelGGL((search_top1_kernel<DT, DIM, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
+                     dim3(kThreads), 0, stream, static_cast<const T *>(q), n, ld_q, static_cast<const T *>(cents),
+                     n_cent, ld_c, c_sqnorm, p.chunk, nullptr, keys);
+}
+
+template <int DT, int METRIC>
+void search_keys_dim(int dim, const void *q, int64_t n, int64_t ld_q, const void *cents, int64_t n_cent,
+                     int64_t ld_c, const float *c_sqnorm, uint64_t *keys, hipStream_t stream) {
+  if (dim == 64)
+    launch_search_keys<DT, 64, METRIC>(q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
+  else
+    launch_search_keys<DT, 128, METRIC>(q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
+}
+
+}  // namespace
+
+bool tm_internal_search_keys_ok(int32_t dtype, int64_t n, int64_t n_cent, int64_t ld_c, int32_t dim,
+                                int32_t top_k) {
+  if (!(dtype == TM_DT_BF16 || dtype == TM_DT_F16) || top_k != 1 || !(dim == 64 || dim == 128)) return false;
+  if (n <= 0 || n >= ((int64_t)1 << 31) || n_cent <= 0 || n_cent >= (int64_t)0x7fffffff || ld_c < dim) return false;
+  if (plan_split(n, n_cent, dim, 1).stream) return false;
+  return ld_c * dma_rows(dim) * 2 < ((int64_t)1 << 31);
+}
+
+int tm_internal_search_keys(int32_t dtype, const void *q, int64_t n, int64_t ld_q, const void *cents,
+                            int64_t n_cent, int64_t ld_c, const float *c_sqnorm, int32_t dim, int32_t metric,
+                            uint64_t *keys, hipStream_t stream) {
+  TM_REQUIRE(tm_internal_search_keys_ok(dtype, n, n_cent, ld_c, dim, 1), TM_EINVAL_SHAPE,
+             "tm_table_forward: search shape not supported by the atomic top-1 path");
+  TM_REQUIRE(metric == TM_METRIC_L2 || metric == TM_METRIC_DOT, TM_EINVAL_ARG, "tm_table_forward: bad metric");
+  TM_REQUIRE(q && cents && keys && (metric != TM_METRIC_L2 || c_sqnorm), TM_EINVAL_ARG,
+             "tm_table_forward: null pointer");
+  TM_REQUIRE(ld_q >= dim && tm_aligned16(q) && tm_aligned16(cents) && (ld_q * 2) % 16 == 0 && (ld_c * 2) % 16 == 0,
+             TM_EINVAL_SHAPE, "tm_table_forward: q and centroid rows must be 16-byte aligned");
+  if (dtype == TM_DT_BF16) {
+    if (metric == TM_METRIC_L2)
+      search_keys_dim<TM_DT_BF16, TM_METRIC_L2>(dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
+    else
+      search_keys_dim<TM_DT_BF16, TM_METRIC_DOT>(dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
+  } else {
+    if (metric == TM_METRIC_L2)
+      search_keys_dim<TM_DT_F16, TM_METRIC_L2>(dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
+    else
+      search_keys_dim<TM_DT_F16, TM_METRIC_DOT>(dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
+  }
+  TM_LAUNCH_CHECK("tm_table_forward(search)");
+  return TM_OK;
 }

@@ -1,7 +1,7 @@
 // Selection kernels: keep-rate radix select (north-star kernel (3)), the
 // reference's keep masks (table_moe/skip/pruning.py) and surviving-weight
 // renormalisation.
-#include "tm_common.h"
+#include "tm_internal.h"
 
 namespace {
 
@@ -173,9 +173,30 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)tm_wave_incl_scan(v), 63);
 }
 
+// Optional source of the scores: packed top-1 search keys of the layer call
+// (see tm_key_to_dist) with the query norms as `parts` partial sums; the
+// kernel then also writes each token's distance, centroid and |q|^2.
+struct KeySrc {
+  const uint64_t *keys;  // null: scores come from `score`
+  const float *qn_part;  // [parts][n]
+  int parts;
+  int l2;
+  float *out_dist;
+  int64_t *out_idx;
+  float *out_qn;
+};
+
+// |q|^2 from the column-group partials in the order of a lane-pair tree over
+// the groups (the order a whole-row reduction across lanes adds them).
+__device__ __forceinline__ float qn_sum(float a0, float a1, float a2, float a3, int parts) {
+  if (parts == 1) return a0;
+  if (parts == 2) return a0 + a1;
+  return (a0 + a1) + (a2 + a3);
+}
+
 __global__ __launch_bounds__(kSelThreads) void keep_select_fast_kernel(const float *__restrict__ score, int64_t n,
                                                                        int64_t ld, int64_t n_keep,
-                                                                       uint8_t *__restrict__ out) {
+                                                                       uint8_t *__restrict__ out, KeySrc ks) {
   // One histogram per pass, all cleared up front while the keys load; every
   // LDS value that all threads need is read by one lane per wave and spread
   // with DPP (LDS instruction issue, not bandwidth, bounds this kernel).
@@ -189,6 +210,45 @@ __global__ __launch_bounds__(kSelThreads) void keep_select_fast_kernel(const flo
   const int64_t hi = (lo + per < n) ? lo + per : n;
   const int cnt = (int)(hi > lo ? hi - lo : 0);
 
+  float sc[kSelRegs];  // key source: this thread's distances
+  if (ks.keys != nullptr) {  // uniform
+    uint64_t kv[kSelRegs];
+    float qn[kSelRegs];
+    if (per == 4 && cnt == 4 && ks.parts <= 4 && (n & 3) == 0) {  // 16-byte loads (lo is a multiple of 4)
+      const uint4 k01 = *reinterpret_cast<const uint4 *>(ks.keys + lo);
+      const uint4 k23 = *reinterpret_cast<const uint4 *>(ks.keys + lo + 2);
+      kv[0] = ((uint64_t)k01.y << 32) | k01.x; kv[1] = ((uint64_t)k01.w << 32) | k01.z;
+      kv[2] = ((uint64_t)k23.y << 32) | k23.x; kv[3] = ((uint64_t)k23.w << 32) | k23.z;
+      float4 qp[4] = {};
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        if (p < ks.parts) qp[p] = *reinterpret_cast<const float4 *>(ks.qn_part + (int64_t)p * n + lo);
+      const float a[4][4] = {{qp[0].x, qp[0].y, qp[0].z, qp[0].w}, {qp[1].x, qp[1].y, qp[1].z, qp[1].w},
+                             {qp[2].x, qp[2].y, qp[2].z, qp[2].w}, {qp[3].x, qp[3].y, qp[3].z, qp[3].w}};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qn[j] = qn_sum(a[0][j], a[1][j], a[2][j], a[3][j], ks.parts);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kSelRegs; ++j)
+        if (j < cnt) {
+          kv[j] = ks.keys[lo + j];
+          float a[4];
+#pragma unroll
+          for (int p = 0; p < 4; ++p) a[p] = p < ks.parts ? ks.qn_part[(int64_t)p * n + lo + j] : 0.f;
+          qn[j] = qn_sum(a[0], a[1], a[2], a[3], ks.parts);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kSelRegs; ++j)
+      if (j < cnt) {
+        int64_t ix;
+        sc[j] = tm_key_to_dist(kv[j], qn[j], ks.l2 != 0, ix);
+        ks.out_dist[lo + j] = sc[j];
+        ks.out_idx[lo + j] = ix;
+        ks.out_qn[lo + j] = qn[j];
+      }
+  }
+
   if (n_keep <= 0 || n_keep >= n) {
     const uint8_t v = n_keep > 0 ? 1 : 0;
     for (int64_t i = lo; i < hi; ++i) out[i] = v;
@@ -196,7 +256,7 @@ __global__ __launch_bounds__(kSelThreads) void keep_select_fast_kernel(const flo
   }
   if (n <= 64) {  // uniform: one wave ranks the keys directly (no LDS, no barrier)
     if (wave == 0) {
-      const uint32_t key = lane < n ? tm_orderable(score[(int64_t)lane * ld]) : 0u;
+      const uint32_t key = lane < n ? tm_orderable(ks.keys ? sc[0] : score[(int64_t)lane * ld]) : 0u;
       uint32_t rank = 0;  // keys ahead of this one: larger, or equal at a lower index
       for (int j = 0; j < (int)n; ++j) {
         const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)key, j);
@@ -212,8 +272,11 @@ __global__ __launch_bounds__(kSelThreads) void keep_select_fast_kernel(const flo
     for (int i = 0; i < kFastPasses * kFastBins / 4 / kSelThreads; ++i) h4[tid + i * kSelThreads] = make_uint4(0, 0, 0, 0);
   }
   uint32_t keys[kSelRegs];
-  const bool vec4 = per == 4 && ld == 1 && (reinterpret_cast<uintptr_t>(score) & 15) == 0;  // uniform
-  if (vec4 && cnt == 4) {
+  const bool vec4 = per == 4 && (ks.keys != nullptr || (ld == 1 && (reinterpret_cast<uintptr_t>(score) & 15) == 0));  // uniform
+  if (ks.keys != nullptr) {
+#pragma unroll
+    for (int j = 0; j < kSelRegs; ++j) keys[j] = (j < cnt) ? tm_orderable(sc[j]) : 0u;
+  } else if (vec4 && cnt == 4) {
     const float4 f = *reinterpret_cast<const float4 *>(score + lo);
     keys[0] = tm_orderable(f.x); keys[1] = tm_orderable(f.y); keys[2] = tm_orderable(f.z); keys[3] = tm_orderable(f.w);
 #pragma unroll
@@ -462,7 +525,7 @@ extern "C" int tm_keep_select(const float *score, int64_t n, int64_t ld_score, i
   TM_REQUIRE(score && out_keep, TM_EINVAL_ARG, "tm_keep_select: null pointer");
   if (n <= (int64_t)kSelThreads * kSelRegs)
     hipLaunchKernelGGL(keep_select_fast_kernel, dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
-                       score, n, ld_score, n_keep, out_keep);
+                       score, n, ld_score, n_keep, out_keep, KeySrc{});
   else
     hipLaunchKernelGGL(keep_select_kernel, dim3(1), dim3(kSelThreads), 0, tm_hip_stream(stream),
                        score, n, ld_score, n_keep, out_keep);
@@ -538,4 +601,21 @@ extern "C" int tm_renormalize(int32_t dtype, const void *weights, int64_t ld_w, 
     TM_LAUNCH_CHECK("tm_renormalize");
     return TM_OK;
   });
+}
+
+bool tm_internal_keep_keys_ok(int64_t n) { return n > 0 && n <= (int64_t)kSelThreads * kSelRegs; }
+
+int tm_internal_keep_keys(const uint64_t *keys, const float *qn_part, int32_t parts, int32_t metric, int64_t n,
+                          int64_t n_keep, float *out_dist, int64_t *out_idx, float *out_qn, uint8_t *out_keep,
+                          hipStream_t stream) {
+  TM_REQUIRE(tm_internal_keep_keys_ok(n) && parts >= 1 && parts <= 4, TM_EINVAL_SHAPE,
+             "tm_table_forward: keep select from keys: bad sizes");
+  TM_REQUIRE(keys && qn_part && out_dist && out_idx && out_qn && out_keep && tm_aligned16(keys) &&
+                 tm_aligned16(qn_part),
+             TM_EINVAL_ARG, "tm_table_forward: keep select from keys: bad buffers");
+  const KeySrc ks{keys, qn_part, parts, metric == TM_METRIC_L2 ? 1 : 0, out_dist, out_idx, out_qn};
+  hipLaunchKernelGGL(keep_select_fast_kernel, dim3(1), dim3(kSelThreads), 0, stream, nullptr, n, (int64_t)1,
+                     n_keep, out_keep, ks);
+  TM_LAUNCH_CHECK("tm_table_forward(keep)");
+  return TM_OK;
 }

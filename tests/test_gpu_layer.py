@@ -445,6 +445,39 @@ def test_layer_forward_one_call_matches_staged(hip_device):
             assert torch.equal(ra[key], rb[key]), key
 
 
+@pytest.mark.parametrize("n,hidden,dim,mix", [(300, 1000, 128, False), (515, 2080, 64, True), (96, 264, 128, True),
+                                             (4096, 2048, 128, True)])
+def test_layer_forward_fused_shapes_match_staged(hip_device, n, hidden, dim, mix):
+    """Top-1 layer calls take the fused plan (column-split projection, search
+    merged by atomic minimum, keep select decoding the packed keys); the
+    result must equal the stage calls bit for bit.  Hidden sizes that end
+    inside a k-step or a 4-k-step chunk, d = 64, ragged row tiles, and
+    modality patterns that mix vision and text rows inside every tile."""
+    from table_moe.cache_engine import GlobalTable
+    from table_moe.synth import make_workload
+
+    dev = hip_device
+    wl = make_workload(2, n=n, hidden=hidden, dim=dim, n_cent=1024)
+    d = wl.to(dev)
+    is_vision = d.is_vision
+    if mix:
+        g = torch.Generator().manual_seed(n)
+        is_vision = (torch.rand(n, generator=g) < 0.5).to(dev)
+    a = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
+    b = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
+    ra = a.layer_forward(d.x, is_vision, d.logits, d.slot_out, d.residual, 8, 1, 0.6)
+    rb = b.layer_forward_staged(d.x, is_vision, d.logits, d.slot_out, d.residual, 8, 1, 0.6)
+    torch.cuda.synchronize()
+    for key in ("weights", "ids", "q", "qn", "dist", "idx", "keep", "out"):
+        assert torch.equal(ra[key], rb[key]), key
+    # and the projection against the oracle
+    q = np64(ra["q"])
+    ref_q = O.project_queries(np64(wl.x), is_vision.cpu().numpy(), (np64(wl.proj_vis), np64(wl.bias_vis)),
+                              (np64(wl.proj_txt), np64(wl.bias_txt)), False, O.BF16)
+    abssum = proj_abssum(np64(wl.x), is_vision.cpu().numpy(), np64(wl.proj_vis), np64(wl.proj_txt))
+    assert_projection_close(q, ref_q, abssum, torch.bfloat16, min_exact=0.95)
+
+
 def test_layer_graph_replays_match_eager(hip_device):
     """A captured tm_table_forward replays correctly: several replays with new
     inputs copied in and eager work in between, each checked against an eager
