@@ -6,7 +6,10 @@ cached expert outputs ``values_buffer`` live in device memory (HBM) instead of
 pinned host memory, so ``gather_values`` is a device gather (``tm_gather_rows``)
 and returns a device tensor; the reference's caller then calls ``.to(device)``,
 which is a no-op.  Reading the on-disk table (PCA + per-(expert, modality)
-``*_cache.pt`` files) is load-time work done with torch as in the reference.
+``*_cache.pt`` files) is load-time work done with torch as in the reference;
+a layer converted to the packed format (``table_file.py``: one file, the
+buffers' own layout) is loaded from it instead when present, with the same
+resulting buffers bit for bit.
 """
 
 from __future__ import annotations
@@ -17,6 +20,7 @@ import os
 import torch
 
 from .. import _native as N
+from . import table_file
 from .config import CacheConfig
 
 
@@ -32,38 +36,32 @@ def _resolve_cache_dtype():
     raise ValueError(f"Unsupported cache dtype: {dtype!r}")
 
 
-def _normalize_last_dim(x: torch.Tensor, eps: float) -> torch.Tensor:
-    """Key normalisation at load: fp32 norm and division, rounded back to the
-    keys' dtype; rows with norm <= eps become 0 (manager.py:24-31)."""
-    x32 = x.float()
-    norm = torch.linalg.vector_norm(x32, dim=-1, keepdim=True)
-    out = x32 / norm.clamp_min(eps)
-    out = torch.where(norm <= eps, torch.zeros_like(out), out)
-    return out.to(dtype=x.dtype)
-
-
-def _parse_cache_name(fname: str):
-    """``L{layer}_E{expert}_{modality}_cache.pt`` -> (expert, modality name)."""
-    parts = fname.replace(".pt", "").split("_")
-    return int(parts[1][1:]), parts[2]
+# key normalisation at load (manager.py:24-31) and the cache file name rule,
+# shared with the packed-format converter
+_normalize_last_dim = table_file.normalize_last_dim
+_parse_cache_name = table_file.parse_cache_name
 
 
 class HybridStorageManager:
-    def __init__(self, layer_idx, num_experts, hidden_dim, device="cuda:0"):
+    def __init__(self, layer_idx, num_experts, hidden_dim, device="cuda:0", use_packed: bool = True):
         self.layer_idx = layer_idx
         self.num_experts = num_experts
         self.hidden_dim = hidden_dim
         self.device = torch.device(device) if not isinstance(device, torch.device) else device
         self.dtype = _resolve_cache_dtype()
 
-        self.pca = self._load_pca()
-        shape = (num_experts, 2, CacheConfig.FIXED_K, CacheConfig.COMPRESSED_DIM)
-        self.keys_buffer = torch.zeros(shape, dtype=self.dtype, device=self.device)
-        self.raw_keys_buffer = torch.zeros(shape, dtype=self.dtype, device=self.device)
-        self.values_buffer = torch.zeros(
-            (num_experts, 2, CacheConfig.FIXED_K, hidden_dim), dtype=self.dtype, device=self.device
-        )
-        self._load_cache_data()
+        packed = table_file.packed_path(layer_idx)
+        if use_packed and os.path.exists(packed):
+            self._load_packed(packed)
+        else:
+            self.pca = self._load_pca()
+            shape = (num_experts, 2, CacheConfig.FIXED_K, CacheConfig.COMPRESSED_DIM)
+            self.keys_buffer = torch.zeros(shape, dtype=self.dtype, device=self.device)
+            self.raw_keys_buffer = torch.zeros(shape, dtype=self.dtype, device=self.device)
+            self.values_buffer = torch.zeros(
+                (num_experts, 2, CacheConfig.FIXED_K, hidden_dim), dtype=self.dtype, device=self.device
+            )
+            self._load_cache_data()
 
         self.enable_online = CacheConfig.ONLINE_MIN_LAYER_IDX <= layer_idx <= CacheConfig.ONLINE_MAX_LAYER_IDX
         self.online_ptr = 0
@@ -86,27 +84,47 @@ class HybridStorageManager:
             self.online_expert_ids = None
 
     # --------------------------------------------------------------- loading
+    def _pca_entry(self, data):
+        """{"mean", "proj"} -> projection and bias -mean @ proj in the model dtype
+        on the table's device (manager.py:157-181)."""
+        if data is None:
+            return {
+                "proj": torch.zeros((self.hidden_dim, CacheConfig.COMPRESSED_DIM), device=self.device,
+                                    dtype=self.dtype),
+                "bias": torch.zeros(CacheConfig.COMPRESSED_DIM, device=self.device, dtype=self.dtype),
+            }
+        mean = data["mean"].to(device=self.device, dtype=self.dtype)
+        proj = data["proj"].to(device=self.device, dtype=self.dtype)
+        return {"proj": proj, "bias": -torch.matmul(mean, proj)}
+
     def _load_pca(self):
         pca_dir = os.path.join(CacheConfig.PCA_DIR, f"layer_{self.layer_idx}")
         out = {}
         for mod in ("vision", "text"):
             path = os.path.join(pca_dir, f"L{self.layer_idx}_{mod}_pca.pt")
-            if os.path.exists(path):
-                data = torch.load(path, map_location=self.device, weights_only=True)
-                mean = data["mean"].to(device=self.device, dtype=self.dtype)
-                proj = data["proj"].to(device=self.device, dtype=self.dtype)
-                out[mod] = {"proj": proj, "bias": -torch.matmul(mean, proj)}
-            else:
-                out[mod] = {
-                    "proj": torch.zeros((self.hidden_dim, CacheConfig.COMPRESSED_DIM), device=self.device,
-                                        dtype=self.dtype),
-                    "bias": torch.zeros(CacheConfig.COMPRESSED_DIM, device=self.device, dtype=self.dtype),
-                }
+            data = torch.load(path, map_location=self.device, weights_only=True) if os.path.exists(path) else None
+            out[mod] = self._pca_entry(data)
         return out
+
+    def _load_packed(self, path):
+        """One packed file (table_file.py): bulk copies of the buffers."""
+        expect = {"num_experts": self.num_experts, "hidden": self.hidden_dim, "fixed_k": int(CacheConfig.FIXED_K),
+                  "dim": int(CacheConfig.COMPRESSED_DIM), "dtype": table_file._TORCH_TO_NAME[self.dtype],
+                  "layer": self.layer_idx}
+        data = table_file.load_layer(path, self.device, expect=expect)
+        self.raw_keys_buffer = data["keys"]
+        self.keys_buffer = data["keys_norm"]
+        self.values_buffer = data["values"]
+        self.pca = {}
+        for mod in ("vision", "text"):
+            entry = None
+            if f"pca_mean_{mod}" in data:
+                entry = {"mean": data[f"pca_mean_{mod}"], "proj": data[f"pca_proj_{mod}"]}
+            self.pca[mod] = self._pca_entry(entry)
 
     def _load_cache_data(self):
         layer_dir = os.path.join(CacheConfig.CACHE_DIR, f"layer_{self.layer_idx}")
-        for path in glob.glob(os.path.join(layer_dir, "*_cache.pt")):
+        for path in sorted(glob.glob(os.path.join(layer_dir, "*_cache.pt"))):
             try:
                 eid, mod = _parse_cache_name(os.path.basename(path))
                 mid = CacheConfig.MODALITY_MAP.get(mod, -1)
