@@ -59,3 +59,39 @@ __attribute__((visibility("hidden"))) int tm_internal_keep_keys(const uint64_t *
                                                                 int64_t n_keep, float *out_dist,
                                                                 int64_t *out_idx, float *out_qn,
                                                                 uint8_t *out_keep, hipStream_t stream);
+
+// Decode plan, search stage: the small-batch stream kernel (n <= 64) alone.
+// Split s writes the sorted top-k lists of its centroid range into
+// lists[(s * n + r) * list_len] and the best key of each query into
+// keys[(s % key_rep) * n + r] by atomic minimum (every replica reset to ~0
+// beforehand).  tm_internal_stream_nsplit gives the split count (0 when the
+// shape is not a stream shape); list_len is 1, 4 or 8 for top_k 1, 2..4, 5..8.
+__attribute__((visibility("hidden"))) int64_t tm_internal_stream_nsplit(int64_t n, int64_t n_cent, int32_t dim,
+                                                                        int32_t top_k);
+__attribute__((visibility("hidden"))) int tm_internal_search_stream(
+    int32_t dtype, const void *q, int64_t n, int64_t ld_q, const void *cents, int64_t n_cent, int64_t ld_c,
+    const float *c_sqnorm, int32_t dim, int32_t top_k, int32_t metric, uint64_t *lists, uint64_t *keys,
+    int32_t key_rep, hipStream_t stream);
+
+// Decode plan of tm_table_forward (n <= 64): three launches — split
+// projection (+ router, + key reset), stream search, and one finishing launch
+// that merges the lists, ranks the keep set and gathers/combines per (token,
+// row chunk).  With stage events, events 2 / 3 / 4 are recorded after the
+// projection / search / search (the keep select rides in the finishing
+// launch).  `cnt` holds one arrival counter per (16-row tile, 16-column
+// block): zero before the first call, left zero by every call.
+struct tm_decode_ws {
+  uint64_t *lists;  // search lists [nsplit][n][list_len]
+  uint64_t *keys;   // best keys [tm_internal_decode_keys(n)]
+  float *qn_blk;    // partial |q|^2 [n][dim / 16]
+  void *part;       // projection partials [tm_internal_decode_part_bytes]
+  uint32_t *cnt;    // arrival counters [ceil(n / 16) * dim / 16] (<= 64)
+};
+__attribute__((visibility("hidden"))) bool tm_internal_decode_ok(const tm_table_layer *t, const tm_layer_io *io);
+__attribute__((visibility("hidden"))) size_t tm_internal_decode_qn_floats(int64_t n, int32_t dim);
+__attribute__((visibility("hidden"))) size_t tm_internal_decode_keys(int64_t n);
+__attribute__((visibility("hidden"))) size_t tm_internal_decode_part_bytes(int64_t n, int32_t dim);
+__attribute__((visibility("hidden"))) int tm_internal_decode_forward(const tm_table_layer *t, const tm_layer_io *io,
+                                                                     const tm_decode_ws &w, const tm_route_args *ra,
+                                                                     int64_t n_keep, void *const *stage_events,
+                                                                     hipStream_t stream);

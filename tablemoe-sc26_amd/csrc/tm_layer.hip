@@ -8,24 +8,51 @@ constexpr size_t kAlign = 256;
 
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
-// Two plans share one workspace layout: the general one (tm_project,
-// tm_search_global, tm_keep_select as exported) and the fused top-1 one
-// (packed keys and partial query norms: column-split projection carrying the
-// router and the key reset, search merging by atomic minimum, keep select
-// decoding the keys), which needs no split-merge launch.
+// Three plans share one workspace layout: the general one (tm_project,
+// tm_search_global, tm_keep_select as exported), the fused top-1 one (packed
+// keys and partial query norms: column-split projection carrying the router
+// and the key reset, search merging by atomic minimum, keep select decoding
+// the keys), and the decode plan (n <= 64: split projection, stream search,
+// one finishing launch).  The first kSync bytes hold the decode plan's
+// arrival counters at the same offset for every n and plan: zero before the
+// first call on a workspace, and left zero by every call.
+constexpr size_t kSync = 256;
+
 struct WsLayout {
-  size_t project, search, keep, keys, qn_part, total;
+  size_t sync, project, search, keep, keys, qn_part, part, total;
 };
 
 WsLayout layout(const tm_table_layer *t, int64_t n, int32_t nn) {
   WsLayout w;
+  w.sync = kSync;
   w.project = align_up(tm_project_workspace_size(n, t->hidden, t->dim));
   w.search = align_up(tm_search_global_workspace_size(n, t->n_cent, t->dim, nn));
   w.keep = align_up(tm_keep_select_workspace_size(n));
-  w.keys = align_up((size_t)n * sizeof(uint64_t));
-  w.qn_part = align_up((size_t)n * 4 * sizeof(float));
-  w.total = w.project + w.search + w.keep + w.keys + w.qn_part;
+  const size_t nkeys = tm_internal_decode_keys(n);  // decode plan: replicated best keys
+  w.keys = align_up((nkeys > (size_t)n ? nkeys : (size_t)n) * sizeof(uint64_t));
+  const size_t qn_floats = tm_internal_decode_qn_floats(n, t->dim);  // decode plan: one partial per 16 columns
+  w.qn_part = align_up((qn_floats > (size_t)n * 4 ? qn_floats : (size_t)n * 4) * sizeof(float));
+  w.part = n <= 64 ? align_up(tm_internal_decode_part_bytes(n, t->dim)) : 0;
+  w.total = w.sync + w.project + w.search + w.keep + w.keys + w.qn_part + w.part;
   return w;
+}
+
+// Region offsets (the sync region first).
+struct WsPtrs {
+  char *project, *search, *keep, *keys, *qn_part, *part;
+  uint32_t *sync;
+};
+
+WsPtrs ptrs(const WsLayout &w, char *ws) {
+  WsPtrs p;
+  p.sync = reinterpret_cast<uint32_t *>(ws);
+  p.project = ws + w.sync;
+  p.search = p.project + w.project;
+  p.keep = p.search + w.search;
+  p.keys = p.keep + w.keep;
+  p.qn_part = p.keys + w.keys;
+  p.part = p.qn_part + w.qn_part;
+  return p;
 }
 
 bool fused_top1_ok(const tm_table_layer *t, const tm_layer_io *io) {
@@ -48,8 +75,9 @@ int record(void *const *events, int i, hipStream_t s) {
 int fused_top1_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout &w, char *ws,
                       const tm_route_args &ra, bool route_fused, int64_t n_keep, void *const *ev, hipStream_t s) {
   const int64_t n = io->n_tokens;
-  uint64_t *keys = reinterpret_cast<uint64_t *>(ws + w.project + w.search + w.keep);
-  float *qn_part = reinterpret_cast<float *>(ws + w.project + w.search + w.keep + w.keys);
+  const WsPtrs p = ptrs(w, ws);
+  uint64_t *keys = reinterpret_cast<uint64_t *>(p.keys);
+  float *qn_part = reinterpret_cast<float *>(p.qn_part);
   int st;
   if ((st = record(ev, 0, s)) != TM_OK) return st;
   if (!route_fused && (st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k,
@@ -69,6 +97,25 @@ int fused_top1_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLa
                                io->dist, io->idx, io->q_sqnorm, io->keep, s);
 }
 
+// Stages 0-4 of the decode plan (n <= 64): split projection (+ router, + key
+// reset), stream search, and the finishing launch that merges, ranks the keep
+// set and combines; events 3 and 4 coincide (the keep select rides in the
+// finishing launch), event 5 is recorded by the caller.
+int decode_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout &w, char *ws,
+                  const tm_route_args &ra, bool route_fused, int64_t n_keep, void *const *ev, hipStream_t s) {
+  const int64_t n = io->n_tokens;
+  const WsPtrs p = ptrs(w, ws);
+  const tm_decode_ws dw{reinterpret_cast<uint64_t *>(p.search), reinterpret_cast<uint64_t *>(p.keys),
+                        reinterpret_cast<float *>(p.qn_part), p.part, p.sync};
+  int st;
+  if ((st = record(ev, 0, s)) != TM_OK) return st;
+  if (!route_fused && (st = tm_topk_softmax(io->router_logits, n, io->n_experts, io->ld_logits, io->router_top_k,
+                                            0, io->weights, io->expert_ids, s)) != TM_OK)
+    return st;
+  if ((st = record(ev, 1, s)) != TM_OK) return st;
+  return tm_internal_decode_forward(t, io, dw, route_fused ? &ra : nullptr, n_keep, ev, s);
+}
+
 // Stages 0-4 of the general plan: the exported entry points; the router rides
 // in the search's split-merge launch when it can.
 int general_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout &w, char *ws,
@@ -80,22 +127,22 @@ int general_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayou
                                             0, io->weights, io->expert_ids, s)) != TM_OK)
     return st;
   if ((st = record(ev, 1, s)) != TM_OK) return st;
+  const WsPtrs p = ptrs(w, ws);
   if ((st = tm_project(t->dtype, io->x, n, t->hidden, io->ld_x, io->is_vision, t->proj_vis, t->bias_vis,
                        t->proj_txt, t->bias_txt, t->ps_h, t->ps_d, t->dim, 0, 1e-6f, io->q, t->dim, io->q_sqnorm,
-                       w.project ? ws : nullptr, w.project, s)) != TM_OK)
+                       w.project ? p.project : nullptr, w.project, s)) != TM_OK)
     return st;
   if ((st = record(ev, 2, s)) != TM_OK) return st;
   if (route_fused)
     st = tm_internal_search_route(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c,
-                                  t->c_sqnorm, t->dim, io->n_nearest, t->metric, io->dist, io->idx, ws + w.project,
+                                  t->c_sqnorm, t->dim, io->n_nearest, t->metric, io->dist, io->idx, p.search,
                                   w.search, &ra, s);
   else
     st = tm_search_global(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c, t->c_sqnorm,
-                          t->dim, io->n_nearest, t->metric, io->dist, io->idx, ws + w.project, w.search, s);
+                          t->dim, io->n_nearest, t->metric, io->dist, io->idx, p.search, w.search, s);
   if (st != TM_OK) return st;
   if ((st = record(ev, 3, s)) != TM_OK) return st;
-  return tm_keep_select(io->dist, n, io->n_nearest, n_keep, io->keep, w.keep ? ws + w.project + w.search : nullptr,
-                        w.keep, s);
+  return tm_keep_select(io->dist, n, io->n_nearest, n_keep, io->keep, w.keep ? p.keep : nullptr, w.keep, s);
 }
 
 }  // namespace
@@ -131,8 +178,13 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
                          io->expert_ids};
   const bool route_fused = stage_events == nullptr && tm_internal_route_fusable(&ra);
   const int64_t n_keep = tm_keep_count(n, io->keep_rate);
-  int st = fused_top1_ok(t, io) ? fused_top1_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s)
-                                : general_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s);
+  int st;
+  if (tm_internal_decode_ok(t, io)) {  // the finishing launch also combines
+    if ((st = decode_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s)) != TM_OK) return st;
+    return record(stage_events, 5, s);
+  }
+  st = fused_top1_ok(t, io) ? fused_top1_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s)
+                            : general_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s);
   if (st != TM_OK) return st;
   if ((st = record(stage_events, 4, s)) != TM_OK) return st;
   if ((st = tm_gather_combine(t->dtype, n, t->hidden, io->keep, io->slot_out, io->so_b, io->so_s, io->weights,

@@ -642,7 +642,8 @@ template <int DT, int DIM, int K, int QS, int METRIC>
 __global__ __launch_bounds__(kThreads) void search_stream_kernel(
     const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
     const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
-    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws) {
+    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws, uint64_t *__restrict__ keys,
+    int key_rep) {
   constexpr int KS = DIM / 16;
   __shared__ uint64_t merge_buf[4][QS * 32][K];
   const int tid = threadIdx.x;
@@ -730,6 +731,9 @@ __global__ __launch_bounds__(kThreads) void search_stream_kernel(
       uint64_t *dst = ws + (split * n + r) * K;
 #pragma unroll
       for (int j = 0; j < K; ++j) dst[j] = l[j];
+      // the query's best key over the splits of replica split % key_rep (reset to ~0 before the launch)
+      if (keys != nullptr)
+        atomicMin(reinterpret_cast<unsigned long long *>(keys + (split % key_rep) * n + r), (unsigned long long)l[0]);
     }
   }
 }
@@ -918,10 +922,10 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
   if (p.stream) {
     if (p.qs == 1)
       hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 1, METRIC>), dim3((unsigned)p.nsplit), block, 0, stream,
-                         Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
+                         Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws, nullptr, 1);
     else
       hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 2, METRIC>), dim3((unsigned)p.nsplit), block, 0, stream,
-                         Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws);
+                         Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws, nullptr, 1);
   } else if (K == 1 && DIM <= 128 && ld_c * dma_rows(DIM) * (int64_t)sizeof(T) < ((int64_t)1 << 31)) {
     // (d = 256 would not fit two waves per SIMD; the stage byte offsets must fit 31 bits)
     hipLaunchKernelGGL((search_top1_kernel<DT, DIM < 256 ? DIM : 128, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
@@ -1092,6 +1096,87 @@ int tm_internal_search_keys(int32_t dtype, const void *q, int64_t n, int64_t ld_
       search_keys_dim<TM_DT_F16, TM_METRIC_L2>(dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
     else
       search_keys_dim<TM_DT_F16, TM_METRIC_DOT>(dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
+  }
+  TM_LAUNCH_CHECK("tm_table_forward(search)");
+  return TM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Decode plan (internal): the stream kernel alone, writing its per-split
+// sorted lists into `lists` and each query's best key into keys[n] (reset to
+// ~0 beforehand); the consumer merges the lists itself.
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int DT, int DIM, int K, int METRIC>
+void launch_stream_keys(const SplitPlan &p, const void *q, int64_t n, int64_t ld_q, const void *cents,
+                        int64_t n_cent, int64_t ld_c, const float *c_sqnorm, uint64_t *lists, uint64_t *keys,
+                        int key_rep, hipStream_t stream) {
+  using T = typename Elem<DT>::T;
+  const T *Q = static_cast<const T *>(q);
+  const T *C = static_cast<const T *>(cents);
+  if (p.qs == 1)
+    hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 1, METRIC>), dim3((unsigned)p.nsplit), dim3(kThreads), 0,
+                       stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, lists, keys, key_rep);
+  else
+    hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 2, METRIC>), dim3((unsigned)p.nsplit), dim3(kThreads), 0,
+                       stream, Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, lists, keys, key_rep);
+}
+
+template <int DT, int METRIC, int K>
+void stream_keys_dim(const SplitPlan &p, int dim, const void *q, int64_t n, int64_t ld_q, const void *cents,
+                     int64_t n_cent, int64_t ld_c, const float *c_sqnorm, uint64_t *lists, uint64_t *keys,
+                     int key_rep, hipStream_t stream) {
+  switch (dim) {
+    case 64: launch_stream_keys<DT, 64, K, METRIC>(p, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream); break;
+    case 128: launch_stream_keys<DT, 128, K, METRIC>(p, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream); break;
+    default: launch_stream_keys<DT, 256, K, METRIC>(p, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream); break;
+  }
+}
+
+template <int DT, int METRIC>
+void stream_keys_k(const SplitPlan &p, int top_k, int dim, const void *q, int64_t n, int64_t ld_q,
+                   const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm, uint64_t *lists,
+                   uint64_t *keys, int key_rep, hipStream_t stream) {
+  switch (list_len(top_k)) {
+    case 1: stream_keys_dim<DT, METRIC, 1>(p, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream); break;
+    case 4: stream_keys_dim<DT, METRIC, 4>(p, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream); break;
+    default: stream_keys_dim<DT, METRIC, 8>(p, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream); break;
+  }
+}
+
+}  // namespace
+
+int64_t tm_internal_stream_nsplit(int64_t n, int64_t n_cent, int32_t dim, int32_t top_k) {
+  if (n <= 0 || n > 64 || n_cent <= 0 || !(dim == 64 || dim == 128 || dim == 256)) return 0;
+  return plan_split(n, n_cent, dim, top_k).nsplit;
+}
+
+int tm_internal_search_stream(int32_t dtype, const void *q, int64_t n, int64_t ld_q, const void *cents,
+                              int64_t n_cent, int64_t ld_c, const float *c_sqnorm, int32_t dim, int32_t top_k,
+                              int32_t metric, uint64_t *lists, uint64_t *keys, int32_t key_rep,
+                              hipStream_t stream) {
+  TM_REQUIRE(key_rep >= 1, TM_EINVAL_ARG, "tm_table_forward: key_rep < 1");
+  TM_REQUIRE(tm_internal_stream_nsplit(n, n_cent, dim, top_k) > 0 && top_k >= 1 && top_k <= 8 &&
+                 n_cent < (int64_t)0x7fffffff && ld_c >= dim && ld_q >= dim,
+             TM_EINVAL_SHAPE, "tm_table_forward: search shape not supported by the decode plan");
+  TM_REQUIRE(metric == TM_METRIC_L2 || metric == TM_METRIC_DOT, TM_EINVAL_ARG, "tm_table_forward: bad metric");
+  TM_REQUIRE(dtype == TM_DT_BF16 || dtype == TM_DT_F16, TM_EINVAL_DTYPE, "tm_table_forward: dtype must be F16 or BF16");
+  TM_REQUIRE(q && cents && lists && keys && (metric != TM_METRIC_L2 || c_sqnorm), TM_EINVAL_ARG,
+             "tm_table_forward: null pointer");
+  TM_REQUIRE(tm_aligned16(q) && tm_aligned16(cents) && (ld_q * 2) % 16 == 0 && (ld_c * 2) % 16 == 0,
+             TM_EINVAL_SHAPE, "tm_table_forward: q and centroid rows must be 16-byte aligned");
+  const SplitPlan p = plan_split(n, n_cent, dim, top_k);
+  if (dtype == TM_DT_BF16) {
+    if (metric == TM_METRIC_L2)
+      stream_keys_k<TM_DT_BF16, TM_METRIC_L2>(p, top_k, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream);
+    else
+      stream_keys_k<TM_DT_BF16, TM_METRIC_DOT>(p, top_k, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream);
+  } else {
+    if (metric == TM_METRIC_L2)
+      stream_keys_k<TM_DT_F16, TM_METRIC_L2>(p, top_k, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream);
+    else
+      stream_keys_k<TM_DT_F16, TM_METRIC_DOT>(p, top_k, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, lists, keys, key_rep, stream);
   }
   TM_LAUNCH_CHECK("tm_table_forward(search)");
   return TM_OK;

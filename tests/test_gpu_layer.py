@@ -424,6 +424,34 @@ def test_layer_forward_config2_end_to_end(hip_device):
     assert_bf16_output(np64(res["out"]), exact, abssum)
 
 
+def check_decode_plan_stagewise(b, ra, d, is_vision, residual, wl, nn, keep_rate=0.6):
+    """A decode-plan layer call (n <= 64) against the stage calls run on the
+    layer's own queries: the projection reduces across workgroups in its own
+    fp32 order, so q may differ from tm_project's in the last bit; given the
+    same q and |q|^2, search, keep and combine must agree bit for bit.  q is
+    checked against the oracle and |q|^2 against the exact sum of squares."""
+    n = d.x.shape[0]
+    topk = d.cfg["router_top_k"]
+    w, ids = b.route(d.logits, topk)
+    assert torch.equal(ra["weights"], w) and torch.equal(ra["ids"], ids)
+    dist, idx = b.search(ra["q"], nn, ra["qn"])
+    assert torch.equal(ra["dist"], dist) and torch.equal(ra["idx"], idx)
+    keep = b.keep_select(dist[:, 0], b.keep_count(n, keep_rate))
+    assert torch.equal(ra["keep"], keep)
+    out = b.gather_combine(keep, d.slot_out, w, idx, dist, residual)
+    torch.cuda.synchronize()
+    assert torch.equal(ra["out"], out)
+    dt = d.x.dtype
+    q = np64(ra["q"])
+    isv = is_vision.cpu().numpy()
+    ref_q = O.project_queries(np64(wl.x), isv, (np64(wl.proj_vis), np64(wl.bias_vis)),
+                              (np64(wl.proj_txt), np64(wl.bias_txt)), False, ODT[dt])
+    abssum = proj_abssum(np64(wl.x), isv, np64(wl.proj_vis), np64(wl.proj_txt))
+    assert_projection_close(q, ref_q, abssum, dt, min_exact=0.95)
+    qn_exact = (q * q).sum(axis=1)
+    np.testing.assert_allclose(np64(ra["qn"]), qn_exact, rtol=2e-6, atol=1e-6)
+
+
 def test_layer_forward_one_call_matches_staged(hip_device):
     """tm_table_forward (one call, router fused into the projection launch for
     64/128 experts) and the five stage calls give identical bits; config 5
@@ -434,11 +462,15 @@ def test_layer_forward_one_call_matches_staged(hip_device):
 
     dev = hip_device
     for cfg, n, nn in ((2, 1000, 1), (3, 32, 4), (5, 77, 1)):
-        d = make_workload(cfg, n=n).to(dev)
+        wl = make_workload(cfg, n=n)
+        d = wl.to(dev)
         a = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
         b = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
         topk = d.cfg["router_top_k"]
         ra = a.layer_forward(d.x, d.is_vision, d.logits, d.slot_out, d.residual, topk, nn, 0.6)
+        if n <= 64:  # decode plan
+            check_decode_plan_stagewise(b, ra, d, d.is_vision, d.residual, wl, nn)
+            continue
         rb = b.layer_forward_staged(d.x, d.is_vision, d.logits, d.slot_out, d.residual, topk, nn, 0.6)
         torch.cuda.synchronize()
         for key in ("weights", "ids", "q", "qn", "dist", "idx", "keep", "out"):
@@ -478,20 +510,100 @@ def test_layer_forward_fused_shapes_match_staged(hip_device, n, hidden, dim, mix
     assert_projection_close(q, ref_q, abssum, torch.bfloat16, min_exact=0.95)
 
 
-def test_layer_graph_replays_match_eager(hip_device):
-    """A captured tm_table_forward replays correctly: several replays with new
-    inputs copied in and eager work in between, each checked against an eager
-    call on the same inputs."""
+@pytest.mark.parametrize("cfg,n,hidden,dim,n_cent,nn,variant", [
+    (3, 1, 2048, 128, 16384, 4, "base"), (3, 8, 2048, 128, 16384, 4, "base"), (3, 32, 2048, 128, 16384, 1, "base"),
+    (3, 64, 1000, 64, 1024, 4, "mix"), (5, 33, 2560, 256, 20000, 4, "mix"), (3, 17, 264, 128, 300, 1, "mix"),
+    (3, 40, 2048, 128, 4096, 4, "nores"), (3, 24, 1504, 128, 2048, 4, "fp16"), (3, 64, 2048, 128, 16384, 4, "base")])
+def test_layer_forward_decode_plan_matches_staged(hip_device, cfg, n, hidden, dim, n_cent, nn, variant):
+    """Batches of at most 64 tokens take the decode plan (split projection
+    reduced by the last workgroup to arrive, stream search with replicated
+    atomic best keys, one finishing launch that merges, ranks and combines),
+    checked stage by stage (check_decode_plan_stagewise).  Covers d =
+    64/128/256, hidden sizes that end inside a k-step or split unevenly over
+    the slices, 1 to 64 tokens, top-1 and top-4, 64/128 experts, up to 157
+    search splits, modality patterns mixed inside the 16-row tiles, no
+    residual, and fp16; each case runs twice on one workspace (the arrival
+    counters must be left at zero)."""
     from table_moe.cache_engine import GlobalTable
     from table_moe.synth import make_workload
 
     dev = hip_device
-    d = make_workload(2, n=768).to(dev)
+    dtype = torch.float16 if variant == "fp16" else None
+    wl = make_workload(cfg, n=n, hidden=hidden, dim=dim, n_cent=n_cent, dtype=dtype, bias_scale=0.3)
+    d = wl.to(dev)
+    is_vision = d.is_vision
+    if variant == "mix":
+        g = torch.Generator().manual_seed(n)
+        is_vision = (torch.rand(n, generator=g) < 0.5).to(dev)
+    residual = None if variant == "nores" else d.residual
+    a = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
+    b = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
+    topk = d.cfg["router_top_k"]
+    for rep in range(2):
+        ra = a.layer_forward(d.x, is_vision, d.logits, d.slot_out, residual, topk, nn, 0.6)
+        torch.cuda.synchronize()
+        if rep == 0:
+            first = {k: v.clone() for k, v in ra.items()}
+        else:
+            for key, v in first.items():
+                assert torch.equal(ra[key], v), ("second call", key)
+    check_decode_plan_stagewise(b, ra, d, is_vision, residual, wl, nn)
+    assert int(ra["keep"].sum()) == O.keep_count(n, 0.6)
+
+
+def test_layer_forward_config3_decode_end_to_end(hip_device):
+    """Config 3 (decode, N=32 text tokens, C=16384, top-4 inverse-distance
+    blend) through the one-call layer, checked stage by stage against the
+    oracle: projection, top-4 lists on the device's queries, the keep set on
+    the device's distances, and the combined rows."""
+    from table_moe.cache_engine import GlobalTable
+    from table_moe.synth import make_workload
+
+    wl = make_workload(3)
+    d = wl.to(hip_device)
+    tbl = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
+    res = tbl.layer_forward(d.x, d.is_vision, d.logits, d.slot_out, d.residual, router_top_k=8, n_nearest=4,
+                            keep_rate=0.6)
+    torch.cuda.synchronize()
+    ww, wids, p = O.topk_softmax(np64(wl.logits), 8)
+    check_topk_rows(p, np64(res["ids"]), wids, True, "router")
+    q = np64(res["q"])
+    ref_q = O.project_queries(np64(wl.x), wl.is_vision.numpy(), (np64(wl.proj_vis), np64(wl.bias_vis)),
+                              (np64(wl.proj_txt), np64(wl.bias_txt)), False, O.BF16)
+    abssum = proj_abssum(np64(wl.x), wl.is_vision.numpy(), np64(wl.proj_vis), np64(wl.proj_txt))
+    assert_projection_close(q, ref_q, abssum, torch.bfloat16, min_exact=0.95)
+    vals, want_idx, exact = O.global_search(q, np64(wl.centroids), 4)
+    gi = np64(res["idx"])
+    check_topk_rows(exact, gi, want_idx, False, "search")
+    gd = np64(res["dist"])
+    np.testing.assert_allclose(gd, exact[np.arange(32)[:, None], gi], rtol=1e-5, atol=1e-3)
+    keep = np64(res["keep"])
+    assert keep.sum() == O.keep_count(32, 0.6) == 19
+    np.testing.assert_array_equal(keep, O.keep_select(gd[:, 0].astype(np.float32).astype(np.float64), 19))
+    exact = O.gather_combine(keep, np64(wl.slot_out), np64(res["weights"]), np64(wl.values), gi, gd,
+                             np64(wl.residual), O.F32)
+    abssum = O.gather_combine(keep, np.abs(np64(wl.slot_out)), np64(res["weights"]), np.abs(np64(wl.values)), gi,
+                              gd, np.abs(np64(wl.residual)), O.F32)
+    assert_bf16_output(np64(res["out"]), exact, abssum)
+
+
+@pytest.mark.parametrize("cfg,n,nn", [(2, 768, 1), (3, 32, 4)])
+def test_layer_graph_replays_match_eager(hip_device, cfg, n, nn):
+    """A captured tm_table_forward replays correctly: several replays with new
+    inputs copied in and eager work in between, each checked against an eager
+    call on the same inputs (the fused top-1 plan, and the decode plan whose
+    arrival counters persist from replay to replay)."""
+    from table_moe.cache_engine import GlobalTable
+    from table_moe.synth import make_workload
+
+    dev = hip_device
+    d = make_workload(cfg, n=n).to(dev)
     tg = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
     te = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
     x = d.x.clone()
     logits = d.logits.clone()
-    args = lambda xx, ll: (xx, d.is_vision, ll, d.slot_out, d.residual, 8, 1, 0.6)  # noqa: E731
+    topk = d.cfg["router_top_k"]
+    args = lambda xx, ll: (xx, d.is_vision, ll, d.slot_out, d.residual, topk, nn, 0.6)  # noqa: E731
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -503,7 +615,7 @@ def test_layer_graph_replays_match_eager(hip_device):
     gen = torch.Generator(device=dev).manual_seed(5)
     for rep in range(4):
         if rep:
-            x.copy_(d.x[torch.randperm(768, device=dev, generator=gen)])
+            x.copy_(d.x[torch.randperm(n, device=dev, generator=gen)])
             logits.copy_(torch.randn(logits.shape, device=dev, generator=gen))
         g.replay()
         ref = te.layer_forward(*args(x, logits))
