@@ -35,7 +35,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kQS = 2;      // query slabs per wave in the tile kernel
 constexpr int kTileRows = 4 * kQS * 32;
-constexpr int kStreamBlocksPerWave = 1;
+constexpr int kStreamChunk = 128;  // centroids per split of the stream kernel (one 32-block per wave)
 
 struct SplitPlan {
   bool stream;  // small-n shape
@@ -59,7 +59,7 @@ SplitPlan plan_split(int64_t n, int64_t c, int dim, int top_k) {
   if (p.stream) {
     p.qs = n <= 32 ? 1 : 2;
     p.row_blocks = 1;
-    p.chunk = 4 * 32 * kStreamBlocksPerWave;  // each wave: kStreamBlocksPerWave blocks of 32
+    p.chunk = kStreamChunk;
     p.nsplit = tm_cdiv(c, p.chunk);
     return p;
   }
@@ -638,106 +638,6 @@ __global__ __launch_bounds__(kThreads, 2) void search_top1_kernel(
   }
 }
 
-template <int DT, int DIM, int K, int QS, int METRIC>
-__global__ __launch_bounds__(kThreads) void search_stream_kernel(
-    const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
-    const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
-    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws, uint64_t *__restrict__ keys,
-    int key_rep) {
-  constexpr int KS = DIM / 16;
-  __shared__ uint64_t merge_buf[4][QS * 32][K];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int64_t split = blockIdx.x;
-  const int64_t c_begin = split * chunk;
-  const int64_t c_end = (c_begin + chunk < n_cent) ? c_begin + chunk : n_cent;
-
-  uint4 qf[QS][KS];
-#pragma unroll
-  for (int sl = 0; sl < QS; ++sl) {
-    const int64_t r = sl * 32 + (lane & 31);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qf[sl][ks] = make_uint4(0, 0, 0, 0);
-      if (r < n) qf[sl][ks] = *reinterpret_cast<const uint4 *>(q + r * ld_q + ks * 16 + 8 * (lane >> 5));
-    }
-  }
-  Best<K> best[QS];
-#pragma unroll
-  for (int sl = 0; sl < QS; ++sl) best[sl].init();
-
-  // this wave's 32-centroid blocks: c_begin + 32*(wave + 4*j)
-  uint4 af[KS];
-  float pen[16];
-  auto fetch = [&](int64_t c0) {
-    const int64_t c = c0 + (lane & 31);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      af[ks] = make_uint4(0, 0, 0, 0);
-      if (c < c_end) af[ks] = *reinterpret_cast<const uint4 *>(cents + c * ld_c + ks * 16 + 8 * (lane >> 5));
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t cm = c0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-      pen[i] = (cm < c_end) ? ((METRIC == TM_METRIC_L2) ? c_sqnorm[cm] : 0.f) : __builtin_huge_valf();
-    }
-  };
-  int64_t c0 = c_begin + 32 * wave;
-  if (c0 < c_end) fetch(c0);
-  while (c0 < c_end) {
-    uint4 a[KS];
-    float p[16];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) a[ks] = af[ks];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = pen[i];
-    const int64_t next = c0 + 128;
-    if (next < c_end) fetch(next);
-    tm_f32x16 acc[QS];
-#pragma unroll
-    for (int sl = 0; sl < QS; ++sl) acc[sl] = tm_f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int sl = 0; sl < QS; ++sl) acc[sl] = tm_mfma32x32x16<DT>(a[ks], qf[sl][ks], acc[sl]);
-#pragma unroll
-    for (int sl = 0; sl < QS; ++sl) block_epilogue<K, METRIC>(acc[sl], p, (int)c0, lane, best[sl]);
-    c0 = next;
-  }
-#pragma unroll
-  for (int sl = 0; sl < QS; ++sl) {
-    best[sl].finalize();
-    best[sl].merge_xor(32);
-    if (lane < 32) {
-#pragma unroll
-      for (int j = 0; j < K; ++j) merge_buf[wave][sl * 32 + lane][j] = best[sl].l[j];
-    }
-  }
-  __syncthreads();
-  // waves saw disjoint centroid blocks of the same queries: merge through LDS
-  if (tid < QS * 32) {
-    const int r = tid;
-    uint64_t l[K];
-#pragma unroll
-    for (int j = 0; j < K; ++j) l[j] = merge_buf[0][r][j];
-    for (int w = 1; w < 4; ++w)
-#pragma unroll
-      for (int j = 0; j < K; ++j) {
-        const uint64_t o = merge_buf[w][r][j];
-        if (o < l[K - 1]) list_insert<K>(l, o);
-      }
-    if (r < n) {
-      uint64_t *dst = ws + (split * n + r) * K;
-#pragma unroll
-      for (int j = 0; j < K; ++j) dst[j] = l[j];
-      // the query's best key over the splits of replica split % key_rep (reset to ~0 before the launch)
-      if (keys != nullptr)
-        atomicMin(reinterpret_cast<unsigned long long *>(keys + (split % key_rep) * n + r), (unsigned long long)l[0]);
-    }
-  }
-}
-
 // The K smallest of two ascending K-lists, ascending: min(a[i], b[K-1-i]) is
 // bitonic and holds exactly the K smallest; a half-cleaner cascade sorts it.
 template <int K>
@@ -754,6 +654,119 @@ __device__ __forceinline__ void merge_min(uint64_t (&a)[K], const uint64_t (&b)[
         a[i] = lo;
         a[i + d] = hi;
       }
+}
+
+// Stream kernel (n <= 64): wave w of split s owns the 32-centroid block
+// s * kStreamChunk + 32 w and every query (QS slabs of 32).  All operand loads
+// are unconditional and issued together: query rows past n re-read row n - 1
+// (their lists are never written), centroid rows past the table re-read its
+// last row, and positions past the split's range carry an infinite penalty,
+// which makes no candidate (key ~0).  The per-lane running lists take every
+// candidate through a branch-free compare-swap chain; the two lanes of a
+// query (l, l ^ 32) and then the four waves (through LDS, entry-major so the
+// reads are conflict-free) are merged with the bitonic min-merge.
+template <int DT, int DIM, int K, int QS, int METRIC>
+__global__ __launch_bounds__(kThreads) void search_stream_kernel(
+    const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
+    const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
+    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ ws, uint64_t *__restrict__ keys,
+    int key_rep) {
+  constexpr int KS = DIM / 16;
+  __shared__ uint64_t merge_buf[4][K][QS * 32];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t split = blockIdx.x;
+  const int64_t c_begin = split * chunk;
+  const int64_t c_end = (c_begin + chunk < n_cent) ? c_begin + chunk : n_cent;
+  const int64_t c0 = c_begin + 32 * wave;
+
+  uint4 qf[QS][KS];
+#pragma unroll
+  for (int sl = 0; sl < QS; ++sl) {
+    const int64_t r = sl * 32 + (lane & 31);
+    const int64_t rr = r < n ? r : n - 1;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[sl][ks] = *reinterpret_cast<const uint4 *>(q + rr * ld_q + ks * 16 + 8 * (lane >> 5));
+  }
+  uint4 af[KS];
+  {
+    const int64_t cr = c0 + (lane & 31);
+    const int64_t crr = cr < n_cent ? cr : n_cent - 1;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      af[ks] = *reinterpret_cast<const uint4 *>(cents + crr * ld_c + ks * 16 + 8 * (lane >> 5));
+  }
+  float pen[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t cm = c0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    pen[i] = (METRIC == TM_METRIC_L2) ? c_sqnorm[cm < n_cent ? cm : n_cent - 1] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t cm = c0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    pen[i] = cm < c_end ? pen[i] : __builtin_huge_valf();
+  }
+
+  tm_f32x16 acc[QS];
+#pragma unroll
+  for (int sl = 0; sl < QS; ++sl) acc[sl] = tm_f32x16{};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int sl = 0; sl < QS; ++sl) acc[sl] = tm_mfma32x32x16<DT>(af[ks], qf[sl][ks], acc[sl]);
+
+#pragma unroll
+  for (int sl = 0; sl < QS; ++sl) {
+    uint64_t l[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) l[j] = ~0ull;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = (int)c0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+      const float dp = (METRIC == TM_METRIC_L2) ? fmaf(-2.f, acc[sl][i], pen[i]) : (pen[i] - acc[sl][i]);
+      uint64_t x = dp == __builtin_huge_valf() ? ~0ull : make_key(dp, c);
+#pragma unroll
+      for (int j = 0; j < K; ++j) {  // compare-swap chain (no branch)
+        const uint64_t lo = l[j] < x ? l[j] : x;
+        x = l[j] < x ? x : l[j];
+        l[j] = lo;
+      }
+    }
+    uint64_t o[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) o[j] = __shfl_xor(l[j], 32, 64);
+    merge_min<K>(l, o);
+    if (lane < 32) {
+#pragma unroll
+      for (int j = 0; j < K; ++j) merge_buf[wave][j][sl * 32 + lane] = l[j];
+    }
+  }
+  __syncthreads();
+  // waves saw disjoint centroid blocks of the same queries: merge through LDS
+  if (tid < QS * 32) {
+    const int r = tid;
+    uint64_t l[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) l[j] = merge_buf[0][j][r];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      uint64_t o[K];
+#pragma unroll
+      for (int j = 0; j < K; ++j) o[j] = merge_buf[w][j][r];
+      merge_min<K>(l, o);
+    }
+    if (r < n) {
+      uint64_t *dst = ws + (split * n + r) * K;
+#pragma unroll
+      for (int j = 0; j < K; ++j) dst[j] = l[j];
+      // the query's best key over the splits of replica split % key_rep (reset to ~0 before the launch)
+      if (keys != nullptr)
+        atomicMin(reinterpret_cast<unsigned long long *>(keys + (split % key_rep) * n + r), (unsigned long long)l[0]);
+    }
+  }
 }
 
 // Output of one query: key ~0 (no candidate) -> index -1 and the worst distance.
