@@ -317,6 +317,49 @@ int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden, const uin
                       int64_t ld_o, tm_stream_t stream);
 
 /* ======================================================================
+ * Recompute path -- the SwiGLU expert MLP of the slots that are recomputed.
+ * tm_expert_swiglu replaces fused_moe_ffn_fp16_into
+ * (table_moe/ops/csrc/fp16_fused_expert/fp16_fused_moe_mlp.cu:107-274,
+ * called by maybe_run_fp16_fused_expert, table_moe/ops/fp16_fused_expert.py:
+ * 223-257) for one expert and any row count; tm_group_slots +
+ * tm_grouped_swiglu replace the per-expert loop of
+ * models/qwen3_vl_moe/cached_layers.py:431-437 (index_select the expert's
+ * tokens, run the expert, scatter into collected[token, slot]).
+ * Per row: g = dtype(x W1^T), f = dtype(silu(g) * (x W3^T)) (the up
+ * projection unrounded, silu in fp32: the SiLU-mul epilogue of
+ * fp16_epilogue_utils.h:51-125), y = dtype(f W2^T).  fp32 accumulation on
+ * bf16/fp16 matrix cores.  Weights as nn.Linear stores them: W1, W3
+ * [n_experts, inter, hidden], W2 [n_experts, hidden, inter], contiguous.
+ * hidden and inter must be multiples of 128.  Workspace: the [rows, inter]
+ * intermediate (tm_swiglu_workspace_size).
+ * ====================================================================== */
+size_t tm_swiglu_workspace_size(int64_t max_rows, int32_t inter, int32_t dtype);
+int tm_expert_swiglu(int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
+                     const void *w1, const void *w3, const void *w2, int32_t inter, void *out, int64_t ld_out,
+                     void *workspace, size_t workspace_bytes, tm_stream_t stream);
+/* Buckets the recomputed (token, slot) pairs by expert, on the device (no
+ * host sync): pair (b, s) is recomputed when mask[b*ms_b + s*ms_s] != 0
+ * (ms_s = 0: a per-token flag) and 0 <= ids[b*ld_ids + s] < n_experts.
+ * Writes expert_offsets [n_experts + 1], one row per pair (row_token = b,
+ * row_out = b*so_b + s*so_s: the element offset of its output row), and
+ * tiles [2 + 2*tm_group_slots_tiles(n_tokens*top_k, n_experts)]: row count,
+ * tile count, then each 128-row tile's expert and first row.  The order of
+ * rows inside an expert is unspecified; results do not depend on it. */
+int64_t tm_group_slots_tiles(int64_t max_rows, int32_t n_experts);
+int tm_group_slots(const int64_t *ids, int64_t n_tokens, int32_t top_k, int64_t ld_ids, const uint8_t *mask,
+                   int64_t ms_b, int64_t ms_s, int32_t n_experts, int64_t so_b, int64_t so_s,
+                   int32_t *expert_offsets, int32_t *row_token, int64_t *row_out, int32_t *tiles,
+                   tm_stream_t stream);
+/* The MLP of every grouped row: row r (expert e by expert_offsets) reads
+ * x[row_token[r]] and writes out[row_out[r] .. + hidden).  max_rows bounds
+ * the row count (n_tokens * top_k of the tm_group_slots call). */
+int tm_grouped_swiglu(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden, int32_t inter,
+                      int32_t n_experts, const void *w1, const void *w3, const void *w2, int64_t max_rows,
+                      const int32_t *expert_offsets, const int32_t *row_token, const int64_t *row_out,
+                      const int32_t *tiles, void *out, void *workspace, size_t workspace_bytes,
+                      tm_stream_t stream);
+
+/* ======================================================================
  * Mode G -- one MoE layer of the table path in ONE call.
  * Enqueues, back to back on `stream`: tm_topk_softmax (router) ->
  * tm_project -> tm_search_global -> tm_keep_select (n_keep =

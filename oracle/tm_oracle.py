@@ -44,6 +44,11 @@ global_search                  brute force sort of all distances, closed form
                                (centroid queries map to themselves)
 keep_select                    brute force sort; invariants
 gather_combine                 closed form on one-hot tables
+swiglu_expert                  torch.nn.functional.silu + matmul (library
+                               routines) and one-hot weights, where the output
+                               is silu(x_a) * x_b through scalar math.exp
+grouped_swiglu                 per-expert swiglu_expert on the pairs of each
+                               expert (brute-force regrouping)
 =============================  =================================================
 """
 
@@ -581,3 +586,42 @@ def layer_forward_g_fp32(x, is_vision, pca_vis, pca_txt, cents, values, logits, 
 
 
 __all__ = [name for name in dir() if not name.startswith("_")]
+
+
+# ---------------------------------------------------------------------------
+# recompute path: the SwiGLU expert MLP
+# ---------------------------------------------------------------------------
+def silu(v):
+    """x * sigmoid(x) = x / (1 + exp(-x)), float64."""
+    v = np.asarray(v, dtype=np.float64)
+    return v / (1.0 + np.exp(-v))
+
+
+def swiglu_expert(x, w1, w3, w2, dt: str = BF16):
+    """One expert's MLP with the rounding points of the reference's fused
+    kernel (ops/csrc/fp16_fused_expert/fp16_fused_moe_mlp.cu:107-274 and the
+    SiLU-mul epilogue fp16_epilogue_utils.h:51-125): g = dt(x W1^T),
+    f = dt(silu(g) * (x W3^T)) with the up projection unrounded,
+    y = dt(f W2^T).  Exact float64 sums of exact products."""
+    x = np.asarray(x, dtype=np.float64)
+    g = round_to(x @ np.asarray(w1, dtype=np.float64).T, dt)
+    u = x @ np.asarray(w3, dtype=np.float64).T
+    f = round_to(silu(g) * u, dt)
+    return round_to(f @ np.asarray(w2, dtype=np.float64).T, dt), f
+
+
+def grouped_swiglu(x, ids, mask, w1, w3, w2, dt: str = BF16):
+    """slot outputs [N, k, H] of every (token, slot) pair with mask set (a
+    per-token [N] mask applies to all k slots); other slots are NaN."""
+    x = np.asarray(x, dtype=np.float64)
+    ids = np.asarray(ids, dtype=np.int64)
+    n, k = ids.shape
+    m = np.asarray(mask, dtype=bool)
+    if m.ndim == 1:
+        m = np.repeat(m[:, None], k, axis=1)
+    out = np.full((n, k, x.shape[1]), np.nan)
+    for e in range(np.asarray(w1).shape[0]):
+        b, s = np.nonzero(m & (ids == e))
+        if len(b):
+            out[b, s] = swiglu_expert(x[b], w1[e], w3[e], w2[e], dt)[0]
+    return out

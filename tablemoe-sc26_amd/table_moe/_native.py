@@ -80,6 +80,11 @@ PROTOTYPES = {
     "tm_keep_select": (C.c_int, [vp, i64, i64, i64, vp, vp, sz, vp]),
     "tm_gather_combine": (C.c_int, [i32, i64, i32, vp, vp, i64, i64, vp, i64, i32, vp, i64, i64, vp, vp, i64, i32,
                                     vp, i64, vp, i64, vp]),
+    "tm_swiglu_workspace_size": (sz, [i64, i32, i32]),
+    "tm_expert_swiglu": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, i32, vp, i64, vp, sz, vp]),
+    "tm_group_slots_tiles": (i64, [i64, i32]),
+    "tm_group_slots": (C.c_int, [vp, i64, i32, i64, vp, i64, i64, i32, i64, i64, vp, vp, vp, vp, vp]),
+    "tm_grouped_swiglu": (C.c_int, [i32, vp, i64, i32, i32, i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]),
     "tm_struct_size": (sz, [i32]),
     "tm_table_forward_workspace_size": (sz, [C.POINTER(TableLayer), i64, i32]),
     "tm_table_forward": (C.c_int, [C.POINTER(TableLayer), C.POINTER(LayerIO), vp, sz, vp, vp]),

@@ -1,0 +1,74 @@
+"""Grouped recompute of the slots that are not reused: every (token, slot)
+pair selected by ``mask`` runs its routed expert's SwiGLU MLP and writes
+``slot_out[token, slot]`` — the collected[token, slot] rows the reference
+fills one expert at a time (models/qwen3_vl_moe/cached_layers.py:431-437)
+and the combine consumes.  Two C-ABI calls: tm_group_slots (bucket the pairs
+by expert on the device, no host sync) and tm_grouped_swiglu (two grouped
+GEMMs on the matrix cores).  Weights are stacked per expert as nn.Linear
+keeps them: w1, w3 [E, I, H], w2 [E, H, I].
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _native as N
+
+
+class GroupedExperts:
+    """Stacked expert weights plus the reusable grouping buffers."""
+
+    def __init__(self, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor):
+        dev = N.require_hip(w1, w3, w2)
+        e, inter, h = w1.shape
+        if w3.shape != (e, inter, h) or w2.shape != (e, h, inter):
+            raise ValueError("w1/w3 must be [E, I, H] and w2 [E, H, I]")
+        if not (w1.dtype == w3.dtype == w2.dtype) or w1.dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError("expert weights must share dtype float16 or bfloat16")
+        self.w1, self.w3, self.w2 = w1.contiguous(), w3.contiguous(), w2.contiguous()
+        self.n_experts, self.inter, self.hidden = e, inter, h
+        self.dtype, self.device = w1.dtype, dev
+        self._bufs: dict = {}
+
+    def _buf(self, name, numel, dtype):
+        t = self._bufs.get(name)
+        if t is None or t.numel() < numel or t.dtype != dtype:
+            t = torch.empty(max(numel, 1), dtype=dtype, device=self.device)
+            self._bufs[name] = t
+        return t
+
+    def group(self, ids: torch.Tensor, mask: torch.Tensor, slot_out: torch.Tensor):
+        """Bucket the masked (token, slot) pairs by expert; ``mask`` is [N, k]
+        or a per-token [N] flag."""
+        n, k = ids.shape
+        m = N.as_u8(mask)
+        ms_b, ms_s = (m.stride(0), 0) if m.dim() == 1 else (m.stride(0), m.stride(1))
+        t_max = N.lib().tm_group_slots_tiles(n * k, self.n_experts)
+        offs = self._buf("offsets", self.n_experts + 1, torch.int32)
+        row_token = self._buf("row_token", n * k, torch.int32)
+        row_out = self._buf("row_out", n * k, torch.int64)
+        tiles = self._buf("tiles", 2 + 2 * t_max, torch.int32)
+        N.call("tm_group_slots", N.ptr(ids), n, k, ids.stride(0), N.ptr(m), ms_b, ms_s, self.n_experts,
+               slot_out.stride(0), slot_out.stride(1), N.ptr(offs), N.ptr(row_token), N.ptr(row_out), N.ptr(tiles),
+               N.stream(self.device))
+        return offs, row_token, row_out, tiles
+
+    def forward(self, hidden: torch.Tensor, ids: torch.Tensor, mask: torch.Tensor, slot_out: torch.Tensor):
+        """slot_out[b, s] = expert(ids[b, s]) MLP of hidden[b] for masked pairs
+        (others untouched); returns slot_out."""
+        N.require_hip(hidden, ids, mask, slot_out)
+        if hidden.dtype != self.dtype or slot_out.dtype != self.dtype:
+            raise ValueError(f"hidden/slot_out must be {self.dtype}")
+        if ids.dtype != torch.long:
+            ids = ids.long()
+        n, k = ids.shape
+        if slot_out.shape != (n, k, self.hidden) or slot_out.stride(-1) != 1:
+            raise ValueError(f"slot_out must be [N, {k}, {self.hidden}] with unit stride along hidden")
+        x = hidden if hidden.stride(-1) == 1 else hidden.contiguous()
+        offs, row_token, row_out, tiles = self.group(ids, mask, slot_out)
+        nbytes = N.lib().tm_swiglu_workspace_size(n * k, self.inter, N.dtype_tag(self.dtype))
+        ws = self._buf("fused", nbytes, torch.uint8)
+        N.call("tm_grouped_swiglu", N.dtype_tag(self.dtype), N.ptr(x), x.stride(0), self.hidden, self.inter,
+               self.n_experts, N.ptr(self.w1), N.ptr(self.w3), N.ptr(self.w2), n * k, N.ptr(offs), N.ptr(row_token),
+               N.ptr(row_out), N.ptr(tiles), N.ptr(slot_out), N.ptr(ws), ws.numel(), N.stream(self.device))
+        return slot_out

@@ -1,0 +1,165 @@
+"""GPU parity of the recompute path: the SwiGLU expert MLP (tm_expert_swiglu),
+the device-side grouping of recomputed slots by expert (tm_group_slots) and
+the grouped MLP writing the slot layout (tm_grouped_swiglu), against the
+oracle (oracle/tm_oracle.py: swiglu_expert, grouped_swiglu)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tm_oracle as O
+from parity_util import ODT, np64
+from table_moe import _native as N
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(g, e, h, inter, dtype, scale=0.02):
+    w1 = (torch.randn(e, inter, h, generator=g) * scale).to(dtype)
+    w3 = (torch.randn(e, inter, h, generator=g) * scale).to(dtype)
+    w2 = (torch.randn(e, h, inter, generator=g) * scale).to(dtype)
+    return w1, w3, w2
+
+
+def assert_mlp_close(got, exact, dtype, min_exact=0.9):
+    """North-star tolerance (atol 1e-2, rtol 2e-3) where it exceeds the
+    type's own half-ulp, plus a floor on the bit-exact fraction: the device
+    accumulates in fp32 (the intermediate can round the other way where an
+    exact value sits on a rounding boundary)."""
+    got, exact = np.asarray(got), np.asarray(exact)
+    small = np.abs(exact) < 8.0
+    np.testing.assert_allclose(got[small], exact[small], atol=1e-2, rtol=2e-3)
+    frac = float(np.mean(got == exact))
+    assert frac >= min_exact, f"only {frac:.4f} bit-exact"
+
+
+@pytest.mark.parametrize("m,h,inter,dtype", [(1, 2048, 768, torch.bfloat16), (7, 2560, 1536, torch.float16),
+                                             (128, 1024, 512, torch.bfloat16), (300, 2560, 1536, torch.bfloat16),
+                                             (129, 256, 128, torch.float16)])
+def test_expert_swiglu_vs_oracle(hip_device, m, h, inter, dtype):
+    from table_moe.ops import expert_swiglu
+
+    g = torch.Generator().manual_seed(m + h + inter)
+    x = torch.randn(m, h, generator=g).to(dtype)
+    w1, w3, w2 = (w[0] for w in _weights(g, 1, h, inter, dtype))
+    y = expert_swiglu(x.to(hip_device), w1.to(hip_device), w3.to(hip_device), w2.to(hip_device))
+    torch.cuda.synchronize()
+    want, _ = O.swiglu_expert(np64(x), np64(w1), np64(w3), np64(w2), ODT[dtype])
+    assert_mlp_close(np64(y), want, dtype)
+
+
+def test_group_slots_buckets_every_pair(hip_device):
+    """Counts, offsets, tiles and the (token, slot) -> row map of the device
+    grouping against a host bincount; every selected pair appears once."""
+    from table_moe.ops import GroupedExperts
+
+    dev = hip_device
+    g = torch.Generator().manual_seed(11)
+    n, k, e, h = 1000, 6, 64, 128
+    ids = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)])
+    ids[5, 2] = -1  # out-of-range ids are skipped
+    ids[6, 0] = e
+    keep = torch.rand(n, generator=g) < 0.6
+    w = torch.zeros(e, 128, h, dtype=torch.bfloat16, device=dev)
+    ge = GroupedExperts(w, w.clone(), torch.zeros(e, h, 128, dtype=torch.bfloat16, device=dev))
+    slot_out = torch.empty(n, k, h, dtype=torch.bfloat16, device=dev)
+    offs, row_token, row_out, tiles = ge.group(ids.to(dev), keep.to(dev), slot_out)
+    torch.cuda.synchronize()
+    sel = keep[:, None].expand(n, k) & (ids >= 0) & (ids < e)
+    counts = np.bincount(ids[sel].numpy(), minlength=e)
+    offs = offs.cpu().numpy()
+    np.testing.assert_array_equal(np.diff(offs[: e + 1]), counts)
+    total = int(counts.sum())
+    tiles = tiles.cpu().numpy()
+    assert tiles[0] == total
+    t_max = N.lib().tm_group_slots_tiles(n * k, e)
+    n_tiles = int(tiles[1])
+    assert n_tiles == int(np.sum((counts + 127) // 128)) <= t_max
+    te, tr = tiles[2: 2 + n_tiles], tiles[2 + t_max: 2 + t_max + n_tiles]
+    for ex in range(e):
+        rows = tr[te == ex]
+        np.testing.assert_array_equal(rows, offs[ex] + 128 * np.arange(len(rows)))
+    rt = row_token[:total].cpu().numpy()
+    ro = row_out[:total].cpu().numpy()
+    b_of, s_of = ro // slot_out.stride(0), (ro % slot_out.stride(0)) // slot_out.stride(1)
+    np.testing.assert_array_equal(b_of, rt)
+    pairs = set(zip(b_of.tolist(), s_of.tolist()))
+    assert len(pairs) == total
+    want = set(zip(*[a.tolist() for a in np.nonzero(sel.numpy())]))
+    assert pairs == want
+    for ex in range(e):  # each row sits in its expert's range
+        bb, ss = b_of[offs[ex]: offs[ex + 1]], s_of[offs[ex]: offs[ex + 1]]
+        assert np.all(ids.numpy()[bb, ss] == ex)
+
+
+@pytest.mark.parametrize("mask_kind", ["token", "slot"])
+def test_grouped_swiglu_vs_oracle_and_single_expert(hip_device, mask_kind):
+    """Config-5 shapes (64 experts, top-6, hidden 2560, intermediate 1536) on
+    300 tokens: every selected slot row against the oracle; unselected slots
+    untouched; and each expert's rows bit-identical to tm_expert_swiglu on the
+    same rows (an output row does not depend on where it sits in a tile)."""
+    from table_moe.ops import GroupedExperts, expert_swiglu
+
+    dev = hip_device
+    g = torch.Generator().manual_seed(17 if mask_kind == "token" else 19)
+    n, k, e, h, inter, dtype = 300, 6, 64, 2560, 1536, torch.bfloat16
+    x = torch.randn(n, h, generator=g).to(dtype)
+    w1, w3, w2 = _weights(g, e, h, inter, dtype)
+    ids = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)])
+    mask = (torch.rand(n, generator=g) < 0.6) if mask_kind == "token" else (torch.rand(n, k, generator=g) < 0.5)
+    ge = GroupedExperts(w1.to(dev), w3.to(dev), w2.to(dev))
+    slot_out = torch.full((n, k, h), 7.0, dtype=dtype, device=dev)
+    ge.forward(x.to(dev), ids.to(dev), mask.to(dev), slot_out)
+    torch.cuda.synchronize()
+    got = np64(slot_out)
+    want = O.grouped_swiglu(np64(x), ids.numpy(), mask.numpy(), np64(w1), np64(w3), np64(w2), O.BF16)
+    m2 = mask.numpy() if mask.dim() == 2 else np.repeat(mask.numpy()[:, None], k, axis=1)
+    assert np.all(got[~m2] == 7.0)
+    assert_mlp_close(got[m2], want[m2], dtype)
+    xd = x.to(dev)
+    for ex in (0, 17, 63):
+        bb, ss = np.nonzero(m2 & (ids.numpy() == ex))
+        if len(bb) == 0:
+            continue
+        y = expert_swiglu(xd[torch.from_numpy(bb).to(dev)].contiguous(), ge.w1[ex], ge.w3[ex], ge.w2[ex])
+        torch.cuda.synchronize()
+        assert torch.equal(y, slot_out[torch.from_numpy(bb).to(dev), torch.from_numpy(ss).to(dev)])
+
+
+def test_maybe_run_fp16_fused_expert_contract(hip_device, monkeypatch):
+    """The reference's entry point: None when it does not apply (more rows than
+    TABLEMOE_FP16_FUSED_MAX_TOKENS, default 1; disabled by
+    TABLEMOE_USE_FP16_FUSED_EXPERT=0; a bias), else the MLP in the owner's
+    reused output buffer."""
+    from table_moe.ops import expert_swiglu, maybe_run_fp16_fused_expert
+
+    dev = hip_device
+    h, inter = 512, 256
+
+    class Wrap:
+        def __init__(self, lin):
+            self.linear_module = lin
+
+    class Owner:
+        pass
+
+    torch.manual_seed(3)
+    owner = Owner()
+    owner.w1 = Wrap(torch.nn.Linear(h, inter, bias=False).to(dev, torch.float16))
+    owner.w3 = Wrap(torch.nn.Linear(h, inter, bias=False).to(dev, torch.float16))
+    owner.w2 = Wrap(torch.nn.Linear(inter, h, bias=False).to(dev, torch.float16))
+    x1 = torch.randn(1, h, device=dev, dtype=torch.float16)
+    y = maybe_run_fp16_fused_expert(owner, x1)
+    ref = expert_swiglu(x1, owner.w1.linear_module.weight, owner.w3.linear_module.weight, owner.w2.linear_module.weight)
+    torch.cuda.synchronize()
+    assert y is not None and torch.equal(y, ref)
+    assert maybe_run_fp16_fused_expert(owner, x1) is y  # the owner's buffer is reused
+    x3 = torch.randn(3, h, device=dev, dtype=torch.float16)
+    assert maybe_run_fp16_fused_expert(owner, x3) is None
+    monkeypatch.setenv("TABLEMOE_FP16_FUSED_MAX_TOKENS", "4")
+    assert maybe_run_fp16_fused_expert(owner, x3) is not None
+    monkeypatch.setenv("TABLEMOE_USE_FP16_FUSED_EXPERT", "0")
+    assert maybe_run_fp16_fused_expert(owner, x1) is None
+    monkeypatch.delenv("TABLEMOE_USE_FP16_FUSED_EXPERT")
+    owner.w2 = Wrap(torch.nn.Linear(inter, h, bias=True).to(dev, torch.float16))
+    assert maybe_run_fp16_fused_expert(owner, x1) is None

@@ -387,3 +387,75 @@ def test_layer_fp32_baseline_agrees_with_oracle():
     ref = O.layer_forward_g(*args, 8, 1, 0.6, dt=O.F32)
     fast = O.layer_forward_g_fp32(*args, 8, 1, 0.6)
     np.testing.assert_allclose(fast, ref["out"], rtol=1e-4, atol=1e-4)
+
+
+# ------------------------------------------------------- recompute: SwiGLU MLP
+def test_swiglu_expert_one_hot_closed_form():
+    """One-hot weights route single coordinates: W1 picks x_a (gate), W3 picks
+    x_b (up), W2 routes intermediate column j to output c.  The output is then
+    dt(dt(silu(dt(x_a))) * x_b)) evaluated with scalar math.exp: pins which
+    matrix is the gate, which the up projection, the orientation of each, and
+    the rounding points (g rounded, up unrounded, f rounded, y rounded)."""
+    import math
+
+    rng = np.random.default_rng(7)
+    H, I = 16, 8
+    x = O.round_to(rng.normal(size=(5, H)) * 3, O.BF16)
+    a = rng.integers(0, H, I)
+    b = rng.integers(0, H, I)
+    c = rng.permutation(H)[:I]
+    w1 = np.zeros((I, H)); w1[np.arange(I), a] = 1.0
+    w3 = np.zeros((I, H)); w3[np.arange(I), b] = 1.0
+    w2 = np.zeros((H, I)); w2[c, np.arange(I)] = 1.0
+    y, f = O.swiglu_expert(x, w1, w3, w2, O.BF16)
+    for r in range(x.shape[0]):
+        for j in range(I):
+            g = float(O.round_to(x[r, a[j]], O.BF16))
+            want_f = float(O.round_to(g / (1.0 + math.exp(-g)) * x[r, b[j]], O.BF16))
+            assert f[r, j] == want_f
+            assert y[r, c[j]] == want_f  # one term: the down projection only rounds it again
+    others = np.setdiff1d(np.arange(H), c)
+    assert np.all(y[:, others] == 0.0)
+
+
+def test_swiglu_expert_matches_torch_silu_and_matmul():
+    """Against torch's own silu and float64 matmul (library routines) with the
+    same rounding points; and the up projection is NOT rounded before the
+    product (rounding it, as the unfused torch expert does, changes results)."""
+    import torch
+
+    rng = np.random.default_rng(3)
+    H, I, M = 64, 32, 9
+    x = O.round_to(rng.normal(size=(M, H)), O.BF16)
+    w1 = O.round_to(rng.normal(size=(I, H)) * 0.2, O.BF16)
+    w3 = O.round_to(rng.normal(size=(I, H)) * 0.2, O.BF16)
+    w2 = O.round_to(rng.normal(size=(H, I)) * 0.2, O.BF16)
+    y, f = O.swiglu_expert(x, w1, w3, w2, O.BF16)
+    tx, t1, t3, t2 = (torch.from_numpy(v) for v in (x, w1, w3, w2))
+    g = torch.from_numpy(O.round_to((tx @ t1.T).numpy(), O.BF16))
+    tf = O.round_to((torch.nn.functional.silu(g) * (tx @ t3.T)).numpy(), O.BF16)
+    np.testing.assert_allclose(f, tf, rtol=0, atol=0)
+    ty = O.round_to((torch.from_numpy(tf) @ t2.T).numpy(), O.BF16)
+    np.testing.assert_array_equal(y, ty)
+    f_rounded_up = O.round_to(O.silu(g.numpy()) * O.round_to((tx @ t3.T).numpy(), O.BF16), O.BF16)
+    assert np.any(f_rounded_up != f)
+
+
+def test_grouped_swiglu_regroups_pairs():
+    rng = np.random.default_rng(5)
+    E, H, I, N, K = 5, 16, 8, 11, 3
+    x = rng.normal(size=(N, H))
+    w1, w3 = rng.normal(size=(E, I, H)) * 0.3, rng.normal(size=(E, I, H)) * 0.3
+    w2 = rng.normal(size=(E, H, I)) * 0.3
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(N)])
+    mask = rng.random((N, K)) < 0.6
+    out = O.grouped_swiglu(x, ids, mask, w1, w3, w2, O.F32)
+    for bb in range(N):
+        for s in range(K):
+            if mask[bb, s]:
+                want = O.swiglu_expert(x[bb:bb + 1], w1[ids[bb, s]], w3[ids[bb, s]], w2[ids[bb, s]], O.F32)[0][0]
+                np.testing.assert_array_equal(out[bb, s], want)
+            else:
+                assert np.all(np.isnan(out[bb, s]))
+    tok = O.grouped_swiglu(x, ids, mask[:, 0], w1, w3, w2, O.F32)  # per-token mask covers every slot
+    assert np.isnan(tok).any(axis=2).sum() == (~mask[:, 0]).sum() * K
