@@ -343,7 +343,7 @@ int tm_expert_swiglu(int32_t dtype, const void *x, int64_t n_rows, int32_t hidde
  * Writes expert_offsets [n_experts + 1], one row per pair (row_token = b,
  * row_out = b*so_b + s*so_s: the element offset of its output row), and
  * tiles [2 + 2*tm_group_slots_tiles(n_tokens*top_k, n_experts)]: row count,
- * tile count, then each 128-row tile's expert and first row.  The order of
+ * tile count, then each 256-row tile's expert and first row.  The order of
  * rows inside an expert is unspecified; results do not depend on it. */
 int64_t tm_group_slots_tiles(int64_t max_rows, int32_t n_experts);
 int tm_group_slots(const int64_t *ids, int64_t n_tokens, int32_t top_k, int64_t ld_ids, const uint8_t *mask,

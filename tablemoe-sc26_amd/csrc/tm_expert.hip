@@ -20,24 +20,34 @@
 // grouped_gemm_kernel computes one BM x BN tile C = A B^T of one expert:
 // A rows gathered (token rows of x, or the grouped rows of the intermediate),
 // B rows k-contiguous (nn.Linear weights [out, in]), K in BK-wide stages.
-// Each stage is loaded into registers while the previous one is multiplied,
-// then written to the other LDS buffer (16-byte chunks XOR-swizzled by row, so
-// the operand reads of 32 rows fall in distinct banks); one barrier per
-// stage.  Four waves own 64 x 64 quadrants (2 x 2 blocks of
-// v_mfma_f32_32x32x16).  Up mode multiplies W1 and W3 against the same A
+// Stages move global -> LDS by direct loads, three in flight (16-byte chunks
+// XOR-swizzled by row, so the operand reads of 32 rows spread over the
+// banks); one barrier per stage.  Four waves own 128 x 64 quadrants (4 x 2
+// blocks of v_mfma_f32_32x32x16).  Up mode multiplies W1 and W3 against the same A
 // fragments and applies the SiLU-mul epilogue; down mode writes each row to
 // its slot of the output.
 #include "tm_internal.h"
+#include "tm_dma.h"
 #include "tm_mfma.h"
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64, kThreads = 256;
-constexpr int kChunksPerRow = BK / 8;  // 16-byte chunks per tile row
+constexpr int BM = 256, BN = 128, BK = 32, kThreads = 256, kRing = 4;
+constexpr int kCPR = BK / 8;                 // 16-byte chunks per tile row
+constexpr int kAStage = BM * kCPR;           // A slots (16 bytes) per stage
+constexpr int kBStage = BN * kCPR;           // slots of each B per stage
+constexpr int kADma = kAStage / 64 / 4;      // A loads per wave per stage (4)
+constexpr int kBDma = kBStage / 64 / 4;      // loads of each B per wave per stage (2)
+constexpr int kMI = 4, kNI = 2;              // 32 x 32 blocks per wave: 128 rows x 64 columns
 
 enum { kModeUp = 0, kModeDown = 1 };
 
-__device__ __forceinline__ int swz(int row, int kc) { return row * kChunksPerRow + (kc ^ (row & 7)); }
+// Slot of (row, 16-byte chunk kc) in a stage.  A row is 64 bytes, so two
+// rows share one 128-byte line of banks; XOR-ing the chunk with (row / 2) % 4
+// puts the 8 rows of a line group on 8 distinct 16-byte bank groups, and an
+// operand read (one chunk of 32 consecutive rows) is conflict-free.
+__device__ __forceinline__ int swz_chunk(int row, int kc) { return kc ^ ((row >> 1) & (kCPR - 1)); }
+__device__ __forceinline__ int swz(int row, int kc) { return row * kCPR + swz_chunk(row, kc); }
 
 // Tile source: the grouped tile list (tiles != nullptr: [0] rows, [1] tiles,
 // then tile_expert[t_max], tile_row0[t_max]) or one dense expert of `rows`.
@@ -48,113 +58,124 @@ struct TileSrc {
   int32_t rows;
 };
 
+// One BM x BN tile, 4 waves in a 2 x 2 grid of 128 x 64 quadrants (one wave
+// per SIMD, accumulators in the AGPRs).  Operands move global -> LDS by
+// direct loads into a kRing-stage ring, kRing - 1 stages in flight: at step i
+// a wave waits for its own loads of stage i, the barrier makes every wave's
+// loads of stage i visible (and retires every wave's reads of stage i - 1),
+// then the loads of stage i + 3 go into that freed slot and stage i is
+// multiplied.  Lane l of a load fills slot p0 + l; it reads the global chunk
+// that belongs there (the inverse of the swizzle).
 template <int DT, int NB, int MODE>
 __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
     const typename Elem<DT>::T *__restrict__ A, int64_t lda, const int32_t *__restrict__ a_rows,
     const typename Elem<DT>::T *__restrict__ B0, const typename Elem<DT>::T *__restrict__ B1, int64_t b_expert,
-    int K, TileSrc ts, typename Elem<DT>::T *__restrict__ C, int64_t ldc, const int64_t *__restrict__ c_rows) {
+    int K, int n_tiles, TileSrc ts, typename Elem<DT>::T *__restrict__ C, int64_t ldc,
+    const int64_t *__restrict__ c_rows) {
   using T = typename Elem<DT>::T;
-  extern __shared__ uint4 lds[];  // [2][(1 + NB) * BM * kChunksPerRow]
-  constexpr int kStage = (1 + NB) * BM * kChunksPerRow;
+  constexpr int kStage = kAStage + NB * kBStage;
+  constexpr int kDma = kADma + NB * kBDma;  // loads per wave per stage
+  __shared__ uint4 lds[kRing * kStage];
 
+  // Block b runs on XCD b % 8 (the dispatcher's round robin): the n_tiles
+  // column tiles of row tile y get ids 8 apart, so they share one XCD and its
+  // L2 copy of the tile's A rows.
+  const int64_t b = blockIdx.x;
+  const int64_t slot = b >> 3;
+  const int64_t y = (slot / n_tiles) * 8 + (b & 7);
+  const int n0 = (int)(slot % n_tiles) * BN;
   int e, r0, r_end;
   if (ts.tiles != nullptr) {
-    if ((int64_t)blockIdx.y >= ts.tiles[1]) return;  // uniform: past the last tile
-    e = ts.tiles[2 + blockIdx.y];
-    r0 = ts.tiles[2 + ts.t_max + blockIdx.y];
+    if (y >= ts.t_max || y >= ts.tiles[1]) return;  // uniform: past the last tile
+    e = ts.tiles[2 + y];
+    r0 = ts.tiles[2 + ts.t_max + y];
     r_end = ts.expert_offsets[e + 1];
   } else {
     e = 0;
-    r0 = (int)blockIdx.y * BM;
+    r0 = (int)y * BM;
     if (r0 >= ts.rows) return;
     r_end = ts.rows;
   }
-  const int n0 = (int)blockIdx.x * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Each thread moves 4 chunks of the A tile and 4 of each B tile per stage:
-  // chunk c = tid + 256 j -> tile row c / 8, k chunk c % 8.
-  const T *a_src[4];
-  const T *b_src[NB][4];
+  // Global source of each of this lane's loads (stage 0); stage s adds s * BK.
+  const T *a_src[kADma];
+  const T *b_src[NB][kBDma];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int c = tid + kThreads * j;
-    const int row = c >> 3, kc = c & 7;
+  for (int j = 0; j < kADma; ++j) {
+    const int p = (wave * kADma + j) * 64 + lane;
+    const int row = p / kCPR, kc = swz_chunk(row, p % kCPR);  // the swizzle is its own inverse
     int gr = r0 + row;
     gr = gr < r_end ? gr : r_end - 1;  // rows past the expert re-read its last row; their results are dropped
     const int64_t ar = a_rows ? (int64_t)a_rows[gr] : (int64_t)gr;
     a_src[j] = A + ar * lda + kc * 8;
+  }
+#pragma unroll
+  for (int j = 0; j < kBDma; ++j) {
+    const int p = (wave * kBDma + j) * 64 + lane;
+    const int row = p / kCPR, kc = swz_chunk(row, p % kCPR);
     const int64_t br = (int64_t)e * b_expert + (int64_t)(n0 + row) * K + kc * 8;
     b_src[0][j] = B0 + br;
     if constexpr (NB > 1) b_src[1][j] = B1 + br;
   }
-  uint4 ra[4], rb[NB][4];
-  auto fetch = [&](int kt) {
+  const int KT = K / BK;
+  auto issue = [&](int stage) {  // stages past the last re-read it (their slot is never multiplied)
+    const int kt = stage < KT ? stage : KT - 1;
+    uint4 *s = lds + (stage % kRing) * kStage;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      ra[j] = *reinterpret_cast<const uint4 *>(a_src[j] + (int64_t)kt * BK);
+    for (int j = 0; j < kADma; ++j) tm_dma16(a_src[j] + (int64_t)kt * BK, s + (wave * kADma + j) * 64);
 #pragma unroll
-      for (int b = 0; b < NB; ++b) rb[b][j] = *reinterpret_cast<const uint4 *>(b_src[b][j] + (int64_t)kt * BK);
-    }
-  };
-  auto stash = [&](int buf) {
-    uint4 *s = lds + buf * kStage;
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = tid + kThreads * j;
-      const int row = c >> 3, kc = c & 7;
-      s[swz(row, kc)] = ra[j];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) s[(1 + b) * BM * kChunksPerRow + swz(row, kc)] = rb[b][j];
-    }
+      for (int j = 0; j < kBDma; ++j)
+        tm_dma16(b_src[b][j] + (int64_t)kt * BK, s + kAStage + b * kBStage + (wave * kBDma + j) * 64);
   };
 
-  tm_f32x16 acc[NB][2][2];
+  tm_f32x16 acc[NB][kMI][kNI];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < kMI; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) acc[b][mi][ni] = tm_f32x16{};
+      for (int ni = 0; ni < kNI; ++ni) acc[b][mi][ni] = tm_f32x16{};
 
-  const int KT = K / BK;
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    fetch(kt + 1 < KT ? kt + 1 : kt);  // the last stage re-reads itself (never stashed for use)
-    const uint4 *s = lds + buf * kStage;
+  issue(0);
+  issue(1);
+  issue(2);
+  for (int i = 0; i < KT; ++i) {
+    tm_wait_vm_lgkm0<2 * kDma>();  // this wave's loads of stage i are done (stages i+1, i+2 may fly)
+    __syncthreads();
+    issue(i + 3);
+    const uint4 *s = lds + (i % kRing) * kStage;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       const int kc = ks * 2 + (lane >> 5);
-      uint4 fa[2], fb[NB][2];
+      uint4 fa[kMI], fb[NB][kNI];
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi) fa[mi] = s[swz(wm * 64 + mi * 32 + (lane & 31), kc)];
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) fb[b][ni] = s[(1 + b) * BM * kChunksPerRow + swz(wn * 64 + ni * 32 + (lane & 31), kc)];
+      for (int mi = 0; mi < kMI; ++mi) fa[mi] = s[swz(wm * 128 + mi * 32 + (lane & 31), kc)];
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int ni = 0; ni < kNI; ++ni) fb[b][ni] = s[kAStage + b * kBStage + swz(wn * 64 + ni * 32 + (lane & 31), kc)];
 #pragma unroll
-          for (int ni = 0; ni < 2; ++ni) acc[b][mi][ni] = tm_mfma32x32x16<DT>(fa[mi], fb[b][ni], acc[b][mi][ni]);
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int mi = 0; mi < kMI; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < kNI; ++ni) acc[b][mi][ni] = tm_mfma32x32x16<DT>(fa[mi], fb[b][ni], acc[b][mi][ni]);
     }
-    stash(buf ^ 1);
-    __syncthreads();
   }
+  tm_wait_vm_lgkm0<0>();  // no load may still target this workgroup's LDS when it exits
 
   // Epilogue: lane owns column (lane % 32) of each block and its 16 rows.
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
+  for (int mi = 0; mi < kMI; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
+    for (int ni = 0; ni < kNI; ++ni)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int row = wm * 64 + mi * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        const int row = wm * 128 + mi * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
         const int col = n0 + wn * 64 + ni * 32 + (lane & 31);
         const int gr = r0 + row;
         if (gr >= r_end) continue;
@@ -236,11 +257,11 @@ void launch_gemm(const void *A, int64_t lda, const int32_t *a_rows, const void *
                  int K, int N, const TileSrc &ts, int64_t grid_y, void *C, int64_t ldc, const int64_t *c_rows,
                  hipStream_t s) {
   using T = typename Elem<DT>::T;
-  const size_t lds_bytes = 2 * (size_t)(1 + NB) * BM * kChunksPerRow * sizeof(uint4);
-  hipLaunchKernelGGL((grouped_gemm_kernel<DT, NB, MODE>), dim3((unsigned)(N / BN), (unsigned)grid_y),
-                     dim3(kThreads), lds_bytes, s, static_cast<const T *>(A), lda, a_rows,
-                     static_cast<const T *>(B0), static_cast<const T *>(B1), b_expert, K, ts, static_cast<T *>(C),
-                     ldc, c_rows);
+  const int n_tiles = N / BN;
+  const int64_t blocks = tm_cdiv(grid_y, 8) * 8 * n_tiles;
+  hipLaunchKernelGGL((grouped_gemm_kernel<DT, NB, MODE>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
+                     static_cast<const T *>(A), lda, a_rows, static_cast<const T *>(B0), static_cast<const T *>(B1),
+                     b_expert, K, n_tiles, ts, static_cast<T *>(C), ldc, c_rows);
 }
 
 // The two GEMMs of the MLP over the rows the tile source names.
@@ -251,15 +272,6 @@ int swiglu_impl(int32_t dtype, const void *x, int64_t ld_x, const int32_t *row_t
     if constexpr (DT == TM_DT_F32) {
       return tm_fail(TM_EINVAL_DTYPE, "tm_grouped_swiglu: dtype must be F16 or BF16");
     } else {
-      static bool attr_set = false;
-      if (!attr_set) {  // the up GEMM's double-buffered stages exceed the default 64 KiB of dynamic LDS
-        const hipError_t ea =
-            hipFuncSetAttribute(reinterpret_cast<const void *>(&grouped_gemm_kernel<DT, 2, kModeUp>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 2 * 3 * BM * kChunksPerRow * 16);
-        if (ea != hipSuccess)
-          return tm_fail(TM_EHIP, "tm_grouped_swiglu: hipFuncSetAttribute: %s", hipGetErrorString(ea));
-        attr_set = true;
-      }
       launch_gemm<DT, 2, kModeUp>(x, ld_x, row_token, w1, w3, (int64_t)inter * hidden, hidden, inter, ts, grid_y,
                                   fused, inter, nullptr, s);
       TM_LAUNCH_CHECK("tm_grouped_swiglu(up)");
@@ -272,7 +284,8 @@ int swiglu_impl(int32_t dtype, const void *x, int64_t ld_x, const int32_t *row_t
 }
 
 bool shapes_ok(int32_t hidden, int32_t inter) {
-  return hidden > 0 && inter > 0 && hidden % BN == 0 && inter % BN == 0 && hidden % BK == 0 && inter % BK == 0;
+  return hidden > 0 && inter > 0 && hidden % BN == 0 && inter % BN == 0 && hidden % BK == 0 && inter % BK == 0 &&
+         hidden / BK >= 1 && inter / BK >= 1;
 }
 
 }  // namespace

@@ -74,11 +74,12 @@ def test_group_slots_buckets_every_pair(hip_device):
     assert tiles[0] == total
     t_max = N.lib().tm_group_slots_tiles(n * k, e)
     n_tiles = int(tiles[1])
-    assert n_tiles == int(np.sum((counts + 127) // 128)) <= t_max
+    rows_per_tile = 256  # tile height of the grouped GEMM
+    assert n_tiles == int(np.sum((counts + rows_per_tile - 1) // rows_per_tile)) <= t_max
     te, tr = tiles[2: 2 + n_tiles], tiles[2 + t_max: 2 + t_max + n_tiles]
     for ex in range(e):
         rows = tr[te == ex]
-        np.testing.assert_array_equal(rows, offs[ex] + 128 * np.arange(len(rows)))
+        np.testing.assert_array_equal(rows, offs[ex] + rows_per_tile * np.arange(len(rows)))
     rt = row_token[:total].cpu().numpy()
     ro = row_out[:total].cpu().numpy()
     b_of, s_of = ro // slot_out.stride(0), (ro % slot_out.stride(0)) // slot_out.stride(1)
