@@ -317,6 +317,34 @@ int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden, const uin
                       int64_t ld_o, tm_stream_t stream);
 
 /* ======================================================================
+ * Importance for the expert-level keep rule: attention probabilities of the
+ * last query over every key, averaged over heads.
+ * Replaces HybridQwen3Attention._compute_and_cache_importance
+ * (models/qwen3_vl_moe/hybrid_attention.py:111-146) and the DeepSeek
+ * _cache_last_token_attention (models/deepseek_vl2/deepseek_attention.py:
+ * 206-249); feeds tm_expert_keep_mask's `attn`.
+ * q(b, h, d) = q[b*qs_b + h*qs_h + d]; k(b, t, g, d) = k[b*ks_b + t*ks_s +
+ * g*ks_h + d]; head h reads KV head h / (n_heads / n_kv_heads) (the
+ * reference's repeat_interleave).  Score of key t:
+ *   TM_SCORE_MODEL  dtype(dtype(q . k) * scale)  (torch.matmul in the model
+ *                   dtype, then `* scaling` in the model dtype: Qwen)
+ *   TM_SCORE_F32    fp32(q . k) * scale          (fp32 einsum: DeepSeek)
+ * (fp32 accumulation).  Keys with key_mask[b*km_b + t] == 0 get probability
+ * 0 and leave the normalisation.  p = softmax over t in fp32;
+ * out[b*ld_out + j] = mean over heads of p at key n_keys - out_len + j.
+ * head_dim in {64, 128, 192, 256}; n_heads <= 256; n_keys <= 524288.
+ * Workspace: tm_importance_workspace_size (scores and chunk statistics).
+ * ====================================================================== */
+#define TM_SCORE_MODEL 0
+#define TM_SCORE_F32 1
+size_t tm_importance_workspace_size(int64_t batch, int32_t n_heads, int64_t n_keys);
+int tm_last_query_importance(int32_t dtype, const void *q, int64_t qs_b, int64_t qs_h, const void *k, int64_t ks_b,
+                             int64_t ks_s, int64_t ks_h, int64_t batch, int32_t n_heads, int32_t n_kv_heads,
+                             int32_t head_dim, int64_t n_keys, float scale, int32_t score_mode,
+                             const uint8_t *key_mask, int64_t km_b, int64_t out_len, float *out, int64_t ld_out,
+                             void *workspace, size_t workspace_bytes, tm_stream_t stream);
+
+/* ======================================================================
  * Recompute path -- the SwiGLU expert MLP of the slots that are recomputed.
  * tm_expert_swiglu replaces fused_moe_ffn_fp16_into
  * (table_moe/ops/csrc/fp16_fused_expert/fp16_fused_moe_mlp.cu:107-274,

@@ -49,6 +49,9 @@ swiglu_expert                  torch.nn.functional.silu + matmul (library
                                is silu(x_a) * x_b through scalar math.exp
 grouped_swiglu                 per-expert swiglu_expert on the pairs of each
                                expert (brute-force regrouping)
+last_query_importance          torch.softmax / matmul (library routines) in
+                               the reference's op order; closed forms (equal
+                               scores give 1/S; one dominant key takes ~1)
 =============================  =================================================
 """
 
@@ -625,3 +628,35 @@ def grouped_swiglu(x, ids, mask, w1, w3, w2, dt: str = BF16):
         if len(b):
             out[b, s] = swiglu_expert(x[b], w1[e], w3[e], w2[e], dt)[0]
     return out
+
+
+# ---------------------------------------------------------------------------
+# importance for the expert keep rule: last-query attention probabilities
+# ---------------------------------------------------------------------------
+def last_query_importance(q, k, n_kv_heads: int, scale: float, score_dt: str, key_mask=None, out_len=None):
+    """q [B, H, D], k [B, S, Hkv, D] -> [B, out_len] float64: per head, the
+    softmax over keys of the last query's scores, averaged over heads, for
+    the last ``out_len`` keys.  score_dt = the model dtype (scores rounded
+    after the dot product and again after the scaling, as
+    hybrid_attention.py:111-146 does) or F32 (deepseek_attention.py:206-249);
+    masked keys (key_mask False) get probability 0."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    b, h, d = q.shape
+    s = k.shape[1]
+    groups = h // n_kv_heads
+    kk = np.repeat(k, groups, axis=2)  # [B, S, H, D]: head h reads KV head h // groups
+    dot = np.einsum("bhd,bshd->bhs", q, kk)
+    if score_dt == F32:
+        sc = f32(f32(dot) * np.float32(scale))
+    else:
+        sc = round_to(round_to(dot, score_dt) * np.float64(np.float32(scale)), score_dt)
+    valid = np.ones((b, s), dtype=bool) if key_mask is None else np.asarray(key_mask, dtype=bool)
+    sc = np.where(valid[:, None, :], sc, -np.inf)
+    m = sc.max(axis=2, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
+    e = np.where(valid[:, None, :], np.exp(sc - m), 0.0)
+    tot = e.sum(axis=2, keepdims=True)
+    p = np.where(tot > 0, e / np.where(tot > 0, tot, 1.0), 0.0)
+    out_len = s if out_len is None else out_len
+    return p[:, :, s - out_len:].mean(axis=1)

@@ -22,6 +22,7 @@ TM_DT_F32, TM_DT_F16, TM_DT_BF16 = 0, 1, 2
 TM_CMP_GE, TM_CMP_GT = 0, 1
 TM_METRIC_L2, TM_METRIC_DOT = 0, 1
 TM_TARGET_ONE, TM_TARGET_ORIG_SUM, TM_TARGET_GIVEN = 0, 1, 2
+TM_SCORE_MODEL, TM_SCORE_F32 = 0, 1
 
 _DTYPE_TAG = {torch.float32: TM_DT_F32, torch.float16: TM_DT_F16, torch.bfloat16: TM_DT_BF16}
 
@@ -80,6 +81,9 @@ PROTOTYPES = {
     "tm_keep_select": (C.c_int, [vp, i64, i64, i64, vp, vp, sz, vp]),
     "tm_gather_combine": (C.c_int, [i32, i64, i32, vp, vp, i64, i64, vp, i64, i32, vp, i64, i64, vp, vp, i64, i32,
                                     vp, i64, vp, i64, vp]),
+    "tm_importance_workspace_size": (sz, [i64, i32, i64]),
+    "tm_last_query_importance": (C.c_int, [i32, vp, i64, i64, vp, i64, i64, i64, i64, i32, i32, i32, i64, f32, i32,
+                                           vp, i64, i64, vp, i64, vp, sz, vp]),
     "tm_swiglu_workspace_size": (sz, [i64, i32, i32]),
     "tm_expert_swiglu": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, i32, vp, i64, vp, sz, vp]),
     "tm_group_slots_tiles": (i64, [i64, i32]),

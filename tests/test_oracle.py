@@ -459,3 +459,51 @@ def test_grouped_swiglu_regroups_pairs():
                 assert np.all(np.isnan(out[bb, s]))
     tok = O.grouped_swiglu(x, ids, mask[:, 0], w1, w3, w2, O.F32)  # per-token mask covers every slot
     assert np.isnan(tok).any(axis=2).sum() == (~mask[:, 0]).sum() * K
+
+
+# ------------------------------------------- importance: last-query attention
+def test_last_query_importance_matches_torch_softmax():
+    """Against the reference's op sequence written with torch library calls
+    (matmul of the model-dtype tensors, * scaling, softmax(dtype=float32),
+    mean over heads; repeat_interleave for grouped KV heads), and the fp32
+    variant with a key padding mask (masked_fill min, softmax, masked_fill 0,
+    last query_length keys)."""
+    import torch
+
+    rng = np.random.default_rng(13)
+    B, H, HKV, D, S = 2, 8, 2, 64, 40
+    q = O.round_to(rng.normal(size=(B, H, D)), O.BF16)
+    k = O.round_to(rng.normal(size=(B, S, HKV, D)), O.BF16)
+    scale = D ** -0.5
+    got = O.last_query_importance(q, k, HKV, scale, O.BF16)
+    tq = torch.from_numpy(q).to(torch.bfloat16)[:, :, None, :]                   # [B, H, 1, D]
+    tk = torch.from_numpy(k).to(torch.bfloat16).transpose(1, 2)                  # [B, HKV, S, D]
+    tk = torch.repeat_interleave(tk, dim=1, repeats=H // HKV)
+    score = torch.matmul(tq.float(), tk.float().transpose(2, 3)).to(torch.bfloat16) * scale  # bf16 rounding twice
+    want = torch.softmax(score, dim=-1, dtype=torch.float32).mean(dim=1).squeeze(1).double().numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-9)
+
+    mask = rng.random((B, S)) < 0.8
+    got = O.last_query_importance(q, k, HKV, scale, O.F32, key_mask=mask, out_len=17)
+    tqf = torch.from_numpy(q).float()
+    tkf = torch.from_numpy(np.repeat(k, H // HKV, axis=2)).float()
+    sc = torch.einsum("bhd,bkhd->bhk", tqf, tkf) * float(scale)
+    km = torch.from_numpy(mask)
+    sc = sc.masked_fill(~km[:, None, :], torch.finfo(sc.dtype).min)
+    p = torch.softmax(sc, dim=-1, dtype=torch.float32).masked_fill(~km[:, None, :], 0.0)
+    want = p[:, :, -17:].mean(dim=1).double().numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-9)
+
+
+def test_last_query_importance_closed_forms():
+    """Equal scores spread 1/S over the keys; one key whose score dominates
+    takes ~all the mass; a fully masked row gives zeros."""
+    B, H, D, S = 1, 4, 64, 10
+    q = np.zeros((B, H, D)); q[..., 0] = 1.0
+    k = np.zeros((B, S, 1, D)); k[..., 0] = 2.0
+    np.testing.assert_allclose(O.last_query_importance(q, k, 1, 1.0, O.F32), np.full((1, S), 1.0 / S))
+    k[0, 3, 0, 0] = 100.0
+    got = O.last_query_importance(q, k, 1, 1.0, O.F32)
+    assert got[0, 3] >= 1 - 1e-12 and np.all(got[0, np.arange(S) != 3] < 1e-40)
+    got = O.last_query_importance(q, k, 1, 1.0, O.F32, key_mask=np.zeros((1, S), dtype=bool))
+    assert np.all(got == 0.0)
