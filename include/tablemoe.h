@@ -317,6 +317,29 @@ int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden, const uin
                       int64_t ld_o, tm_stream_t stream);
 
 /* ======================================================================
+ * Online window, decode step of one token: the slot combine of
+ * tm_slot_combine (n_tokens = 1) and the ring write of tm_online_update in
+ * one launch.  Replaces the tail of QwenMoeWrapperCached._forward_decode_bs1
+ * (table_moe/models/qwen3_vl_moe/cached_layers.py:213-267: online/offline
+ * fills of collected, effective weights, matmul) together with
+ * update_online_cache_bs1 (table_moe/cache_engine/manager.py:89-106).
+ * Slot sources, coefficients and `out` are exactly tm_slot_combine's; then
+ * ring row `ring_row` takes x (online_keys row stride = hidden), the slot
+ * ids (-1 where the slot did not survive) and each slot's source row (zeros
+ * where dropped).  A source in the overwritten row itself is read first.
+ * top_k = online_topk <= 8; 16-byte aligned rows.  The caller advances its
+ * ring pointer (as the reference's host-side online_ptr).
+ * ====================================================================== */
+int tm_decode_combine_update(int32_t dtype, int32_t top_k, int32_t hidden, const float *weights,
+                             const uint8_t *compute_mask, const void *computed, int64_t cs_s, const uint8_t *off_hit,
+                             const int64_t *off_idx, const int64_t *sel, const uint8_t *is_vision, const void *values,
+                             int64_t n_experts, int64_t n_centroids, int64_t vs_e, int64_t vs_m, int64_t vs_c,
+                             const uint8_t *on_hit, const int64_t *on_idx, const int64_t *on_slot,
+                             void *online_values, int64_t n_online, int32_t online_topk, int64_t ov_w, int64_t ov_s,
+                             int32_t target_mode, const void *residual, void *out, const void *x, void *online_keys,
+                             int64_t *online_ids, int64_t ring_row, tm_stream_t stream);
+
+/* ======================================================================
  * Importance for the expert-level keep rule: attention probabilities of the
  * last query over every key, averaged over heads.
  * Replaces HybridQwen3Attention._compute_and_cache_importance

@@ -387,6 +387,96 @@ __global__ __launch_bounds__(kThreads) void slot_combine_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Decode step of one token (reference _forward_decode_bs1,
+// cached_layers.py:161-269): the slot combine above plus the ring write of
+// update_online_cache_bs1 (manager.py:89-106) in one launch.  Ring row r
+// takes the token's hidden row, its expert ids (-1 for slots that did not
+// survive) and each slot's source row (zeros when dropped).  Every thread
+// loads all sources of its 8 columns before it writes them, so a source in
+// ring row r itself (the window's oldest entry) is read before it is
+// overwritten; other threads never touch those columns.
+// ---------------------------------------------------------------------------
+constexpr int kDecodeSlots = 8;
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void slot_combine_update_kernel(
+    int top_k, int hidden, const float *__restrict__ w, const uint8_t *__restrict__ compute_mask,
+    const typename Elem<DT>::T *__restrict__ computed, int64_t cs_s, const uint8_t *__restrict__ off_hit,
+    const int64_t *__restrict__ off_idx, const int64_t *__restrict__ sel, const uint8_t *__restrict__ is_vision,
+    const typename Elem<DT>::T *__restrict__ values, int64_t n_exp, int64_t n_cent, int64_t vs_e, int64_t vs_m,
+    int64_t vs_c, const uint8_t *__restrict__ on_hit, const int64_t *__restrict__ on_idx,
+    const int64_t *__restrict__ on_slot, typename Elem<DT>::T *online_values, int64_t n_online, int online_topk,
+    int64_t ov_w, int64_t ov_s, int target_mode, const typename Elem<DT>::T *__restrict__ residual,
+    typename Elem<DT>::T *__restrict__ out, const typename Elem<DT>::T *__restrict__ x,
+    typename Elem<DT>::T *__restrict__ ring_keys, int64_t *__restrict__ ring_ids, int64_t r) {
+  using T = typename Elem<DT>::T;
+  __shared__ const T *s_src[kDecodeSlots];
+  __shared__ float s_coef[kDecodeSlots];
+  if (threadIdx.x == 0) {  // the source and coefficient of each slot, as slot_combine_kernel forms them
+    float wv[kDecodeSlots];
+    float kept = 0.f, full = 0.f;
+    const int m = (is_vision == nullptr || is_vision[0]) ? 0 : 1;
+    for (int s = 0; s < top_k; ++s) {
+      const T *p = nullptr;
+      if (off_hit && off_hit[s]) {
+        const int64_t e = sel[s], c = off_idx[s];
+        if (e >= 0 && e < n_exp && c >= 0 && c < n_cent) p = values + e * vs_e + m * vs_m + c * vs_c;
+      } else if (on_hit && on_hit[s]) {
+        const int64_t rr = on_idx[0], j = on_slot[s];
+        if (rr >= 0 && rr < n_online && j >= 0 && j < online_topk) p = online_values + rr * ov_w + j * ov_s;
+      } else if (compute_mask && compute_mask[s]) {
+        p = computed + s * cs_s;
+      }
+      wv[s] = w[s];
+      full += wv[s];
+      s_src[s] = p;
+      if (p) kept += wv[s];
+    }
+    for (int s = 0; s < top_k; ++s) {
+      float c = 0.f;
+      if (s_src[s] && kept > 0.f) {
+        c = wv[s] / kept;
+        c = (target_mode == TM_TARGET_ORIG_SUM) ? c * full : tm_round<DT>(c);
+      }
+      s_coef[s] = c;
+      ring_ids[r * online_topk + s] = s_src[s] ? sel[s] : -1;
+    }
+  }
+  __syncthreads();
+  for (int h0 = threadIdx.x * 8; h0 < hidden; h0 += kThreads * 8) {
+    float v[kDecodeSlots][8];
+#pragma unroll
+    for (int s = 0; s < kDecodeSlots; ++s) {
+      if (s < top_k && s_src[s]) {  // uniform
+        tm_load8<DT>(s_src[s] + h0, v[s]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[s][i] = 0.f;
+      }
+    }
+    float xin[8], acc[8];
+    tm_load8<DT>(x + h0, xin);
+    if (residual) {
+      tm_load8<DT>(residual + h0, acc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < kDecodeSlots; ++s)
+      if (s < top_k && s_src[s]) {  // sources in slot order, as combine_row adds them
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(s_coef[s], v[s][i], acc[i]);
+      }
+    tm_store8<DT>(out + h0, acc);
+    tm_store8<DT>(ring_keys + r * (int64_t)hidden + h0, xin);
+#pragma unroll
+    for (int s = 0; s < kDecodeSlots; ++s)
+      if (s < top_k) tm_store8<DT>(online_values + r * ov_w + s * ov_s + h0, v[s]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // a12: ring write of the online window
 // ---------------------------------------------------------------------------
 template <int DT, bool VEC>
@@ -600,6 +690,51 @@ extern "C" int tm_online_update(int32_t dtype, const void *hidden, int64_t ld_h,
     if (vec) launch(std::true_type{});
     else launch(std::false_type{});
     TM_LAUNCH_CHECK("tm_online_update");
+    return TM_OK;
+  });
+}
+
+extern "C" int tm_decode_combine_update(int32_t dtype, int32_t top_k, int32_t hidden, const float *weights,
+                                        const uint8_t *compute_mask, const void *computed, int64_t cs_s,
+                                        const uint8_t *off_hit, const int64_t *off_idx, const int64_t *sel,
+                                        const uint8_t *is_vision, const void *values, int64_t n_experts,
+                                        int64_t n_centroids, int64_t vs_e, int64_t vs_m, int64_t vs_c,
+                                        const uint8_t *on_hit, const int64_t *on_idx, const int64_t *on_slot,
+                                        void *online_values, int64_t n_online, int32_t online_topk, int64_t ov_w,
+                                        int64_t ov_s, int32_t target_mode, const void *residual, void *out,
+                                        const void *x, void *online_keys, int64_t *online_ids, int64_t ring_row,
+                                        tm_stream_t stream) {
+  TM_REQUIRE(top_k >= 1 && top_k <= kDecodeSlots && hidden > 0 && hidden % 8 == 0 && top_k == online_topk &&
+                 n_online >= 1 && ring_row >= 0 && ring_row < n_online && ov_w >= (int64_t)top_k * ov_s &&
+                 ov_s >= hidden,
+             TM_EINVAL_SHAPE, "tm_decode_combine_update: bad sizes (top_k <= %d, hidden %% 8 == 0, ring row in range)",
+             kDecodeSlots);
+  TM_REQUIRE(target_mode == TM_TARGET_ONE || target_mode == TM_TARGET_ORIG_SUM, TM_EINVAL_ARG,
+             "tm_decode_combine_update: bad target mode %d", target_mode);
+  TM_REQUIRE(weights && out && x && online_values && online_keys && online_ids, TM_EINVAL_ARG,
+             "tm_decode_combine_update: null pointer");
+  TM_REQUIRE(!compute_mask || computed, TM_EINVAL_ARG, "tm_decode_combine_update: compute_mask needs computed");
+  TM_REQUIRE(!off_hit || (off_idx && sel && values), TM_EINVAL_ARG,
+             "tm_decode_combine_update: off_hit needs off_idx, sel and values");
+  TM_REQUIRE(sel, TM_EINVAL_ARG, "tm_decode_combine_update: sel is required (the ring stores the ids)");
+  TM_REQUIRE(!on_hit || (on_idx && on_slot), TM_EINVAL_ARG, "tm_decode_combine_update: on_hit needs on_idx, on_slot");
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    using T = typename Elem<DT>::T;
+    const int E = Elem<DT>::kBytes;
+    const bool aligned = tm_aligned16(out) && tm_aligned16(x) && tm_aligned16(online_keys) &&
+                         tm_aligned16(online_values) && (ov_w * E) % 16 == 0 && (ov_s * E) % 16 == 0 &&
+                         (computed == nullptr || (tm_aligned16(computed) && (cs_s * E) % 16 == 0)) &&
+                         (values == nullptr || (tm_aligned16(values) && (vs_e * E) % 16 == 0 &&
+                                                (vs_m * E) % 16 == 0 && (vs_c * E) % 16 == 0)) &&
+                         (residual == nullptr || tm_aligned16(residual));
+    TM_REQUIRE(aligned, TM_EINVAL_SHAPE, "tm_decode_combine_update: rows must be 16-byte aligned");
+    hipLaunchKernelGGL((slot_combine_update_kernel<DT>), dim3(1), dim3(kThreads), 0, tm_hip_stream(stream), top_k,
+                       hidden, weights, compute_mask, static_cast<const T *>(computed), cs_s, off_hit, off_idx, sel,
+                       is_vision, static_cast<const T *>(values), n_experts, n_centroids, vs_e, vs_m, vs_c, on_hit,
+                       on_idx, on_slot, static_cast<T *>(online_values), n_online, online_topk, ov_w, ov_s,
+                       target_mode, static_cast<const T *>(residual), static_cast<T *>(out),
+                       static_cast<const T *>(x), static_cast<T *>(online_keys), online_ids, ring_row);
+    TM_LAUNCH_CHECK("tm_decode_combine_update");
     return TM_OK;
   });
 }

@@ -197,6 +197,48 @@ class HybridStorageManager:
             N.ptr(self.online_expert_ids), N.ptr(self.online_values), N.stream(dev),
         )
 
+    @torch.no_grad()
+    def combine_and_update_bs1(self, hidden_state, routing_weights_row, selected_experts_row, is_vision,
+                               compute_mask_row, computed, on_hit, on_idx, on_slot, off_hit, off_idx, out,
+                               target: str = "one"):
+        """The decode step's tail for one token in one launch
+        (tm_decode_combine_update): out = sum of the surviving slots' sources
+        (computed / online window / offline table) with renormalised weights,
+        then the token enters the online window (ring row online_ptr, as
+        update_online_cache_bs1 with the survivor mask).  Without an online
+        window only the combine runs (tm_slot_combine)."""
+        dev = N.require_hip(hidden_state, routing_weights_row, selected_experts_row, out)
+        k = int(selected_experts_row.numel())
+        mode = N.TM_TARGET_ORIG_SUM if target == "orig_sum" else N.TM_TARGET_ONE
+        w = routing_weights_row.reshape(-1).to(torch.float32).contiguous()
+        sel = selected_experts_row.reshape(-1).to(torch.long).contiguous()
+        u8 = lambda t: None if t is None else N.as_u8(t.reshape(-1).to(device=dev, dtype=torch.bool).contiguous())  # noqa: E731
+        cm, oh, fh = u8(compute_mask_row), u8(on_hit), u8(off_hit)
+        isv = None if is_vision is None else u8(is_vision)
+        ix = lambda t: None if t is None else t.reshape(-1).to(device=dev, dtype=torch.long).contiguous()  # noqa: E731
+        oi, osl, fi = ix(on_idx), ix(on_slot), ix(off_idx)
+        x = hidden_state.reshape(-1)
+        comp = None if computed is None else computed.reshape(k, -1)
+        v = self.values_buffer
+        if self.enable_online:
+            ov = self.online_values
+            N.call("tm_decode_combine_update", N.dtype_tag(self.dtype), k, self.hidden_dim, N.ptr(w), N.ptr(cm),
+                   N.ptr(comp), 0 if comp is None else comp.stride(0), N.ptr(fh), N.ptr(fi), N.ptr(sel), N.ptr(isv),
+                   N.ptr(v), v.shape[0], v.shape[2], v.stride(0), v.stride(1), v.stride(2), N.ptr(oh), N.ptr(oi),
+                   N.ptr(osl), N.ptr(ov), self.online_size, ov.shape[1], ov.stride(0), ov.stride(1), mode, None,
+                   N.ptr(out), N.ptr(x), N.ptr(self.online_keys), N.ptr(self.online_expert_ids),
+                   int(self.online_ptr), N.stream(dev))
+            self.online_ptr = (self.online_ptr + 1) % self.online_size
+            if self.online_ptr == 0:
+                self.online_full = True
+        else:
+            N.call("tm_slot_combine", N.dtype_tag(self.dtype), 1, k, self.hidden_dim, N.ptr(w), k, N.ptr(cm),
+                   N.ptr(comp), 0, 0 if comp is None else comp.stride(0), N.ptr(fh), N.ptr(fi), N.ptr(sel), k,
+                   N.ptr(isv), N.ptr(v), v.shape[0], v.shape[2], v.stride(0), v.stride(1), v.stride(2), None, None,
+                   None, None, 0, 1, 0, 0, mode, None, 0, N.ptr(out), out.stride(0) if out.dim() > 1 else
+                   self.hidden_dim, N.stream(dev))
+        return out
+
     # ---------------------------------------------------------------- gather
     def _gather_into(self, expert_ids, modality_ids, modality, cluster_ids, dst_rows, out):
         dev = out.device

@@ -624,3 +624,63 @@ def test_layer_graph_replays_match_eager(hip_device, cfg, n, nn):
         assert torch.isfinite(junk)
         for key in ("weights", "ids", "q", "dist", "idx", "keep", "out"):
             assert torch.equal(res[key], ref[key]), (rep, key)
+
+
+@pytest.mark.parametrize("hazard", [True, False])
+def test_decode_combine_update_matches_unfused(hip_device, hazard):
+    """The fused decode tail (tm_decode_combine_update) equals tm_slot_combine
+    followed by update_online_cache_bs1 with the collected slot rows and the
+    survivor mask, bit for bit, in the output and in the whole ring state --
+    also when an online source is the ring row being overwritten."""
+    from table_moe import _native as N
+
+    dev = hip_device
+    mgr, g = _mode_r_manager(dev, seed=201)
+    H, k, W = 512, 8, 64
+    hist = torch.randn(W, H, generator=g).to(torch.bfloat16).to(dev)
+    hist_ids = torch.stack([torch.randperm(16, generator=g)[:k] for _ in range(W)]).to(dev)
+    mgr.update_online_cache(hist, hist_ids, torch.randn(W, k, H, generator=g).to(torch.bfloat16).to(dev))
+    assert mgr.online_ptr == 0 and mgr.online_full
+    x = torch.randn(H, generator=g).to(torch.bfloat16).to(dev)
+    sel = torch.randperm(16, generator=g)[:k].to(dev)
+    w = torch.softmax(torch.randn(k, generator=g), 0).to(dev)
+    compute = torch.tensor([1, 1, 1, 1, 0, 0, 0, 0], dtype=torch.bool, device=dev)
+    computed = torch.randn(k, H, generator=g).to(torch.bfloat16).to(dev)
+    on_hit = torch.tensor([0, 0, 0, 0, 1, 0, 1, 0], dtype=torch.bool, device=dev)
+    on_idx = torch.tensor([0 if hazard else 17], device=dev)  # row 0 is the next ring row
+    on_slot = torch.tensor([0, 0, 0, 0, 2, 0, 7, 0], device=dev)
+    off_hit = torch.tensor([0, 0, 0, 0, 0, 1, 0, 0], dtype=torch.bool, device=dev)
+    off_idx = torch.tensor([0, 0, 0, 0, 0, 33, 0, 0], device=dev)
+    vis = torch.tensor(False, device=dev)
+    state0 = [t.clone() for t in (mgr.online_keys, mgr.online_expert_ids, mgr.online_values)]
+
+    out_f = torch.empty(H, dtype=torch.bfloat16, device=dev)
+    mgr.combine_and_update_bs1(x, w, sel, vis, compute, computed, on_hit, on_idx, on_slot, off_hit, off_idx, out_f)
+    torch.cuda.synchronize()
+    fused = [t.clone() for t in (mgr.online_keys, mgr.online_expert_ids, mgr.online_values)]
+    assert mgr.online_ptr == 1
+
+    for t, s0 in zip((mgr.online_keys, mgr.online_expert_ids, mgr.online_values), state0):
+        t.copy_(s0)
+    mgr.online_ptr = 0
+    out_u = torch.empty(1, H, dtype=torch.bfloat16, device=dev)
+    v = mgr.values_buffer
+    ov = mgr.online_values
+    u8 = N.as_u8
+    N.call("tm_slot_combine", N.dtype_tag(torch.bfloat16), 1, k, H, N.ptr(w.float()), k, N.ptr(u8(compute)),
+           N.ptr(computed), 0, computed.stride(0), N.ptr(u8(off_hit)), N.ptr(off_idx), N.ptr(sel), k,
+           N.ptr(u8(vis.reshape(1))), N.ptr(v), v.shape[0], v.shape[2], v.stride(0), v.stride(1), v.stride(2),
+           N.ptr(u8(on_hit)), N.ptr(on_idx), N.ptr(on_slot), N.ptr(ov), W, ov.shape[1], ov.stride(0), ov.stride(1),
+           N.TM_TARGET_ONE, None, 0, N.ptr(out_u), H, N.stream(dev))
+    collected = torch.zeros(k, H, dtype=torch.bfloat16, device=dev)
+    collected[:4] = computed[:4]
+    collected[4] = state0[2][on_idx[0], 2]
+    collected[6] = state0[2][on_idx[0], 7]
+    collected[5] = v[sel[5], 1, 33]
+    survivor = compute | on_hit | off_hit
+    mgr.update_online_cache_bs1(x, sel, collected, survivor)
+    torch.cuda.synchronize()
+    assert torch.equal(out_f, out_u[0])
+    for a, b_ in zip(fused, (mgr.online_keys, mgr.online_expert_ids, mgr.online_values)):
+        assert torch.equal(a, b_)
+    assert int(mgr.online_expert_ids[0, 7]) == -1 and torch.all(mgr.online_values[0, 7] == 0)
