@@ -17,7 +17,9 @@ device time of each stage's C-ABI call (graphs of 32 back-to-back calls timed
 with HIP events on the stream the kernels run on), the roofline of the
 dominant call (HBM bytes from the committed rocprofv3 PMC summary when
 present), the decode (N=32, C=16384, top-4) layer, and the reference path
-restated on the host CPU (oracle, numpy fp32) as the CPU baseline.
+restated on the host CPU (oracle, numpy fp32) as the CPU baseline, and the
+config-5 recompute (grouped SwiGLU expert MLP of the kept tokens' slots plus
+the shared experts) in its own "recompute" object.
 """
 
 from __future__ import annotations
@@ -207,6 +209,83 @@ def stage_kernel_times(reps, tables, outs, topk, nn, kr, launches=32, replays=3)
     return out
 
 
+def run_recompute_bench(steps, warmup):
+    """Config 5 recompute (DeepSeek-VL2-style layer, hidden 2560, 64 routed
+    experts top-6 + shared experts, intermediate 1536, N=4096): the kept
+    tokens' routed slots through tm_group_slots + tm_grouped_swiglu (written
+    in the slot layout the combine reads), and the shared-expert MLP (one
+    SwiGLU of intermediate 2 x 1536) over every token.  The keep set and the
+    router ids come from the config-5 table layer itself; weights are
+    random-init N(0, 0.02) bf16 (no checkpoint offline).  Timed as graph
+    replays with HIP events on the calls' stream."""
+    import torch
+
+    from table_moe.cache_engine import GlobalTable
+    from table_moe.ops import GroupedExperts, expert_swiglu
+    from table_moe.synth import make_workload
+
+    dev = torch.device("cuda:0")
+    wl = make_workload(5)
+    cfg = wl.cfg
+    d = wl.to(dev)
+    tbl = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
+    res = tbl.layer_forward(d.x, d.is_vision, d.logits, d.slot_out, d.residual, cfg["router_top_k"], 1,
+                            cfg["keep_rate"])
+    keep, ids = res["keep"].clone(), res["ids"].clone()
+    n, h, e, k, inter = cfg["n"], cfg["hidden"], cfg["n_experts"], cfg["router_top_k"], 1536
+    shared_inter = 2 * inter
+    g = torch.Generator(device=dev).manual_seed(55)
+    rnd = lambda *shape: (torch.randn(*shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)  # noqa: E731
+    ge = GroupedExperts(rnd(e, inter, h), rnd(e, inter, h), rnd(e, h, inter))
+    s1, s3, s2 = rnd(shared_inter, h), rnd(shared_inter, h), rnd(h, shared_inter)
+    slot_out = torch.empty(n, k, h, dtype=torch.bfloat16, device=dev)
+    shared_out = torch.empty(n, h, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(n * shared_inter * 2, dtype=torch.uint8, device=dev)
+
+    def timed(fn, reps):
+        for _ in range(max(1, warmup // 4)):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(graph):
+            fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return 1000.0 * e0.elapsed_time(e1) / reps
+
+    reps = max(3, min(steps, 20))
+    routed_us = timed(lambda: ge.forward(d.x, ids, keep, slot_out), reps)
+    shared_us = timed(lambda: expert_swiglu(d.x, s1, s3, s2, out=shared_out, workspace=ws), reps)
+    rows = int(keep.sum().item()) * k
+    routed_flops = rows * 6.0 * h * inter
+    shared_flops = n * 6.0 * h * shared_inter
+    tf = lambda f, us: f / (us * 1e-6) / 1e12  # noqa: E731
+    return {
+        "workload": "config 5 recompute: N=4096, hidden 2560, 64 routed experts top-6 (kept tokens' slots, keep set "
+                    "from the config-5 table layer) + shared experts (SwiGLU intermediate 3072, all tokens), routed "
+                    "intermediate 1536, random-init bf16 weights",
+        "routed_rows": rows,
+        "routed_us": routed_us,
+        "routed_tflops": tf(routed_flops, routed_us),
+        "routed_mfma_frac": tf(routed_flops, routed_us) / BF16_PEAK_TFLOPS,
+        "routed_weight_GBps": 3 * e * h * inter * 2 / (routed_us * 1e-6) / 1e9,
+        "shared_us": shared_us,
+        "shared_tflops": tf(shared_flops, shared_us),
+        "shared_mfma_frac": tf(shared_flops, shared_us) / BF16_PEAK_TFLOPS,
+    }
+
+
 COPY_CAL_BYTES = 256 << 20  # bytes read (and written) by the calibration copy
 
 
@@ -390,6 +469,10 @@ def main() -> int:
             "layer_hbm_GBps": sum(dec["bytes"].values()) / (dec["graph_device_us"] * 1e-6) / 1e9,
         },
     }
+    rec = run_recompute_bench(args.steps, args.warmup)
+    log(f"config 5 recompute: routed {rec['routed_us']:.1f} us ({rec['routed_tflops']:.0f} TFLOP/s), shared "
+        f"{rec['shared_us']:.1f} us ({rec['shared_tflops']:.0f} TFLOP/s)")
+    result["recompute"] = rec
     copy_calibration()
     if not args.no_cpu:
         log("timing the CPU baseline")

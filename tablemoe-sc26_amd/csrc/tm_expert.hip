@@ -208,13 +208,11 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
   const int tid = threadIdx.x;
   for (int e = tid; e < n_experts; e += kGroupThreads) hist[e] = 0;
   __syncthreads();
-  const int64_t total = n * top_k;
-  for (int64_t p = tid; p < total; p += kGroupThreads) {
-    const int64_t b = p / top_k;
-    const int s = (int)(p - b * top_k);
-    const int64_t e = ids[b * ld_ids + s];
-    if (mask[b * ms_b + s * ms_s] && e >= 0 && e < n_experts) atomicAdd(&hist[e], 1);
-  }
+  for (int64_t b = tid; b < n; b += kGroupThreads)  // a token per thread, its slots in order
+    for (int s = 0; s < top_k; ++s) {
+      const int64_t e = ids[b * ld_ids + s];
+      if (mask[b * ms_b + s * ms_s] && e >= 0 && e < n_experts) atomicAdd(&hist[e], 1);
+    }
   __syncthreads();
   if (tid == 0) {  // offsets and tile bases (n_experts <= 1024: a short serial scan)
     int32_t run = 0, tr = 0;
@@ -240,16 +238,15 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
     }
   }
   __syncthreads();  // cursor[] is read above before the placement below advances it
-  for (int64_t p = tid; p < total; p += kGroupThreads) {
-    const int64_t b = p / top_k;
-    const int s = (int)(p - b * top_k);
-    const int64_t e = ids[b * ld_ids + s];
-    if (mask[b * ms_b + s * ms_s] && e >= 0 && e < n_experts) {
-      const int32_t pos = atomicAdd(&cursor[e], 1);
-      row_token[pos] = (int32_t)b;
-      row_out[pos] = b * so_b + (int64_t)s * so_s;
+  for (int64_t b = tid; b < n; b += kGroupThreads)
+    for (int s = 0; s < top_k; ++s) {
+      const int64_t e = ids[b * ld_ids + s];
+      if (mask[b * ms_b + s * ms_s] && e >= 0 && e < n_experts) {
+        const int32_t pos = atomicAdd(&cursor[e], 1);
+        row_token[pos] = (int32_t)b;
+        row_out[pos] = b * so_b + (int64_t)s * so_s;
+      }
     }
-  }
 }
 
 template <int DT, int NB, int MODE>
