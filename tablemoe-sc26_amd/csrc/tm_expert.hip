@@ -197,6 +197,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
 // per-token flag); ids outside [0, n_experts) are skipped.
 constexpr int kGroupThreads = 1024;
 constexpr int kMaxExperts = 1024;
+constexpr int kGroupTok = 4;    // tokens per thread on the register path (n <= 4096)
+constexpr int kGroupSlots = 8;  // slots per token on the register path (top_k <= 8)
 
 __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
     const int64_t *__restrict__ ids, int64_t n, int top_k, int64_t ld_ids, const uint8_t *__restrict__ mask,
@@ -207,12 +209,38 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
   __shared__ int32_t tile_base[kMaxExperts + 1];
   const int tid = threadIdx.x;
   for (int e = tid; e < n_experts; e += kGroupThreads) hist[e] = 0;
-  __syncthreads();
-  for (int64_t b = tid; b < n; b += kGroupThreads)  // a token per thread, its slots in order
-    for (int s = 0; s < top_k; ++s) {
-      const int64_t e = ids[b * ld_ids + s];
-      if (mask[b * ms_b + s * ms_s] && e >= 0 && e < n_experts) atomicAdd(&hist[e], 1);
+  // Each thread keeps the experts of its tokens (b = tid + 1024 j, j < kGroupTok)
+  // in registers: all of their loads are issued before the first count.
+  int32_t ex[kGroupTok][kGroupSlots];
+  const bool fast = n <= (int64_t)kGroupTok * kGroupThreads && top_k <= kGroupSlots;  // uniform
+  if (fast) {
+#pragma unroll
+    for (int j = 0; j < kGroupTok; ++j) {
+      const int64_t b = tid + (int64_t)kGroupThreads * j;
+      const int64_t bb = b < n ? b : n - 1;
+#pragma unroll
+      for (int s = 0; s < kGroupSlots; ++s) {
+        const int ss = s < top_k ? s : top_k - 1;
+        const int64_t e = ids[bb * ld_ids + ss];
+        const bool use = b < n && s < top_k && mask[bb * ms_b + ss * ms_s] && e >= 0 && e < n_experts;
+        ex[j][s] = use ? (int32_t)e : -1;
+      }
     }
+  }
+  __syncthreads();
+  if (fast) {
+#pragma unroll
+    for (int j = 0; j < kGroupTok; ++j)
+#pragma unroll
+      for (int s = 0; s < kGroupSlots; ++s)
+        if (ex[j][s] >= 0) atomicAdd(&hist[ex[j][s]], 1);
+  } else {
+    for (int64_t b = tid; b < n; b += kGroupThreads)  // a token per thread, its slots in order
+      for (int s = 0; s < top_k; ++s) {
+        const int64_t e = ids[b * ld_ids + s];
+        if (mask[b * ms_b + s * ms_s] && e >= 0 && e < n_experts) atomicAdd(&hist[e], 1);
+      }
+  }
   __syncthreads();
   if (tid == 0) {  // offsets and tile bases (n_experts <= 1024: a short serial scan)
     int32_t run = 0, tr = 0;
@@ -238,15 +266,28 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
     }
   }
   __syncthreads();  // cursor[] is read above before the placement below advances it
-  for (int64_t b = tid; b < n; b += kGroupThreads)
-    for (int s = 0; s < top_k; ++s) {
-      const int64_t e = ids[b * ld_ids + s];
-      if (mask[b * ms_b + s * ms_s] && e >= 0 && e < n_experts) {
-        const int32_t pos = atomicAdd(&cursor[e], 1);
-        row_token[pos] = (int32_t)b;
-        row_out[pos] = b * so_b + (int64_t)s * so_s;
+  if (fast) {
+#pragma unroll
+    for (int j = 0; j < kGroupTok; ++j)
+#pragma unroll
+      for (int s = 0; s < kGroupSlots; ++s)
+        if (ex[j][s] >= 0) {
+          const int64_t b = tid + (int64_t)kGroupThreads * j;
+          const int32_t pos = atomicAdd(&cursor[ex[j][s]], 1);
+          row_token[pos] = (int32_t)b;
+          row_out[pos] = b * so_b + (int64_t)s * so_s;
+        }
+  } else {
+    for (int64_t b = tid; b < n; b += kGroupThreads)
+      for (int s = 0; s < top_k; ++s) {
+        const int64_t e = ids[b * ld_ids + s];
+        if (mask[b * ms_b + s * ms_s] && e >= 0 && e < n_experts) {
+          const int32_t pos = atomicAdd(&cursor[e], 1);
+          row_token[pos] = (int32_t)b;
+          row_out[pos] = b * so_b + (int64_t)s * so_s;
+        }
       }
-    }
+  }
 }
 
 template <int DT, int NB, int MODE>

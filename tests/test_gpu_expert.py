@@ -48,14 +48,16 @@ def test_expert_swiglu_vs_oracle(hip_device, m, h, inter, dtype):
     assert_mlp_close(np64(y), want, dtype)
 
 
-def test_group_slots_buckets_every_pair(hip_device):
+@pytest.mark.parametrize("n,k", [(1000, 6), (4096, 8), (5000, 8), (300, 10)])
+def test_group_slots_buckets_every_pair(hip_device, n, k):
     """Counts, offsets, tiles and the (token, slot) -> row map of the device
-    grouping against a host bincount; every selected pair appears once."""
+    grouping against a host bincount; every selected pair appears once (the
+    register path up to 4096 tokens x 8 slots, the looped path beyond)."""
     from table_moe.ops import GroupedExperts
 
     dev = hip_device
-    g = torch.Generator().manual_seed(11)
-    n, k, e, h = 1000, 6, 64, 128
+    g = torch.Generator().manual_seed(11 + n + k)
+    e, h = 64, 128
     ids = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)])
     ids[5, 2] = -1  # out-of-range ids are skipped
     ids[6, 0] = e
