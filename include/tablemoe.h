@@ -471,10 +471,11 @@ typedef struct tm_layer_io {
  * (lets a binding check its mirror of the two structs). */
 size_t tm_struct_size(int32_t which);
 /* Workspace of tm_table_forward.  Its first 256 bytes hold arrival counters
- * (batches of at most 64 tokens reduce the projection across workgroups):
- * they must be zero before the first call on a workspace (allocate it
- * zero-filled) and every call leaves them zero.  Calls that share one
- * workspace must not overlap (one stream). */
+ * (batches of at most 64 tokens reduce the projection across workgroups;
+ * larger top-1 batches decode each query tile's search result in the tile's
+ * last workgroup): they must be zero before the first call on a workspace
+ * (allocate it zero-filled) and every call leaves them zero.  Calls that
+ * share one workspace must not overlap (one stream). */
 size_t tm_table_forward_workspace_size(const tm_table_layer *table, int64_t n_tokens, int32_t n_nearest);
 int tm_table_forward(const tm_table_layer *table, const tm_layer_io *io, void *workspace,
                      size_t workspace_bytes, void *const *stage_events, tm_stream_t stream);

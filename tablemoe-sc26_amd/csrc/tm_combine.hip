@@ -193,18 +193,64 @@ __global__ __launch_bounds__(kThreads) void gather_combine_fast_kernel(
 // accesses; gathered value rows use ordinary loads (centroids repeat).
 // Same arithmetic as gather_combine_fast_kernel: fp32 accumulation starting
 // from the residual, sources added in order with fmaf, one rounding.
-template <int DT, int TK, int NN>
+// Keep decision of token b when the keep set is ranked in the combine:
+// b is kept when fewer than n_keep tokens are ahead of it (a larger
+// distance, or the same at a lower index), the set the radix select gives.
+// dist: n contiguous floats, 16-byte aligned.
+struct RankKeep {
+  int64_t n;
+  int64_t n_keep;
+  uint8_t *keep_out;
+};
+
+__device__ __forceinline__ bool rank_keep(const float *__restrict__ dist, int64_t n, int64_t n_keep, int64_t b) {
+  __shared__ uint32_t s_ahead[kThreads / 64];
+  const uint32_t kb = tm_orderable(dist[b]);
+  uint32_t ahead = 0;
+  const float4 *d4 = reinterpret_cast<const float4 *>(dist);
+  const int64_t n4 = n >> 2;
+  for (int64_t i = threadIdx.x; i < n4; i += kThreads) {
+    const float4 v = d4[i];
+    const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t k = tm_orderable(e[u]);
+      const int64_t j = 4 * i + u;
+      ahead += (k > kb || (k == kb && j < b)) ? 1u : 0u;
+    }
+  }
+  for (int64_t j = 4 * n4 + threadIdx.x; j < n; j += kThreads) {
+    const uint32_t k = tm_orderable(dist[j]);
+    ahead += (k > kb || (k == kb && j < b)) ? 1u : 0u;
+  }
+  ahead = (uint32_t)__builtin_amdgcn_readlane((int)tm_wave_incl_scan(ahead), 63);
+  if ((threadIdx.x & 63) == 0) s_ahead[threadIdx.x >> 6] = ahead;
+  __syncthreads();
+  uint32_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) total += s_ahead[w];
+  return (int64_t)total < n_keep;
+}
+
+template <int DT, int TK, int NN, bool RANK>
 __global__ __launch_bounds__(kThreads) void gather_combine_tk_kernel(
     int hidden, const uint8_t *__restrict__ keep, const typename Elem<DT>::T *__restrict__ slot_out, int64_t so_b,
     int64_t so_s, const float *__restrict__ w, int64_t ld_w, const typename Elem<DT>::T *__restrict__ values,
     int64_t n_cent, int64_t ld_v, const int64_t *__restrict__ idx, const float *__restrict__ dist, int64_t ld_idx,
     const typename Elem<DT>::T *__restrict__ residual, int64_t ld_r, typename Elem<DT>::T *__restrict__ out,
-    int64_t ld_o) {
+    int64_t ld_o, RankKeep rk) {
   using T = typename Elem<DT>::T;
   const int64_t b = blockIdx.x;
   const T *res_row = residual ? residual + b * ld_r : nullptr;
   T *dst = out + b * ld_o;
-  if (keep[b]) {  // uniform
+  bool kept;
+  if constexpr (RANK) {
+    kept = rank_keep(dist, rk.n, rk.n_keep, b);
+    if (threadIdx.x == 0) rk.keep_out[b] = kept ? 1 : 0;
+  } else {
+    kept = keep[b] != 0;
+  }
+  if (kept) {  // uniform
     float coef[TK];
     float sum = 0.f;
 #pragma unroll
@@ -548,10 +594,10 @@ extern "C" int tm_gather_rows(int32_t dtype, const void *values, int64_t n_exper
 // Launch of the shape-specialised combine when (top_k, n_nearest) matches.
 #define TM_GC_TK(TK_, NN_)                                                                                     \
   if (top_k == TK_ && n_nearest == NN_) {                                                                      \
-    hipLaunchKernelGGL((gather_combine_tk_kernel<DT, TK_, NN_>), grid, block, 0, s, hidden, keep,              \
+    hipLaunchKernelGGL((gather_combine_tk_kernel<DT, TK_, NN_, false>), grid, block, 0, s, hidden, keep,       \
                        static_cast<const T *>(slot_out), so_b, so_s, weights, ld_w, static_cast<const T *>(values), \
                        n_cent, ld_v, idx, dist, ld_idx, static_cast<const T *>(residual), ld_r, static_cast<T *>(out), \
-                       ld_o);                                                                                  \
+                       ld_o, RankKeep{});                                                                      \
     TM_LAUNCH_CHECK("tm_gather_combine");                                                                      \
     return TM_OK;                                                                                              \
   }
@@ -611,6 +657,48 @@ extern "C" int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden
 }
 
 #undef TM_GC_TK
+
+bool tm_internal_combine_rank_ok(int32_t dtype, int32_t hidden, const void *slot_out, int64_t so_b, int64_t so_s,
+                                 int32_t top_k, const void *values, int64_t ld_v, const float *dist,
+                                 const void *residual, int64_t ld_r, const void *out, int64_t ld_o) {
+  if (!(dtype == TM_DT_BF16 || dtype == TM_DT_F16) || !(top_k == 6 || top_k == 8) || hidden <= 0) return false;
+  return hidden % 8 == 0 && tm_aligned16(slot_out) && (so_b * 2) % 16 == 0 && (so_s * 2) % 16 == 0 &&
+         rows_aligned(values, ld_v, 2) && rows_aligned(residual, ld_r, 2) && rows_aligned(out, ld_o, 2) &&
+         ld_o >= hidden && ld_v >= hidden && dist != nullptr && tm_aligned16(dist);
+}
+
+int tm_internal_combine_rank(int32_t dtype, int64_t n_tokens, int32_t hidden, const void *slot_out, int64_t so_b,
+                             int64_t so_s, const float *weights, int64_t ld_w, int32_t top_k, const void *values,
+                             int64_t n_cent, int64_t ld_v, const int64_t *idx, const float *dist,
+                             const void *residual, int64_t ld_r, void *out, int64_t ld_o, int64_t n_keep,
+                             uint8_t *keep_out, hipStream_t s) {
+  TM_REQUIRE(tm_internal_combine_rank_ok(dtype, hidden, slot_out, so_b, so_s, top_k, values, ld_v, dist, residual,
+                                         ld_r, out, ld_o) &&
+                 n_tokens > 0 && n_tokens < (int64_t)0x7fffffff && ld_w >= top_k,
+             TM_EINVAL_SHAPE, "tm_table_forward: combine shape not supported by the ranked path");
+  TM_REQUIRE(weights && idx && keep_out && values && slot_out && out, TM_EINVAL_ARG,
+             "tm_table_forward: combine: null pointer");
+  const RankKeep rk{n_tokens, n_keep, keep_out};
+  auto launch = [&](auto dt_tag, auto tk_tag) {
+    constexpr int DT = decltype(dt_tag)::value;
+    constexpr int TK = decltype(tk_tag)::value;
+    using T = typename Elem<DT>::T;
+    hipLaunchKernelGGL((gather_combine_tk_kernel<DT, TK, 1, true>), dim3((unsigned)n_tokens), dim3(kThreads), 0, s,
+                       hidden, nullptr, static_cast<const T *>(slot_out), so_b, so_s, weights, ld_w,
+                       static_cast<const T *>(values), n_cent, ld_v, idx, dist, (int64_t)1,
+                       static_cast<const T *>(residual), ld_r, static_cast<T *>(out), ld_o, rk);
+  };
+  using BF = std::integral_constant<int, TM_DT_BF16>;
+  using HF = std::integral_constant<int, TM_DT_F16>;
+  using K8 = std::integral_constant<int, 8>;
+  using K6 = std::integral_constant<int, 6>;
+  if (dtype == TM_DT_BF16)
+    top_k == 8 ? launch(BF{}, K8{}) : launch(BF{}, K6{});
+  else
+    top_k == 8 ? launch(HF{}, K8{}) : launch(HF{}, K6{});
+  TM_LAUNCH_CHECK("tm_table_forward(combine)");
+  return TM_OK;
+}
 
 extern "C" int tm_slot_combine(int32_t dtype, int64_t n_tokens, int32_t top_k, int32_t hidden,
                                const float *weights, int64_t ld_w, const uint8_t *compute_mask,

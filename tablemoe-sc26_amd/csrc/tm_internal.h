@@ -50,6 +50,37 @@ __attribute__((visibility("hidden"))) int tm_internal_search_keys(
     int32_t dtype, const void *q, int64_t n, int64_t ld_q, const void *cents, int64_t n_cent, int64_t ld_c,
     const float *c_sqnorm, int32_t dim, int32_t metric, uint64_t *keys, hipStream_t stream);
 
+// The same search for large n (wide kernel: 8-wave workgroups, one per CU):
+// the workgroup that finishes a 256-query tile last also decodes the tile's
+// keys into dist[i], idx[i] and q_sqnorm[i] (|q|^2 = the sum of `parts`
+// partial norms qn_part[p][i]).  `cnt` holds one arrival counter per tile,
+// zero before the call and left zero.  tm_internal_search_decode_tiles gives
+// the tile count (0: shape not supported).
+__attribute__((visibility("hidden"))) int64_t tm_internal_search_decode_tiles(int32_t dtype, int64_t n,
+                                                                              int64_t n_cent, int64_t ld_q,
+                                                                              int64_t ld_c, int32_t dim);
+__attribute__((visibility("hidden"))) int tm_internal_search_decode(
+    int32_t dtype, const void *q, int64_t n, int64_t ld_q, const void *cents, int64_t n_cent, int64_t ld_c,
+    const float *c_sqnorm, int32_t dim, int32_t metric, uint64_t *keys, const float *qn_part, int32_t parts,
+    float *out_dist, int64_t *out_idx, float *out_qn, uint32_t *cnt, hipStream_t stream);
+
+// tm_gather_combine for top-1 tables whose keep set is not yet known: each
+// token's workgroup ranks its distance among all n (larger first, ties ->
+// lower index), keeps the token when fewer than n_keep are ahead of it and
+// writes keep[i] (the set tm_keep_select gives).  Shapes: 16-bit data,
+// top_k 6 or 8, contiguous 16-byte aligned dist.
+__attribute__((visibility("hidden"))) bool tm_internal_combine_rank_ok(int32_t dtype, int32_t hidden,
+                                                                       const void *slot_out, int64_t so_b,
+                                                                       int64_t so_s, int32_t top_k,
+                                                                       const void *values, int64_t ld_v,
+                                                                       const float *dist, const void *residual,
+                                                                       int64_t ld_r, const void *out, int64_t ld_o);
+__attribute__((visibility("hidden"))) int tm_internal_combine_rank(
+    int32_t dtype, int64_t n_tokens, int32_t hidden, const void *slot_out, int64_t so_b, int64_t so_s,
+    const float *weights, int64_t ld_w, int32_t top_k, const void *values, int64_t n_cent, int64_t ld_v,
+    const int64_t *idx, const float *dist, const void *residual, int64_t ld_r, void *out, int64_t ld_o,
+    int64_t n_keep, uint8_t *keep_out, hipStream_t stream);
+
 // tm_keep_select over the distances the packed keys give (|q|^2 = the sum of
 // `parts` partial norms qn_part[p][i]); also writes dist[i], idx[i] and
 // q_sqnorm[i].  n <= 16384.

@@ -12,11 +12,16 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // tm_search_global, tm_keep_select as exported), the fused top-1 one (packed
 // keys and partial query norms: column-split projection carrying the router
 // and the key reset, search merging by atomic minimum, keep select decoding
-// the keys), and the decode plan (n <= 64: split projection, stream search,
-// one finishing launch).  The first kSync bytes hold the decode plan's
+// the keys; for up to 4096 tokens the search decodes the keys and the
+// combine ranks the keep set), and the decode plan (n <= 64: split
+// projection, stream search, one finishing launch).  The first kSync bytes hold the decode plan's
 // arrival counters at the same offset for every n and plan: zero before the
-// first call on a workspace, and left zero by every call.
+// first call on a workspace, and left zero by every call.  The decode plan
+// uses counters 0 .. 31, the ranked top-1 plan one per query tile from
+// kTileCnt on.
 constexpr size_t kSync = 256;
+constexpr int kTileCnt = 32;
+constexpr int kMaxTiles = kSync / 4 - kTileCnt;
 
 struct WsLayout {
   size_t sync, project, search, keep, keys, qn_part, part, total;
@@ -55,6 +60,17 @@ WsPtrs ptrs(const WsLayout &w, char *ws) {
   return p;
 }
 
+// The ranked top-1 plan: the keep set is ranked in the combine, each token's
+// workgroup reading all n distances, so n is kept moderate.
+bool ranked_ok(const tm_table_layer *t, const tm_layer_io *io) {
+  const int64_t n = io->n_tokens;
+  if (n > 4096) return false;
+  const int64_t tiles = tm_internal_search_decode_tiles(t->dtype, n, t->n_cent, t->dim, t->ld_c, t->dim);
+  return tiles > 0 && tiles <= kMaxTiles &&
+         tm_internal_combine_rank_ok(t->dtype, t->hidden, io->slot_out, io->so_b, io->so_s, io->router_top_k,
+                                     t->values, t->ld_v, io->dist, io->residual, io->ld_r, io->out, io->ld_o);
+}
+
 bool fused_top1_ok(const tm_table_layer *t, const tm_layer_io *io) {
   const int64_t n = io->n_tokens;
   return io->n_nearest == 1 &&
@@ -71,9 +87,12 @@ int record(void *const *events, int i, hipStream_t s) {
 }
 
 // Stages 0-4 of the fused top-1 plan (events 0..4 bracket router, projection,
-// search, keep select).
+// search, keep select).  Ranked form (large n, up to 4096 tokens): the wide
+// search decodes the keys itself and the combine ranks the keep set, so the
+// keep stage has no launch (events 3 and 4 coincide).
 int fused_top1_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout &w, char *ws,
-                      const tm_route_args &ra, bool route_fused, int64_t n_keep, void *const *ev, hipStream_t s) {
+                      const tm_route_args &ra, bool route_fused, bool ranked, int64_t n_keep, void *const *ev,
+                      hipStream_t s) {
   const int64_t n = io->n_tokens;
   const WsPtrs p = ptrs(w, ws);
   uint64_t *keys = reinterpret_cast<uint64_t *>(p.keys);
@@ -89,12 +108,20 @@ int fused_top1_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLa
                                      qn_part, keys, route_fused ? &ra : nullptr, s)) != TM_OK)
     return st;
   if ((st = record(ev, 2, s)) != TM_OK) return st;
+  const int32_t parts = (int32_t)tm_internal_project_cols_parts(t->dim);
+  if (ranked) {  // the search decodes the keys; the keep set is ranked in the combine
+    if ((st = tm_internal_search_decode(t->dtype, io->q, n, t->dim, t->cents, t->n_cent, t->ld_c, t->c_sqnorm,
+                                        t->dim, t->metric, keys, qn_part, parts, io->dist, io->idx, io->q_sqnorm,
+                                        p.sync + kTileCnt, s)) != TM_OK)
+      return st;
+    return record(ev, 3, s);
+  }
   if ((st = tm_internal_search_keys(t->dtype, io->q, n, t->dim, t->cents, t->n_cent, t->ld_c, t->c_sqnorm, t->dim,
                                     t->metric, keys, s)) != TM_OK)
     return st;
   if ((st = record(ev, 3, s)) != TM_OK) return st;
-  return tm_internal_keep_keys(keys, qn_part, (int32_t)tm_internal_project_cols_parts(t->dim), t->metric, n, n_keep,
-                               io->dist, io->idx, io->q_sqnorm, io->keep, s);
+  return tm_internal_keep_keys(keys, qn_part, parts, t->metric, n, n_keep, io->dist, io->idx, io->q_sqnorm, io->keep,
+                               s);
 }
 
 // Stages 0-4 of the decode plan (n <= 64): split projection (+ router, + key
@@ -183,14 +210,20 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
     if ((st = decode_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s)) != TM_OK) return st;
     return record(stage_events, 5, s);
   }
-  st = fused_top1_ok(t, io) ? fused_top1_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s)
-                            : general_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s);
+  const bool fused = fused_top1_ok(t, io);
+  const bool ranked = fused && ranked_ok(t, io);
+  st = fused ? fused_top1_stages(t, io, w, ws, ra, route_fused, ranked, n_keep, stage_events, s)
+             : general_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s);
   if (st != TM_OK) return st;
   if ((st = record(stage_events, 4, s)) != TM_OK) return st;
-  if ((st = tm_gather_combine(t->dtype, n, t->hidden, io->keep, io->slot_out, io->so_b, io->so_s, io->weights,
-                              io->router_top_k, io->router_top_k, t->values, t->n_cent, t->ld_v, io->idx,
-                              io->dist, io->n_nearest, io->n_nearest, io->residual, io->ld_r, io->out, io->ld_o,
-                              stream)) != TM_OK)
-    return st;
+  if (ranked)
+    st = tm_internal_combine_rank(t->dtype, n, t->hidden, io->slot_out, io->so_b, io->so_s, io->weights,
+                                  io->router_top_k, io->router_top_k, t->values, t->n_cent, t->ld_v, io->idx,
+                                  io->dist, io->residual, io->ld_r, io->out, io->ld_o, n_keep, io->keep, s);
+  else
+    st = tm_gather_combine(t->dtype, n, t->hidden, io->keep, io->slot_out, io->so_b, io->so_s, io->weights,
+                           io->router_top_k, io->router_top_k, t->values, t->n_cent, t->ld_v, io->idx, io->dist,
+                           io->n_nearest, io->n_nearest, io->residual, io->ld_r, io->out, io->ld_o, stream);
+  if (st != TM_OK) return st;
   return record(stage_events, 5, s);
 }

@@ -30,6 +30,7 @@
 #include "tm_mfma.h"
 #include "tm_route_dev.h"
 #include "tm_dma.h"
+#include "tm_keep_dev.h"
 
 namespace {
 
@@ -615,6 +616,303 @@ __global__ __launch_bounds__(kThreads, 2) void search_top1_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Top-1 tile kernel, wide form (the layer call's fused top-1 plan, large n):
+// one 8-wave workgroup per CU owns 256 queries and one range of centroids.
+// Waves w and w + 4 hold the same 64 queries (two slabs of 32) and take the
+// even and the odd 32-row blocks of each 32 KiB stage, so a CU fetches its
+// queries once and every centroid stage once for all 8 waves (per CU:
+// 64 KiB of queries + the range's centroids, against 2 x (64 + 64) KiB for
+// two 4-wave workgroups).
+//
+// The query tile travels through the ring: direct global->LDS loads bring
+// whole rows (4 rows of 256 bytes per wave instruction, where register loads
+// in the operand layout touch 32 rows per instruction) into ring slots 2
+// and 3 while stage 0 fills slot 0; the waves read their fragments into
+// registers and the slots go back to the ring (stage 2, then 3).  The swizzle
+// of a query row is the one of a centroid row, so the fragment offsets are
+// those of the A operand.
+//
+// Blocks: stage s, block i of a wave is the stage's block 2i + half (half =
+// wave / 4).  The accumulator sets, the one-block-behind epilogue and the
+// stage waits are those of search_top1_kernel.  The two halves' keys of a
+// query meet in LDS; one atomic minimum per query and workgroup.
+//
+// With DEC, the workgroup that finishes a query tile last (one arrival
+// counter per tile, zero before the launch and left zero) decodes the
+// tile's finished keys into distance, centroid and |q|^2 (device-coherent
+// key loads: the other splits' minima were made on other CUs in this launch).
+// ---------------------------------------------------------------------------
+constexpr int kWideThreads = 512;
+constexpr int kWideQ = 256;  // queries per workgroup
+constexpr int kWideStageBytes = 32768;
+
+struct WideDecode {
+  const float *qn_part;  // [parts][n] partial |q|^2
+  int parts;
+  float *out_dist;
+  int64_t *out_idx;
+  float *out_qn;
+  uint32_t *cnt;  // one per query tile
+};
+
+template <int DT, int DIM, int METRIC, bool DEC>
+__global__ __launch_bounds__(kWideThreads, 1) void search_top1_wide_kernel(
+    const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
+    const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
+    const float *__restrict__ c_sqnorm, int64_t chunk, uint64_t *__restrict__ keys, WideDecode wd) {
+  using T = typename Elem<DT>::T;
+  constexpr int KS = DIM / 16;
+  constexpr int CH = DIM / 8;
+  constexpr int ROWS = kWideStageBytes / (DIM * 2);
+  constexpr int NSUB = ROWS / 32;
+  constexpr int NBW = NSUB / 2;  // blocks per stage of one wave
+  constexpr int SLOTS = ROWS * CH;
+  constexpr int NDMA = SLOTS / kWideThreads;
+  constexpr int QST = kWideQ / ROWS;  // ring slots of the query tile
+  static_assert(SLOTS % kWideThreads == 0 && NBW % 2 == 0 && (QST == 1 || QST == 2), "stage shape");
+  static_assert(CH <= 16 && (kWideThreads / CH) % CH == 0, "one swizzle period per load row group");
+  __shared__ uint4 ring[4 * SLOTS];
+  __shared__ float init_s[kDmaMaxChunk];
+  __shared__ uint64_t half_keys[4][64];  // odd-block waves' keys of each query group
+  __shared__ uint32_t s_last;
+  uint4 *const st0 = ring;
+  uint4 *const st1 = ring + SLOTS;
+  uint4 *const st2 = ring + 2 * SLOTS;
+  uint4 *const st3 = ring + 3 * SLOTS;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int qg = wave & 3;
+  const int half = wave >> 2;
+  // x: centroid range (the 8 XCDs each see a few ranges), y: query tile
+  const int64_t split = blockIdx.x;
+  const int64_t tile0 = (int64_t)blockIdx.y * kWideQ;
+  const int64_t row_base = tile0 + qg * 64;
+  const int64_t c_begin = split * chunk;
+  const int64_t c_end = (c_begin + chunk < n_cent) ? c_begin + chunk : n_cent;
+  const int64_t c_last = c_end - 1;
+  const int nstage = (int)((c_end - c_begin + ROWS - 1) / ROWS);
+  const int nstage4 = (nstage + 3) / 4 * 4;  // <= kDmaMaxChunk / ROWS
+
+  // Ring fills: thread t's chunk u of a stage is row t / CH + u * (512 / CH),
+  // global chunk (t % CH) ^ (row % CH), LDS slot u * 512 + t.  Rows past the
+  // table (or past n for the query tile) read nothing.  The host keeps
+  // ROWS * row stride below 2^31 bytes.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint64_t ldb = (uint64_t)ld_c * sizeof(T);
+  const uint64_t ldqb = (uint64_t)ld_q * sizeof(T);
+  constexpr int kRowsPerU = kWideThreads / CH;
+  uint32_t voff[NDMA];
+#pragma unroll
+  for (int u = 0; u < NDMA; ++u) {
+    const int r = tid / CH + u * kRowsPerU;
+    const int j = (tid % CH) ^ (r % CH);
+    voff[u] = (uint32_t)r * (uint32_t)ldb + (uint32_t)j * 16u;
+  }
+  auto issue = [&](uint4 *buf, int s) {
+    const uint32_t lds0 = (uint32_t)(uintptr_t)buf + (uint32_t)wave_u * 1024u;
+    const int64_t row0 = __builtin_elementwise_min(c_begin + (int64_t)s * ROWS, n_cent);
+    const tm_rsrc_t rs = tm_make_rsrc(cents + row0 * ld_c, (uint64_t)(n_cent - row0) * ldb);
+#pragma unroll
+    for (int u = 0; u < NDMA; ++u) tm_dma16_buf(rs, voff[u], lds0 + (uint32_t)(u * kWideThreads * 16));
+  };
+  auto issue_q = [&](uint4 *buf, int part) {
+    const uint32_t lds0 = (uint32_t)(uintptr_t)buf + (uint32_t)wave_u * 1024u;
+    const int64_t row0 = __builtin_elementwise_min(tile0 + (int64_t)part * ROWS, n);
+    const tm_rsrc_t rs = tm_make_rsrc(q + row0 * ld_q, (uint64_t)(n - row0) * ldqb);
+#pragma unroll
+    for (int u = 0; u < NDMA; ++u) {
+      const int r = tid / CH + u * kRowsPerU;
+      const int j = (tid % CH) ^ (r % CH);
+      tm_dma16_buf(rs, (uint32_t)r * (uint32_t)ldqb + (uint32_t)j * 16u, lds0 + (uint32_t)(u * kWideThreads * 16));
+    }
+  };
+  constexpr int IPT = kDmaMaxChunk / kWideThreads;
+  float init_v[IPT];
+#pragma unroll
+  for (int u = 0; u < IPT; ++u) {
+    const int64_t c = c_begin + tid + u * kWideThreads;
+    const float v = (METRIC == TM_METRIC_L2) ? -0.5f * c_sqnorm[c < c_last ? c : c_last] : 0.f;
+    init_v[u] = (c < c_end) ? v : -__builtin_huge_valf();
+  }
+  issue_q(st2, 0);
+  if constexpr (QST == 2) issue_q(st3, 1);
+  issue(st0, 0);
+  tm_wait_vm_lgkm0<0>();  // start values, the query tile and stage 0 (this thread's loads)
+#pragma unroll
+  for (int u = 0; u < IPT; ++u) init_s[tid + u * kWideThreads] = init_v[u];
+  issue(st1, 1);
+  tm_wait_vm_lgkm0<NDMA>();  // init_s written; stage 1 may still load
+  __builtin_amdgcn_s_barrier();
+
+  // Lane byte offsets of operand k within a 32-row block (see
+  // search_top1_kernel); the query fragments use them as they are, the
+  // centroid blocks of this half one block further.
+  uint32_t a_off[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    const int row = lane & 31;
+    const int j = 2 * k + (lane >> 5);
+    a_off[k] = (uint32_t)(row * CH + (j ^ (row % CH))) * 16u;
+  }
+  uint4 qf[2][KS];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+    const int t0 = qg * 64 + sl * 32;  // tile row of the slab
+    const char *qb = reinterpret_cast<const char *>(t0 < ROWS ? st2 : st3) + (t0 % ROWS) * CH * 16;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) qf[sl][k] = *reinterpret_cast<const uint4 *>(qb + a_off[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    a_off[k] += (uint32_t)(half * 32 * CH * 16);
+    asm volatile("" : "+v"(a_off[k]));
+  }
+  uint32_t i_off = (uint32_t)(16 * (lane >> 5) + 128 * half);
+  asm volatile("" : "+v"(i_off));
+
+  Top1Lane top[2];
+  tm_f32x16 accs[2][2];
+  int cbs[2] = {0, 0};
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+    top1_init(top[sl]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) accs[1][sl][i] = -__builtin_huge_valf();
+  }
+  constexpr int kAhead = KS >= 8 ? 3 : 2;
+  static_assert(KS >= 4 && kAhead < KS, "window shorter than a block");
+  uint4 fa[KS];
+  float fi[16];
+  auto read_a = [&](const uint4 *buf, int i, int k) {
+    fa[k] = *reinterpret_cast<const uint4 *>(reinterpret_cast<const char *>(buf) + i * 64 * CH * 16 + a_off[k]);
+  };
+  auto read_start = [&](int s, int i) {
+    const int sc = s < nstage4 ? s : nstage4 - 1;  // the read past the last stage: any in-range values
+    const char *ib = reinterpret_cast<const char *>(init_s) + (sc * ROWS + i * 64) * 4 + i_off;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 p4 = *reinterpret_cast<const float4 *>(ib + 32 * g);
+      fi[4 * g + 0] = p4.x; fi[4 * g + 1] = p4.y; fi[4 * g + 2] = p4.z; fi[4 * g + 3] = p4.w;
+    }
+  };
+  read_start(0, 0);
+#pragma unroll
+  for (int k = 0; k < kAhead; ++k) read_a(st0, 0, k);
+  tm_wait_vm_lgkm0<NDMA>();  // query fragments in registers
+  __builtin_amdgcn_s_barrier();  // ... in every wave: slots 2 and 3 go back to the ring
+  issue(st2, 2);
+
+  auto step = [&](const uint4 *cur, const uint4 *nxt, uint4 *old, int s) {
+    const int64_t s0 = c_begin + (int64_t)s * ROWS + half * 32;
+    tm_static_for<NBW>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      constexpr int PA = i & 1;
+      if (i == NBW - 1) {
+        tm_wait_vm_lgkm0<NDMA>();      // stage s+1 landed (stage s+2 may be in flight)
+        __builtin_amdgcn_s_barrier();  // ... in every wave; stage s-1's slot is no longer read
+        issue(old, s + 3);
+      }
+      tm_f32x16 (&acc)[2] = accs[PA];
+      tm_f32x16 start;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) start[e] = fi[e];
+      tm_static_for<KS>([&](auto k_c) {
+        constexpr int k = decltype(k_c)::value;
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) acc[sl] = tm_mfma32x32x16<DT>(fa[k], qf[sl][k], k == 0 ? start : acc[sl]);
+        constexpr int kk = k + kAhead;
+        if constexpr (kk < KS)
+          read_a(cur, i, kk);
+        else if constexpr (i + 1 < NBW)
+          read_a(cur, i + 1, kk - KS);
+        else
+          read_a(nxt, 0, kk - KS);
+        if constexpr (k == KS - 3) {
+          if constexpr (i + 1 < NBW)
+            read_start(s, i + 1);
+          else
+            read_start(s + 1, 0);
+        }
+      });
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) top1_update(top[sl], accs[PA ^ 1][sl], cbs[PA ^ 1]);
+      cbs[PA] = (int)(s0 + i * 64);
+      constexpr int kValu = (30 * 2 + KS - 1) / KS;
+      tm_static_for<KS>([&](auto k_c) {
+        constexpr int k = decltype(k_c)::value;
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, k == KS - 3 ? 5 : 1, 0);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  for (int s = 0; s < nstage4; s += 4) {
+    step(st0, st1, st3, s);
+    step(st1, st2, st0, s + 1);
+    step(st2, st3, st1, s + 2);
+    step(st3, st0, st2, s + 3);
+  }
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) top1_update(top[sl], accs[1][sl], cbs[1]);  // the last block is odd
+  tm_wait_vm_lgkm0<0>();  // no load may still target this workgroup's LDS when it exits
+
+  uint64_t bk[2];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+    Best<1> best;
+    best.init();
+    top1_to_best<METRIC>(top[sl], lane, best);
+    best.finalize();
+    best.merge_xor(32);  // the two half-waves saw disjoint centroids of the same query
+    bk[sl] = best.l[0];
+    if (half == 1 && lane < 32) half_keys[qg][sl * 32 + lane] = bk[sl];
+  }
+  __syncthreads();
+  if (half == 0) {
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      const int64_t r = row_base + sl * 32 + (lane & 31);
+      const uint64_t o = half_keys[qg][sl * 32 + (lane & 31)];
+      const uint64_t key = bk[sl] < o ? bk[sl] : o;
+      if (lane < 32 && r < n && key != ~0ull)
+        atomicMin(reinterpret_cast<unsigned long long *>(keys + r), (unsigned long long)key);
+    }
+  }
+  if constexpr (DEC) {
+    // arrival: every thread's key updates performed, then one ticket per tile
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    tm_wait_vm_lgkm0<0>();
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t *cnt = wd.cnt + blockIdx.y;
+      const uint32_t ticket = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = ticket == gridDim.x - 1;
+      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last ? 1u : 0u;
+    }
+    __syncthreads();
+    if (s_last == 0u) return;  // uniform
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const int64_t r = tile0 + tid;
+    if (tid < kWideQ && r < n) {
+      const uint64_t key = __hip_atomic_load(keys + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      float a[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) a[p] = p < wd.parts ? wd.qn_part[(int64_t)p * n + r] : 0.f;
+      const float qn = qn_sum(a[0], a[1], a[2], a[3], wd.parts);
+      int64_t ix;
+      const float d = tm_key_to_dist(key, qn, METRIC == TM_METRIC_L2, ix);
+      wd.out_dist[r] = d;
+      wd.out_idx[r] = ix;
+      wd.out_qn[r] = qn;
+    }
+  }
+}
+
 // The K smallest of two ascending K-lists, ascending: min(a[i], b[K-1-i]) is
 // bitonic and holds exactly the K smallest; a half-cleaner cascade sorts it.
 template <int K>
@@ -1086,6 +1384,97 @@ int tm_internal_search_keys(int32_t dtype, const void *q, int64_t n, int64_t ld_
       search_keys_dim<TM_DT_F16, TM_METRIC_L2>(dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
     else
       search_keys_dim<TM_DT_F16, TM_METRIC_DOT>(dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, stream);
+  }
+  TM_LAUNCH_CHECK("tm_table_forward(search)");
+  return TM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Fused top-1 plan, large n (internal): the wide search kernel with the keep
+// selection in its last workgroup.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct WidePlan {
+  int64_t tiles, nsplit, chunk;
+};
+
+inline int64_t wide_rows(int dim) { return kWideStageBytes / (dim * 2); }
+
+// One workgroup per CU where the shape allows: ranges of whole ring rounds
+// (4 stages), at most kDmaMaxChunk centroids (the start-value array).
+WidePlan plan_wide(int64_t n, int64_t c, int dim) {
+  WidePlan p;
+  p.tiles = tm_cdiv(n, kWideQ);
+  const int64_t unit = 4 * wide_rows(dim);
+  const int64_t max_split = tm_cdiv(c, unit);
+  const int64_t min_split = tm_cdiv(c, kDmaMaxChunk);
+  int64_t want = tm_cdiv(256, p.tiles);
+  if (want < min_split) want = min_split;
+  if (want > max_split) want = max_split;
+  if (want < 1) want = 1;
+  p.chunk = tm_cdiv(tm_cdiv(c, want), unit) * unit;
+  p.nsplit = tm_cdiv(c, p.chunk);
+  return p;
+}
+
+template <int DT, int DIM, int METRIC>
+void launch_search_decode(const WidePlan &p, const void *q, int64_t n, int64_t ld_q, const void *cents,
+                          int64_t n_cent, int64_t ld_c, const float *c_sqnorm, uint64_t *keys, const WideDecode &wd,
+                          hipStream_t stream) {
+  using T = typename Elem<DT>::T;
+  hipLaunchKernelGGL((search_top1_wide_kernel<DT, DIM, METRIC, true>), dim3((unsigned)p.nsplit, (unsigned)p.tiles),
+                     dim3(kWideThreads), 0, stream, static_cast<const T *>(q), n, ld_q, static_cast<const T *>(cents),
+                     n_cent, ld_c, c_sqnorm, p.chunk, keys, wd);
+}
+
+template <int DT, int METRIC>
+void search_decode_dim(const WidePlan &p, int dim, const void *q, int64_t n, int64_t ld_q, const void *cents,
+                       int64_t n_cent, int64_t ld_c, const float *c_sqnorm, uint64_t *keys, const WideDecode &wd,
+                       hipStream_t stream) {
+  if (dim == 64)
+    launch_search_decode<DT, 64, METRIC>(p, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, wd, stream);
+  else
+    launch_search_decode<DT, 128, METRIC>(p, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, wd, stream);
+}
+
+}  // namespace
+
+int64_t tm_internal_search_decode_tiles(int32_t dtype, int64_t n, int64_t n_cent, int64_t ld_q, int64_t ld_c,
+                                        int32_t dim) {
+  if (!tm_internal_search_keys_ok(dtype, n, n_cent, ld_c, dim, 1) || ld_q < dim) return 0;
+  const WidePlan p = plan_wide(n, n_cent, dim);
+  if (p.tiles * p.nsplit < 192) return 0;  // leaves too many CUs idle: the 4-wave kernel
+  const int64_t rows = wide_rows(dim);
+  if (ld_c * 2 * rows >= ((int64_t)1 << 31) || ld_q * 2 * rows >= ((int64_t)1 << 31) || p.chunk > kDmaMaxChunk)
+    return 0;
+  return p.tiles;
+}
+
+int tm_internal_search_decode(int32_t dtype, const void *q, int64_t n, int64_t ld_q, const void *cents,
+                              int64_t n_cent, int64_t ld_c, const float *c_sqnorm, int32_t dim, int32_t metric,
+                              uint64_t *keys, const float *qn_part, int32_t parts, float *out_dist, int64_t *out_idx,
+                              float *out_qn, uint32_t *cnt, hipStream_t stream) {
+  TM_REQUIRE(tm_internal_search_decode_tiles(dtype, n, n_cent, ld_q, ld_c, dim) > 0, TM_EINVAL_SHAPE,
+             "tm_table_forward: search shape not supported by the wide top-1 path");
+  TM_REQUIRE(metric == TM_METRIC_L2 || metric == TM_METRIC_DOT, TM_EINVAL_ARG, "tm_table_forward: bad metric");
+  TM_REQUIRE(q && cents && keys && (metric != TM_METRIC_L2 || c_sqnorm) && qn_part && out_dist && out_idx &&
+                 out_qn && cnt && parts >= 1 && parts <= 4,
+             TM_EINVAL_ARG, "tm_table_forward: null pointer");
+  TM_REQUIRE(tm_aligned16(q) && tm_aligned16(cents) && (ld_q * 2) % 16 == 0 && (ld_c * 2) % 16 == 0,
+             TM_EINVAL_SHAPE, "tm_table_forward: q and centroid rows must be 16-byte aligned");
+  const WidePlan p = plan_wide(n, n_cent, dim);
+  const WideDecode wd{qn_part, parts, out_dist, out_idx, out_qn, cnt};
+  if (dtype == TM_DT_BF16) {
+    if (metric == TM_METRIC_L2)
+      search_decode_dim<TM_DT_BF16, TM_METRIC_L2>(p, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, wd, stream);
+    else
+      search_decode_dim<TM_DT_BF16, TM_METRIC_DOT>(p, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, wd, stream);
+  } else {
+    if (metric == TM_METRIC_L2)
+      search_decode_dim<TM_DT_F16, TM_METRIC_L2>(p, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, wd, stream);
+    else
+      search_decode_dim<TM_DT_F16, TM_METRIC_DOT>(p, dim, q, n, ld_q, cents, n_cent, ld_c, c_sqnorm, keys, wd, stream);
   }
   TM_LAUNCH_CHECK("tm_table_forward(search)");
   return TM_OK;

@@ -477,37 +477,60 @@ def test_layer_forward_one_call_matches_staged(hip_device):
             assert torch.equal(ra[key], rb[key]), key
 
 
-@pytest.mark.parametrize("n,hidden,dim,mix", [(300, 1000, 128, False), (515, 2080, 64, True), (96, 264, 128, True),
-                                             (4096, 2048, 128, True)])
-def test_layer_forward_fused_shapes_match_staged(hip_device, n, hidden, dim, mix):
+@pytest.mark.parametrize("n,hidden,dim,mix,n_cent,dup", [
+    (300, 1000, 128, False, 1024, False), (515, 2080, 64, True, 1024, False), (96, 264, 128, True, 1024, False),
+    (4096, 2048, 128, True, 1024, False),
+    # ranked form (wide search decoding the keys, keep set ranked in the
+    # combine): config-2 shape, repeated tokens (tied distances at the keep
+    # boundary), d = 64, a ragged last query tile and centroid range
+    (4096, 2048, 128, True, 8192, False), (4096, 2048, 128, False, 8192, True), (4096, 1000, 64, False, 16384, False),
+    (4000, 2080, 128, True, 12000, False),
+    # above the ranked form's token limit: keep select launch
+    (8192, 1024, 128, False, 8192, False)])
+def test_layer_forward_fused_shapes_match_staged(hip_device, n, hidden, dim, mix, n_cent, dup):
     """Top-1 layer calls take the fused plan (column-split projection, search
-    merged by atomic minimum, keep select decoding the packed keys); the
-    result must equal the stage calls bit for bit.  Hidden sizes that end
-    inside a k-step or a 4-k-step chunk, d = 64, ragged row tiles, and
-    modality patterns that mix vision and text rows inside every tile."""
+    merged by atomic minimum, keep select decoding the packed keys; for up to
+    4096 tokens the search decodes the keys and the combine ranks the keep
+    set); the result must equal the stage calls bit for bit.  Hidden sizes
+    that end inside a k-step or a 4-k-step chunk, d = 64, ragged row tiles and
+    centroid ranges, modality patterns that mix vision and text rows inside
+    every tile, and repeated tokens.  Each table is called twice: the second
+    call checks that the arrival counters were left at zero."""
     from table_moe.cache_engine import GlobalTable
     from table_moe.synth import make_workload
 
     dev = hip_device
-    wl = make_workload(2, n=n, hidden=hidden, dim=dim, n_cent=1024)
+    wl = make_workload(2, n=n, hidden=hidden, dim=dim, n_cent=n_cent)
     d = wl.to(dev)
+    if dup:  # every token of the second quarter repeats one of the first: equal distances
+        src = torch.arange(n // 4, device=dev) % (n // 8)
+        d.x[n // 4:n // 2] = d.x[src]
     is_vision = d.is_vision
     if mix:
         g = torch.Generator().manual_seed(n)
         is_vision = (torch.rand(n, generator=g) < 0.5).to(dev)
     a = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
     b = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
-    ra = a.layer_forward(d.x, is_vision, d.logits, d.slot_out, d.residual, 8, 1, 0.6)
     rb = b.layer_forward_staged(d.x, is_vision, d.logits, d.slot_out, d.residual, 8, 1, 0.6)
-    torch.cuda.synchronize()
-    for key in ("weights", "ids", "q", "qn", "dist", "idx", "keep", "out"):
-        assert torch.equal(ra[key], rb[key]), key
+    for rep in range(2):
+        ra = a.layer_forward(d.x, is_vision, d.logits, d.slot_out, d.residual, 8, 1, 0.6)
+        torch.cuda.synchronize()
+        for key in ("weights", "ids", "q", "qn", "dist", "idx", "keep", "out"):
+            assert torch.equal(ra[key], rb[key]), (key, rep)
     # and the projection against the oracle
     q = np64(ra["q"])
-    ref_q = O.project_queries(np64(wl.x), is_vision.cpu().numpy(), (np64(wl.proj_vis), np64(wl.bias_vis)),
+    x = np64(d.x)
+    ref_q = O.project_queries(x, is_vision.cpu().numpy(), (np64(wl.proj_vis), np64(wl.bias_vis)),
                               (np64(wl.proj_txt), np64(wl.bias_txt)), False, O.BF16)
-    abssum = proj_abssum(np64(wl.x), is_vision.cpu().numpy(), np64(wl.proj_vis), np64(wl.proj_txt))
+    abssum = proj_abssum(x, is_vision.cpu().numpy(), np64(wl.proj_vis), np64(wl.proj_txt))
     assert_projection_close(q, ref_q, abssum, torch.bfloat16, min_exact=0.95)
+    if dup:  # the repeated tokens tie with their originals, and some ties sit at the keep boundary
+        dist = ra["dist"][:, 0]
+        src = torch.arange(n // 4, device=dev) % (n // 8)
+        assert torch.equal(dist[n // 4:n // 2], dist[src])
+        keep = ra["keep"].bool()
+        kept_d = dist[keep]
+        assert (dist[~keep] <= kept_d.min()).all()
 
 
 @pytest.mark.parametrize("cfg,n,hidden,dim,n_cent,nn,variant", [
@@ -587,7 +610,7 @@ def test_layer_forward_config3_decode_end_to_end(hip_device):
     assert_bf16_output(np64(res["out"]), exact, abssum)
 
 
-@pytest.mark.parametrize("cfg,n,nn", [(2, 768, 1), (3, 32, 4)])
+@pytest.mark.parametrize("cfg,n,nn", [(2, 768, 1), (2, 4096, 1), (3, 32, 4)])
 def test_layer_graph_replays_match_eager(hip_device, cfg, n, nn):
     """A captured tm_table_forward replays correctly: several replays with new
     inputs copied in and eager work in between, each checked against an eager
