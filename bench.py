@@ -163,12 +163,23 @@ def run_layer_bench(cfg_id, steps, warmup, n=None):
                 bytes=_stage_bytes(cfg, N, n_keep, nn, topk))
 
 
+def ranked_layer(n, nn, topk, hidden):
+    """tm_table_forward ranks the keep set inside the combine for these shapes."""
+    return nn == 1 and n <= 4096 and topk in (6, 8) and hidden <= 2048 and hidden % 8 == 0
+
+
 def stage_kernel_times(reps, tables, outs, topk, nn, kr, launches=32, replays=3):
     """Average device time of each stage's C-ABI call: `launches` back-to-back
     calls (rotating over the table replicas, so reads stay HBM-cold) captured
     in one HIP graph, replayed `replays` times between two HIP events recorded
-    on the stream the kernels run on."""
+    on the stream the kernels run on.  The combine stage is the call the layer
+    runs: tm_gather_combine_ranked (keep set ranked in the combine) for top-1
+    batches of up to 4096 tokens, tm_gather_combine otherwise."""
     import torch
+
+    n0 = reps[0].x.shape[0]
+    ranked = ranked_layer(n0, nn, topk, reps[0].x.shape[1])
+    rk = [torch.zeros(n0, dtype=torch.bool, device=reps[0].x.device) for _ in reps]
 
     def calls(name, i):
         r, t, o = reps[i % len(reps)], tables[i % len(tables)], outs[i % len(outs)]
@@ -182,6 +193,9 @@ def stage_kernel_times(reps, tables, outs, topk, nn, kr, launches=32, replays=3)
             t.search(b["q"][: n * t.dim].view(n, t.dim), nn, b["qn"][:n])
         elif name == "keep":
             t.keep_select(b["dist"][: n * nn].view(n, nn)[:, 0], t.keep_count(n, kr))
+        elif ranked:  # the layer's combine: keep set ranked in the same launch
+            t.gather_combine_ranked(r.slot_out, b["route_w"][: n * topk].view(n, topk), b["idx"][: n * nn].view(n, nn),
+                                    b["dist"][:n], t.keep_count(n, kr), r.residual, o, keep=rk[i % len(rk)])
         else:
             t.gather_combine(b["keep"][:n], r.slot_out, b["route_w"][: n * topk].view(n, topk),
                              b["idx"][: n * nn].view(n, nn), b["dist"][: n * nn].view(n, nn), r.residual, o)
@@ -405,8 +419,9 @@ def main() -> int:
     log(f"prefill per-call device times (graph of 32 calls): {json.dumps({k: round(v, 2) for k, v in ku.items()})}")
     # dominant kernel (longest average call) and its roofline
     dom = max(ku, key=ku.get)
-    entry = {"combine": "tm_gather_combine", "project": "tm_project", "router": "tm_topk_softmax",
-             "keep": "tm_keep_select", "search": "tm_search_global"}[dom]
+    ranked = ranked_layer(N, cfg["n_nearest"], cfg["router_top_k"], cfg["hidden"])
+    entry = {"combine": "tm_gather_combine_ranked" if ranked else "tm_gather_combine", "project": "tm_project",
+             "router": "tm_topk_softmax", "keep": "tm_keep_select", "search": "tm_search_global"}[dom]
     if dom == "search":
         flops = 2.0 * N * C * d
         achieved = flops / (ku[dom] * 1e-6) / 1e12

@@ -316,6 +316,22 @@ int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden, const uin
                       int32_t n_nearest, const void *residual, int64_t ld_r, void *out,
                       int64_t ld_o, tm_stream_t stream);
 
+/* (3)+(4) in one launch for top-1 tables: tm_gather_combine (n_nearest = 1)
+ * with the keep set decided from `dist` (fp32 [n], contiguous) instead of
+ * read: token i is kept when fewer than n_keep tokens are ahead of it (a
+ * larger distance, or the same at a lower index) -- the set tm_keep_select
+ * gives -- and out_keep[i] is written.  No single counterpart in the
+ * reference: it replaces the keep selection (table_moe/skip/pruning.py:45
+ * count) followed by the gather + combine of tm_gather_combine.  dtype F16
+ * or BF16, top_k 6 or 8, hidden <= 2048 and a multiple of 8, 16-byte aligned
+ * rows and dist; each token's workgroup reads all n distances, so it suits
+ * n up to a few thousand. */
+int tm_gather_combine_ranked(int32_t dtype, int64_t n_tokens, int32_t hidden, const void *slot_out,
+                             int64_t so_b, int64_t so_s, const float *weights, int64_t ld_w, int32_t top_k,
+                             const void *values, int64_t n_cent, int64_t ld_v, const int64_t *idx,
+                             const float *dist, const void *residual, int64_t ld_r, void *out, int64_t ld_o,
+                             int64_t n_keep, uint8_t *out_keep, tm_stream_t stream);
+
 /* ======================================================================
  * Online window, decode step of one token: the slot combine of
  * tm_slot_combine (n_tokens = 1) and the ring write of tm_online_update in
@@ -415,7 +431,8 @@ int tm_grouped_swiglu(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden
  * Enqueues, back to back on `stream`: tm_topk_softmax (router) ->
  * tm_project -> tm_search_global -> tm_keep_select (n_keep =
  * tm_keep_count(n, keep_rate)) -> tm_gather_combine, with the semantics of
- * each of those entry points.  One FFI call per layer keeps host overhead
+ * each of those entry points (for top-1 batches of up to 4096 tokens the
+ * last two run as tm_gather_combine_ranked).  One FFI call per layer keeps host overhead
  * out of the layer time.  The table descriptor is fixed per layer; the I/O
  * descriptor names the token batch, the caller's output and intermediate
  * buffers.  `stage_events` (nullable) is an array of 6 hipEvent_t recorded

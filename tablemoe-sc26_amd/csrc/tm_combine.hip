@@ -5,7 +5,7 @@
 // All are HBM-bound row streams: one workgroup of 256 threads per output row,
 // 16-byte vector loads/stores (8 bf16/fp16 or 2x4 fp32 per thread per step)
 // when every row pointer is 16-byte aligned, element loops otherwise.
-#include "tm_common.h"
+#include "tm_internal.h"
 
 namespace {
 
@@ -76,6 +76,7 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(
 // of a chunk are issued before the FMAs so they are in flight together.
 // ---------------------------------------------------------------------------
 constexpr int kFastSrc = 8;
+constexpr int kRankTokens = 1;  // tokens per workgroup of the ranked combine
 constexpr int kRowsPerGroup = 1;  // rows per workgroup of the fast kernel (more in flight per CU with 1)
 
 // Sources and coefficients of one row (wave-uniform).
@@ -193,64 +194,68 @@ __global__ __launch_bounds__(kThreads) void gather_combine_fast_kernel(
 // accesses; gathered value rows use ordinary loads (centroids repeat).
 // Same arithmetic as gather_combine_fast_kernel: fp32 accumulation starting
 // from the residual, sources added in order with fmaf, one rounding.
-// Keep decision of token b when the keep set is ranked in the combine:
-// b is kept when fewer than n_keep tokens are ahead of it (a larger
-// distance, or the same at a lower index), the set the radix select gives.
-// dist: n contiguous floats, 16-byte aligned.
+// Keep decisions when the keep set is ranked in the combine: token b is
+// kept when fewer than n_keep tokens are ahead of it (a larger distance, or
+// the same at a lower index), the set the radix select gives.  One pass over
+// the n distances (contiguous, 16-byte aligned) serves the TPB tokens of the
+// workgroup (token b0 + g for g < TPB; TPB * 256 threads).
 struct RankKeep {
   int64_t n;
   int64_t n_keep;
   uint8_t *keep_out;
 };
 
-__device__ __forceinline__ bool rank_keep(const float *__restrict__ dist, int64_t n, int64_t n_keep, int64_t b) {
-  __shared__ uint32_t s_ahead[kThreads / 64];
-  const uint32_t kb = tm_orderable(dist[b]);
-  uint32_t ahead = 0;
+template <int TPB>
+__device__ __forceinline__ bool rank_keep(const float *__restrict__ dist, int64_t n, int64_t n_keep, int64_t b0,
+                                          int g) {
+  constexpr int NT = TPB * kThreads;
+  constexpr int NW = NT / 64;
+  __shared__ uint32_t s_ahead[NW][TPB];
+  uint32_t kb[TPB];
+#pragma unroll
+  for (int t = 0; t < TPB; ++t) kb[t] = tm_orderable(dist[b0 + t < n ? b0 + t : n - 1]);
+  uint32_t ahead[TPB];
+#pragma unroll
+  for (int t = 0; t < TPB; ++t) ahead[t] = 0;
+  auto count = [&](uint32_t k, int64_t j) {
+#pragma unroll
+    for (int t = 0; t < TPB; ++t) ahead[t] += (k > kb[t] || (k == kb[t] && j < b0 + t)) ? 1u : 0u;
+  };
   const float4 *d4 = reinterpret_cast<const float4 *>(dist);
   const int64_t n4 = n >> 2;
-  for (int64_t i = threadIdx.x; i < n4; i += kThreads) {
+  for (int64_t i = threadIdx.x; i < n4; i += NT) {
     const float4 v = d4[i];
-    const float e[4] = {v.x, v.y, v.z, v.w};
+    count(tm_orderable(v.x), 4 * i);
+    count(tm_orderable(v.y), 4 * i + 1);
+    count(tm_orderable(v.z), 4 * i + 2);
+    count(tm_orderable(v.w), 4 * i + 3);
+  }
+  for (int64_t j = 4 * n4 + threadIdx.x; j < n; j += NT) count(tm_orderable(dist[j]), j);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t k = tm_orderable(e[u]);
-      const int64_t j = 4 * i + u;
-      ahead += (k > kb || (k == kb && j < b)) ? 1u : 0u;
-    }
+  for (int t = 0; t < TPB; ++t) {
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)tm_wave_incl_scan(ahead[t]), 63);
+    if (lane == 0) s_ahead[wave][t] = a;
   }
-  for (int64_t j = 4 * n4 + threadIdx.x; j < n; j += kThreads) {
-    const uint32_t k = tm_orderable(dist[j]);
-    ahead += (k > kb || (k == kb && j < b)) ? 1u : 0u;
-  }
-  ahead = (uint32_t)__builtin_amdgcn_readlane((int)tm_wave_incl_scan(ahead), 63);
-  if ((threadIdx.x & 63) == 0) s_ahead[threadIdx.x >> 6] = ahead;
   __syncthreads();
   uint32_t total = 0;
 #pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) total += s_ahead[w];
+  for (int w = 0; w < NW; ++w) total += s_ahead[w][g];
   return (int64_t)total < n_keep;
 }
 
-template <int DT, int TK, int NN, bool RANK>
+template <int DT, int TK, int NN>
 __global__ __launch_bounds__(kThreads) void gather_combine_tk_kernel(
     int hidden, const uint8_t *__restrict__ keep, const typename Elem<DT>::T *__restrict__ slot_out, int64_t so_b,
     int64_t so_s, const float *__restrict__ w, int64_t ld_w, const typename Elem<DT>::T *__restrict__ values,
     int64_t n_cent, int64_t ld_v, const int64_t *__restrict__ idx, const float *__restrict__ dist, int64_t ld_idx,
     const typename Elem<DT>::T *__restrict__ residual, int64_t ld_r, typename Elem<DT>::T *__restrict__ out,
-    int64_t ld_o, RankKeep rk) {
+    int64_t ld_o) {
   using T = typename Elem<DT>::T;
   const int64_t b = blockIdx.x;
   const T *res_row = residual ? residual + b * ld_r : nullptr;
   T *dst = out + b * ld_o;
-  bool kept;
-  if constexpr (RANK) {
-    kept = rank_keep(dist, rk.n, rk.n_keep, b);
-    if (threadIdx.x == 0) rk.keep_out[b] = kept ? 1 : 0;
-  } else {
-    kept = keep[b] != 0;
-  }
-  if (kept) {  // uniform
+  if (keep[b]) {  // uniform
     float coef[TK];
     float sum = 0.f;
 #pragma unroll
@@ -319,6 +324,63 @@ __global__ __launch_bounds__(kThreads) void gather_combine_tk_kernel(
       tm_store8_nt<DT>(dst + h0, acc);
     }
   }
+}
+
+// Top-1 combine that also decides the keep set (rank_keep), TPB tokens per
+// workgroup (256 threads each, one 8-element chunk per thread: hidden <=
+// 2048), so the distances are read once per TPB tokens.  The residual chunk
+// (needed either way) is loaded before the ranking.  The arithmetic is
+// gather_combine_tk_kernel's (NN = 1).
+template <int DT, int TK, int TPB>
+__global__ __launch_bounds__(TPB * kThreads) void gather_combine_rank_kernel(
+    int hidden, const typename Elem<DT>::T *__restrict__ slot_out, int64_t so_b, int64_t so_s,
+    const float *__restrict__ w, int64_t ld_w, const typename Elem<DT>::T *__restrict__ values, int64_t n_cent,
+    int64_t ld_v, const int64_t *__restrict__ idx, const float *__restrict__ dist,
+    const typename Elem<DT>::T *__restrict__ residual, int64_t ld_r, typename Elem<DT>::T *__restrict__ out,
+    int64_t ld_o, RankKeep rk) {
+  using T = typename Elem<DT>::T;
+  const int g = threadIdx.x / kThreads;
+  const int64_t b0 = (int64_t)blockIdx.x * TPB;
+  const int64_t b = b0 + g;
+  const int h0 = (threadIdx.x % kThreads) * 8;
+  const bool act = h0 < hidden && b < rk.n;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  if (residual != nullptr && act) tm_load8_nt<DT>(residual + b * ld_r + h0, acc);
+  const bool kept = rank_keep<TPB>(dist, rk.n, rk.n_keep, b0, g);
+  if (!act) return;
+  if (h0 == 0) rk.keep_out[b] = kept ? 1 : 0;
+  if (kept) {  // uniform over the token's 256 threads
+    float coef[TK];
+    float sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < TK; ++s) {
+      coef[s] = w[b * ld_w + s];
+      sum += coef[s];
+    }
+    if (sum > 0.f) {  // rows whose weights sum to 0 contribute nothing
+#pragma unroll
+      for (int s = 0; s < TK; ++s) coef[s] = coef[s] / sum;
+      const T *src = slot_out + b * so_b + h0;
+      float v[TK][8];
+#pragma unroll
+      for (int s = 0; s < TK; ++s) tm_load8_nt<DT>(src + (int64_t)s * so_s, v[s]);
+#pragma unroll
+      for (int s = 0; s < TK; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], v[s][i], acc[i]);
+    }
+  } else {
+    const int64_t c = idx[b];
+    if (c >= 0 && c < n_cent) {
+      float val[8];
+      tm_load8<DT>(values + c * ld_v + h0, val);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = fmaf(1.f, val[i], acc[i]);
+    }
+  }
+  tm_store8_nt<DT>(out + b * ld_o + h0, acc);
 }
 
 // General path (more than 8 sources): sources staged through LDS.
@@ -594,10 +656,10 @@ extern "C" int tm_gather_rows(int32_t dtype, const void *values, int64_t n_exper
 // Launch of the shape-specialised combine when (top_k, n_nearest) matches.
 #define TM_GC_TK(TK_, NN_)                                                                                     \
   if (top_k == TK_ && n_nearest == NN_) {                                                                      \
-    hipLaunchKernelGGL((gather_combine_tk_kernel<DT, TK_, NN_, false>), grid, block, 0, s, hidden, keep,       \
+    hipLaunchKernelGGL((gather_combine_tk_kernel<DT, TK_, NN_>), grid, block, 0, s, hidden, keep,              \
                        static_cast<const T *>(slot_out), so_b, so_s, weights, ld_w, static_cast<const T *>(values), \
                        n_cent, ld_v, idx, dist, ld_idx, static_cast<const T *>(residual), ld_r, static_cast<T *>(out), \
-                       ld_o, RankKeep{});                                                                      \
+                       ld_o);                                                                                  \
     TM_LAUNCH_CHECK("tm_gather_combine");                                                                      \
     return TM_OK;                                                                                              \
   }
@@ -658,10 +720,35 @@ extern "C" int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden
 
 #undef TM_GC_TK
 
+extern "C" int tm_gather_combine_ranked(int32_t dtype, int64_t n_tokens, int32_t hidden, const void *slot_out,
+                                        int64_t so_b, int64_t so_s, const float *weights, int64_t ld_w,
+                                        int32_t top_k, const void *values, int64_t n_cent, int64_t ld_v,
+                                        const int64_t *idx, const float *dist, const void *residual, int64_t ld_r,
+                                        void *out, int64_t ld_o, int64_t n_keep, uint8_t *out_keep,
+                                        tm_stream_t stream) {
+  TM_REQUIRE(n_tokens >= 0 && n_tokens < (int64_t)0x7fffffff && hidden > 0 && ld_w >= top_k && ld_o >= hidden &&
+                 ld_v >= hidden,
+             TM_EINVAL_SHAPE, "tm_gather_combine_ranked: bad sizes");
+  if (n_tokens == 0) return TM_OK;
+  TM_REQUIRE(dtype == TM_DT_BF16 || dtype == TM_DT_F16, TM_EINVAL_DTYPE,
+             "tm_gather_combine_ranked: dtype must be F16 or BF16");
+  TM_REQUIRE(slot_out && weights && values && idx && dist && out && out_keep, TM_EINVAL_ARG,
+             "tm_gather_combine_ranked: null pointer");
+  TM_REQUIRE(tm_internal_combine_rank_ok(dtype, hidden, slot_out, so_b, so_s, top_k, values, ld_v, dist, residual,
+                                         ld_r, out, ld_o),
+             TM_EINVAL_SHAPE,
+             "tm_gather_combine_ranked: needs top_k 6 or 8, hidden <= 2048 and a multiple of 8, aligned rows");
+  return tm_internal_combine_rank(dtype, n_tokens, hidden, slot_out, so_b, so_s, weights, ld_w, top_k, values,
+                                  n_cent, ld_v, idx, dist, residual, ld_r, out, ld_o, n_keep, out_keep,
+                                  tm_hip_stream(stream));
+}
+
 bool tm_internal_combine_rank_ok(int32_t dtype, int32_t hidden, const void *slot_out, int64_t so_b, int64_t so_s,
                                  int32_t top_k, const void *values, int64_t ld_v, const float *dist,
                                  const void *residual, int64_t ld_r, const void *out, int64_t ld_o) {
-  if (!(dtype == TM_DT_BF16 || dtype == TM_DT_F16) || !(top_k == 6 || top_k == 8) || hidden <= 0) return false;
+  if (!(dtype == TM_DT_BF16 || dtype == TM_DT_F16) || !(top_k == 6 || top_k == 8) || hidden <= 0 ||
+      hidden > kThreads * 8)
+    return false;
   return hidden % 8 == 0 && tm_aligned16(slot_out) && (so_b * 2) % 16 == 0 && (so_s * 2) % 16 == 0 &&
          rows_aligned(values, ld_v, 2) && rows_aligned(residual, ld_r, 2) && rows_aligned(out, ld_o, 2) &&
          ld_o >= hidden && ld_v >= hidden && dist != nullptr && tm_aligned16(dist);
@@ -683,9 +770,9 @@ int tm_internal_combine_rank(int32_t dtype, int64_t n_tokens, int32_t hidden, co
     constexpr int DT = decltype(dt_tag)::value;
     constexpr int TK = decltype(tk_tag)::value;
     using T = typename Elem<DT>::T;
-    hipLaunchKernelGGL((gather_combine_tk_kernel<DT, TK, 1, true>), dim3((unsigned)n_tokens), dim3(kThreads), 0, s,
-                       hidden, nullptr, static_cast<const T *>(slot_out), so_b, so_s, weights, ld_w,
-                       static_cast<const T *>(values), n_cent, ld_v, idx, dist, (int64_t)1,
+    hipLaunchKernelGGL((gather_combine_rank_kernel<DT, TK, kRankTokens>), dim3((unsigned)tm_cdiv(n_tokens, kRankTokens)),
+                       dim3(kRankTokens * kThreads), 0, s, hidden, static_cast<const T *>(slot_out), so_b, so_s,
+                       weights, ld_w, static_cast<const T *>(values), n_cent, ld_v, idx, dist,
                        static_cast<const T *>(residual), ld_r, static_cast<T *>(out), ld_o, rk);
   };
   using BF = std::integral_constant<int, TM_DT_BF16>;

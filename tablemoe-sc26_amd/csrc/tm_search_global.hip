@@ -37,15 +37,53 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kQS = 2;      // query slabs per wave in the tile kernel
 constexpr int kTileRows = 4 * kQS * 32;
+constexpr int kDmaMaxChunk = 2048;  // centroids per workgroup of the tile kernels (start values in LDS)
 constexpr int kStreamChunk = 128;  // centroids per split of the stream kernel (one 32-block per wave)
 
 struct SplitPlan {
   bool stream;  // small-n shape
+  bool wide;    // top-1 wide tile kernel (8-wave workgroups)
   int qs;       // query slabs per wave
   int64_t row_blocks;
   int64_t nsplit;
   int64_t chunk;  // centroids per split
 };
+
+// Wide top-1 tile kernel (search_top1_wide_kernel): 256 queries and one
+// centroid range per 8-wave workgroup, 32 KiB stages.
+constexpr int kWideThreads = 512;
+constexpr int kWideQ = 256;  // queries per workgroup
+constexpr int kWideStageBytes = 32768;
+constexpr int kWideMinGroups = 192;  // fewer leave too many of the 256 CUs idle
+
+struct WidePlan {
+  int64_t tiles, nsplit, chunk;
+};
+
+inline int64_t wide_rows(int dim) { return kWideStageBytes / (dim * 2); }
+
+// One workgroup per CU where the shape allows: ranges of whole ring rounds
+// (4 stages), at most kDmaMaxChunk centroids (the start-value array).
+WidePlan plan_wide(int64_t n, int64_t c, int dim) {
+  WidePlan p;
+  p.tiles = tm_cdiv(n, kWideQ);
+  const int64_t unit = 4 * wide_rows(dim);
+  const int64_t max_split = tm_cdiv(c, unit);
+  const int64_t min_split = tm_cdiv(c, kDmaMaxChunk);
+  int64_t want = tm_cdiv(256, p.tiles);
+  if (want < min_split) want = min_split;
+  if (want > max_split) want = max_split;
+  if (want < 1) want = 1;
+  p.chunk = tm_cdiv(tm_cdiv(c, want), unit) * unit;
+  p.nsplit = tm_cdiv(c, p.chunk);
+  return p;
+}
+
+// Row strides the wide kernel's 32-bit buffer offsets cover.
+inline bool wide_strides_ok(int64_t ld_q, int64_t ld_c, int dim) {
+  const int64_t rows = wide_rows(dim);
+  return ld_c * 2 * rows < ((int64_t)1 << 31) && ld_q * 2 * rows < ((int64_t)1 << 31);
+}
 
 // Centroid rows per pipelined stage of the tile kernel (16 KiB stages).
 static inline int64_t dma_rows(int dim) { return 16384 / (dim * 2); }
@@ -58,6 +96,7 @@ static inline bool top1_tile(int dim, int top_k) { return top_k <= 1 && dim <= 1
 SplitPlan plan_split(int64_t n, int64_t c, int dim, int top_k) {
   SplitPlan p;
   p.stream = n <= 64;
+  p.wide = false;
   if (p.stream) {
     p.qs = n <= 32 ? 1 : 2;
     p.row_blocks = 1;
@@ -66,6 +105,17 @@ SplitPlan plan_split(int64_t n, int64_t c, int dim, int top_k) {
     return p;
   }
   p.qs = kQS;
+  p.wide = false;
+  if (top1_tile(dim, top_k)) {
+    const WidePlan w = plan_wide(n, c, dim);
+    if (w.tiles * w.nsplit >= kWideMinGroups) {
+      p.wide = true;
+      p.row_blocks = w.tiles;  // = tm_cdiv(n, kTileRows): the 4-wave kernels can run the same plan
+      p.nsplit = w.nsplit;
+      p.chunk = w.chunk;
+      return p;
+    }
+  }
   p.row_blocks = tm_cdiv(n, kTileRows);
   const int64_t rows = dma_rows(dim);
   const int64_t max_split = tm_cdiv(c, rows);
@@ -168,7 +218,6 @@ __device__ __forceinline__ void block_epilogue(const tm_f32x16 &acc, const float
 // ---------------------------------------------------------------------------
 constexpr int kDmaBufs = 4;
 constexpr int kDmaStageBytes = 16384;
-constexpr int kDmaMaxChunk = 2048;  // centroids per workgroup (penalty array in LDS)
 
 // The same direct-to-LDS load through a buffer resource (4 SGPRs: base,
 // stride 0, size in bytes, raw 32-bit format): lanes whose byte offset is at
@@ -636,17 +685,16 @@ __global__ __launch_bounds__(kThreads, 2) void search_top1_kernel(
 // Blocks: stage s, block i of a wave is the stage's block 2i + half (half =
 // wave / 4).  The accumulator sets, the one-block-behind epilogue and the
 // stage waits are those of search_top1_kernel.  The two halves' keys of a
-// query meet in LDS; one atomic minimum per query and workgroup.
+// query meet in LDS; then one store per query and workgroup into the
+// per-split key array keys[split][n] (DEC false: tm_search_global, merged by
+// merge_top1_kernel) or one atomic minimum into keys[n] (DEC true: the layer
+// call).
 //
 // With DEC, the workgroup that finishes a query tile last (one arrival
 // counter per tile, zero before the launch and left zero) decodes the
 // tile's finished keys into distance, centroid and |q|^2 (device-coherent
 // key loads: the other splits' minima were made on other CUs in this launch).
 // ---------------------------------------------------------------------------
-constexpr int kWideThreads = 512;
-constexpr int kWideQ = 256;  // queries per workgroup
-constexpr int kWideStageBytes = 32768;
-
 struct WideDecode {
   const float *qn_part;  // [parts][n] partial |q|^2
   int parts;
@@ -878,8 +926,12 @@ __global__ __launch_bounds__(kWideThreads, 1) void search_top1_wide_kernel(
       const int64_t r = row_base + sl * 32 + (lane & 31);
       const uint64_t o = half_keys[qg][sl * 32 + (lane & 31)];
       const uint64_t key = bk[sl] < o ? bk[sl] : o;
-      if (lane < 32 && r < n && key != ~0ull)
-        atomicMin(reinterpret_cast<unsigned long long *>(keys + r), (unsigned long long)key);
+      if (lane < 32 && r < n) {
+        if constexpr (!DEC)
+          keys[split * n + r] = key;  // per-split keys, merged by merge_top1_kernel
+        else if (key != ~0ull)
+          atomicMin(reinterpret_cast<unsigned long long *>(keys + r), (unsigned long long)key);
+      }
     }
   }
   if constexpr (DEC) {
@@ -1214,6 +1266,10 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
     else
       hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 2, METRIC>), dim3((unsigned)p.nsplit), block, 0, stream,
                          Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws, nullptr, 1);
+  } else if (K == 1 && p.wide && wide_strides_ok(ld_q, ld_c, DIM)) {
+    hipLaunchKernelGGL((search_top1_wide_kernel<DT, DIM < 256 ? DIM : 128, METRIC, false>),
+                       dim3((unsigned)p.nsplit, (unsigned)p.row_blocks), dim3(kWideThreads), 0, stream, Q, n, ld_q, C,
+                       n_cent, ld_c, c_sqnorm, p.chunk, ws, WideDecode{});
   } else if (K == 1 && DIM <= 128 && ld_c * dma_rows(DIM) * (int64_t)sizeof(T) < ((int64_t)1 << 31)) {
     // (d = 256 would not fit two waves per SIMD; the stage byte offsets must fit 31 bits)
     hipLaunchKernelGGL((search_top1_kernel<DT, DIM < 256 ? DIM : 128, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
@@ -1395,29 +1451,6 @@ int tm_internal_search_keys(int32_t dtype, const void *q, int64_t n, int64_t ld_
 // ---------------------------------------------------------------------------
 namespace {
 
-struct WidePlan {
-  int64_t tiles, nsplit, chunk;
-};
-
-inline int64_t wide_rows(int dim) { return kWideStageBytes / (dim * 2); }
-
-// One workgroup per CU where the shape allows: ranges of whole ring rounds
-// (4 stages), at most kDmaMaxChunk centroids (the start-value array).
-WidePlan plan_wide(int64_t n, int64_t c, int dim) {
-  WidePlan p;
-  p.tiles = tm_cdiv(n, kWideQ);
-  const int64_t unit = 4 * wide_rows(dim);
-  const int64_t max_split = tm_cdiv(c, unit);
-  const int64_t min_split = tm_cdiv(c, kDmaMaxChunk);
-  int64_t want = tm_cdiv(256, p.tiles);
-  if (want < min_split) want = min_split;
-  if (want > max_split) want = max_split;
-  if (want < 1) want = 1;
-  p.chunk = tm_cdiv(tm_cdiv(c, want), unit) * unit;
-  p.nsplit = tm_cdiv(c, p.chunk);
-  return p;
-}
-
 template <int DT, int DIM, int METRIC>
 void launch_search_decode(const WidePlan &p, const void *q, int64_t n, int64_t ld_q, const void *cents,
                           int64_t n_cent, int64_t ld_c, const float *c_sqnorm, uint64_t *keys, const WideDecode &wd,
@@ -1444,10 +1477,7 @@ int64_t tm_internal_search_decode_tiles(int32_t dtype, int64_t n, int64_t n_cent
                                         int32_t dim) {
   if (!tm_internal_search_keys_ok(dtype, n, n_cent, ld_c, dim, 1) || ld_q < dim) return 0;
   const WidePlan p = plan_wide(n, n_cent, dim);
-  if (p.tiles * p.nsplit < 192) return 0;  // leaves too many CUs idle: the 4-wave kernel
-  const int64_t rows = wide_rows(dim);
-  if (ld_c * 2 * rows >= ((int64_t)1 << 31) || ld_q * 2 * rows >= ((int64_t)1 << 31) || p.chunk > kDmaMaxChunk)
-    return 0;
+  if (p.tiles * p.nsplit < kWideMinGroups || !wide_strides_ok(ld_q, ld_c, dim)) return 0;
   return p.tiles;
 }
 

@@ -81,6 +81,8 @@ PROTOTYPES = {
     "tm_keep_select": (C.c_int, [vp, i64, i64, i64, vp, vp, sz, vp]),
     "tm_gather_combine": (C.c_int, [i32, i64, i32, vp, vp, i64, i64, vp, i64, i32, vp, i64, i64, vp, vp, i64, i32,
                                     vp, i64, vp, i64, vp]),
+    "tm_gather_combine_ranked": (C.c_int, [i32, i64, i32, vp, i64, i64, vp, i64, i32, vp, i64, i64, vp, vp, vp, i64,
+                                           vp, i64, i64, vp, vp]),
     "tm_decode_combine_update": (C.c_int, [i32, i32, i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
                                            vp, vp, vp, vp, i64, i32, i64, i64, i32, vp, vp, vp, vp, vp, i64, vp]),
     "tm_importance_workspace_size": (sz, [i64, i32, i64]),

@@ -140,6 +140,28 @@ class GlobalTable:
                N.stream(self.device))
         return out
 
+    def gather_combine_ranked(self, slot_out, weights, idx, dist, n_keep: int, residual=None, out=None, keep=None):
+        """gather_combine for a top-1 table whose keep set is decided in the
+        same launch: token i is kept when fewer than n_keep tokens have a
+        larger distance (ties -> lower index), as keep_select would choose.
+        Returns (out, keep)."""
+        N.require_hip(slot_out, weights, idx, dist)
+        n, top_k = weights.shape
+        if out is None:
+            out = self._buf("out", (n, self.hidden), self.dtype)
+        if keep is None:
+            keep = self._buf("keep", (n,), torch.bool)
+        d = dist.reshape(-1) if dist.dim() > 1 else dist
+        if d.numel() != n or not d.is_contiguous():
+            raise ValueError("gather_combine_ranked: dist must hold one contiguous distance per token")
+        so = slot_out
+        N.call("tm_gather_combine_ranked", N.dtype_tag(self.dtype), n, self.hidden, N.ptr(so), so.stride(0),
+               so.stride(1), N.ptr(weights), weights.stride(0), top_k, N.ptr(self.values), self.n_cent,
+               self.values.stride(0), N.ptr(idx), N.ptr(d), N.ptr(residual),
+               0 if residual is None else residual.stride(0), N.ptr(out), out.stride(0), int(n_keep),
+               N.ptr(N.as_u8(keep)), N.stream(self.device))
+        return out, keep
+
     def route(self, router_logits: torch.Tensor, top_k: int):
         n, e = router_logits.shape
         w = self._buf("route_w", (n, top_k), torch.float32)

@@ -383,6 +383,58 @@ def test_gather_combine_vs_oracle(hip_device, k, nn, hidden, with_residual):
     assert_bf16_output(np64(out), exact, abssum)
 
 
+@pytest.mark.parametrize("n,k,hidden,with_residual,ties,dt", [
+    (4096, 8, 2048, True, False, torch.bfloat16), (4096, 8, 2048, True, True, torch.bfloat16),
+    (1001, 6, 1000, False, True, torch.float16), (5, 8, 64, True, False, torch.bfloat16),
+    (515, 8, 2048, True, False, torch.bfloat16)])
+def test_gather_combine_ranked_matches_keep_select(hip_device, n, k, hidden, with_residual, ties, dt):
+    """tm_gather_combine_ranked (keep set ranked inside the combine) gives the
+    keep mask of tm_keep_select and the output of tm_gather_combine with that
+    mask, bit for bit: ragged token counts (not a multiple of 4), tied
+    distances across the keep boundary, no residual, fp16, hidden < 2048,
+    every n_keep from 1 to n at the boundaries; the output is also checked
+    against the oracle."""
+    from table_moe.cache_engine import GlobalTable
+
+    g = _gen(907 + n + k + hidden)
+    dev = hip_device
+    C, d = 300, 64
+    values = torch.randn(C, hidden, generator=g).to(dt)
+    slot_out = torch.randn(n, k, hidden, generator=g).to(dt)
+    w = torch.rand(n, k, generator=g) + 0.01
+    w[0] = 0.0  # weights summing to 0: no slot contribution
+    idx = torch.randint(0, C, (n, 1), generator=g)
+    idx[1, 0] = -1  # no centroid: residual only when not kept
+    dist = torch.rand(n, 1, generator=g) * 10
+    if ties:  # a few distinct values only: many ties at every boundary
+        dist = torch.floor(dist * 2) / 2
+    resid = torch.randn(n, hidden, generator=g).to(dt) if with_residual else None
+    tbl = GlobalTable(torch.zeros(C, d, dtype=dt, device=dev), values.to(dev),
+                      (torch.zeros(hidden, d, dtype=dt, device=dev), torch.zeros(d, dtype=dt, device=dev)))
+    dd, so, wd, idd = dist.to(dev), slot_out.to(dev), w.to(dev), idx.to(dev)
+    rd = None if resid is None else resid.to(dev)
+    for n_keep in sorted({1, max(1, int(n * 0.6)), n - 1 if n > 1 else 1, n}):
+        out, keep = tbl.gather_combine_ranked(so, wd, idd, dd, n_keep, rd, out=torch.empty(n, hidden, dtype=dt,
+                                                                                           device=dev),
+                                              keep=torch.zeros(n, dtype=torch.bool, device=dev))
+        want_keep = tbl.keep_select(dd[:, 0], n_keep).clone()
+        want = tbl.gather_combine(want_keep, so, wd, idd, dd, rd, out=torch.empty(n, hidden, dtype=dt, device=dev))
+        torch.cuda.synchronize()
+        assert torch.equal(keep, want_keep), n_keep
+        assert int(keep.sum()) == n_keep
+        assert torch.equal(out, want), n_keep
+    kn = keep.cpu().numpy()
+    np.testing.assert_array_equal(kn, O.keep_select(np64(dist)[:, 0], n_keep))
+    # the oracle's combine on the rows without the zero-weight / no-centroid cases
+    r = np.zeros((n, hidden)) if resid is None else np64(resid)
+    sl = slice(2, None)
+    exact = O.gather_combine(kn[sl], np64(slot_out)[sl], np64(w)[sl], np64(values), idx.numpy()[sl], np64(dist)[sl],
+                             r[sl], O.F32)
+    abssum = O.gather_combine(kn[sl], np.abs(np64(slot_out))[sl], np64(w)[sl], np.abs(np64(values)),
+                              idx.numpy()[sl], np64(dist)[sl], np.abs(r)[sl], O.F32)
+    assert_bf16_output(np64(out)[sl], exact, abssum)
+
+
 # ------------------------------------------ mode G: full layer at config 2
 def test_layer_forward_config2_end_to_end(hip_device):
     from table_moe.cache_engine import GlobalTable
