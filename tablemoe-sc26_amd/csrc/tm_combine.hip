@@ -245,7 +245,7 @@ __device__ __forceinline__ bool rank_keep(const float *__restrict__ dist, int64_
 }
 
 template <int DT, int TK, int NN>
-__global__ __launch_bounds__(kThreads) void gather_combine_tk_kernel(
+__global__ __launch_bounds__(kThreads, 8) void gather_combine_tk_kernel(
     int hidden, const uint8_t *__restrict__ keep, const typename Elem<DT>::T *__restrict__ slot_out, int64_t so_b,
     int64_t so_s, const float *__restrict__ w, int64_t ld_w, const typename Elem<DT>::T *__restrict__ values,
     int64_t n_cent, int64_t ld_v, const int64_t *__restrict__ idx, const float *__restrict__ dist, int64_t ld_idx,
@@ -276,13 +276,16 @@ __global__ __launch_bounds__(kThreads) void gather_combine_tk_kernel(
         for (int i = 0; i < 8; ++i) acc[i] = 0.f;
       }
       if (any) {
-        float v[TK][8];
-#pragma unroll
-        for (int s = 0; s < TK; ++s) tm_load8_nt<DT>(src + (int64_t)s * so_s + h0, v[s]);
+        tm_u32x4 raw[TK];  // 16-bit values until used: 4 registers per slot instead of 8
 #pragma unroll
         for (int s = 0; s < TK; ++s)
+          raw[s] = __builtin_nontemporal_load(reinterpret_cast<const tm_u32x4 *>(src + (int64_t)s * so_s + h0));
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], v[s][i], acc[i]);
+        for (int s = 0; s < TK; ++s) {
+          const T *e = reinterpret_cast<const T *>(&raw[s]);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], Elem<DT>::to_f(e[i]), acc[i]);
+        }
       }
       tm_store8_nt<DT>(dst + h0, acc);
     }
@@ -332,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void gather_combine_tk_kernel(
 // (needed either way) is loaded before the ranking.  The arithmetic is
 // gather_combine_tk_kernel's (NN = 1).
 template <int DT, int TK, int TPB>
-__global__ __launch_bounds__(TPB * kThreads) void gather_combine_rank_kernel(
+__global__ __launch_bounds__(TPB * kThreads, 8) void gather_combine_rank_kernel(
     int hidden, const typename Elem<DT>::T *__restrict__ slot_out, int64_t so_b, int64_t so_s,
     const float *__restrict__ w, int64_t ld_w, const typename Elem<DT>::T *__restrict__ values, int64_t n_cent,
     int64_t ld_v, const int64_t *__restrict__ idx, const float *__restrict__ dist,
@@ -363,13 +366,15 @@ __global__ __launch_bounds__(TPB * kThreads) void gather_combine_rank_kernel(
 #pragma unroll
       for (int s = 0; s < TK; ++s) coef[s] = coef[s] / sum;
       const T *src = slot_out + b * so_b + h0;
-      float v[TK][8];
+      tm_u32x4 raw[TK];  // 16-bit values until used: 4 registers per slot instead of 8
 #pragma unroll
-      for (int s = 0; s < TK; ++s) tm_load8_nt<DT>(src + (int64_t)s * so_s, v[s]);
+      for (int s = 0; s < TK; ++s) raw[s] = __builtin_nontemporal_load(reinterpret_cast<const tm_u32x4 *>(src + (int64_t)s * so_s));
 #pragma unroll
-      for (int s = 0; s < TK; ++s)
+      for (int s = 0; s < TK; ++s) {
+        const T *e = reinterpret_cast<const T *>(&raw[s]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], v[s][i], acc[i]);
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], Elem<DT>::to_f(e[i]), acc[i]);
+      }
     }
   } else {
     const int64_t c = idx[b];
