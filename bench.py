@@ -306,7 +306,7 @@ COPY_CAL_BYTES = 256 << 20  # bytes read (and written) by the calibration copy
 def copy_calibration(reps=3):
     """A plain device copy pass over COPY_CAL_BYTES, launched `reps` times: under
     `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` its counters give the scale
-    from counter KiB to bytes moved (profiles/gather_combine_config2_traffic.txt)."""
+    from counter KiB to bytes moved (profiles/gather_combine_ranked_config2_traffic.txt)."""
     import torch
 
     a = torch.empty(COPY_CAL_BYTES // 2, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
@@ -317,11 +317,12 @@ def copy_calibration(reps=3):
     del a, b
 
 
-def traffic_from_profile(kernel_prefix):
+def traffic_from_profile(kernel_prefix, summary):
     """HBM bytes per launch of `kernel_prefix` from the committed PMC summary
-    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by the same
-    counter's reading for the calibration copy), or None without a summary."""
-    path = REPO / "profiles" / "gather_combine_config2_traffic.txt"
+    profiles/<summary> (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each
+    scaled by the same counter's reading for the calibration copy), or None
+    without a summary."""
+    path = REPO / "profiles" / summary
     if not path.exists():
         return None
     vals = {}
@@ -432,7 +433,8 @@ def main() -> int:
         achieved = by[dom] / (ku[dom] * 1e-6) / 1e9
         roof = {"kernel": entry, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBPS,
-                "traffic": traffic_from_profile("gather_combine") if dom == "combine" else None,
+                "traffic": (traffic_from_profile("gather_combine_rank", "gather_combine_ranked_config2_traffic.txt")
+                            if dom == "combine" and ranked else None),
                 "algorithmic_per_launch": by[dom]}
     roof["avg_launch_us"] = ku[dom]
 
