@@ -1,7 +1,7 @@
 // Keep-rate selection of the n_keep largest of n <= NT * kKeepRegs scores
-// (ties -> lower index), as a block-level device routine shared by the
-// keep-select kernel (one 1024-thread workgroup) and the search kernel whose
-// last-arriving workgroup runs it on the finished top-1 keys.
+// (ties -> lower index) as a block-level device routine, and the decoding of
+// packed top-1 search keys into distances (also used by the search kernel
+// that decodes its own keys).
 #pragma once
 
 #include "tm_common.h"
@@ -57,10 +57,8 @@ struct __align__(16) KeepSmem {
 // bins of rank NT - 1 - t).  Ties at the boundary: lower token index first.
 // Thread t owns the contiguous score range [t * per, (t + 1) * per).  With
 // `ks.keys` set, the scores are decoded from packed top-1 search keys and the
-// routine also writes each token's distance, centroid and |q|^2; COHERENT
-// reads those keys with device-coherent loads (their last writers ran in the
-// same launch, on other CUs).
-template <int NT, bool COHERENT>
+// routine also writes each token's distance, centroid and |q|^2.
+template <int NT>
 __device__ __forceinline__ void tm_keep_select_fast(const float *__restrict__ score, int64_t n, int64_t ld,
                                                     int64_t n_keep, uint8_t *__restrict__ out, const KeySrc &ks,
                                                     KeepSmem<NT> &sm) {
@@ -84,7 +82,7 @@ __device__ __forceinline__ void tm_keep_select_fast(const float *__restrict__ sc
   if (ks.keys != nullptr) {  // uniform
     uint64_t kv[kKeepRegs];
     float qn[kKeepRegs];
-    if (!COHERENT && per == 4 && cnt == 4 && ks.parts <= 4 && (n & 3) == 0) {  // 16-byte loads (lo is a multiple of 4)
+    if (per == 4 && cnt == 4 && ks.parts <= 4 && (n & 3) == 0) {  // 16-byte loads (lo is a multiple of 4)
       const uint4 k01 = *reinterpret_cast<const uint4 *>(ks.keys + lo);
       const uint4 k23 = *reinterpret_cast<const uint4 *>(ks.keys + lo + 2);
       kv[0] = ((uint64_t)k01.y << 32) | k01.x; kv[1] = ((uint64_t)k01.w << 32) | k01.z;
@@ -101,8 +99,7 @@ __device__ __forceinline__ void tm_keep_select_fast(const float *__restrict__ sc
 #pragma unroll
       for (int j = 0; j < kKeepRegs; ++j)
         if (j < cnt) {
-          kv[j] = COHERENT ? __hip_atomic_load(ks.keys + lo + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                           : ks.keys[lo + j];
+          kv[j] = ks.keys[lo + j];
           float a[4];
 #pragma unroll
           for (int p = 0; p < 4; ++p) a[p] = p < ks.parts ? ks.qn_part[(int64_t)p * n + lo + j] : 0.f;

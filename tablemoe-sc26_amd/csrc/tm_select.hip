@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kSelThreads) void keep_select_fast_kernel(const flo
                                                                        int64_t ld, int64_t n_keep,
                                                                        uint8_t *__restrict__ out, KeySrc ks) {
   __shared__ KeepSmem<kSelThreads> sm;
-  tm_keep_select_fast<kSelThreads, false>(score, n, ld, n_keep, out, ks, sm);
+  tm_keep_select_fast<kSelThreads>(score, n, ld, n_keep, out, ks, sm);
 }
 
 // ---------------------------------------------------------------------------
