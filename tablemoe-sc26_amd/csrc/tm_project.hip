@@ -356,11 +356,16 @@ __global__ __launch_bounds__(256, 2) void project_cols_kernel(
   };
   uint4 *xw = &xs[wave][0];
   auto store_x = [&](int u, int c) {
+    if ((ks_begin + 4 * c + 4) * 32 <= hidden) {  // uniform: the whole chunk lies inside `hidden`
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 4 * i + xr0;
-      const int kk = (ks_begin + 4 * c) * 32 + 8 * (xslot ^ (r & 15));
-      xw[r * 16 + xslot] = kk < hidden ? xr[u][i] : make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < 8; ++i) xw[(4 * i + xr0) * 16 + xslot] = xr[u][i];
+    } else {  // (a select per element here made the compiler branch and wait around each one)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 4 * i + xr0;
+        const int kk = (ks_begin + 4 * c) * 32 + 8 * (xslot ^ (r & 15));
+        xw[r * 16 + xslot] = kk < hidden ? xr[u][i] : make_uint4(0, 0, 0, 0);
+      }
     }
   };
   // A fragment of k-step t of the chunk in LDS, rows 16*rb + lane%16
