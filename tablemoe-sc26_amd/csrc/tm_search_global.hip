@@ -778,19 +778,26 @@ __global__ __launch_bounds__(kWideThreads, 1) void search_top1_wide_kernel(
     }
   };
   constexpr int IPT = kDmaMaxChunk / kWideThreads;
-  float init_v[IPT];
+  float sqn[IPT];
 #pragma unroll
   for (int u = 0; u < IPT; ++u) {
     const int64_t c = c_begin + tid + u * kWideThreads;
-    const float v = (METRIC == TM_METRIC_L2) ? -0.5f * c_sqnorm[c < c_last ? c : c_last] : 0.f;
-    init_v[u] = (c < c_end) ? v : -__builtin_huge_valf();
+    sqn[u] = (METRIC == TM_METRIC_L2) ? c_sqnorm[c < c_last ? c : c_last] : 0.f;
   }
   issue_q(st2, 0);
   if constexpr (QST == 2) issue_q(st3, 1);
   issue(st0, 0);
-  tm_wait_vm_lgkm0<0>();  // start values, the query tile and stage 0 (this thread's loads)
+  // The start values are formed only now: left to itself the compiler
+  // computed them (waiting for the norms) before issuing the ring loads.
 #pragma unroll
-  for (int u = 0; u < IPT; ++u) init_s[tid + u * kWideThreads] = init_v[u];
+  for (int u = 0; u < IPT; ++u) asm volatile("" : "+v"(sqn[u]));
+  tm_wait_vm_lgkm0<0>();  // norms, the query tile and stage 0 (this thread's loads)
+#pragma unroll
+  for (int u = 0; u < IPT; ++u) {
+    const int64_t c = c_begin + tid + u * kWideThreads;
+    init_s[tid + u * kWideThreads] = (c < c_end) ? ((METRIC == TM_METRIC_L2) ? -0.5f * sqn[u] : 0.f)
+                                                 : -__builtin_huge_valf();
+  }
   issue(st1, 1);
   tm_wait_vm_lgkm0<NDMA>();  // init_s written; stage 1 may still load
   __builtin_amdgcn_s_barrier();
