@@ -585,6 +585,28 @@ def test_layer_forward_fused_shapes_match_staged(hip_device, n, hidden, dim, mix
         assert (dist[~keep] <= kept_d.min()).all()
 
 
+@pytest.mark.parametrize("dtype,metric", [(torch.float16, "l2"), (torch.bfloat16, "dot"), (torch.float16, "dot")])
+def test_layer_forward_ranked_plan_dtypes_metrics(hip_device, dtype, metric):
+    """The ranked top-1 plan (wide search decoding its keys, keep set ranked
+    in the combine) with fp16 data and the dot metric equals the stage calls
+    bit for bit, on two calls in a row."""
+    from table_moe.cache_engine import GlobalTable
+    from table_moe.synth import make_workload
+
+    dev = hip_device
+    wl = make_workload(2, dtype=dtype)
+    d = wl.to(dev)
+    a = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt), metric=metric)
+    b = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt), metric=metric)
+    rb = b.layer_forward_staged(d.x, d.is_vision, d.logits, d.slot_out, d.residual, 8, 1, 0.6)
+    for rep in range(2):
+        ra = a.layer_forward(d.x, d.is_vision, d.logits, d.slot_out, d.residual, 8, 1, 0.6)
+        torch.cuda.synchronize()
+        for key in ("weights", "ids", "q", "qn", "dist", "idx", "keep", "out"):
+            assert torch.equal(ra[key], rb[key]), (key, rep)
+    assert int(ra["keep"].sum()) == 2457
+
+
 @pytest.mark.parametrize("cfg,n,hidden,dim,n_cent,nn,variant", [
     (3, 1, 2048, 128, 16384, 4, "base"), (3, 8, 2048, 128, 16384, 4, "base"), (3, 32, 2048, 128, 16384, 1, "base"),
     (3, 64, 1000, 64, 1024, 4, "mix"), (5, 33, 2560, 256, 20000, 4, "mix"), (3, 17, 264, 128, 300, 1, "mix"),

@@ -344,6 +344,9 @@ GLOBAL_CASES = [
     (77, 5000, 256, 2, "dot", torch.bfloat16),
     (33, 129, 128, 3, "l2", torch.float16),
     (130, 77, 128, 1, "dot", torch.float16),
+    # wide top-1 kernel (8-wave workgroups, one per CU): dot metric and fp16, d = 64
+    (4096, 8192, 128, 1, "dot", torch.float16),
+    (4096, 16384, 64, 1, "l2", torch.float16),
 ]
 
 
@@ -380,6 +383,8 @@ def test_search_global_vs_oracle(hip_device, n, c, dim, top_k, metric, dtype):
     (300, 1000, 128, 4, "l2"),    # top-k tile kernel
     (40, 3000, 128, 1, "l2"),     # decode-sized stream kernel
     (40, 3000, 128, 4, "l2"),
+    (4096, 8192, 128, 1, "l2"),   # wide top-1 kernel: ties across its two block halves and ranges
+    (4096, 8192, 128, 1, "dot"),
 ])
 def test_search_global_exact_ties(hip_device, n, c, dim, top_k, metric):
     """Centroid rows repeat (row i equals row i % 97), so every distance is tied
