@@ -34,6 +34,7 @@ from pathlib import Path
 REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO / "tablemoe-sc26_amd"))
 sys.path.insert(0, str(REPO))
+sys.path.insert(0, str(REPO / "tests"))  # synth.py: seeded workloads of the BASELINE configs
 
 HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
@@ -63,7 +64,7 @@ def run_layer_bench(cfg_id, steps, warmup, n=None):
     import torch
 
     from table_moe.cache_engine import GlobalTable
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     dev = torch.device("cuda:0")
     t0 = time.time()
@@ -236,7 +237,7 @@ def run_recompute_bench(steps, warmup):
 
     from table_moe.cache_engine import GlobalTable
     from table_moe.ops import GroupedExperts, expert_swiglu
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     dev = torch.device("cuda:0")
     wl = make_workload(5)

@@ -324,8 +324,10 @@ int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden, const uin
  * reference: it replaces the keep selection (table_moe/skip/pruning.py:45
  * count) followed by the gather + combine of tm_gather_combine.  dtype F16
  * or BF16, top_k 6 or 8, hidden <= 2048 and a multiple of 8, 16-byte aligned
- * rows and dist; each token's workgroup reads all n distances, so it suits
- * n up to a few thousand. */
+ * rows and dist; each token's workgroup reads all n distances (the work grows
+ * as n^2), so n_tokens <= TM_RANKED_MAX_TOKENS (TM_EINVAL_SHAPE beyond: run
+ * tm_keep_select + tm_gather_combine instead). */
+#define TM_RANKED_MAX_TOKENS 16384
 int tm_gather_combine_ranked(int32_t dtype, int64_t n_tokens, int32_t hidden, const void *slot_out,
                              int64_t so_b, int64_t so_s, const float *weights, int64_t ld_w, int32_t top_k,
                              const void *values, int64_t n_cent, int64_t ld_v, const int64_t *idx,

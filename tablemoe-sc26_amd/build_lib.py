@@ -73,7 +73,16 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> Path:
+def _up_to_date(src: Path) -> bool:
+    """True when src's object is newer than src and every header it may include."""
+    obj = BUILD_DIR / (src.stem + ".o")
+    if not obj.exists():
+        return False
+    deps = [src, *CSRC.glob("*.h"), *INCLUDE.glob("*.h")]
+    return obj.stat().st_mtime > max(d.stat().st_mtime for d in deps)
+
+
+def build(jobs: int | None = None, verbose: bool = True, incremental: bool = False) -> Path:
     if not HIPCC.exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
@@ -84,8 +93,10 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     jobs = jobs or min(len(sources), max(1, os.cpu_count() or 1), 8)
     if verbose:
         print(f"[build_lib] compiling {len(sources)} sources for {ARCH} with {jobs} jobs", flush=True)
+    stale = [s for s in sources if not (incremental and _up_to_date(s))]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
+        list(ex.map(_compile, stale))
+    objs = [BUILD_DIR / (s.stem + ".o") for s in sources]
     tlib = torch_lib_dir()
     if not (tlib / "libamdhip64.so").exists():
         raise RuntimeError(f"torch's HIP runtime not found in {tlib}")
@@ -108,8 +119,10 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--incremental", action="store_true",
+                    help="recompile only sources whose object is older than the source or a header")
     args = ap.parse_args()
-    build(args.jobs)
+    build(args.jobs, incremental=args.incremental)
     return 0
 
 

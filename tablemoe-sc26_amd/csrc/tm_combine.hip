@@ -731,9 +731,12 @@ extern "C" int tm_gather_combine_ranked(int32_t dtype, int64_t n_tokens, int32_t
                                         const int64_t *idx, const float *dist, const void *residual, int64_t ld_r,
                                         void *out, int64_t ld_o, int64_t n_keep, uint8_t *out_keep,
                                         tm_stream_t stream) {
-  TM_REQUIRE(n_tokens >= 0 && n_tokens < (int64_t)0x7fffffff && hidden > 0 && ld_w >= top_k && ld_o >= hidden &&
-                 ld_v >= hidden,
-             TM_EINVAL_SHAPE, "tm_gather_combine_ranked: bad sizes");
+  TM_REQUIRE(n_tokens >= 0 && hidden > 0 && ld_w >= top_k && ld_o >= hidden && ld_v >= hidden, TM_EINVAL_SHAPE,
+             "tm_gather_combine_ranked: bad sizes");
+  // each token's workgroup reads all n distances: the work grows as n^2
+  TM_REQUIRE(n_tokens <= TM_RANKED_MAX_TOKENS, TM_EINVAL_SHAPE,
+             "tm_gather_combine_ranked: %lld tokens > %d (use tm_keep_select + tm_gather_combine)",
+             (long long)n_tokens, TM_RANKED_MAX_TOKENS);
   if (n_tokens == 0) return TM_OK;
   TM_REQUIRE(dtype == TM_DT_BF16 || dtype == TM_DT_F16, TM_EINVAL_DTYPE,
              "tm_gather_combine_ranked: dtype must be F16 or BF16");

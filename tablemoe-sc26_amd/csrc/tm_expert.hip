@@ -212,7 +212,9 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
   // Each thread keeps the experts of its tokens (b = tid + 1024 j, j < kGroupTok)
   // in registers: all of their loads are issued before the first count.
   int32_t ex[kGroupTok][kGroupSlots];
-  const bool fast = n <= (int64_t)kGroupTok * kGroupThreads && top_k <= kGroupSlots;  // uniform
+  // n == 0 takes the loop path, whose loops run no iteration: the register
+  // path clamps to token n - 1 and would read below `ids` and `mask`.
+  const bool fast = n > 0 && n <= (int64_t)kGroupTok * kGroupThreads && top_k <= kGroupSlots;  // uniform
   if (fast) {
 #pragma unroll
     for (int j = 0; j < kGroupTok; ++j) {

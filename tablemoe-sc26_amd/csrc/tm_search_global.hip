@@ -942,7 +942,21 @@ __global__ __launch_bounds__(kWideThreads, 1) void search_top1_wide_kernel(
     }
   }
   if constexpr (DEC) {
-    // arrival: every thread's key updates performed, then one ticket per tile
+    // Arrival: every thread's key updates performed, then one ticket per tile.
+    // Ordering argument (the same as the decode plan's projection hand-off):
+    // the keys are only ever touched by device-scope atomics (atomicMin here,
+    // the relaxed agent-scope load below), which the hardware performs at
+    // one point of coherence per address for every XCD, bypassing the
+    // non-coherent per-XCD L2 for the load (sc1).  On gfx9 vmcnt also counts
+    // returnless atomics, so the s_waitcnt vmcnt(0) below returns only after
+    // this workgroup's atomicMins are acknowledged, and only then is the
+    // ticket taken; the last ticket therefore follows every tile workgroup's
+    // updates, and its keys load is issued after it returns.  The HIP memory
+    // model proper would ask for agent-scope release/acquire fences around
+    // the ticket instead; those write back and invalidate the whole L2
+    // (buffer_wbl2 / buffer_inv), measured at several microseconds per
+    // launch of this shape, so the kernel relies on the per-address
+    // coherence of its atomics and the explicit wait.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     tm_wait_vm_lgkm0<0>();
     __syncthreads();

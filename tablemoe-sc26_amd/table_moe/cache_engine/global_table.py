@@ -180,11 +180,10 @@ class GlobalTable:
         y = self.gather_combine(keep, slot_out, w, idx, dist, residual, out)
         return {"weights": w, "ids": ids, "q": q, "qn": qn, "dist": dist, "idx": idx, "keep": keep, "out": y}
 
-    def layer_forward(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k: int = 8,
-                      n_nearest: int = 1, keep_rate: float = 0.6, out=None, stage_events=None):
-        """One MoE layer of the table path in one C-ABI call (tm_table_forward);
-        returns a dict of every stage's output.  ``stage_events``: optional six
-        torch.cuda.Event recorded around the stages."""
+    def _layer_io(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k, n_nearest, keep_rate,
+                  out):
+        """The tm_layer_io of one layer call (buffers from this table's pool)
+        and the dict of every stage's output it fills."""
         N.require_hip(hidden, router_logits, slot_out)
         if hidden.dtype != self.dtype or slot_out.dtype != self.dtype:
             raise RuntimeError(f"hidden/slot_out dtype must be the table dtype {self.dtype}")
@@ -212,6 +211,21 @@ class GlobalTable:
             residual=N.ptr(residual), ld_r=0 if residual is None else residual.stride(0), out=N.ptr(out),
             ld_o=out.stride(0), weights=N.ptr(w), expert_ids=N.ptr(ids), q=N.ptr(q), q_sqnorm=N.ptr(qn),
             dist=N.ptr(dist), idx=N.ptr(idx), keep=N.ptr(N.as_u8(keep)))
+        # the tensors the io points at stay referenced by the returned dict
+        res = {"weights": w, "ids": ids, "q": q, "qn": qn, "dist": dist, "idx": idx, "keep": keep, "out": out,
+               "_inputs": (x, logits, slot_out, isv)}
+        return io, res
+
+    def layer_forward(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k: int = 8,
+                      n_nearest: int = 1, keep_rate: float = 0.6, out=None, stage_events=None):
+        """One MoE layer of the table path in one C-ABI call (tm_table_forward);
+        returns a dict of every stage's output.  ``stage_events``: optional six
+        torch.cuda.Event recorded around the stages.  The returned tensors are
+        this table's reusable buffers: the next call overwrites them (pass
+        ``out`` to keep an output)."""
+        io, res = self._layer_io(hidden, is_vision, router_logits, slot_out, residual, router_top_k, n_nearest,
+                                 keep_rate, out)
+        n = io.n_tokens
         nbytes = N.lib().tm_table_forward_workspace_size(C.byref(self._desc), n, n_nearest)
         ws = self._buf("layer_ws", (max(nbytes, 1),), torch.uint8)
         evs = None
@@ -219,4 +233,5 @@ class GlobalTable:
             evs = (C.c_void_p * 6)(*[e.cuda_event for e in stage_events])
         N.check(N.lib().tm_table_forward(C.byref(self._desc), C.byref(io), N.ptr(ws), ws.numel(), evs,
                                          N.stream(self.device)), "tm_table_forward")
-        return {"weights": w, "ids": ids, "q": q, "qn": qn, "dist": dist, "idx": idx, "keep": keep, "out": out}
+        res.pop("_inputs")
+        return res

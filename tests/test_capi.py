@@ -107,3 +107,13 @@ def test_argument_validation_without_device(lib):
                                None) == N.TM_EWORKSPACE
     assert lib.tm_project_pack(N.TM_DT_F32, C.c_void_p(16), 2048, 128, 128, 1, C.c_void_p(16), 1 << 20,
                                None) == N.TM_EINVAL_DTYPE
+
+
+
+def test_ranked_limit_without_device(lib):
+    """The ranked combine rejects a token count beyond its bound before any
+    HIP call (each token's workgroup reads all n distances)."""
+    p = C.c_void_p(256)
+    assert lib.tm_gather_combine_ranked(N.TM_DT_BF16, 16385, 2048, p, 8 * 2048, 2048, p, 8, 8, p, 8192, 2048, p, p,
+                                        p, 2048, p, 2048, 100, p, None) == N.TM_EINVAL_SHAPE
+    assert b"16384" in lib.tm_last_error()

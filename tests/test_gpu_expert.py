@@ -95,6 +95,33 @@ def test_group_slots_buckets_every_pair(hip_device, n, k):
         assert np.all(ids.numpy()[bb, ss] == ex)
 
 
+def test_group_slots_empty_batch(hip_device):
+    """An empty recompute batch (no tokens, null id/mask pointers) groups
+    nothing: zero offsets and a zero row/tile count, and the grouped MLP after
+    it is a no-op; the offsets/tiles buffers start non-zero so the kernel's
+    writes are what the test sees."""
+    from table_moe.ops import GroupedExperts
+
+    dev = hip_device
+    e, h, k = 64, 128, 6
+    w = torch.zeros(e, 128, h, dtype=torch.bfloat16, device=dev)
+    ge = GroupedExperts(w, w.clone(), torch.zeros(e, h, 128, dtype=torch.bfloat16, device=dev))
+    ids = torch.empty(0, k, dtype=torch.long, device=dev)
+    keep = torch.empty(0, dtype=torch.bool, device=dev)
+    slot_out = torch.empty(0, k, h, dtype=torch.bfloat16, device=dev)
+    t_max = N.lib().tm_group_slots_tiles(0, e)
+    offs = torch.full((e + 1,), 7, dtype=torch.int32, device=dev)
+    tiles = torch.full((2 + 2 * t_max,), 7, dtype=torch.int32, device=dev)
+    N.call("tm_group_slots", None, 0, k, k, None, 1, 0, e, k * h, h, N.ptr(offs), None, None, N.ptr(tiles),
+           N.stream(dev))
+    torch.cuda.synchronize()
+    assert (offs.cpu() == 0).all()
+    assert tiles[0].item() == 0 and tiles[1].item() == 0
+    out = ge.forward(torch.empty(0, h, dtype=torch.bfloat16, device=dev), ids, keep, slot_out)
+    torch.cuda.synchronize()
+    assert out.shape == (0, k, h)
+
+
 @pytest.mark.parametrize("mask_kind", ["token", "slot"])
 def test_grouped_swiglu_vs_oracle_and_single_expert(hip_device, mask_kind):
     """Config-5 shapes (64 experts, top-6, hidden 2560, intermediate 1536) on

@@ -442,7 +442,7 @@ def test_gather_combine_ranked_matches_keep_select(hip_device, n, k, hidden, wit
 # ------------------------------------------ mode G: full layer at config 2
 def test_layer_forward_config2_end_to_end(hip_device):
     from table_moe.cache_engine import GlobalTable
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     wl = make_workload(2)
     dev = hip_device
@@ -514,7 +514,7 @@ def test_layer_forward_one_call_matches_staged(hip_device):
     shapes (64 experts, top-6, hidden 2560) at a token count that leaves a
     partial routing workgroup."""
     from table_moe.cache_engine import GlobalTable
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     dev = hip_device
     for cfg, n, nn in ((2, 1000, 1), (3, 32, 4), (5, 77, 1)):
@@ -553,7 +553,7 @@ def test_layer_forward_fused_shapes_match_staged(hip_device, n, hidden, dim, mix
     every tile, and repeated tokens.  Each table is called twice: the second
     call checks that the arrival counters were left at zero."""
     from table_moe.cache_engine import GlobalTable
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     dev = hip_device
     wl = make_workload(2, n=n, hidden=hidden, dim=dim, n_cent=n_cent)
@@ -595,7 +595,7 @@ def test_layer_forward_ranked_plan_dtypes_metrics(hip_device, dtype, metric):
     in the combine) with fp16 data and the dot metric equals the stage calls
     bit for bit, on two calls in a row."""
     from table_moe.cache_engine import GlobalTable
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     dev = hip_device
     wl = make_workload(2, dtype=dtype)
@@ -626,7 +626,7 @@ def test_layer_forward_decode_plan_matches_staged(hip_device, cfg, n, hidden, di
     residual, and fp16; each case runs twice on one workspace (the arrival
     counters must be left at zero)."""
     from table_moe.cache_engine import GlobalTable
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     dev = hip_device
     dtype = torch.float16 if variant == "fp16" else None
@@ -658,7 +658,7 @@ def test_layer_forward_config3_decode_end_to_end(hip_device):
     oracle: projection, top-4 lists on the device's queries, the keep set on
     the device's distances, and the combined rows."""
     from table_moe.cache_engine import GlobalTable
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     wl = make_workload(3)
     d = wl.to(hip_device)
@@ -695,7 +695,7 @@ def test_layer_graph_replays_match_eager(hip_device, cfg, n, nn):
     call on the same inputs (the fused top-1 plan, and the decode plan whose
     arrival counters persist from replay to replay)."""
     from table_moe.cache_engine import GlobalTable
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     dev = hip_device
     d = make_workload(cfg, n=n).to(dev)

@@ -95,7 +95,7 @@ def test_no_cpu_fallback_for_host_tensors():
 
 
 def test_synthetic_workload_properties():
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     wl = make_workload(2, n=512)
     assert wl.x.shape == (512, 2048) and wl.x.dtype == torch.bfloat16

@@ -376,7 +376,7 @@ def test_gather_combine_closed_form_one_hot():
 
 
 def test_layer_fp32_baseline_agrees_with_oracle():
-    from table_moe.synth import make_workload
+    from synth import make_workload
 
     wl = make_workload(1, n=64)
     args = [t.double().numpy() if isinstance(t, torch.Tensor) else t for t in
