@@ -499,6 +499,22 @@ size_t tm_table_forward_workspace_size(const tm_table_layer *table, int64_t n_to
 int tm_table_forward(const tm_table_layer *table, const tm_layer_io *io, void *workspace,
                      size_t workspace_bytes, void *const *stage_events, tm_stream_t stream);
 
+/* ======================================================================
+ * tm_table_forward without a workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same semantics and results as tm_table_forward (no stage events); the
+ * workspace is a static device array of TM_NOALLOC_SCRATCH_BYTES inside the
+ * library (one per GPU, held until the process ends; looked up, and its
+ * arrival counters cleared by a kernel on `stream`, on the first call on
+ * each device).  A layer whose tm_table_forward_workspace_size exceeds
+ * TM_NOALLOC_SCRATCH_BYTES is rejected with TM_EWORKSPACE.  Allocates
+ * nothing.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race.
+ * ====================================================================== */
+#define TM_NOALLOC_SCRATCH_BYTES (16u << 20)
+int tm_table_forward_noalloc(const tm_table_layer *table, const tm_layer_io *io, tm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,15 @@
 // One MoE layer of the global-table path in one call: the stage entry points
 // enqueued back to back on one stream, the workspace split between them.
+#include <mutex>
+
 #include "tm_internal.h"
+
+// Scratch of tm_table_forward_noalloc: the layer workspace as a static device
+// array (each GPU the library runs on holds its own copy until the process
+// ends).  Host code never passes the array's name to a kernel -- on the host
+// it is only a stand-in -- but the per-device address hipGetSymbolAddress
+// returns for it.
+static __device__ __align__(256) unsigned char scratch[TM_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -174,6 +183,48 @@ int general_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayou
 
 }  // namespace
 
+namespace {
+
+// Per-device address of `scratch` and whether its counter region has been
+// cleared by a launch (set-up of tm_table_forward_noalloc on each device).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+bool g_scratch_cleared[kMaxDevices];
+
+__global__ void clear_sync_kernel(uint32_t *p) {
+  if (threadIdx.x < kSync / 4) p[threadIdx.x] = 0u;
+}
+
+// The current device's scratch address; on a device's first call, looks it
+// up and enqueues the clear of the arrival counters on `s` (a kernel, not a
+// memset, so a caller may capture the call into a graph).
+int scratch_for_current_device(hipStream_t s, void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return tm_fail(TM_EHIP, "tm_table_forward_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  TM_REQUIRE(dev >= 0 && dev < kMaxDevices, TM_EINVAL_ARG, "tm_table_forward_noalloc: device %d beyond %d", dev,
+             kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return tm_fail(TM_EHIP, "tm_table_forward_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                     hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  if (!g_scratch_cleared[dev]) {
+    hipLaunchKernelGGL(clear_sync_kernel, dim3(1), dim3(kSync / 4), 0, s, static_cast<uint32_t *>(g_scratch_ptr[dev]));
+    TM_LAUNCH_CHECK("tm_table_forward_noalloc(clear)");
+    g_scratch_cleared[dev] = true;
+  }
+  *out = g_scratch_ptr[dev];
+  return TM_OK;
+}
+
+}  // namespace
+
 extern "C" size_t tm_struct_size(int32_t which) {
   return which == 0 ? sizeof(tm_table_layer) : (which == 1 ? sizeof(tm_layer_io) : 0);
 }
@@ -226,4 +277,18 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
                            io->n_nearest, io->n_nearest, io->residual, io->ld_r, io->out, io->ld_o, stream);
   if (st != TM_OK) return st;
   return record(stage_events, 5, s);
+}
+
+extern "C" int tm_table_forward_noalloc(const tm_table_layer *t, const tm_layer_io *io, tm_stream_t stream) {
+  TM_REQUIRE(t && io, TM_EINVAL_ARG, "tm_table_forward_noalloc: null descriptor");
+  TM_REQUIRE(io->n_tokens >= 0, TM_EINVAL_SHAPE, "tm_table_forward_noalloc: negative token count");
+  if (io->n_tokens == 0) return TM_OK;
+  const size_t need = layout(t, io->n_tokens, io->n_nearest).total;
+  TM_REQUIRE(need <= (size_t)TM_NOALLOC_SCRATCH_BYTES, TM_EWORKSPACE,
+             "tm_table_forward_noalloc: the layer needs %zu bytes of scratch > TM_NOALLOC_SCRATCH_BYTES (%zu)", need,
+             (size_t)TM_NOALLOC_SCRATCH_BYTES);
+  void *ws = nullptr;
+  const int st = scratch_for_current_device(tm_hip_stream(stream), &ws);
+  if (st != TM_OK) return st;
+  return tm_table_forward(t, io, ws, (size_t)TM_NOALLOC_SCRATCH_BYTES, nullptr, stream);
 }

@@ -96,7 +96,11 @@ PROTOTYPES = {
     "tm_struct_size": (sz, [i32]),
     "tm_table_forward_workspace_size": (sz, [C.POINTER(TableLayer), i64, i32]),
     "tm_table_forward": (C.c_int, [C.POINTER(TableLayer), C.POINTER(LayerIO), vp, sz, vp, vp]),
+    "tm_table_forward_noalloc": (C.c_int, [C.POINTER(TableLayer), C.POINTER(LayerIO), vp]),
 }
+
+# tm_table_forward_noalloc's static scratch (TM_NOALLOC_SCRATCH_BYTES, include/tablemoe.h)
+TM_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 _lock = threading.Lock()
 _lib = None

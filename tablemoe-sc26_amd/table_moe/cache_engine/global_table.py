@@ -235,3 +235,15 @@ class GlobalTable:
                                          N.stream(self.device)), "tm_table_forward")
         res.pop("_inputs")
         return res
+
+    def layer_forward_noalloc(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k: int = 8,
+                              n_nearest: int = 1, keep_rate: float = 0.6, out=None):
+        """layer_forward through tm_table_forward_noalloc: the library's static
+        scratch instead of a workspace (at most TM_NOALLOC_SCRATCH_BYTES; calls
+        overlapping on one GPU race for it)."""
+        io, res = self._layer_io(hidden, is_vision, router_logits, slot_out, residual, router_top_k, n_nearest,
+                                 keep_rate, out)
+        N.check(N.lib().tm_table_forward_noalloc(C.byref(self._desc), C.byref(io), N.stream(self.device)),
+                "tm_table_forward_noalloc")
+        res.pop("_inputs")
+        return res

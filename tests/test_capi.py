@@ -117,3 +117,17 @@ def test_ranked_limit_without_device(lib):
     assert lib.tm_gather_combine_ranked(N.TM_DT_BF16, 16385, 2048, p, 8 * 2048, 2048, p, 8, 8, p, 8192, 2048, p, p,
                                         p, 2048, p, 2048, 100, p, None) == N.TM_EINVAL_SHAPE
     assert b"16384" in lib.tm_last_error()
+
+
+def test_noalloc_limit_without_device(lib):
+    """tm_table_forward_noalloc rejects a layer whose workspace exceeds its
+    static scratch before any HIP call."""
+    t = N.TableLayer(dtype=N.TM_DT_BF16, metric=N.TM_METRIC_L2, dim=128, hidden=2048, n_cent=8192, ld_c=128,
+                     ld_v=2048, ps_h=0, ps_d=0)
+    io = N.LayerIO(n_tokens=4096, n_nearest=8, router_top_k=8, n_experts=128, keep_rate=0.6)
+    assert lib.tm_table_forward_workspace_size(C.byref(t), 4096, 8) > N.TM_NOALLOC_SCRATCH_BYTES
+    assert lib.tm_table_forward_noalloc(C.byref(t), C.byref(io), None) == N.TM_EWORKSPACE
+    assert b"TM_NOALLOC_SCRATCH_BYTES" in lib.tm_last_error()
+    io.n_tokens = 0
+    assert lib.tm_table_forward_noalloc(C.byref(t), C.byref(io), None) == N.TM_OK
+    assert lib.tm_table_forward_noalloc(None, C.byref(io), None) == N.TM_EINVAL_ARG
