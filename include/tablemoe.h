@@ -283,7 +283,9 @@ int tm_centroid_sqnorms(int32_t dtype, const void *cents, int64_t n_cent, int32_
  * L2: dist = ||q||^2 - 2 q.c + ||c||^2 in fp32, ascending; DOT: q.c
  * descending; ties -> lower centroid index.  out_dist/out_idx [n, top_k].
  * workspace >= tm_search_global_workspace_size(...).
- * Limits: dim in {64, 128, 256}, 1 <= top_k <= 8, dtype F16 or BF16. */
+ * Limits: dim in {64, 128, 256}, 1 <= top_k <= 8; dtype F16 or BF16 (matrix
+ * cores) or F32 (fp32 FMAs in dimension order: the CPU-reference config);
+ * 16-byte aligned rows. */
 size_t tm_search_global_workspace_size(int64_t n_tokens, int64_t n_cent, int32_t dim,
                                        int32_t top_k);
 int tm_search_global(int32_t dtype, const void *q, int64_t n_tokens, int64_t ld_q,
@@ -406,6 +408,18 @@ size_t tm_swiglu_workspace_size(int64_t max_rows, int32_t inter, int32_t dtype);
 int tm_expert_swiglu(int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
                      const void *w1, const void *w3, const void *w2, int32_t inter, void *out, int64_t ld_out,
                      void *workspace, size_t workspace_bytes, tm_stream_t stream);
+/* tm_expert_swiglu with an addend folded into the down projection's
+ * epilogue: y = dtype(addend + f W2^T) (fp32 sum, one rounding), addend
+ * [n_rows, hidden] with row stride ld_add, not overlapping `out`.
+ * For a DeepSeek layer's shared experts (models/deepseek_vl2/
+ * deepseek_layers.py:743 adds them to the routed output, which the decoder
+ * layer adds to the residual): with the residual as the addend, the shared
+ * MLP writes residual + shared in one pass, and the table combine
+ * (tm_gather_combine) adds the routed part on top. */
+int tm_expert_swiglu_add(int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
+                         const void *w1, const void *w3, const void *w2, int32_t inter, const void *addend,
+                         int64_t ld_add, void *out, int64_t ld_out, void *workspace, size_t workspace_bytes,
+                         tm_stream_t stream);
 /* Buckets the recomputed (token, slot) pairs by expert, on the device (no
  * host sync): pair (b, s) is recomputed when mask[b*ms_b + s*ms_s] != 0
  * (ms_s = 0: a per-token flag) and 0 <= ids[b*ld_ids + s] < n_experts.
@@ -441,7 +455,7 @@ int tm_grouped_swiglu(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden
  * before the router and after each stage (timing hook).
  * ====================================================================== */
 typedef struct tm_table_layer {
-  int32_t dtype;            /* TM_DT_BF16 or TM_DT_F16                     */
+  int32_t dtype;            /* TM_DT_BF16, TM_DT_F16 or TM_DT_F32          */
   int32_t metric;           /* TM_METRIC_L2 or TM_METRIC_DOT               */
   int32_t dim;              /* PCA dimension (64, 128 or 256)              */
   int32_t hidden;           /* model hidden size                           */
@@ -468,7 +482,7 @@ typedef struct tm_layer_io {
   int32_t n_experts;
   int32_t router_top_k;
   int32_t n_nearest;        /* 1..8                                        */
-  int32_t reserved;
+  int32_t flags;            /* 0 or TM_LAYER_NO_COMBINE                    */
   double keep_rate;
   const void *slot_out;     /* [n, router_top_k, hidden] strides so_b, so_s */
   int64_t so_b, so_s;
@@ -485,6 +499,13 @@ typedef struct tm_layer_io {
   int64_t *idx;             /* [n, n_nearest]                              */
   uint8_t *keep;            /* [n]                                         */
 } tm_layer_io;
+
+/* tm_layer_io.flags: stop after the keep set (weights, expert_ids, q,
+ * q_sqnorm, dist, idx and keep are written; slot_out, residual and out are
+ * not used), so a caller can recompute the kept tokens' slots and then run
+ * tm_gather_combine itself (a DeepSeek-style layer whose recompute and
+ * shared experts sit between the keep selection and the combine). */
+#define TM_LAYER_NO_COMBINE 1
 
 /* sizeof(tm_table_layer) for which == 0, sizeof(tm_layer_io) for which == 1
  * (lets a binding check its mirror of the two structs). */

@@ -46,7 +46,9 @@ keep_select                    brute force sort; invariants
 gather_combine                 closed form on one-hot tables
 swiglu_expert                  torch.nn.functional.silu + matmul (library
                                routines) and one-hot weights, where the output
-                               is silu(x_a) * x_b through scalar math.exp
+                               is silu(x_a) * x_b through scalar math.exp; the
+                               addend form by its two closed forms (zero
+                               addend = the plain MLP, zero W2 = the addend)
 grouped_swiglu                 per-expert swiglu_expert on the pairs of each
                                expert (brute-force regrouping)
 last_query_importance          torch.softmax / matmul (library routines) in
@@ -600,17 +602,22 @@ def silu(v):
     return v / (1.0 + np.exp(-v))
 
 
-def swiglu_expert(x, w1, w3, w2, dt: str = BF16):
+def swiglu_expert(x, w1, w3, w2, dt: str = BF16, addend=None):
     """One expert's MLP with the rounding points of the reference's fused
     kernel (ops/csrc/fp16_fused_expert/fp16_fused_moe_mlp.cu:107-274 and the
     SiLU-mul epilogue fp16_epilogue_utils.h:51-125): g = dt(x W1^T),
     f = dt(silu(g) * (x W3^T)) with the up projection unrounded,
-    y = dt(f W2^T).  Exact float64 sums of exact products."""
+    y = dt(f W2^T).  Exact float64 sums of exact products.  With ``addend``
+    (a DeepSeek layer's residual under its shared experts,
+    deepseek_layers.py:743): y = dt(addend + f W2^T), one rounding."""
     x = np.asarray(x, dtype=np.float64)
     g = round_to(x @ np.asarray(w1, dtype=np.float64).T, dt)
     u = x @ np.asarray(w3, dtype=np.float64).T
     f = round_to(silu(g) * u, dt)
-    return round_to(f @ np.asarray(w2, dtype=np.float64).T, dt), f
+    y = f @ np.asarray(w2, dtype=np.float64).T
+    if addend is not None:
+        y = y + np.asarray(addend, dtype=np.float64)
+    return round_to(y, dt), f
 
 
 def grouped_swiglu(x, ids, mask, w1, w3, w2, dt: str = BF16):

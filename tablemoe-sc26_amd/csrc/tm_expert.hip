@@ -71,7 +71,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
     const typename Elem<DT>::T *__restrict__ A, int64_t lda, const int32_t *__restrict__ a_rows,
     const typename Elem<DT>::T *__restrict__ B0, const typename Elem<DT>::T *__restrict__ B1, int64_t b_expert,
     int K, int n_tiles, TileSrc ts, typename Elem<DT>::T *__restrict__ C, int64_t ldc,
-    const int64_t *__restrict__ c_rows) {
+    const int64_t *__restrict__ c_rows, const typename Elem<DT>::T *__restrict__ addend, int64_t ld_add) {
   using T = typename Elem<DT>::T;
   constexpr int kStage = kAStage + NB * kBStage;
   constexpr int kDma = kADma + NB * kBDma;  // loads per wave per stage
@@ -186,6 +186,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
           v = (g / (1.f + __expf(-g))) * u;
         } else {
           v = acc[0][mi][ni][i];
+          if (addend != nullptr) v += Elem<DT>::to_f(addend[(int64_t)gr * ld_add + col]);  // dense rows only
         }
         const int64_t dst = c_rows ? c_rows[gr] + col : (int64_t)gr * ldc + col;
         C[dst] = Elem<DT>::from_f(v);
@@ -295,28 +296,32 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
 template <int DT, int NB, int MODE>
 void launch_gemm(const void *A, int64_t lda, const int32_t *a_rows, const void *B0, const void *B1, int64_t b_expert,
                  int K, int N, const TileSrc &ts, int64_t grid_y, void *C, int64_t ldc, const int64_t *c_rows,
-                 hipStream_t s) {
+                 const void *addend, int64_t ld_add, hipStream_t s) {
   using T = typename Elem<DT>::T;
   const int n_tiles = N / BN;
   const int64_t blocks = tm_cdiv(grid_y, 8) * 8 * n_tiles;
   hipLaunchKernelGGL((grouped_gemm_kernel<DT, NB, MODE>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
                      static_cast<const T *>(A), lda, a_rows, static_cast<const T *>(B0), static_cast<const T *>(B1),
-                     b_expert, K, n_tiles, ts, static_cast<T *>(C), ldc, c_rows);
+                     b_expert, K, n_tiles, ts, static_cast<T *>(C), ldc, c_rows, static_cast<const T *>(addend),
+                     ld_add);
 }
 
-// The two GEMMs of the MLP over the rows the tile source names.
+// The two GEMMs of the MLP over the rows the tile source names; `addend`
+// (dense rows only, nullable) is added to the down projection before its
+// rounding.
 int swiglu_impl(int32_t dtype, const void *x, int64_t ld_x, const int32_t *row_token, int32_t hidden,
                 int32_t inter, const void *w1, const void *w3, const void *w2, const TileSrc &ts, int64_t grid_y,
-                void *out, int64_t ld_out, const int64_t *row_out, void *fused, hipStream_t s) {
+                void *out, int64_t ld_out, const int64_t *row_out, void *fused, const void *addend, int64_t ld_add,
+                hipStream_t s) {
   return TM_DISPATCH_DTYPE(dtype, DT, [&] {
     if constexpr (DT == TM_DT_F32) {
       return tm_fail(TM_EINVAL_DTYPE, "tm_grouped_swiglu: dtype must be F16 or BF16");
     } else {
       launch_gemm<DT, 2, kModeUp>(x, ld_x, row_token, w1, w3, (int64_t)inter * hidden, hidden, inter, ts, grid_y,
-                                  fused, inter, nullptr, s);
+                                  fused, inter, nullptr, nullptr, 0, s);
       TM_LAUNCH_CHECK("tm_grouped_swiglu(up)");
       launch_gemm<DT, 1, kModeDown>(fused, inter, nullptr, w2, nullptr, (int64_t)hidden * inter, inter, hidden, ts,
-                                    grid_y, out, ld_out, row_out, s);
+                                    grid_y, out, ld_out, row_out, addend, ld_add, s);
       TM_LAUNCH_CHECK("tm_grouped_swiglu(down)");
       return TM_OK;
     }
@@ -377,24 +382,46 @@ extern "C" int tm_grouped_swiglu(int32_t dtype, const void *x, int64_t ld_x, int
   const int64_t t_max = tm_group_slots_tiles(max_rows, n_experts);
   const TileSrc ts{tiles, expert_offsets, t_max, 0};
   return swiglu_impl(dtype, x, ld_x, row_token, hidden, inter, w1, w3, w2, ts, t_max, out, 0, row_out, workspace,
-                     tm_hip_stream(stream));
+                     nullptr, 0, tm_hip_stream(stream));
 }
+
+namespace {
+
+int expert_swiglu_impl(const char *name, int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
+                       const void *w1, const void *w3, const void *w2, int32_t inter, const void *addend,
+                       int64_t ld_add, void *out, int64_t ld_out, void *workspace, size_t workspace_bytes,
+                       tm_stream_t stream) {
+  TM_REQUIRE(shapes_ok(hidden, inter), TM_EINVAL_SHAPE, "%s: hidden and inter must be positive multiples of %d",
+             name, BN);
+  TM_REQUIRE(n_rows >= 0 && n_rows < ((int64_t)1 << 31) && ld_x >= hidden && ld_out >= hidden &&
+                 (addend == nullptr || ld_add >= hidden),
+             TM_EINVAL_SHAPE, "%s: bad sizes", name);
+  if (n_rows == 0) return TM_OK;
+  TM_REQUIRE(x && w1 && w3 && w2 && out, TM_EINVAL_ARG, "%s: null pointer", name);
+  TM_REQUIRE(tm_aligned16(x) && (ld_x * 2) % 16 == 0 && tm_aligned16(w1) && tm_aligned16(w3) && tm_aligned16(w2),
+             TM_EINVAL_SHAPE, "%s: x rows and weights must be 16-byte aligned", name);
+  const size_t need = tm_swiglu_workspace_size(n_rows, inter, dtype);
+  TM_REQUIRE(workspace != nullptr && workspace_bytes >= need && tm_aligned16(workspace), TM_EWORKSPACE,
+             "%s: workspace %zu bytes < %zu", name, workspace_bytes, need);
+  const TileSrc ts{nullptr, nullptr, 0, (int32_t)n_rows};
+  return swiglu_impl(dtype, x, ld_x, nullptr, hidden, inter, w1, w3, w2, ts, tm_cdiv(n_rows, BM), out, ld_out,
+                     nullptr, workspace, addend, ld_add, tm_hip_stream(stream));
+}
+
+}  // namespace
 
 extern "C" int tm_expert_swiglu(int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
                                 const void *w1, const void *w3, const void *w2, int32_t inter, void *out,
                                 int64_t ld_out, void *workspace, size_t workspace_bytes, tm_stream_t stream) {
-  TM_REQUIRE(shapes_ok(hidden, inter), TM_EINVAL_SHAPE,
-             "tm_expert_swiglu: hidden and inter must be positive multiples of %d", BN);
-  TM_REQUIRE(n_rows >= 0 && n_rows < ((int64_t)1 << 31) && ld_x >= hidden && ld_out >= hidden, TM_EINVAL_SHAPE,
-             "tm_expert_swiglu: bad sizes");
-  if (n_rows == 0) return TM_OK;
-  TM_REQUIRE(x && w1 && w3 && w2 && out, TM_EINVAL_ARG, "tm_expert_swiglu: null pointer");
-  TM_REQUIRE(tm_aligned16(x) && (ld_x * 2) % 16 == 0 && tm_aligned16(w1) && tm_aligned16(w3) && tm_aligned16(w2),
-             TM_EINVAL_SHAPE, "tm_expert_swiglu: x rows and weights must be 16-byte aligned");
-  const size_t need = tm_swiglu_workspace_size(n_rows, inter, dtype);
-  TM_REQUIRE(workspace != nullptr && workspace_bytes >= need && tm_aligned16(workspace), TM_EWORKSPACE,
-             "tm_expert_swiglu: workspace %zu bytes < %zu", workspace_bytes, need);
-  const TileSrc ts{nullptr, nullptr, 0, (int32_t)n_rows};
-  return swiglu_impl(dtype, x, ld_x, nullptr, hidden, inter, w1, w3, w2, ts, tm_cdiv(n_rows, BM), out, ld_out,
-                     nullptr, workspace, tm_hip_stream(stream));
+  return expert_swiglu_impl("tm_expert_swiglu", dtype, x, n_rows, hidden, ld_x, w1, w3, w2, inter, nullptr, 0, out,
+                            ld_out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int tm_expert_swiglu_add(int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
+                                    const void *w1, const void *w3, const void *w2, int32_t inter,
+                                    const void *addend, int64_t ld_add, void *out, int64_t ld_out, void *workspace,
+                                    size_t workspace_bytes, tm_stream_t stream) {
+  TM_REQUIRE(addend != nullptr, TM_EINVAL_ARG, "tm_expert_swiglu_add: null addend");
+  return expert_swiglu_impl("tm_expert_swiglu_add", dtype, x, n_rows, hidden, ld_x, w1, w3, w2, inter, addend, ld_add,
+                            out, ld_out, workspace, workspace_bytes, stream);
 }

@@ -256,17 +256,21 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
                          io->expert_ids};
   const bool route_fused = stage_events == nullptr && tm_internal_route_fusable(&ra);
   const int64_t n_keep = tm_keep_count(n, io->keep_rate);
+  TM_REQUIRE((io->flags & ~TM_LAYER_NO_COMBINE) == 0, TM_EINVAL_ARG, "tm_table_forward: unknown flags 0x%x",
+             (unsigned)io->flags);
+  const bool combine = (io->flags & TM_LAYER_NO_COMBINE) == 0;
   int st;
-  if (tm_internal_decode_ok(t, io)) {  // the finishing launch also combines
+  if (combine && tm_internal_decode_ok(t, io)) {  // the finishing launch also combines
     if ((st = decode_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s)) != TM_OK) return st;
     return record(stage_events, 5, s);
   }
   const bool fused = fused_top1_ok(t, io);
-  const bool ranked = fused && ranked_ok(t, io);
+  const bool ranked = combine && fused && ranked_ok(t, io);  // the ranked plan decides the keep set in the combine
   st = fused ? fused_top1_stages(t, io, w, ws, ra, route_fused, ranked, n_keep, stage_events, s)
              : general_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s);
   if (st != TM_OK) return st;
   if ((st = record(stage_events, 4, s)) != TM_OK) return st;
+  if (!combine) return record(stage_events, 5, s);
   if (ranked)
     st = tm_internal_combine_rank(t->dtype, n, t->hidden, io->slot_out, io->so_b, io->so_s, io->weights,
                                   io->router_top_k, io->router_top_k, t->values, t->n_cent, t->ld_v, io->idx,

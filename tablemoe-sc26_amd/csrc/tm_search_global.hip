@@ -1333,6 +1333,138 @@ int dispatch_dim(int dim, int top_k, const void *q, int64_t n, int64_t ld_q, con
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 tables (the CPU-reference configuration): a lane per query, blocks of
+// kF32Block centroid rows staged in LDS and read as broadcasts (every lane
+// reads the same address), fp32 FMAs in dimension order, and the same
+// per-lane packed-key lists and split merge as the 16-bit forms.  The split
+// plan never uses more splits than the 16-bit plan of the same shape, so
+// tm_search_global_workspace_size covers it.
+// ---------------------------------------------------------------------------
+constexpr int kF32Block = 32;  // centroids per LDS block
+
+SplitPlan plan_f32(int64_t n, int64_t c, int dim, int top_k) {
+  SplitPlan p = plan_split(n, c, dim, top_k);
+  const int64_t bound = p.nsplit;
+  p.stream = false;
+  p.wide = false;
+  p.row_blocks = tm_cdiv(n, kThreads);
+  int64_t want = tm_cdiv(512, p.row_blocks);
+  if (want > bound) want = bound;
+  if (want > tm_cdiv(c, kF32Block)) want = tm_cdiv(c, kF32Block);
+  if (want < 1) want = 1;
+  p.chunk = tm_cdiv(tm_cdiv(c, want), kF32Block) * kF32Block;
+  p.nsplit = tm_cdiv(c, p.chunk);
+  return p;
+}
+
+template <int DIM, int K, int METRIC>
+__global__ __launch_bounds__(kThreads) void search_f32_kernel(const float *__restrict__ q, int64_t n, int64_t ld_q,
+                                                              const float *__restrict__ cents, int64_t n_cent,
+                                                              int64_t ld_c, const float *__restrict__ c_sqnorm,
+                                                              int64_t chunk, uint64_t *__restrict__ ws) {
+  constexpr int QC = DIM <= 128 ? DIM : 64;  // query elements held in registers at a time
+  constexpr int V4 = DIM / 4;                // float4 per centroid row
+  __shared__ float4 cs[kF32Block * V4];
+  __shared__ float pen_s[kF32Block];
+  const int tid = threadIdx.x;
+  const int64_t r = (int64_t)blockIdx.x * kThreads + tid;
+  const float *qrow = q + (r < n ? r : n - 1) * ld_q;
+  const int64_t c0 = (int64_t)blockIdx.y * chunk;
+  const int64_t c1 = c0 + chunk < n_cent ? c0 + chunk : n_cent;
+  float qv[QC];
+  auto load_q = [&](int kc) {
+#pragma unroll
+    for (int k = 0; k < QC; k += 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(qrow + kc + k);
+      qv[k] = v.x; qv[k + 1] = v.y; qv[k + 2] = v.z; qv[k + 3] = v.w;
+    }
+  };
+  if constexpr (QC == DIM) load_q(0);
+  Best<K> best;
+  best.init();
+  for (int64_t cb = c0; cb < c1; cb += kF32Block) {
+    __syncthreads();  // the previous block's reads are done
+    for (int e = tid; e < kF32Block * V4; e += kThreads) {
+      const int64_t c = cb + e / V4;
+      cs[e] = c < c1 ? *reinterpret_cast<const float4 *>(cents + c * ld_c + 4 * (e % V4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (tid < kF32Block) pen_s[tid] = (METRIC == TM_METRIC_L2 && cb + tid < c1) ? c_sqnorm[cb + tid] : 0.f;
+    __syncthreads();
+    float acc[kF32Block];
+#pragma unroll
+    for (int j = 0; j < kF32Block; ++j) acc[j] = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < DIM; kc += QC) {
+      if constexpr (QC != DIM) load_q(kc);
+#pragma unroll
+      for (int j = 0; j < kF32Block; ++j)
+#pragma unroll
+        for (int k = 0; k < QC; k += 4) {
+          const float4 cv = cs[j * V4 + (kc + k) / 4];
+          acc[j] = fmaf(qv[k], cv.x, acc[j]);
+          acc[j] = fmaf(qv[k + 1], cv.y, acc[j]);
+          acc[j] = fmaf(qv[k + 2], cv.z, acc[j]);
+          acc[j] = fmaf(qv[k + 3], cv.w, acc[j]);
+        }
+    }
+    const int valid = (int)(c1 - cb < kF32Block ? c1 - cb : kF32Block);  // uniform
+#pragma unroll
+    for (int j = 0; j < kF32Block; ++j)
+      if (j < valid) {
+        const float dp = (METRIC == TM_METRIC_L2) ? fmaf(-2.f, acc[j], pen_s[j]) : -acc[j];
+        best.push(dp, (int)(cb + j));
+      }
+  }
+  best.finalize();
+  if (r < n) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) ws[((int64_t)blockIdx.y * n + r) * K + j] = best.l[j];
+  }
+}
+
+template <int DIM, int K, int METRIC>
+int launch_search_f32(int top_k, const void *q, int64_t n, int64_t ld_q, const float *q_sqnorm, const void *cents,
+                      int64_t n_cent, int64_t ld_c, const float *c_sqnorm, float *out_dist, int64_t *out_idx,
+                      uint64_t *ws, const tm_route_args *ra, hipStream_t stream) {
+  const SplitPlan p = plan_f32(n, n_cent, DIM, top_k);
+  const float *Q = static_cast<const float *>(q);
+  hipLaunchKernelGGL((search_f32_kernel<DIM, K, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
+                     dim3(kThreads), 0, stream, Q, n, ld_q, static_cast<const float *>(cents), n_cent, ld_c, c_sqnorm,
+                     p.chunk, ws);
+  TM_LAUNCH_CHECK("tm_search_global(f32)");
+  if (ra == nullptr)
+    launch_merge<TM_DT_F32, K, METRIC, 0>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, ra, stream);
+  else if (ra->n_experts == 64)
+    launch_merge<TM_DT_F32, K, METRIC, 8>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, ra, stream);
+  else
+    launch_merge<TM_DT_F32, K, METRIC, 16>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, ra, stream);
+  TM_LAUNCH_CHECK("tm_search_global(merge)");
+  return TM_OK;
+}
+
+template <int METRIC>
+int dispatch_f32(int dim, int top_k, const void *q, int64_t n, int64_t ld_q, const float *q_sqnorm,
+                 const void *cents, int64_t n_cent, int64_t ld_c, const float *c_sqnorm, float *out_dist,
+                 int64_t *out_idx, uint64_t *ws, const tm_route_args *ra, hipStream_t s) {
+#define TM_F32_K(D)                                                                                                 \
+  switch (list_len(top_k)) {                                                                                        \
+    case 1: return launch_search_f32<D, 1, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm,      \
+                                                   out_dist, out_idx, ws, ra, s);                                   \
+    case 4: return launch_search_f32<D, 4, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm,      \
+                                                   out_dist, out_idx, ws, ra, s);                                   \
+    default: return launch_search_f32<D, 8, METRIC>(top_k, q, n, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm,     \
+                                                    out_dist, out_idx, ws, ra, s);                                  \
+  }
+  switch (dim) {
+    case 64: TM_F32_K(64)
+    case 128: TM_F32_K(128)
+    case 256: TM_F32_K(256)
+    default: return tm_fail(TM_EINVAL_SHAPE, "tm_search_global: dim %d not in {64, 128, 256}", dim);
+  }
+#undef TM_F32_K
+}
+
 }  // namespace
 
 extern "C" int tm_centroid_sqnorms(int32_t dtype, const void *cents, int64_t n_cent, int32_t dim,
@@ -1365,17 +1497,23 @@ static int search_impl(int32_t dtype, const void *q, int64_t n_tokens, int64_t l
   TM_REQUIRE(ld_q >= dim && ld_c >= dim, TM_EINVAL_SHAPE, "tm_search_global: bad row strides");
   TM_REQUIRE(top_k >= 1 && top_k <= 8, TM_EINVAL_SHAPE, "tm_search_global: top_k %d not in [1, 8]", top_k);
   TM_REQUIRE(metric == TM_METRIC_L2 || metric == TM_METRIC_DOT, TM_EINVAL_ARG, "tm_search_global: bad metric");
-  TM_REQUIRE(dtype == TM_DT_BF16 || dtype == TM_DT_F16, TM_EINVAL_DTYPE,
-             "tm_search_global: dtype must be F16 or BF16");
+  TM_REQUIRE(dtype == TM_DT_BF16 || dtype == TM_DT_F16 || dtype == TM_DT_F32, TM_EINVAL_DTYPE,
+             "tm_search_global: dtype must be F32, F16 or BF16");
   if (n_tokens == 0) return TM_OK;
   TM_REQUIRE(q && cents && out_dist && out_idx, TM_EINVAL_ARG, "tm_search_global: null pointer");
   TM_REQUIRE(metric != TM_METRIC_L2 || c_sqnorm, TM_EINVAL_ARG, "tm_search_global: L2 needs c_sqnorm");
-  TM_REQUIRE(tm_aligned16(q) && tm_aligned16(cents) && (ld_q * 2) % 16 == 0 && (ld_c * 2) % 16 == 0,
+  const int64_t esz = dtype == TM_DT_F32 ? 4 : 2;
+  TM_REQUIRE(tm_aligned16(q) && tm_aligned16(cents) && (ld_q * esz) % 16 == 0 && (ld_c * esz) % 16 == 0,
              TM_EINVAL_SHAPE, "tm_search_global: q and centroid rows must be 16-byte aligned");
   const size_t need = tm_search_global_workspace_size(n_tokens, n_cent, dim, top_k);
   TM_REQUIRE(workspace != nullptr && workspace_bytes >= need, TM_EWORKSPACE,
              "tm_search_global: workspace %zu bytes < %zu", workspace_bytes, need);
   uint64_t *ws = static_cast<uint64_t *>(workspace);
+  if (dtype == TM_DT_F32) {
+    if (metric == TM_METRIC_L2)
+      return dispatch_f32<TM_METRIC_L2>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, s);
+    return dispatch_f32<TM_METRIC_DOT>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, s);
+  }
   if (dtype == TM_DT_BF16) {
     if (metric == TM_METRIC_L2)
       return dispatch_dim<TM_DT_BF16, TM_METRIC_L2>(dim, top_k, q, n_tokens, ld_q, q_sqnorm, cents, n_cent, ld_c, c_sqnorm, out_dist, out_idx, ws, ra, s);

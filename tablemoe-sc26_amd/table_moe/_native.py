@@ -23,6 +23,7 @@ TM_CMP_GE, TM_CMP_GT = 0, 1
 TM_METRIC_L2, TM_METRIC_DOT = 0, 1
 TM_TARGET_ONE, TM_TARGET_ORIG_SUM, TM_TARGET_GIVEN = 0, 1, 2
 TM_SCORE_MODEL, TM_SCORE_F32 = 0, 1
+TM_LAYER_NO_COMBINE = 1
 
 _DTYPE_TAG = {torch.float32: TM_DT_F32, torch.float16: TM_DT_F16, torch.bfloat16: TM_DT_BF16}
 
@@ -43,7 +44,7 @@ class LayerIO(C.Structure):
 
     _fields_ = [("n_tokens", i64), ("x", vp), ("ld_x", i64), ("is_vision", vp), ("router_logits", vp),
                 ("ld_logits", i64), ("n_experts", i32), ("router_top_k", i32), ("n_nearest", i32),
-                ("reserved", i32), ("keep_rate", f64), ("slot_out", vp), ("so_b", i64), ("so_s", i64),
+                ("flags", i32), ("keep_rate", f64), ("slot_out", vp), ("so_b", i64), ("so_s", i64),
                 ("residual", vp), ("ld_r", i64), ("out", vp), ("ld_o", i64), ("weights", vp), ("expert_ids", vp),
                 ("q", vp), ("q_sqnorm", vp), ("dist", vp), ("idx", vp), ("keep", vp)]
 
@@ -90,6 +91,7 @@ PROTOTYPES = {
                                            vp, i64, i64, vp, i64, vp, sz, vp]),
     "tm_swiglu_workspace_size": (sz, [i64, i32, i32]),
     "tm_expert_swiglu": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, i32, vp, i64, vp, sz, vp]),
+    "tm_expert_swiglu_add": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, i32, vp, i64, vp, i64, vp, sz, vp]),
     "tm_group_slots_tiles": (i64, [i64, i32]),
     "tm_group_slots": (C.c_int, [vp, i64, i32, i64, vp, i64, i64, i32, i64, i64, vp, vp, vp, vp, vp]),
     "tm_grouped_swiglu": (C.c_int, [i32, vp, i64, i32, i32, i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]),

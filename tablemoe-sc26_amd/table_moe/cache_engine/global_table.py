@@ -29,11 +29,12 @@ _METRICS = {"l2": N.TM_METRIC_L2, "dot": N.TM_METRIC_DOT}
 
 class GlobalTable:
     def __init__(self, centroids: torch.Tensor, values: torch.Tensor, pca_vis, pca_txt=None, metric: str = "l2"):
-        """centroids [C, d] and values [C, H] in bf16/fp16 on a HIP device;
-        pca_vis / pca_txt = (proj [H, d], bias [d]) in the same dtype."""
+        """centroids [C, d] and values [C, H] in bf16/fp16 (matrix-core
+        search) or fp32 on a HIP device; pca_vis / pca_txt = (proj [H, d],
+        bias [d]) in the same dtype."""
         dev = N.require_hip(centroids, values)
-        if centroids.dtype not in (torch.bfloat16, torch.float16) or values.dtype != centroids.dtype:
-            raise ValueError("centroids/values must share dtype bfloat16 or float16")
+        if centroids.dtype not in (torch.bfloat16, torch.float16, torch.float32) or values.dtype != centroids.dtype:
+            raise ValueError("centroids/values must share dtype bfloat16, float16 or float32")
         if metric not in _METRICS:
             raise ValueError(f"metric must be one of {sorted(_METRICS)}")
         self.device = dev
@@ -181,21 +182,25 @@ class GlobalTable:
         return {"weights": w, "ids": ids, "q": q, "qn": qn, "dist": dist, "idx": idx, "keep": keep, "out": y}
 
     def _layer_io(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k, n_nearest, keep_rate,
-                  out):
+                  out, flags=0):
         """The tm_layer_io of one layer call (buffers from this table's pool)
-        and the dict of every stage's output it fills."""
-        N.require_hip(hidden, router_logits, slot_out)
-        if hidden.dtype != self.dtype or slot_out.dtype != self.dtype:
+        and the dict of every stage's output it fills.  With
+        TM_LAYER_NO_COMBINE, slot_out/residual/out are not used."""
+        combine = not (flags & N.TM_LAYER_NO_COMBINE)
+        N.require_hip(hidden, router_logits, *( (slot_out,) if combine else ()))
+        if hidden.dtype != self.dtype or (combine and slot_out.dtype != self.dtype):
             raise RuntimeError(f"hidden/slot_out dtype must be the table dtype {self.dtype}")
         x = hidden if hidden.stride(-1) == 1 else hidden.contiguous()
         logits = router_logits.float()
         if logits.stride(-1) != 1:
             logits = logits.contiguous()
-        if slot_out.stride(-1) != 1:
+        if combine and slot_out.stride(-1) != 1:
             slot_out = slot_out.contiguous()
         n = x.shape[0]
-        if out is None:
+        if combine and out is None:
             out = self._buf("out", (n, self.hidden), self.dtype)
+        if not combine:
+            slot_out = residual = out = None
         w = self._buf("route_w", (n, router_top_k), torch.float32)
         ids = self._buf("route_ids", (n, router_top_k), torch.long)
         q = self._buf("q", (n, self.dim), self.dtype)
@@ -207,10 +212,11 @@ class GlobalTable:
         io = N.LayerIO(
             n_tokens=n, x=N.ptr(x), ld_x=x.stride(0), is_vision=N.ptr(isv), router_logits=N.ptr(logits),
             ld_logits=logits.stride(0), n_experts=logits.shape[1], router_top_k=router_top_k, n_nearest=n_nearest,
-            keep_rate=float(keep_rate), slot_out=N.ptr(slot_out), so_b=slot_out.stride(0), so_s=slot_out.stride(1),
+            keep_rate=float(keep_rate), flags=int(flags), slot_out=N.ptr(slot_out),
+            so_b=0 if slot_out is None else slot_out.stride(0), so_s=0 if slot_out is None else slot_out.stride(1),
             residual=N.ptr(residual), ld_r=0 if residual is None else residual.stride(0), out=N.ptr(out),
-            ld_o=out.stride(0), weights=N.ptr(w), expert_ids=N.ptr(ids), q=N.ptr(q), q_sqnorm=N.ptr(qn),
-            dist=N.ptr(dist), idx=N.ptr(idx), keep=N.ptr(N.as_u8(keep)))
+            ld_o=0 if out is None else out.stride(0), weights=N.ptr(w), expert_ids=N.ptr(ids), q=N.ptr(q),
+            q_sqnorm=N.ptr(qn), dist=N.ptr(dist), idx=N.ptr(idx), keep=N.ptr(N.as_u8(keep)))
         # the tensors the io points at stay referenced by the returned dict
         res = {"weights": w, "ids": ids, "q": q, "qn": qn, "dist": dist, "idx": idx, "keep": keep, "out": out,
                "_inputs": (x, logits, slot_out, isv)}
@@ -234,6 +240,55 @@ class GlobalTable:
         N.check(N.lib().tm_table_forward(C.byref(self._desc), C.byref(io), N.ptr(ws), ws.numel(), evs,
                                          N.stream(self.device)), "tm_table_forward")
         res.pop("_inputs")
+        return res
+
+    def layer_search(self, hidden, is_vision, router_logits, router_top_k: int = 8, n_nearest: int = 1,
+                     keep_rate: float = 0.6):
+        """The layer call up to the keep set (tm_table_forward with
+        TM_LAYER_NO_COMBINE): router, projection, nearest centroids and the
+        tokens to recompute, for callers that recompute the kept tokens before
+        combining (layer_forward_recompute)."""
+        io, res = self._layer_io(hidden, is_vision, router_logits, None, None, router_top_k, n_nearest, keep_rate,
+                                 None, flags=N.TM_LAYER_NO_COMBINE)
+        nbytes = N.lib().tm_table_forward_workspace_size(C.byref(self._desc), io.n_tokens, n_nearest)
+        ws = self._buf("layer_ws", (max(nbytes, 1),), torch.uint8)
+        N.check(N.lib().tm_table_forward(C.byref(self._desc), C.byref(io), N.ptr(ws), ws.numel(), None,
+                                         N.stream(self.device)), "tm_table_forward")
+        res.pop("_inputs")
+        del res["out"]
+        return res
+
+    def layer_forward_recompute(self, hidden, is_vision, router_logits, experts, residual, router_top_k: int = 6,
+                                keep_rate: float = 0.6, shared=None, out=None):
+        """A DeepSeek-style MoE layer on the table (models/deepseek_vl2/
+        deepseek_layers.py:569-745 shape): the layer call up to the keep set,
+        the kept tokens' routed slots recomputed by ``experts``
+        (GroupedExperts, on the device, no host sync), the shared experts
+        ``shared`` = (w1, w3, w2) run over every token with the residual folded
+        into their down projection (dtype(residual + shared)), then the
+        gather + combine on top: out = dtype(dtype(residual + shared) + y),
+        y = the renormalised routed slots (kept tokens) or the cached output
+        of the nearest centroid (the others).  Top-1 table.  Returns the
+        stage outputs and ``slot_out``; buffers are reused by the next call."""
+        from ..ops import expert_swiglu
+
+        res = self.layer_search(hidden, is_vision, router_logits, router_top_k, 1, keep_rate)
+        n = hidden.shape[0]
+        slot_out = self._buf("recompute_slots", (n, router_top_k, self.hidden), self.dtype)
+        experts.forward(hidden, res["ids"], res["keep"], slot_out)
+        base = residual
+        if shared is not None:
+            w1, w3, w2 = shared
+            base = self._buf("shared_plus_residual", (n, self.hidden), self.dtype)
+            nbytes = N.lib().tm_swiglu_workspace_size(n, w1.shape[0], N.dtype_tag(self.dtype))
+            ws = self._buf("shared_ws", (max(nbytes, 1),), torch.uint8)
+            if residual is None:
+                expert_swiglu(hidden, w1, w3, w2, out=base, workspace=ws)
+            else:
+                expert_swiglu(hidden, w1, w3, w2, out=base, workspace=ws, addend=residual)
+        out = self.gather_combine(res["keep"], slot_out, res["weights"], res["idx"], res["dist"], base, out)
+        res["slot_out"] = slot_out
+        res["out"] = out
         return res
 
     def layer_forward_noalloc(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k: int = 8,

@@ -62,9 +62,13 @@ def _eligible_weight(linear_wrapper):
 
 
 def expert_swiglu(hidden_states: torch.Tensor, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor,
-                  out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                  addend: torch.Tensor | None = None) -> torch.Tensor:
     """y = SwiGLU expert MLP of ``hidden_states`` [M, H] with nn.Linear weights
-    w1, w3 [I, H] and w2 [H, I] (one tm_expert_swiglu call)."""
+    w1, w3 [I, H] and w2 [H, I] (one tm_expert_swiglu call).  With ``addend``
+    [M, H] (not overlapping ``out``): y = dtype(addend + MLP) in one rounding
+    (tm_expert_swiglu_add), e.g. a DeepSeek layer's shared experts added to
+    the residual stream."""
     dev = N.require_hip(hidden_states, w1, w3, w2)
     m, h = hidden_states.shape
     inter = w1.shape[0]
@@ -76,9 +80,17 @@ def expert_swiglu(hidden_states: torch.Tensor, w1: torch.Tensor, w3: torch.Tenso
     nbytes = N.lib().tm_swiglu_workspace_size(m, inter, N.dtype_tag(dt))
     if workspace is None or workspace.numel() < nbytes:
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-    N.call("tm_expert_swiglu", N.dtype_tag(dt), N.ptr(hidden_states), m, h, hidden_states.stride(0), N.ptr(w1),
-           N.ptr(w3), N.ptr(w2), inter, N.ptr(out), out.stride(0), N.ptr(workspace), workspace.numel(),
-           N.stream(dev))
+    if addend is None:
+        N.call("tm_expert_swiglu", N.dtype_tag(dt), N.ptr(hidden_states), m, h, hidden_states.stride(0), N.ptr(w1),
+               N.ptr(w3), N.ptr(w2), inter, N.ptr(out), out.stride(0), N.ptr(workspace), workspace.numel(),
+               N.stream(dev))
+    else:
+        N.require_hip(addend)
+        if addend.shape != (m, h) or addend.dtype != dt or addend.stride(-1) != 1:
+            raise ValueError(f"expert_swiglu: addend must be [{m}, {h}] {dt} with unit stride along hidden")
+        N.call("tm_expert_swiglu_add", N.dtype_tag(dt), N.ptr(hidden_states), m, h, hidden_states.stride(0),
+               N.ptr(w1), N.ptr(w3), N.ptr(w2), inter, N.ptr(addend), addend.stride(0), N.ptr(out), out.stride(0),
+               N.ptr(workspace), workspace.numel(), N.stream(dev))
     return out
 
 

@@ -11,6 +11,11 @@ table dtype, then moved to the requested device):
 * "near" tokens: x = P_m (mu_c + sigma_w eps) + 0.05 (I - P_m P_m^T) g;
   outliers: x ~ U(-sqrt(3), sqrt(3))^H.
 
+``gen_device`` (e.g. "cuda") draws the large tensors (hidden states, cached
+outputs, router logits, slot outputs, residual) with a generator on that
+device instead: the same distributions, other random streams, and seconds
+instead of minutes for the 48-layer stack.
+
 Configs (BASELINE.json):
   1  CPU reference: N=256, H=2048, d=64, C=1024, fp32, top-1, 100 % near
   2  Qwen3-VL-30B-A3B prefill: N=4096 (3584 vision + 512 text), H=2048, d=128,
@@ -71,7 +76,7 @@ def _orthonormal(gen, hidden, dim):
 
 def make_workload(config: int = 2, *, n: int | None = None, seed: int | None = None,
                   dtype: torch.dtype | None = None, device="cpu", bias_scale: float = 0.0,
-                  sigma_w: float = 0.2, with_slot_out: bool = True, **overrides) -> Workload:
+                  sigma_w: float = 0.2, with_slot_out: bool = True, gen_device=None, **overrides) -> Workload:
     cfg = dict(CONFIGS[config])
     cfg.update(overrides)
     if n is not None:
@@ -100,24 +105,30 @@ def make_workload(config: int = 2, *, n: int | None = None, seed: int | None = N
     cluster_of = torch.full((N,), -1, dtype=torch.long)
     cluster_of[near_rows] = torch.randint(0, C, (n_near,), generator=gen)
 
-    x = (torch.rand(N, H, generator=gen) * 2.0 - 1.0) * math.sqrt(3.0)
+    if gen_device is None:
+        gd, g2 = torch.device("cpu"), gen
+    else:
+        gd = torch.device(gen_device)
+        g2 = torch.Generator(device=gd).manual_seed(int(cfg["seed"]))
+    rnd = lambda *shape: torch.randn(*shape, generator=g2, device=gd)  # noqa: E731
+    x = (torch.rand(N, H, generator=g2, device=gd) * 2.0 - 1.0) * math.sqrt(3.0)
     if n_near:
-        c = cluster_of[near_rows]
-        z = mu[c] + sigma_w * torch.randn(n_near, d, generator=gen)
-        g = torch.randn(n_near, H, generator=gen)
-        vis = is_vision[near_rows]
-        xn = torch.empty(n_near, H)
-        for sel, P, b in ((vis, pv, bv), (~vis, pt, bt)):
+        c = cluster_of[near_rows].to(gd)
+        z = mu.to(gd)[c] + sigma_w * rnd(n_near, d)
+        g = rnd(n_near, H)
+        vis = is_vision[near_rows].to(gd)
+        xn = torch.empty(n_near, H, device=gd)
+        for sel, P, b in ((vis, pv.to(gd), bv.to(gd)), (~vis, pt.to(gd), bt.to(gd))):
             if sel.any():
                 # x = P (z - b) + 0.05 (I - P P^T) g, so that x @ P + b = z
                 gs = g[sel]
                 xn[sel] = (z[sel] - b) @ P.T + 0.05 * (gs - (gs @ P) @ P.T)
-        x[near_rows] = xn
+        x[near_rows.to(gd)] = xn
 
-    values = torch.randn(C, H, generator=gen)
-    logits = torch.randn(N, E, generator=gen)
-    slot_out = torch.randn(N, k, H, generator=gen) if with_slot_out else torch.empty(0)
-    residual = torch.randn(N, H, generator=gen)
+    values = rnd(C, H)
+    logits = rnd(N, E)
+    slot_out = rnd(N, k, H) if with_slot_out else torch.empty(0, device=gd)
+    residual = rnd(N, H)
 
     def cvt(t):
         return t.to(dt).to(device)
@@ -127,3 +138,12 @@ def make_workload(config: int = 2, *, n: int | None = None, seed: int | None = N
         proj_txt=cvt(pt), bias_txt=cvt(bt), centroids=cvt(mu), values=cvt(values),
         logits=logits.to(device), slot_out=cvt(slot_out), residual=cvt(residual), cluster_of=cluster_of.to(device),
     )
+
+
+def make_stack(n_layers: int = 48, *, n: int | None = None, device="cuda", gen_device="cuda",
+               **overrides) -> list[Workload]:
+    """Config 4: ``n_layers`` independent layers (seed 40 + l), each with its
+    own table (C=8192, d=128, cached outputs 8192x2048 bf16), hidden states,
+    router logits, slot outputs and residual, drawn on ``gen_device``."""
+    return [make_workload(4, n=n, seed=CONFIGS[4]["seed"] + l, device=device, gen_device=gen_device, **overrides)
+            for l in range(n_layers)]

@@ -78,7 +78,7 @@ def test_argument_validation_without_device(lib):
     assert lib.tm_search_global(N.TM_DT_BF16, None, 10, 128, None, None, 100, 128, None, 128, 9, 0, None, None,
                                 None, 0, None) == N.TM_EINVAL_SHAPE
     assert b"top_k 9" in lib.tm_last_error()
-    assert lib.tm_search_global(N.TM_DT_F32, None, 10, 128, None, None, 100, 128, None, 128, 1, 0, None, None,
+    assert lib.tm_search_global(7, None, 10, 128, None, None, 100, 128, None, 128, 1, 0, None, None,
                                 None, 0, None) == N.TM_EINVAL_DTYPE
     assert lib.tm_search_gated(7, C.c_void_p(16), 4, 64, C.c_void_p(16), 8, 256, 64, 0, 0, 64, C.c_void_p(16), 8,
                                8, 1, None, None, 0, 0, 0, 0.6, 0.7, 0, C.c_void_p(16), C.c_void_p(16), 8, 1,

@@ -418,6 +418,31 @@ def test_swiglu_expert_one_hot_closed_form():
     assert np.all(y[:, others] == 0.0)
 
 
+def test_swiglu_expert_addend_closed_forms():
+    """The addend form (shared experts folded into the residual): a zero
+    addend gives the plain MLP bit for bit; zero down weights give the addend
+    rounded once; with one-hot weights, dt(addend + f) where f is the routed
+    intermediate, so the addend enters before the single final rounding (the
+    sum of two bf16 values generally needs that rounding)."""
+    rng = np.random.default_rng(11)
+    H, I, M = 16, 8, 6
+    x = O.round_to(rng.normal(size=(M, H)), O.BF16)
+    w1 = O.round_to(rng.normal(size=(I, H)) * 0.3, O.BF16)
+    w3 = O.round_to(rng.normal(size=(I, H)) * 0.3, O.BF16)
+    w2 = O.round_to(rng.normal(size=(H, I)) * 0.3, O.BF16)
+    r = O.round_to(rng.normal(size=(M, H)) * 5, O.BF16)
+    plain, _ = O.swiglu_expert(x, w1, w3, w2, O.BF16)
+    zero, _ = O.swiglu_expert(x, w1, w3, w2, O.BF16, addend=np.zeros((M, H)))
+    np.testing.assert_array_equal(plain, zero)
+    only, _ = O.swiglu_expert(x, w1, w3, np.zeros((H, I)), O.BF16, addend=r)
+    np.testing.assert_array_equal(only, r)
+    c = rng.permutation(H)[:I]
+    w2h = np.zeros((H, I)); w2h[c, np.arange(I)] = 1.0
+    y, f = O.swiglu_expert(x, w1, w3, w2h, O.BF16, addend=r)
+    np.testing.assert_array_equal(y[:, c], O.round_to(r[:, c] + f, O.BF16))
+    assert not np.array_equal(y[:, c], r[:, c] + f)  # the exact sum is not a bf16 value everywhere
+
+
 def test_swiglu_expert_matches_torch_silu_and_matmul():
     """Against torch's own silu and float64 matmul (library routines) with the
     same rounding points; and the up projection is NOT rounded before the
