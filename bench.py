@@ -1,6 +1,6 @@
 """Benchmark of the table-search path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--sections LIST] [--no-cpu]
 
 A step is one MoE layer of the table path on the config-2 workload of
 BASELINE.json (Qwen3-VL-30B-A3B-shaped prefill: N=4096 tokens, hidden 2048
@@ -11,15 +11,19 @@ selection -> gather + combine + residual.  Inputs are resident in HBM before
 timing; steps rotate over replicas of the workload totalling > 2x the 256 MB
 Infinity Cache so reads come from HBM.
 
-Prints ONE JSON line: tokens/s per MoE layer (value, from replays of one HIP
-graph holding four consecutive layers, one tm_table_forward call each), per-stage device times, the average
-device time of each stage's C-ABI call (graphs of 32 back-to-back calls timed
-with HIP events on the stream the kernels run on), the roofline of the
-dominant call (HBM bytes from the committed rocprofv3 PMC summary when
-present), the decode (N=32, C=16384, top-4) layer, and the reference path
-restated on the host CPU (oracle, numpy fp32) as the CPU baseline, and the
-config-5 recompute (grouped SwiGLU expert MLP of the kept tokens' slots plus
-the shared experts) in its own "recompute" object.
+Prints ONE JSON line: the headline (tokens/s per MoE layer from replays of a
+HIP graph of four consecutive layers), the roofline of the layer's dominant
+kernel (timed live with HIP events on the stream it runs on), and one object
+per other BASELINE configuration:
+  decode   config 3 at N = 1, 8 and 32 over 128 table replicas (704 MiB of
+           distinct tables, so every search reads HBM)
+  config1  the fp32 CPU-reference layer on the GPU
+  config4  the 48-layer stack, one graph of 48 layers per keep_rate
+  config5  the DeepSeek-VL2-style layer end to end (search, grouped
+           recompute of the kept slots, shared experts, combine)
+  mode_r   the reference's own per-expert searches at Qwen shapes
+and the torch-CPU restatement of the reference's fallback path (oracle/
+tm_cpu_ref.py) timed on this host's cores for every configuration.
 """
 
 from __future__ import annotations
@@ -27,6 +31,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -40,14 +45,53 @@ HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "table-search tokens/s per MoE layer (N=4096 prefill, N=32 decode) + HBM GB/s"
 N_REPLICAS = 4
+DECODE_REPLICAS = 128
+KEEP_RATES = [0.1, 0.25, 0.5, 0.75, 0.9, 1.0]
+SECTIONS = ["prefill", "decode", "config1", "config4", "config5", "mode_r", "cpu"]
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+# --------------------------------------------------------------------------- timing helpers
+def graph_of(fn):
+    """fn() captured in one HIP graph (after an eager run on a side stream, so
+    every buffer it uses exists before capture)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def replay_times_us(g, replays, warm=1):
+    """Device time of each of `replays` replays of graph g (HIP events on the
+    stream the graph runs on), after `warm` untimed replays."""
+    import torch
+
+    for _ in range(warm):
+        g.replay()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(replays)]
+    for a, b in evs:
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    return [1000.0 * a.elapsed_time(b) for a, b in evs]
+
+
 def _stage_bytes(cfg, n, n_keep, nn, top_k):
-    """Algorithmic HBM bytes of each stage of one layer (bf16 = 2 bytes)."""
+    """Algorithmic HBM bytes of each stage of one layer (2-byte data)."""
     H, d, C, E = cfg["hidden"], cfg["dim"], cfg["n_cent"], cfg["n_experts"]
     n_reuse = n - n_keep
     return {
@@ -60,29 +104,38 @@ def _stage_bytes(cfg, n, n_keep, nn, top_k):
     }
 
 
-def run_layer_bench(cfg_id, steps, warmup, n=None):
+def _tables(reps):
+    from table_moe.cache_engine import GlobalTable
+
+    return [GlobalTable(r.centroids, r.values, (r.proj_vis, r.bias_vis), (r.proj_txt, r.bias_txt)) for r in reps]
+
+
+def _replicas(base, count):
+    """`count` copies of a device workload in distinct memory."""
     import torch
 
-    from table_moe.cache_engine import GlobalTable
+    out = [base]
+    for _ in range(count - 1):
+        kw = {k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in base.__dict__.items()}
+        out.append(type(base)(**kw))
+    return out
+
+
+# --------------------------------------------------------------------------- config 2 (headline)
+def run_prefill(steps, warmup):
+    import torch
+
     from synth import make_workload
 
     dev = torch.device("cuda:0")
     t0 = time.time()
-    wl = make_workload(cfg_id, n=n)
-    log(f"config {cfg_id}: workload generated in {time.time() - t0:.1f}s")
-    cfg = wl.cfg
-    base = wl.to(dev)
-    reps = [base] + [base.to(dev) for _ in range(N_REPLICAS - 1)]
-    for r in reps[1:]:
-        for k, v in r.__dict__.items():
-            if isinstance(v, torch.Tensor):
-                setattr(r, k, v.clone())
-    tables = [GlobalTable(r.centroids, r.values, (r.proj_vis, r.bias_vis), (r.proj_txt, r.bias_txt)) for r in reps]
+    base = make_workload(2).to(dev)
+    log(f"config 2: workload generated in {time.time() - t0:.1f}s")
+    cfg = base.cfg
+    reps = _replicas(base, N_REPLICAS)
+    tables = _tables(reps)
     outs = [torch.empty_like(r.residual) for r in reps]
-    topk, nn, kr = cfg["router_top_k"], cfg["n_nearest"], cfg["keep_rate"]
-    N = cfg["n"]
-
-    stage_names = ["router", "project", "search", "keep", "combine"]
+    topk, nn, kr, N = cfg["router_top_k"], cfg["n_nearest"], cfg["keep_rate"], cfg["n"]
 
     def step(i, ev=None):
         r, t, o = reps[i % N_REPLICAS], tables[i % N_REPLICAS], outs[i % N_REPLICAS]
@@ -92,76 +145,55 @@ def run_layer_bench(cfg_id, steps, warmup, n=None):
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    # 1) timed region: K layers back to back, no instrumentation inside
-    ev_all = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-    torch.cuda.synchronize()
+    # eager: K layers back to back, one C-ABI call each
     t_start = time.perf_counter()
-    ev_all[0].record()
     for i in range(steps):
         step(i)
-    ev_all[1].record()
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t_start
-    device_us = 1000.0 * ev_all[0].elapsed_time(ev_all[1]) / steps
-    # 1b) the same layers replayed from one HIP graph holding N_REPLICAS
-    #     consecutive layers (one per replica, as a model runs its layers):
-    #     identical kernels and work, without host launch cost
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for i in range(N_REPLICAS):
-            step(i)
-    torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(N_REPLICAS):
-            step(i)
-    tail = None  # the last steps % N_REPLICAS layers, so exactly `steps` layers are timed
-    if steps % N_REPLICAS:
-        tail = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(tail):
-            for i in range(steps % N_REPLICAS):
-                step(i)
-    torch.cuda.synchronize()
+    eager_s = time.perf_counter() - t_start
+    # the timed region of the contract: exactly K layers replayed from HIP
+    # graphs of N_REPLICAS consecutive layers (one per replica)
+    graph = graph_of(lambda: [step(i) for i in range(N_REPLICAS)])
+    tail = graph_of(lambda: [step(i) for i in range(steps % N_REPLICAS)]) if steps % N_REPLICAS else None
     for _ in range(max(1, warmup // N_REPLICAS)):
         graph.replay()
     torch.cuda.synchronize()
-    g_steps = steps
-    g_ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     t_g = time.perf_counter()
-    g_ev[0].record()
+    ev[0].record()
     for _ in range(steps // N_REPLICAS):
         graph.replay()
     if tail is not None:
         tail.replay()
-    g_ev[1].record()
+    ev[1].record()
     torch.cuda.synchronize()
-    graph_elapsed = time.perf_counter() - t_g
-    graph_device_us = 1000.0 * g_ev[0].elapsed_time(g_ev[1]) / g_steps
+    graph_s = time.perf_counter() - t_g
+    graph_device_us = 1000.0 * ev[0].elapsed_time(ev[1]) / steps
+    # median over >= 100 layers: 32 individually timed replays of the 4-layer graph
+    med_us = statistics.median(replay_times_us(graph, 32)) / N_REPLICAS
     del graph, tail
-    # 2) instrumented pass over the same steps: HIP events between the stages
-    #    (an event record adds a few microseconds of its own between stages)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
-    for e in evs:  # create the underlying HIP events first
+    # instrumented pass: HIP events between the stages.  A bounded device spin
+    # (~10 ms) queued first lets the host enqueue every step before the GPU
+    # reaches them, so the stage intervals hold device time, not the host's
+    # launch latency.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(min(steps, 32))]
+    for e in evs:
         for x in e:
             x.record()
     torch.cuda.synchronize()
-    for i in range(steps):
-        step(i, evs[i])
+    torch.cuda._sleep(25_000_000)
+    for i, e in enumerate(evs):
+        step(i, e)
     torch.cuda.synchronize()
-    stage_ms = {s: 0.0 for s in stage_names}
-    for e in evs:
-        for j, s in enumerate(stage_names):
-            stage_ms[s] += e[j].elapsed_time(e[j + 1])
-    stage_us = {s: 1000.0 * v / steps for s, v in stage_ms.items()}
+    names = ["router", "project", "search", "keep", "combine"]
+    stage_us = {s: 1000.0 * sum(e[j].elapsed_time(e[j + 1]) for e in evs) / len(evs) for j, s in enumerate(names)}
     keep = step(0)
     torch.cuda.synchronize()
     n_keep = int(keep.sum().item())
-    kernel_us = stage_kernel_times(reps, tables, outs, topk, nn, kr)
-    return dict(cfg=cfg, wl=wl, elapsed=elapsed, eager_ms_per_step=1000.0 * elapsed / steps,
-                ms_per_step=1000.0 * graph_elapsed / g_steps, graph_device_us=graph_device_us, stage_us=stage_us,
-                kernel_us=kernel_us, device_us=device_us, n_keep=n_keep,
-                bytes=_stage_bytes(cfg, N, n_keep, nn, topk))
+    kernel_us = stage_call_times(reps, tables, outs, topk, nn, kr)
+    return dict(cfg=cfg, reps=reps, eager_us=1e6 * eager_s / steps, graph_us=1e6 * graph_s / steps,
+                graph_device_us=graph_device_us, median_us=med_us, stage_us=stage_us, kernel_us=kernel_us,
+                n_keep=n_keep, bytes=_stage_bytes(cfg, N, n_keep, nn, topk))
 
 
 def ranked_layer(n, nn, topk, hidden):
@@ -169,13 +201,12 @@ def ranked_layer(n, nn, topk, hidden):
     return nn == 1 and n <= 4096 and topk in (6, 8) and hidden <= 2048 and hidden % 8 == 0
 
 
-def stage_kernel_times(reps, tables, outs, topk, nn, kr, launches=32, replays=3):
+def stage_call_times(reps, tables, outs, topk, nn, kr, launches=32, replays=3):
     """Average device time of each stage's C-ABI call: `launches` back-to-back
     calls (rotating over the table replicas, so reads stay HBM-cold) captured
-    in one HIP graph, replayed `replays` times between two HIP events recorded
-    on the stream the kernels run on.  The combine stage is the call the layer
-    runs: tm_gather_combine_ranked (keep set ranked in the combine) for top-1
-    batches of up to 4096 tokens, tm_gather_combine otherwise."""
+    in one HIP graph, replayed `replays` times between HIP events on the
+    stream the kernels run on.  The combine stage is the call the layer runs:
+    tm_gather_combine_ranked for top-1 batches of up to 4096 tokens."""
     import torch
 
     n0 = reps[0].x.shape[0]
@@ -194,7 +225,7 @@ def stage_kernel_times(reps, tables, outs, topk, nn, kr, launches=32, replays=3)
             t.search(b["q"][: n * t.dim].view(n, t.dim), nn, b["qn"][:n])
         elif name == "keep":
             t.keep_select(b["dist"][: n * nn].view(n, nn)[:, 0], t.keep_count(n, kr))
-        elif ranked:  # the layer's combine: keep set ranked in the same launch
+        elif ranked:
             t.gather_combine_ranked(r.slot_out, b["route_w"][: n * topk].view(n, topk), b["idx"][: n * nn].view(n, nn),
                                     b["dist"][:n], t.keep_count(n, kr), r.residual, o, keep=rk[i % len(rk)])
         else:
@@ -203,102 +234,12 @@ def stage_kernel_times(reps, tables, outs, topk, nn, kr, launches=32, replays=3)
 
     out = {}
     for name in ("router", "project", "search", "keep", "combine"):
-        for i in range(len(tables)):  # allocate the stage's own buffers outside capture
+        for i in range(len(tables)):
             calls(name, i)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(launches):
-                calls(name, i)
-        torch.cuda.synchronize()
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(replays):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        out[name] = 1000.0 * e0.elapsed_time(e1) / (replays * launches)
+        g = graph_of(lambda: [calls(name, i) for i in range(launches)])
+        out[name] = sum(replay_times_us(g, replays)) / (replays * launches)
         del g
     return out
-
-
-def run_recompute_bench(steps, warmup):
-    """Config 5 recompute (DeepSeek-VL2-style layer, hidden 2560, 64 routed
-    experts top-6 + shared experts, intermediate 1536, N=4096): the kept
-    tokens' routed slots through tm_group_slots + tm_grouped_swiglu (written
-    in the slot layout the combine reads), and the shared-expert MLP (one
-    SwiGLU of intermediate 2 x 1536) over every token.  The keep set and the
-    router ids come from the config-5 table layer itself; weights are
-    random-init N(0, 0.02) bf16 (no checkpoint offline).  Timed as graph
-    replays with HIP events on the calls' stream."""
-    import torch
-
-    from table_moe.cache_engine import GlobalTable
-    from table_moe.ops import GroupedExperts, expert_swiglu
-    from synth import make_workload
-
-    dev = torch.device("cuda:0")
-    wl = make_workload(5)
-    cfg = wl.cfg
-    d = wl.to(dev)
-    tbl = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
-    res = tbl.layer_forward(d.x, d.is_vision, d.logits, d.slot_out, d.residual, cfg["router_top_k"], 1,
-                            cfg["keep_rate"])
-    keep, ids = res["keep"].clone(), res["ids"].clone()
-    n, h, e, k, inter = cfg["n"], cfg["hidden"], cfg["n_experts"], cfg["router_top_k"], 1536
-    shared_inter = 2 * inter
-    g = torch.Generator(device=dev).manual_seed(55)
-    rnd = lambda *shape: (torch.randn(*shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)  # noqa: E731
-    ge = GroupedExperts(rnd(e, inter, h), rnd(e, inter, h), rnd(e, h, inter))
-    s1, s3, s2 = rnd(shared_inter, h), rnd(shared_inter, h), rnd(h, shared_inter)
-    slot_out = torch.empty(n, k, h, dtype=torch.bfloat16, device=dev)
-    shared_out = torch.empty(n, h, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(n * shared_inter * 2, dtype=torch.uint8, device=dev)
-
-    def timed(fn, reps):
-        for _ in range(max(1, warmup // 4)):
-            fn()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            fn()
-        torch.cuda.current_stream().wait_stream(side)
-        with torch.cuda.graph(graph):
-            fn()
-        graph.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return 1000.0 * e0.elapsed_time(e1) / reps
-
-    reps = max(3, min(steps, 20))
-    routed_us = timed(lambda: ge.forward(d.x, ids, keep, slot_out), reps)
-    shared_us = timed(lambda: expert_swiglu(d.x, s1, s3, s2, out=shared_out, workspace=ws), reps)
-    rows = int(keep.sum().item()) * k
-    routed_flops = rows * 6.0 * h * inter
-    shared_flops = n * 6.0 * h * shared_inter
-    tf = lambda f, us: f / (us * 1e-6) / 1e12  # noqa: E731
-    return {
-        "workload": "config 5 recompute: N=4096, hidden 2560, 64 routed experts top-6 (kept tokens' slots, keep set "
-                    "from the config-5 table layer) + shared experts (SwiGLU intermediate 3072, all tokens), routed "
-                    "intermediate 1536, random-init bf16 weights",
-        "routed_rows": rows,
-        "routed_us": routed_us,
-        "routed_tflops": tf(routed_flops, routed_us),
-        "routed_mfma_frac": tf(routed_flops, routed_us) / BF16_PEAK_TFLOPS,
-        "routed_weight_GBps": 3 * e * h * inter * 2 / (routed_us * 1e-6) / 1e9,
-        "shared_us": shared_us,
-        "shared_tflops": tf(shared_flops, shared_us),
-        "shared_mfma_frac": tf(shared_flops, shared_us) / BF16_PEAK_TFLOPS,
-    }
 
 
 COPY_CAL_BYTES = 256 << 20  # bytes read (and written) by the calibration copy
@@ -307,7 +248,7 @@ COPY_CAL_BYTES = 256 << 20  # bytes read (and written) by the calibration copy
 def copy_calibration(reps=3):
     """A plain device copy pass over COPY_CAL_BYTES, launched `reps` times: under
     `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` its counters give the scale
-    from counter KiB to bytes moved (profiles/gather_combine_ranked_config2_traffic.txt)."""
+    from counter KiB to bytes moved."""
     import torch
 
     a = torch.empty(COPY_CAL_BYTES // 2, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
@@ -318,19 +259,23 @@ def copy_calibration(reps=3):
     del a, b
 
 
+def profile_values(summary):
+    """key = value lines of a committed profile summary under profiles/."""
+    path = REPO / "profiles" / summary
+    vals = {}
+    if path.exists():
+        for line in path.read_text().splitlines():
+            if "=" in line and not line.lstrip().startswith("#"):
+                k, v = line.split("=", 1)
+                vals[k.strip()] = v.strip()
+    return vals
+
+
 def traffic_from_profile(kernel_prefix, summary):
     """HBM bytes per launch of `kernel_prefix` from the committed PMC summary
-    profiles/<summary> (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each
-    scaled by the same counter's reading for the calibration copy), or None
-    without a summary."""
-    path = REPO / "profiles" / summary
-    if not path.exists():
-        return None
-    vals = {}
-    for line in path.read_text().splitlines():
-        if "=" in line and not line.lstrip().startswith("#"):
-            k, v = line.split("=", 1)
-            vals[k.strip()] = v.strip()
+    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by the same
+    counter's reading for the calibration copy), or None without one."""
+    vals = profile_values(summary)
     try:
         fetch = float(vals[f"{kernel_prefix}.FETCH_SIZE_KiB"]) * 1024.0 * float(vals["copy.fetch_scale"])
         write = float(vals[f"{kernel_prefix}.WRITE_SIZE_KiB"]) * 1024.0 * float(vals["copy.write_scale"])
@@ -339,65 +284,409 @@ def traffic_from_profile(kernel_prefix, summary):
     return fetch + write
 
 
-def cpu_baseline(wl, budget_s=12.0):
-    """The reference op sequence restated in numpy fp32 (oracle), on a bounded sample."""
-    import numpy as np
+# --------------------------------------------------------------------------- config 3 (decode)
+def run_decode(replicas=DECODE_REPLICAS, replays=5):
+    """Config 3 at N = 1, 8, 32: one HIP graph of `replicas` consecutive layer
+    calls, each on its own table (centroids 4 MiB + norms + packed
+    projections + cached outputs, all distinct memory), replayed; per-layer
+    time = replay time / replicas."""
+    import torch
 
-    from oracle import tm_oracle as O
+    from synth import make_workload
 
-    try:
-        from threadpoolctl import threadpool_info, threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_info = threadpool_limits = None
-    f = lambda t: t.detach().cpu().float().numpy()  # noqa: E731
+    dev = torch.device("cuda:0")
+    base = make_workload(3, n=32, device=dev, gen_device=dev)
+    cfg = base.cfg
+    reps = _replicas(base, replicas)
+    tables = _tables(reps)
+    res = {}
+    for n in (1, 8, 32):
+        outs = [torch.empty(n, cfg["hidden"], dtype=torch.bfloat16, device=dev) for _ in reps]
+
+        def layers():
+            for r, t, o in zip(reps, tables, outs):
+                t.layer_forward(r.x[:n], r.is_vision[:n], r.logits[:n], r.slot_out[:n], r.residual[:n], 8, 4, 0.6,
+                                out=o)
+
+        g = graph_of(layers)
+        per = [t / replicas for t in replay_times_us(g, replays)]
+        del g
+        n_keep = max(1, int(n * 0.6))
+        by = _stage_bytes(cfg, n, n_keep, 4, 8)
+        layer_bytes = (cfg["n_cent"] * cfg["dim"] * 2 + cfg["n_cent"] * 4 + cfg["hidden"] * cfg["dim"] * 2
+                       + n * cfg["hidden"] * 2 + 4 * (n - n_keep) * cfg["hidden"] * 2
+                       + n_keep * 8 * cfg["hidden"] * 2 + 2 * n * cfg["hidden"] * 2 + n * 8 * 12)
+        us = statistics.median(per)
+        res[f"N={n}"] = {
+            "tokens": n, "n_keep": n_keep, "us_per_layer_median": us, "us_per_layer_mean": statistics.mean(per),
+            "tokens_per_s": n / (us * 1e-6), "algorithmic_bytes": layer_bytes,
+            "layer_hbm_GBps": layer_bytes / (us * 1e-6) / 1e9,
+            "layer_hbm_frac": layer_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+            "search_bytes": by["search"] + cfg["hidden"] * cfg["dim"] * 2,
+        }
+        log(f"decode N={n}: {us:.2f} us/layer (median of {replays} replays of {replicas} layers)")
+    del reps, tables
+    torch.cuda.empty_cache()
+    return {"workload": f"config 3: N in {{1, 8, 32}} text tokens, C=16384 x 128 bf16, cached outputs 16384x2048, "
+                        f"top-4 inverse-distance blend, keep_rate 0.6; {replicas} distinct tables rotated "
+                        f"(704 MiB, > 2x the 256 MB Infinity Cache), one graph of {replicas} layers",
+            **res}
+
+
+# --------------------------------------------------------------------------- config 1
+def run_config1(replays=20):
+    import torch
+
+    from synth import make_workload
+
+    dev = torch.device("cuda:0")
+    reps = _replicas(make_workload(1).to(dev), 8)
+    tables = _tables(reps)
+    outs = [torch.empty_like(r.residual) for r in reps]
+
+    def layers():
+        for r, t, o in zip(reps, tables, outs):
+            t.layer_forward(r.x, r.is_vision, r.logits, r.slot_out, r.residual, 8, 1, 0.6, out=o)
+
+    g = graph_of(layers)
+    us = statistics.median(replay_times_us(g, replays)) / len(reps)
+    del g
+    log(f"config 1 (fp32): {us:.2f} us/layer")
+    return {"workload": "config 1: N=256, hidden 2048 fp32, PCA 2048x64, C=1024 fp32, cached outputs 1024x2048 "
+                        "fp32, router 128 experts top-8, top-1, keep_rate 0.6 (153 kept)",
+            "dtype": "f32", "us_per_layer": us, "tokens_per_s": 256 / (us * 1e-6)}
+
+
+# --------------------------------------------------------------------------- config 4
+def run_config4(replays=3):
+    """The 48-layer stack: per keep_rate one HIP graph of the 48 layers in
+    sequence (layer l's output is layer l + 1's residual)."""
+    import torch
+
+    from synth import make_stack
+
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    wls = make_stack(48, device=dev)
+    torch.cuda.synchronize()
+    log(f"config 4: 48 layers generated in {time.time() - t0:.1f}s")
+    tables = _tables(wls)
+    outs = [torch.empty_like(w.residual) for w in wls]
+    cfg = wls[0].cfg
+    n = cfg["n"]
+    rows = []
+    for kr in KEEP_RATES:
+        def stack():
+            resid = wls[0].residual
+            for w, t, o in zip(wls, tables, outs):
+                t.layer_forward(w.x, w.is_vision, w.logits, w.slot_out, resid, 8, 1, kr, out=o)
+                resid = o
+
+        g = graph_of(stack)
+        us = statistics.median(replay_times_us(g, replays)) / len(wls)
+        del g
+        n_keep = max(1, int(n * kr))
+        by = _stage_bytes(cfg, n, n_keep, 1, 8)
+        layer_bytes = sum(by.values())
+        rows.append({"keep_rate": kr, "n_keep": n_keep, "us_per_layer": us, "tokens_per_s": n / (us * 1e-6),
+                     "algorithmic_bytes_per_layer": layer_bytes, "hbm_GBps": layer_bytes / (us * 1e-6) / 1e9,
+                     "hbm_frac": layer_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS})
+        log(f"config 4 keep {kr}: {us:.2f} us/layer")
+    del wls, tables, outs
+    torch.cuda.empty_cache()
+    return {"workload": "config 4: 48 independent layers (C=8192 x 128, cached outputs 8192x2048 bf16: 1.61 GB of "
+                        "tables), N=2048 tokens per layer run in sequence from one HIP graph of 48 layers",
+            "keep_rates": rows}
+
+
+# --------------------------------------------------------------------------- config 5
+def run_config5(replays=10):
+    """The DeepSeek-VL2-style layer end to end (GlobalTable.layer_forward_recompute)
+    and its parts, each as a replayed HIP graph."""
+    import torch
+
+    from synth import make_workload
+    from table_moe.ops import GroupedExperts, expert_swiglu
+
+    dev = torch.device("cuda:0")
+    wl = make_workload(5, with_slot_out=False, device=dev, gen_device=dev)
     cfg = wl.cfg
-    n_sample = min(cfg["n"], 1024)
-    args = (f(wl.x[:n_sample]), wl.is_vision[:n_sample].cpu().numpy(), (f(wl.proj_vis), f(wl.bias_vis)),
-            (f(wl.proj_txt), f(wl.bias_txt)), f(wl.centroids), f(wl.values), f(wl.logits[:n_sample]),
-            f(wl.slot_out[:n_sample]), f(wl.residual[:n_sample]), cfg["router_top_k"], cfg["n_nearest"],
-            cfg["keep_rate"])
-    cores = len(os.sched_getaffinity(0))
-    threads = cores
-    ctx = threadpool_limits(limits=cores) if threadpool_limits else None
-    try:
-        O.layer_forward_g_fp32(*args)  # warm-up
-        times = []
-        t_all = time.perf_counter()
-        while time.perf_counter() - t_all < budget_s or len(times) < 3:
-            t0 = time.perf_counter()
-            O.layer_forward_g_fp32(*args)
-            times.append(time.perf_counter() - t0)
-            if len(times) >= 50:
-                break
-        if threadpool_info:
-            info = threadpool_info()
-            if info:
-                threads = max(int(i.get("num_threads", 1)) for i in info)
-    finally:
-        if ctx is not None:
-            ctx.unregister() if hasattr(ctx, "unregister") else None
-    med = float(np.median(times))
+    n, h, e, k, inter = cfg["n"], cfg["hidden"], cfg["n_experts"], cfg["router_top_k"], 1536
+    g = torch.Generator(device=dev).manual_seed(55)
+    rnd = lambda *shape: (torch.randn(*shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)  # noqa: E731
+    ex = GroupedExperts(rnd(e, inter, h), rnd(e, inter, h), rnd(e, h, inter))
+    shared = (rnd(2 * inter, h), rnd(2 * inter, h), rnd(h, 2 * inter))
+    tbl = _tables([wl])[0]
+    out = torch.empty_like(wl.residual)
+
+    def layer():
+        tbl.layer_forward_recompute(wl.x, wl.is_vision, wl.logits, ex, wl.residual, k, 0.6, shared=shared, out=out)
+
+    gl = graph_of(layer)
+    layer_us = statistics.median(replay_times_us(gl, replays))
+    del gl
+    res = tbl.layer_forward_recompute(wl.x, wl.is_vision, wl.logits, ex, wl.residual, k, 0.6, shared=shared, out=out)
+    keep, ids = res["keep"].clone(), res["ids"].clone()
+    w, idx, dist = res["weights"].clone(), res["idx"].clone(), res["dist"].clone()
+    slot = res["slot_out"]
+    base = torch.empty_like(wl.residual)
+    ws = torch.empty(n * 2 * inter * 2, dtype=torch.uint8, device=dev)
+    parts = {
+        "search_us": lambda: tbl.layer_search(wl.x, wl.is_vision, wl.logits, k, 1, 0.6),
+        "routed_recompute_us": lambda: ex.forward(wl.x, ids, keep, slot),
+        "shared_us": lambda: expert_swiglu(wl.x, *shared, out=base, workspace=ws, addend=wl.residual),
+        "combine_us": lambda: tbl.gather_combine(keep, slot, w, idx, dist, base, out),
+    }
+    times = {}
+    for name, fn in parts.items():
+        gp = graph_of(fn)
+        times[name] = statistics.median(replay_times_us(gp, replays))
+        del gp
+    rows = int(keep.sum().item()) * k
+    routed_flops = rows * 6.0 * h * inter
+    shared_flops = n * 6.0 * h * 2 * inter
+    search_flops = 2.0 * n * h * cfg["dim"] + 2.0 * n * cfg["n_cent"] * cfg["dim"]
+    total_flops = routed_flops + shared_flops + search_flops
+    log(f"config 5 layer: {layer_us:.1f} us ({json.dumps({k_: round(v, 1) for k_, v in times.items()})})")
     return {
-        "value": n_sample / med,
-        "unit": "tokens/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{n_sample} tokens of the config-2 layer (all C={cfg['n_cent']} centroids), "
-                  f"median of {len(times)} runs, numpy fp32, {threads} threads on {cores} host cores",
+        "workload": "config 5: N=4096, hidden 2560 bf16, 64 routed experts top-6 (intermediate 1536) + shared experts "
+                    "(intermediate 2 x 1536), C=8192 x 128, keep_rate 0.6 (2457 kept tokens: 14742 recomputed slot "
+                    "rows), random-init N(0, 0.02) bf16 weights; table search -> grouped recompute -> shared experts "
+                    "folded into the residual -> gather + combine",
+        "us_per_layer": layer_us, "tokens_per_s": n / (layer_us * 1e-6), **times,
+        "routed_rows": rows, "routed_tflops": routed_flops / (times["routed_recompute_us"] * 1e-6) / 1e12,
+        "routed_mfma_frac": routed_flops / (times["routed_recompute_us"] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
+        "shared_tflops": shared_flops / (times["shared_us"] * 1e-6) / 1e12,
+        "shared_mfma_frac": shared_flops / (times["shared_us"] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
+        "layer_tflops": total_flops / (layer_us * 1e-6) / 1e12,
     }
 
 
+# --------------------------------------------------------------------------- mode R
+def mode_r_setup(dev, E=128, H=2048, d=64, K=256, seed=7):
+    """A HybridStorageManager of the reference's default shape (128 experts x
+    2 modalities x 256 centroids in 64-d, hidden 2048) filled on the device:
+    random keys (normalised copy as the loader makes it), cached outputs, PCA
+    pairs, a full 64-entry online window."""
+    import torch
+
+    from table_moe.cache_engine import CacheConfig, HybridStorageManager
+    from table_moe.cache_engine.table_file import normalize_last_dim
+
+    saved = {k: getattr(CacheConfig, k) for k in ("FIXED_K", "COMPRESSED_DIM", "MODEL_DTYPE", "ONLINE_CACHE_SIZE",
+                                                  "ONLINE_TOP_K")}
+    CacheConfig.FIXED_K, CacheConfig.COMPRESSED_DIM, CacheConfig.MODEL_DTYPE = K, d, torch.bfloat16
+    CacheConfig.ONLINE_CACHE_SIZE, CacheConfig.ONLINE_TOP_K = 64, 8
+    try:
+        mgr = HybridStorageManager(2, E, H, dev)
+    finally:
+        for k_, v in saved.items():
+            setattr(CacheConfig, k_, v)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    raw = torch.randn(E, 2, K, d, generator=g, device=dev)
+    mgr.raw_keys_buffer.copy_(raw.to(torch.bfloat16))
+    mgr.keys_buffer.copy_(normalize_last_dim(raw, 1e-6).to(torch.bfloat16))
+    mgr.values_buffer.copy_(torch.randn(E, 2, K, H, generator=g, device=dev).to(torch.bfloat16))
+    for mod in ("vision", "text"):
+        p = torch.linalg.qr(torch.randn(H, d, generator=g, device=dev, dtype=torch.float32))[0]
+        mgr.pca[mod] = {"proj": p.to(torch.bfloat16), "bias": (torch.randn(d, generator=g, device=dev) * 0.05)
+                        .to(torch.bfloat16)}
+    hist = torch.randn(64, H, generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, device=dev)[:8] for _ in range(64)])
+    mgr.update_online_cache(hist, ids, torch.randn(64, 8, H, generator=g, device=dev).to(torch.bfloat16))
+    return mgr
+
+
+def run_mode_r(replays=20):
+    """The reference's own semantics at Qwen3-VL-30B-A3B shapes:
+    search_prefill_offline (N=4096, top-8 of 128 experts, reuse = the slots of
+    experts outside the 60 % kept by importance) and the decode bs1 hybrid
+    search, as replayed HIP graphs."""
+    import torch
+
+    from synth import make_workload
+    from table_moe.cache_engine import VectorSearchEngine
+    from table_moe.ops import qwen_topk_softmax
+    from table_moe.skip import build_prefill_keep_mask
+
+    dev = torch.device("cuda:0")
+    mgr = mode_r_setup(dev)
+    eng = VectorSearchEngine(mgr)
+    wl = make_workload(2, with_slot_out=False, device=dev, gen_device=dev)
+    n, k = wl.x.shape[0], 8
+    w, sel = qwen_topk_softmax(wl.logits, k)
+    attn = torch.rand(n, device=dev)
+    compute = build_prefill_keep_mask(sel, w, attn, 128, 0.6)
+    reuse = ~compute
+    # queries that hit their tables: half the tokens sit near a key of their first routed expert
+    kb = mgr.keys_buffer
+    near = torch.rand(n, device=dev) < 0.5
+    src = kb[sel[:, 0], (~wl.is_vision).long(), torch.randint(0, 256, (n,), device=dev)].float()
+    p_v, p_t = mgr.pca["vision"]["proj"].float(), mgr.pca["text"]["proj"].float()
+    lift = torch.where(wl.is_vision[:, None], src @ p_v.T, src @ p_t.T) * 4.0
+    x = torch.where(near[:, None], (wl.x.float() * 0.2 + lift), wl.x.float()).to(torch.bfloat16)
+    reuse_frac = float(reuse.float().mean())
+
+    def prefill():
+        eng.search_prefill_offline(0, x, sel, wl.is_vision, reuse)
+
+    g = graph_of(prefill)
+    prefill_us = statistics.median(replay_times_us(g, replays))
+    del g
+    hit, _ = eng.search_prefill_offline(0, x, sel, wl.is_vision, reuse)
+    q = eng.prefill_query_workspace[:n]
+    ho = torch.empty(n, k, dtype=torch.bool, device=dev)
+    io = torch.empty(n, k, dtype=torch.long, device=dev)
+    g = graph_of(lambda: eng._search_prefill_offline_into(q, sel, wl.is_vision, reuse, ho, io))
+    gated_us = statistics.median(replay_times_us(g, replays))
+    del g
+    hit_frac = float(hit.float().sum() / reuse.float().sum())
+    # decode bs1 hybrid (keep_k 4 of top-8, full 64-entry online window), 64 calls per graph
+    outs = [torch.empty(k, dtype=torch.bool, device=dev), torch.empty(1, dtype=torch.long, device=dev),
+            torch.empty(k, dtype=torch.bool, device=dev), torch.empty(k, dtype=torch.long, device=dev),
+            torch.empty(k, dtype=torch.long, device=dev)]
+    xs = x[:64]
+
+    def decode():
+        for i in range(64):
+            eng.search_decode_hybrid_bs1_into(xs[i], sel[i], wl.is_vision[i], 4, *outs)
+
+    g = graph_of(decode)
+    dec_us = statistics.median(replay_times_us(g, replays)) / 64
+    del g
+    pairs = int(reuse.sum().item())
+    table_bytes = 128 * 2 * 256 * 64 * 2
+    log(f"mode R: search_prefill_offline {prefill_us:.1f} us (gated search {gated_us:.1f} us, {pairs} pairs), "
+        f"decode bs1 hybrid {dec_us:.2f} us")
+    return {
+        "workload": "mode R (the reference's per-(expert, modality) tables) at Qwen3-VL-30B-A3B shapes: E=128 x 2 "
+                    "modalities x K=256 centroids, d=64, hidden 2048 bf16, N=4096 (3584 vision + 512 text), top-8; "
+                    "reuse = slots of experts outside the top 60 % by importance",
+        "reuse_frac": reuse_frac, "searched_pairs": pairs, "hit_frac": hit_frac,
+        "search_prefill_offline_us": prefill_us, "gated_search_us": gated_us,
+        "gated_pairs_per_s": pairs / (gated_us * 1e-6),
+        "gated_table_GBps": table_bytes / (gated_us * 1e-6) / 1e9,
+        "search_decode_hybrid_bs1_us": dec_us,
+    }
+
+
+# --------------------------------------------------------------------------- CPU baseline
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baselines(budget_s=30.0):
+    """The torch-CPU restatement of the reference fallback path (oracle/
+    tm_cpu_ref.py) on this host's cores, fp32 (the CPU's native precision;
+    the model dtype would be slower there), median of >= 10 runs after 2
+    warm-ups, per configuration; the config-4 and config-5 entries time a
+    bounded sample (stated in each)."""
+    import torch
+
+    from oracle import tm_cpu_ref as R
+    from synth import make_stack, make_workload
+
+    cores = len(os.sched_getaffinity(0))
+    threads = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores) or cores))
+    torch.set_num_threads(threads)
+    per_config_budget = budget_s / 6
+
+    def timed(fn, min_runs=10):
+        for _ in range(2):
+            fn()
+        ts = []
+        t_all = time.perf_counter()
+        while len(ts) < min_runs or (time.perf_counter() - t_all < per_config_budget and len(ts) < 50):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts), len(ts)
+
+    def f32(wl):
+        kw = {k: (v.float() if isinstance(v, torch.Tensor) and v.is_floating_point() else v)
+              for k, v in wl.__dict__.items()}
+        return type(wl)(**kw)
+
+    def layer(w, nn, kr, shared=None):
+        return lambda: R.layer_forward_g(w.x, w.is_vision, (w.proj_vis, w.bias_vis), (w.proj_txt, w.bias_txt),
+                                         w.centroids, w.values, w.logits, w.slot_out, w.residual,
+                                         w.cfg["router_top_k"], nn, kr, shared)
+
+    out = {}
+    w1 = f32(make_workload(1))
+    t, runs = timed(layer(w1, 1, 0.6))
+    out["config1"] = {"us_per_layer": t * 1e6, "tokens_per_s": 256 / t, "runs": runs, "sample": "full layer"}
+    log(f"cpu config 1: {t * 1e6:.0f} us/layer")
+    w2 = f32(make_workload(2))
+    t, runs = timed(layer(w2, 1, 0.6))
+    out["config2"] = {"us_per_layer": t * 1e6, "tokens_per_s": 4096 / t, "runs": runs, "sample": "full layer"}
+    log(f"cpu config 2: {t * 1e6:.0f} us/layer")
+    del w2
+    w3 = f32(make_workload(3, n=32))
+    for n in (1, 8, 32):
+        wn = type(w3)(**{k: (v[:n] if isinstance(v, torch.Tensor) and v.shape[:1] == (32,) else v)
+                         for k, v in w3.__dict__.items()})
+        t, runs = timed(layer(wn, 4, 0.6))
+        out[f"config3_N{n}"] = {"us_per_layer": t * 1e6, "tokens_per_s": n / t, "runs": runs, "sample": "full layer"}
+    log(f"cpu config 3 N=32: {out['config3_N32']['us_per_layer']:.0f} us/layer")
+    stack = [f32(w) for w in make_stack(2, device="cpu", gen_device="cpu")]
+    rows = []
+    for kr in KEEP_RATES:
+        t, runs = timed(lambda: [layer(w, 1, kr)() for w in stack])
+        rows.append({"keep_rate": kr, "us_per_layer": t * 1e6 / len(stack), "tokens_per_s": 2048 * len(stack) / t,
+                     "runs": runs})
+    out["config4"] = {"sample": "2 of the 48 layers per keep_rate (every layer does the same work)",
+                      "keep_rates": rows}
+    log(f"cpu config 4 keep 0.5: {rows[2]['us_per_layer']:.0f} us/layer")
+    del stack
+    ns = 512
+    w5 = f32(make_workload(5, n=ns))
+    g = torch.Generator().manual_seed(55)
+    e, h, inter = 64, 2560, 1536
+    ws = [torch.randn(*s, generator=g) * 0.02 for s in ((e, inter, h), (e, inter, h), (e, h, inter))]
+    sh = [torch.randn(*s, generator=g) * 0.02 for s in ((2 * inter, h), (2 * inter, h), (h, 2 * inter))]
+
+    def layer5():
+        shared = R.swiglu(w5.x, *sh)
+        first = R.layer_forward_g(w5.x, w5.is_vision, (w5.proj_vis, w5.bias_vis), (w5.proj_txt, w5.bias_txt),
+                                  w5.centroids, w5.values, w5.logits, w5.slot_out, w5.residual, 6, 1, 0.6, shared)
+        R.recompute_slots(w5.x, first["ids"], first["keep"], *ws, w5.slot_out)
+
+    t, runs = timed(layer5)
+    out["config5"] = {"us_per_layer_sample": t * 1e6, "tokens_per_s": ns / t, "runs": runs,
+                      "sample": f"{ns} of the 4096 tokens: search + combine, per-expert recompute of the kept slots "
+                                f"and the shared experts (the per-token work of the full layer)"}
+    log(f"cpu config 5 ({ns} tokens): {t * 1e3:.1f} ms")
+    return {"threads": threads, "cores": cores, "cpu_model": cpu_model(), "dtype": "f32",
+            "op_order": "torch-CPU restatement of the reference fallback (oracle/tm_cpu_ref.py): softmax+topk -> "
+                        "addmm projection -> addmm distances + min/topk -> keep count -> fancy-index gather -> "
+                        "renormalise -> bmm combine (+ residual)",
+            "timing": "median of >= 10 runs after 2 warm-ups", **out}
+
+
+# --------------------------------------------------------------------------- main
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sections", default=",".join(SECTIONS),
+                    help=f"comma-separated subset of {SECTIONS} (the headline config 2 always runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the table-search path runs on a single device in this build "
               "(multi-GPU sharding is a design note only); run with --gpus 1", file=sys.stderr)
         return 2
+    sections = {s.strip() for s in args.sections.split(",") if s.strip()}
+    if args.no_cpu:
+        sections.discard("cpu")
 
     import torch
 
@@ -408,18 +697,13 @@ def main() -> int:
     torch.cuda.set_device(0)
     log(f"device {torch.cuda.get_device_name(0)}")
 
-    pre = run_layer_bench(2, args.steps, args.warmup)
-    log(f"prefill: {pre['ms_per_step'] * 1000:.1f} us/layer (graph), {pre['eager_ms_per_step'] * 1000:.1f} eager, "
-        f"stages {json.dumps(pre['stage_us'])}")
-    dec = run_layer_bench(3, args.steps, args.warmup, n=32)
-    log(f"decode N=32: {dec['ms_per_step'] * 1000:.1f} us/layer (graph), {dec['eager_ms_per_step'] * 1000:.1f} eager, "
-        f"stages {json.dumps(dec['stage_us'])}")
-
+    pre = run_prefill(args.steps, args.warmup)
     cfg = pre["cfg"]
     N, C, d = cfg["n"], cfg["n_cent"], cfg["dim"]
     st, by, ku = pre["stage_us"], pre["bytes"], pre["kernel_us"]
-    log(f"prefill per-call device times (graph of 32 calls): {json.dumps({k: round(v, 2) for k, v in ku.items()})}")
-    # dominant kernel (longest average call) and its roofline
+    log(f"prefill: {pre['graph_us']:.1f} us/layer (graph, wall), {pre['median_us']:.1f} median device, "
+        f"{pre['eager_us']:.1f} eager; calls {json.dumps({k: round(v, 2) for k, v in ku.items()})}")
+    # dominant call of the layer (longest average call) and its roofline
     dom = max(ku, key=ku.get)
     ranked = ranked_layer(N, cfg["n_nearest"], cfg["router_top_k"], cfg["hidden"])
     entry = {"combine": "tm_gather_combine_ranked" if ranked else "tm_gather_combine", "project": "tm_project",
@@ -438,18 +722,15 @@ def main() -> int:
                             if dom == "combine" and ranked else None),
                 "algorithmic_per_launch": by[dom]}
     roof["avg_launch_us"] = ku[dom]
-
-    total_bytes = sum(by.values())
-    ds = dec["stage_us"]
     search_tflops = 2.0 * N * C * d / (ku["search"] * 1e-6) / 1e12
     result = {
         "metric": METRIC,
-        "value": N / (pre["ms_per_step"] * 1e-3),
+        "value": N / (pre["graph_us"] * 1e-6),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": pre["ms_per_step"],
+        "ms_per_step": pre["graph_us"] / 1000.0,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -462,39 +743,40 @@ def main() -> int:
             "tokens": N, "centroids": C, "pca_dim": d, "hidden": cfg["hidden"], "n_keep": pre["n_keep"],
             "replicas": N_REPLICAS,
         },
+        "timing": "ms_per_step: exactly `steps` layers replayed from HIP graphs of four consecutive layers (one "
+                  "tm_table_forward per table replica), wall clock; layer_us_median: median over 128 layers (32 "
+                  "individually timed replays); eager_us_per_layer: one C-ABI call per layer from Python",
+        "layer_us_median": pre["median_us"],
+        "layer_device_us_mean": pre["graph_device_us"],
+        "eager_us_per_layer": pre["eager_us"],
         "stages_us": {k: round(v, 2) for k, v in st.items()},
         "calls_us": {k: round(v, 2) for k, v in ku.items()},
-        "timing": "ms_per_step: layers replayed from one HIP graph of four consecutive layers (one "
-                  "tm_table_forward per replica); eager_ms_per_step: one tm_table_forward call per layer "
-                  "from Python",
-        "eager_ms_per_step": pre["eager_ms_per_step"],
-        "eager_tokens_per_s": N / (pre["eager_ms_per_step"] * 1e-3),
-        "layer_device_us": pre["graph_device_us"],
-        "layer_hbm_GBps": total_bytes / (pre["graph_device_us"] * 1e-6) / 1e9,
+        "layer_hbm_GBps": sum(by.values()) / (pre["median_us"] * 1e-6) / 1e9,
         "search_mfma_tflops": search_tflops,
         "search_mfma_frac": search_tflops / BF16_PEAK_TFLOPS,
+        "project_hbm_frac": by["project"] / (ku["project"] * 1e-6) / 1e9 / HBM_PEAK_GBPS,
         "roofline": roof,
-        "decode": {
-            "workload": "config 3: N=32 text tokens, C=16384 x 128 bf16, cached outputs 16384x2048, top-4 "
-                        "inverse-distance blend, keep_rate 0.6",
-            "us_per_layer": dec["ms_per_step"] * 1000.0,
-            "eager_us_per_layer": dec["eager_ms_per_step"] * 1000.0,
-            "layer_device_us": dec["graph_device_us"],
-            "tokens_per_s": 32 / (dec["ms_per_step"] * 1e-3),
-            "stages_us": {k: round(v, 2) for k, v in ds.items()},
-            "calls_us": {k: round(v, 2) for k, v in dec["kernel_us"].items()},
-            "search_hbm_GBps": dec["bytes"]["search"] / (dec["kernel_us"]["search"] * 1e-6) / 1e9,
-            "layer_hbm_GBps": sum(dec["bytes"].values()) / (dec["graph_device_us"] * 1e-6) / 1e9,
-        },
     }
-    rec = run_recompute_bench(args.steps, args.warmup)
-    log(f"config 5 recompute: routed {rec['routed_us']:.1f} us ({rec['routed_tflops']:.0f} TFLOP/s), shared "
-        f"{rec['shared_us']:.1f} us ({rec['shared_tflops']:.0f} TFLOP/s)")
-    result["recompute"] = rec
+    del pre
+    torch.cuda.empty_cache()
+    runners = {"decode": run_decode, "config1": run_config1, "config4": run_config4, "config5": run_config5,
+               "mode_r": run_mode_r}
+    for name, fn in runners.items():
+        if name in sections:
+            result[name] = fn()
+            torch.cuda.empty_cache()
     copy_calibration()
-    if not args.no_cpu:
+    if "cpu" in sections:
         log("timing the CPU baseline")
-        result["cpu_baseline"] = cpu_baseline(pre["wl"])
+        cpu = cpu_baselines()
+        c2 = cpu["config2"]
+        result["cpu_baseline"] = {
+            "value": c2["tokens_per_s"], "unit": "tokens/s", "cores": cpu["threads"], "kind": "port",
+            "sample": f"config 2 full layer (4096 tokens, all 8192 centroids), torch-CPU fp32 restatement of the "
+                      f"reference fallback, median of {c2['runs']} runs after 2 warm-ups, {cpu['threads']} threads on "
+                      f"{cpu['cores']} cores ({cpu['cpu_model']})",
+        }
+        result["cpu"] = cpu
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

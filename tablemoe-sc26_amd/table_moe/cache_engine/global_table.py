@@ -70,6 +70,14 @@ class GlobalTable:
             bias_txt=N.ptr(self.bias[1]), ps_h=self.ps[0], ps_d=self.ps[1])
 
     # --------------------------------------------------------------- buffers
+    def _out_buf(self, n, residual):
+        """The pooled output buffer, or its twin when ``residual`` is the
+        pooled buffer itself (chained calls: y = layer_forward(..., y))."""
+        out = self._buf("out", (n, self.hidden), self.dtype)
+        if residual is not None and residual.data_ptr() == out.data_ptr():
+            out = self._buf("out_alt", (n, self.hidden), self.dtype)
+        return out
+
     def _buf(self, name, shape, dtype):
         t = self._bufs.get(name)
         numel = 1
@@ -132,7 +140,7 @@ class GlobalTable:
         N.require_hip(keep, slot_out, weights, idx)
         n, top_k = weights.shape
         if out is None:
-            out = self._buf("out", (n, self.hidden), self.dtype)
+            out = self._out_buf(n, residual)
         so = slot_out
         N.call("tm_gather_combine", N.dtype_tag(self.dtype), n, self.hidden, N.ptr(N.as_u8(keep)), N.ptr(so),
                so.stride(0), so.stride(1), N.ptr(weights), weights.stride(0), top_k, N.ptr(self.values),
@@ -149,7 +157,7 @@ class GlobalTable:
         N.require_hip(slot_out, weights, idx, dist)
         n, top_k = weights.shape
         if out is None:
-            out = self._buf("out", (n, self.hidden), self.dtype)
+            out = self._out_buf(n, residual)
         if keep is None:
             keep = self._buf("keep", (n,), torch.bool)
         d = dist.reshape(-1) if dist.dim() > 1 else dist
@@ -198,7 +206,7 @@ class GlobalTable:
             slot_out = slot_out.contiguous()
         n = x.shape[0]
         if combine and out is None:
-            out = self._buf("out", (n, self.hidden), self.dtype)
+            out = self._out_buf(n, residual)
         if not combine:
             slot_out = residual = out = None
         w = self._buf("route_w", (n, router_top_k), torch.float32)

@@ -31,7 +31,9 @@ def build_fixed_keep_mask(selected_experts: torch.Tensor, keep_k: int | None) ->
 
 
 def _workspace(device, nbytes):
-    key = device
+    # one scratch buffer per (device, stream): calls enqueued on different
+    # streams must not share it
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
     ws = _ws_cache.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
