@@ -463,40 +463,6 @@ def run_config5(replays=10):
 
 
 # --------------------------------------------------------------------------- mode R
-def mode_r_setup(dev, E=128, H=2048, d=64, K=256, seed=7):
-    """A HybridStorageManager of the reference's default shape (128 experts x
-    2 modalities x 256 centroids in 64-d, hidden 2048) filled on the device:
-    random keys (normalised copy as the loader makes it), cached outputs, PCA
-    pairs, a full 64-entry online window."""
-    import torch
-
-    from table_moe.cache_engine import CacheConfig, HybridStorageManager
-    from table_moe.cache_engine.table_file import normalize_last_dim
-
-    saved = {k: getattr(CacheConfig, k) for k in ("FIXED_K", "COMPRESSED_DIM", "MODEL_DTYPE", "ONLINE_CACHE_SIZE",
-                                                  "ONLINE_TOP_K")}
-    CacheConfig.FIXED_K, CacheConfig.COMPRESSED_DIM, CacheConfig.MODEL_DTYPE = K, d, torch.bfloat16
-    CacheConfig.ONLINE_CACHE_SIZE, CacheConfig.ONLINE_TOP_K = 64, 8
-    try:
-        mgr = HybridStorageManager(2, E, H, dev)
-    finally:
-        for k_, v in saved.items():
-            setattr(CacheConfig, k_, v)
-    g = torch.Generator(device=dev).manual_seed(seed)
-    raw = torch.randn(E, 2, K, d, generator=g, device=dev)
-    mgr.raw_keys_buffer.copy_(raw.to(torch.bfloat16))
-    mgr.keys_buffer.copy_(normalize_last_dim(raw, 1e-6).to(torch.bfloat16))
-    mgr.values_buffer.copy_(torch.randn(E, 2, K, H, generator=g, device=dev).to(torch.bfloat16))
-    for mod in ("vision", "text"):
-        p = torch.linalg.qr(torch.randn(H, d, generator=g, device=dev, dtype=torch.float32))[0]
-        mgr.pca[mod] = {"proj": p.to(torch.bfloat16), "bias": (torch.randn(d, generator=g, device=dev) * 0.05)
-                        .to(torch.bfloat16)}
-    hist = torch.randn(64, H, generator=g, device=dev).to(torch.bfloat16)
-    ids = torch.stack([torch.randperm(E, device=dev)[:8] for _ in range(64)])
-    mgr.update_online_cache(hist, ids, torch.randn(64, 8, H, generator=g, device=dev).to(torch.bfloat16))
-    return mgr
-
-
 def run_mode_r(replays=20):
     """The reference's own semantics at Qwen3-VL-30B-A3B shapes:
     search_prefill_offline (N=4096, top-8 of 128 experts, reuse = the slots of
@@ -504,13 +470,13 @@ def run_mode_r(replays=20):
     search, as replayed HIP graphs."""
     import torch
 
-    from synth import make_workload
+    from synth import make_mode_r_manager, make_workload
     from table_moe.cache_engine import VectorSearchEngine
     from table_moe.ops import qwen_topk_softmax
     from table_moe.skip import build_prefill_keep_mask
 
     dev = torch.device("cuda:0")
-    mgr = mode_r_setup(dev)
+    mgr = make_mode_r_manager(dev)
     eng = VectorSearchEngine(mgr)
     wl = make_workload(2, with_slot_out=False, device=dev, gen_device=dev)
     n, k = wl.x.shape[0], 8

@@ -160,10 +160,13 @@ int tm_search_gated(int32_t dtype, const void *q_low, int64_t n_tokens, int64_t 
  * Slots that are not online hits are searched offline with the raw
  * projection q = dtype(x @ P_m + bias_m) against keys with hit = max >= 0.
  * All outputs are written for every (b, s): on_hit/off_hit 0, on_slot/off_idx
- * 0, on_idx -1 where nothing was found.
- * workspace: >= n_tokens * dim * sizeof(dtype) bytes (the projected queries).
+ * 0, on_idx -1 where nothing was found.  q_out (nullable, row stride
+ * ld_q_out) receives the projected queries when any slot is searched.
+ * workspace: >= tm_search_hybrid_workspace_size(n_tokens, hidden, dim) bytes
+ * (16-byte aligned): fp32 projection partials and window scores.
  * Limits: n_online_valid <= 1024, online_topk <= 64, dim <= 256.
  * ====================================================================== */
+size_t tm_search_hybrid_workspace_size(int64_t n_tokens, int32_t hidden, int32_t dim);
 int tm_search_hybrid(int32_t dtype, const void *x, int64_t n_tokens, int32_t hidden, int64_t ld_x,
                      const uint8_t *is_vision, const void *proj_vis, const void *bias_vis,
                      const void *proj_txt, const void *bias_txt, int64_t ps_h, int64_t ps_d,
@@ -173,7 +176,8 @@ int tm_search_hybrid(int32_t dtype, const void *x, int64_t n_tokens, int32_t hid
                      int64_t ks_m, int64_t ks_c, const int64_t *sel, int32_t top_k, int64_t ss_b,
                      int64_t ss_s, int32_t keep_k, uint8_t *on_hit, int64_t *on_idx,
                      uint8_t *off_hit, int64_t *off_idx, int64_t *on_slot, int64_t os_b,
-                     int64_t os_s, void *workspace, size_t workspace_bytes, tm_stream_t stream);
+                     int64_t os_s, void *q_out, int64_t ld_q_out, void *workspace, size_t workspace_bytes,
+                     tm_stream_t stream);
 
 /* ======================================================================
  * a3 -- keep masks.

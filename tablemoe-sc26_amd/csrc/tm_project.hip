@@ -53,6 +53,27 @@ ProjPlan plan_project(int64_t n, int hidden) {
   return p;
 }
 
+// Split plan of the fp32 kernel (its vector-unit k loop is slower per
+// element than the matrix cores, so small batches split hidden further):
+// up to 32 chunks of at least 64, with partials of at most 4 MiB unless the
+// 16-bit plan's are larger.
+ProjPlan plan_project_f32(int64_t n, int hidden, int dim) {
+  ProjPlan p;
+  p.row_blocks = tm_cdiv(n, kBM);
+  const int ksteps = (int)tm_cdiv(hidden, kBK);
+  int64_t want = tm_cdiv(1024, p.row_blocks);
+  if (want > 32) want = 32;
+  int64_t cap = (int64_t)(4u << 20) / (n * (int64_t)dim * 4);
+  const int64_t s16 = plan_project(n, hidden).nsplit;
+  if (cap < s16) cap = s16;
+  if (want > cap) want = cap;
+  if (want > ksteps) want = ksteps;
+  if (want < 1) want = 1;
+  p.k_chunk = (int)tm_cdiv(ksteps, want) * kBK;
+  p.nsplit = (int)tm_cdiv(hidden, p.k_chunk);
+  return p;
+}
+
 // Row epilogue shared by the fused kernel and the split epilogue: one row is
 // handled by TPR consecutive lanes, 8 columns each.  v[] holds the rounded
 // pre-normalisation values.
@@ -723,6 +744,126 @@ __global__ __launch_bounds__(kThreads) void project_epilogue_kernel(
                       (ok && part == 0 && q_sqnorm) ? q_sqnorm + r : nullptr);
 }
 
+// fp32 path (DIM in {32, 64, 128, 256}): fp32 FMAs on the vector units.  A
+// workgroup owns kBM rows and all DIM columns over one k chunk of the split
+// plan and writes fp32 partials [split][n][DIM] (summed in split order by
+// project_epilogue_kernel, which also adds the bias, rounds and normalises).
+// k advances 32 at a time through LDS: the x tile [kBM][32] and the P tile
+// [32][DIM] of each modality present in the tile, loaded along whichever of
+// P's axes is contiguous.  Thread (row group, column group) accumulates RPT
+// rows x 4 columns, each output a sequential sum over its k chunk.
+template <int DIM>
+__global__ __launch_bounds__(kThreads) void project_f32_kernel(
+    const float *__restrict__ x, int64_t n, int hidden, int64_t ld_x, const uint8_t *__restrict__ is_vision,
+    const float *__restrict__ pv, const float *__restrict__ pt, int64_t ps_h, int64_t ps_d, int k_chunk,
+    float *__restrict__ partial) {
+  constexpr int KT = 32;
+  constexpr int CG = DIM / 4;           // column groups of 4
+  constexpr int RG = kThreads / CG;     // row groups
+  constexpr int RPT = kBM / RG;         // rows per thread
+  static_assert(RPT >= 1 && RG * RPT == kBM, "tile shape");
+  __shared__ float xs[kBM][KT + 1];
+  __shared__ float4 ps[2][KT][CG];
+  __shared__ int s_mods;
+  const int tid = threadIdx.x;
+  const int cg = tid % CG, rg = tid / CG;
+  const int64_t r0 = (int64_t)blockIdx.x * kBM;
+  const int k0 = blockIdx.y * k_chunk;
+  const int k1 = k0 + k_chunk < hidden ? k0 + k_chunk : hidden;
+  if (tid == 0) s_mods = 0;
+  __syncthreads();
+  if (tid < kBM) {
+    const int64_t r = r0 + tid;
+    if (r < n) atomicOr(&s_mods, (is_vision == nullptr || is_vision[r]) ? 1 : 2);
+  }
+  __syncthreads();
+  const int mods = s_mods;  // bit 0: a vision row, bit 1: a text row
+  int mrow[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int64_t r = r0 + rg * RPT + i;
+    mrow[i] = (r < n && is_vision != nullptr && !is_vision[r]) ? 1 : 0;
+  }
+  float acc[RPT][4];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[i][c] = 0.f;
+  // Tile kb's operands are loaded into registers one tile ahead (the loads
+  // of tile kb + KT are in flight while tile kb is multiplied).
+  constexpr int XE = kBM * KT / kThreads;  // x elements per thread per tile
+  constexpr int PE = KT * DIM / kThreads;  // P elements per thread per tile and modality
+  float xr[XE], pr[2][PE];
+  auto load = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < XE; ++u) {
+      const int e = tid + u * kThreads, row = e / KT, kk = e % KT;
+      const int64_t r = r0 + row;
+      xr[u] = (r < n && kb + kk < k1) ? x[r * ld_x + kb + kk] : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      if (!(mods & (1 << m))) continue;  // uniform
+      const float *P = m == 0 ? pv : pt;
+#pragma unroll
+      for (int u = 0; u < PE; ++u) {
+        const int e = tid + u * kThreads;
+        int kk, j;
+        if (ps_d == 1) { kk = e / DIM; j = e % DIM; }  // row-major [hidden, DIM]: contiguous along j
+        else { j = e / KT; kk = e % KT; }              // k-contiguous copy: contiguous along h
+        const int h = kb + kk;
+        pr[m][u] = h < k1 ? P[(int64_t)h * ps_h + (int64_t)j * ps_d] : 0.f;
+      }
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int u = 0; u < XE; ++u) {
+      const int e = tid + u * kThreads;
+      xs[e / KT][e % KT] = xr[u];
+    }
+    float *psf = reinterpret_cast<float *>(ps);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      if (!(mods & (1 << m))) continue;
+#pragma unroll
+      for (int u = 0; u < PE; ++u) {
+        const int e = tid + u * kThreads;
+        int kk, j;
+        if (ps_d == 1) { kk = e / DIM; j = e % DIM; }
+        else { j = e / KT; kk = e % KT; }
+        psf[(m * KT + kk) * DIM + j] = pr[m][u];
+      }
+    }
+  };
+  if (k0 < k1) load(k0);
+  for (int kb = k0; kb < k1; kb += KT) {
+    __syncthreads();  // the previous tile's reads are done
+    stash();
+    __syncthreads();
+    if (kb + KT < k1) load(kb + KT);
+#pragma unroll 8
+    for (int kk = 0; kk < KT; ++kk) {
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const float xv = xs[rg * RPT + i][kk];
+        const float4 pw = ps[mrow[i]][kk][cg];
+        acc[i][0] = fmaf(xv, pw.x, acc[i][0]);
+        acc[i][1] = fmaf(xv, pw.y, acc[i][1]);
+        acc[i][2] = fmaf(xv, pw.z, acc[i][2]);
+        acc[i][3] = fmaf(xv, pw.w, acc[i][3]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int64_t r = r0 + rg * RPT + i;
+    if (r < n)
+      *reinterpret_cast<float4 *>(partial + ((int64_t)blockIdx.y * n + r) * DIM + 4 * cg) =
+          make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+  }
+}
+
 // Generic path (any dtype, dim <= 256): one thread per output element,
 // sequential fp32 accumulation over hidden.  Every thread reaches every
 // barrier; inactive threads carry zeros.
@@ -873,6 +1014,34 @@ int launch_project(const void *x, int64_t n, int hidden, int64_t ld_x, const uin
     }
   }
   }
+  if constexpr (DT == TM_DT_F32) {
+    const ProjPlan pl = plan_project_f32(n, hidden, dim);
+    const size_t need = (size_t)pl.nsplit * (size_t)n * (size_t)dim * sizeof(float);
+    const bool tiled = (dim == 32 || dim == 64 || dim == 128 || dim == 256) && !packed && workspace != nullptr &&
+                       workspace_bytes >= need && tm_aligned16(workspace) && tm_aligned16(q) && (ld_q % 4) == 0;
+    if (tiled) {
+      float *partial = static_cast<float *>(workspace);
+      const dim3 grid((unsigned)pl.row_blocks, (unsigned)pl.nsplit);
+      switch (dim) {
+#define TM_PROJ_F32(D)                                                                                         \
+  case D:                                                                                                      \
+    hipLaunchKernelGGL((project_f32_kernel<D>), grid, dim3(kThreads), 0, stream, X, n, hidden, ld_x, is_vision, \
+                       PV, PT, ps_h, ps_d, pl.k_chunk, partial);                                                \
+    TM_LAUNCH_CHECK("tm_project");                                                                             \
+    hipLaunchKernelGGL((project_epilogue_kernel<DT, D>), dim3((unsigned)tm_cdiv(n, kThreads / (D / 8))),        \
+                       dim3(kThreads), 0, stream, partial, pl.nsplit, n, is_vision, BV, BT, normalize, eps, Q,  \
+                       ld_q, q_sqnorm);                                                                         \
+    TM_LAUNCH_CHECK("tm_project(epilogue)");                                                                   \
+    return TM_OK;
+        TM_PROJ_F32(32)
+        TM_PROJ_F32(64)
+        TM_PROJ_F32(128)
+        TM_PROJ_F32(256)
+#undef TM_PROJ_F32
+        default: break;
+      }
+    }
+  }
   const int rows_per_block = kThreads / dim;
   dim3 grid((unsigned)tm_cdiv(n, rows_per_block)), block(kThreads);
   hipLaunchKernelGGL((project_scalar_kernel<DT>), grid, block, 0, stream, X, n, hidden, ld_x,
@@ -885,9 +1054,11 @@ int launch_project(const void *x, int64_t n, int hidden, int64_t ld_x, const uin
 
 extern "C" size_t tm_project_workspace_size(int64_t n_tokens, int32_t hidden, int32_t dim) {
   if (n_tokens <= 0 || hidden <= 0 || dim <= 0) return 0;
-  const ProjPlan pl = plan_project(n_tokens, hidden);
-  if (pl.nsplit <= 1) return 0;
-  return (size_t)pl.nsplit * (size_t)n_tokens * (size_t)dim * sizeof(float);
+  const int s16 = plan_project(n_tokens, hidden).nsplit;      // 16-bit operands, matrix cores
+  const int s32 = plan_project_f32(n_tokens, hidden, dim).nsplit;  // fp32 operands
+  const int ns = s16 > s32 ? s16 : s32;
+  if (ns <= 1) return 0;
+  return (size_t)ns * (size_t)n_tokens * (size_t)dim * sizeof(float);
 }
 
 extern "C" int tm_project(int32_t dtype, const void *x, int64_t n_tokens, int32_t hidden,

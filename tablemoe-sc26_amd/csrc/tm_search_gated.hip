@@ -6,9 +6,20 @@
 //   - tm_search_hybrid: the decode online-window + offline search with the
 //     projection fused (search.py:839-954, :987-1105, :778-806; Triton :258-385).
 //
-// Scores are fp32 sums in a fixed order; the arg-max keeps the first index
-// among equal maxima, as torch.max / tl.max(return_indices) do.
+// Scores are fp32 sums of the model-dtype products; the arg-max keeps the
+// first index among equal maxima, as torch.max / tl.max(return_indices) do.
+//
+// tm_search_gated runs gated_seg_kernel for 16-bit tables whose dimension is
+// a multiple of 16: the reference's grid is one program per (token, slot),
+// each streaming its whole 256 x 64 table (at Qwen prefill ~13k searched
+// pairs x 32 KiB); here the pairs that share a table are searched together.
+// A workgroup owns one expert and one chunk of tokens: it scans the chunk's
+// slots for that expert, compacts the searched pairs per modality into LDS,
+// and scores them 32 at a time on the matrix cores (v_mfma_f32_32x32x16:
+// A = 32 table rows, B = the 32 pairs' queries), its four waves splitting
+// the table's 32-row blocks; every table row is read once per 32 pairs.
 #include "tm_common.h"
+#include "tm_mfma.h"
 
 namespace {
 
@@ -24,6 +35,35 @@ __device__ __forceinline__ void wave_table_argmax(const typename Elem<DT>::T *ta
   const int lane = threadIdx.x & 63;
   best = -__builtin_huge_valf();
   best_i = 0x7fffffff;
+  if constexpr (VEC && Elem<DT>::kBytes == 2) {
+    if (dim == 64) {  // the reference's table width: a lane's rows in groups of 4, all of a group's loads in flight
+      for (int64_t c0 = lane; c0 < n_cent; c0 += 4 * 64) {
+        uint4 raw[4][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          int64_t c = c0 + 64 * u;
+          c = c < n_cent ? c : n_cent - 1;  // clamped in bounds; masked below
+          const uint4 *row = reinterpret_cast<const uint4 *>(table + c * ks_c);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) raw[u][t] = row[t];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int64_t c = c0 + 64 * u;
+          float acc = 0.f;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const typename Elem<DT>::T *e = reinterpret_cast<const typename Elem<DT>::T *>(&raw[u][t]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc = fmaf(qv[8 * t + i], Elem<DT>::to_f(e[i]), acc);
+          }
+          if (c < n_cent && acc > best) { best = acc; best_i = (int)c; }
+        }
+      }
+      tm_wave_argmax(best, best_i);
+      return;
+    }
+  }
   for (int64_t c = lane; c < n_cent; c += 64) {
     const typename Elem<DT>::T *row = table + c * ks_c;
     float acc = 0.f;
@@ -81,57 +121,328 @@ __global__ __launch_bounds__(kThreads) void gated_kernel(
   }
 }
 
-// Decode hybrid search: one workgroup per token.
-template <int DT, bool VEC>
-__global__ __launch_bounds__(kThreads) void hybrid_kernel(
-    const typename Elem<DT>::T *__restrict__ x, int hidden, int64_t ld_x, const uint8_t *__restrict__ is_vision,
-    const typename Elem<DT>::T *__restrict__ pv, const typename Elem<DT>::T *__restrict__ bv,
-    const typename Elem<DT>::T *__restrict__ pt, const typename Elem<DT>::T *__restrict__ bt, int64_t ps_h,
-    int64_t ps_d, int dim, const typename Elem<DT>::T *__restrict__ on_keys, int64_t ld_on, int n_valid,
-    const int64_t *__restrict__ on_ids, int on_topk, int64_t ld_on_ids,
+// ---------------------------------------------------------------------------
+// Segment-grouped gated search (16-bit tables, DIM % 16 == 0).
+// ---------------------------------------------------------------------------
+constexpr int kSegThreads = 256;
+constexpr int kSegList = 8192;  // pair slots per workgroup (LDS); tokens per chunk <= kSegList / top_k
+
+// REG: tables of at most 256 rows with DIM <= 128 -- each wave loads its
+// (at most two) 32-row blocks of every modality table that has pairs once,
+// right after the scan, and keeps them in registers for all pair blocks.
+template <int DT, int DIM, bool REG>
+__global__ __launch_bounds__(kSegThreads) void gated_seg_kernel(
+    const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
     const typename Elem<DT>::T *__restrict__ keys, int64_t n_exp, int64_t n_cent, int64_t ks_e, int64_t ks_m,
-    int64_t ks_c, const int64_t *__restrict__ sel, int top_k, int64_t ss_b, int64_t ss_s, int keep_k,
+    int64_t ks_c, const int64_t *__restrict__ sel, int top_k, int64_t ss_b, int64_t ss_s,
+    const uint8_t *__restrict__ is_vision, const uint8_t *__restrict__ reuse, int64_t rs_b, int64_t rs_s,
+    int col_offset, float thr_v, float thr_t, int cmp, uint8_t *__restrict__ out_hit,
+    int64_t *__restrict__ out_idx, int64_t os_b, int64_t os_s, int64_t tok_per_wg) {
+  using T = typename Elem<DT>::T;
+  constexpr int KS = DIM / 16;  // k-steps
+  __shared__ uint32_t list[kSegList];  // vision pairs from the front, text pairs from the back
+  __shared__ int cnt[2];
+  __shared__ float red_v[4][32];
+  __shared__ int red_i[4][32];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t e = blockIdx.x;
+  const int64_t b0 = (int64_t)blockIdx.y * tok_per_wg;
+  const int64_t b1 = b0 + tok_per_wg < n ? b0 + tok_per_wg : n;
+  if (tid < 2) cnt[tid] = 0;
+  __syncthreads();
+  // 1) scan: pairs routed to expert e (and, in expert 0's workgroups, pairs
+  // whose id is out of range); searched ones are listed, the rest written
+  // as (0, 0) here -- every pair is written by exactly one workgroup.  A
+  // thread takes tokens tid, tid + 256, ... and loads the slot ids of
+  // kScanTok of them (up to kScanSlots slots each) before testing any, so
+  // the loads are in flight together; pair p = token * top_k + slot.
+  constexpr int kScanTok = 4, kScanSlots = 8;
+  const int ntok = (int)(b1 - b0);
+  auto test_pair = [&](int bl, int s, int64_t ex) {
+    const bool valid = ex >= 0 && ex < n_exp;
+    if (ex == e || (!valid && e == 0)) {
+      const int64_t b = b0 + bl;
+      const bool searched = valid && s >= col_offset && (reuse == nullptr || reuse[b * rs_b + s * rs_s]);
+      if (searched) {
+        const int m = (is_vision == nullptr || is_vision[b]) ? 0 : 1;
+        const int pos = atomicAdd(&cnt[m], 1);
+        list[m == 0 ? pos : kSegList - 1 - pos] = (uint32_t)(bl * top_k + s);
+      } else {
+        const int64_t o = b * os_b + s * os_s;
+        out_hit[o] = 0;
+        out_idx[o] = 0;
+      }
+    }
+  };
+  for (int t0 = 0; t0 < ntok; t0 += kSegThreads * kScanTok) {
+    int64_t ex[kScanTok][kScanSlots];
+#pragma unroll
+    for (int u = 0; u < kScanTok; ++u) {
+      const int bl = t0 + u * kSegThreads + tid;
+      const int blc = bl < ntok ? bl : ntok - 1;
+#pragma unroll
+      for (int s = 0; s < kScanSlots; ++s) {
+        const int sc = s < top_k ? s : top_k - 1;
+        ex[u][s] = sel[(b0 + blc) * ss_b + sc * ss_s];  // clamped: every load is in bounds
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kScanTok; ++u) {
+      const int bl = t0 + u * kSegThreads + tid;
+      if (bl >= ntok) continue;
+#pragma unroll
+      for (int s = 0; s < kScanSlots; ++s)
+        if (s < top_k) test_pair(bl, s, ex[u][s]);
+      for (int s = kScanSlots; s < top_k; ++s) test_pair(bl, s, sel[(b0 + bl) * ss_b + s * ss_s]);
+    }
+  }
+  __syncthreads();
+  const int counts[2] = {cnt[0], cnt[1]};
+  // 2) search, 32 pairs of one modality at a time
+  auto row_ptr = [&](int m, int64_t cb) {
+    int64_t c = cb + (lane & 31);
+    c = c < n_cent ? c : n_cent - 1;  // rows past the table re-read its last row (masked below)
+    return keys + e * ks_e + m * ks_m + c * ks_c + 8 * (lane >> 5);
+  };
+  uint4 kreg[REG ? 2 : 1][REG ? 2 : 1][KS];
+  if constexpr (REG) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+      if (counts[m] > 0)  // uniform
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+          const T *krow = row_ptr(m, (int64_t)wave * 32 + bi * 128);
+#pragma unroll
+          for (int t = 0; t < KS; ++t) kreg[m][bi][t] = *reinterpret_cast<const uint4 *>(krow + 16 * t);
+        }
+  }
+  for (int m = 0; m < 2; ++m) {
+    const int c_m = counts[m];
+    for (int blk = 0; blk < c_m; blk += 32) {  // uniform
+      const int j = blk + (lane & 31);
+      const int jj = j < c_m ? j : blk;  // past the end: the block's first pair (result dropped)
+      const uint32_t p = list[m == 0 ? jj : kSegList - 1 - jj];
+      const T *qrow = q + (b0 + (int64_t)(p / (uint32_t)top_k)) * ld_q + 8 * (lane >> 5);
+      uint4 qf[KS];
+#pragma unroll
+      for (int t = 0; t < KS; ++t) qf[t] = *reinterpret_cast<const uint4 *>(qrow + 16 * t);
+      float best = -__builtin_huge_valf();
+      int best_i = 0x7fffffff;
+      auto score_block = [&](const uint4 (&kf)[KS], int64_t cb) {
+        tm_f32x16 acc{};
+#pragma unroll
+        for (int t = 0; t < KS; ++t) acc = tm_mfma32x32x16<DT>(kf[t], qf[t], acc);
+        // lane holds pair (lane % 32) against rows 8(i/4) + 4(lane/32) + i%4 of the block, ascending in i
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int64_t ci = cb + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+          if (ci < n_cent && acc[i] > best) {
+            best = acc[i];
+            best_i = (int)ci;
+          }
+        }
+      };
+      if constexpr (REG) {
+#pragma unroll
+        for (int bi = 0; bi < 2; ++bi) {
+          const int64_t cb = (int64_t)wave * 32 + bi * 128;
+          if (cb < n_cent) score_block(kreg[m][bi], cb);  // uniform per wave
+        }
+      } else {
+        for (int64_t cb = (int64_t)wave * 32; cb < n_cent; cb += 4 * 32) {  // uniform per wave
+          const T *krow = row_ptr(m, cb);
+          uint4 kf[KS];
+#pragma unroll
+          for (int t = 0; t < KS; ++t) kf[t] = *reinterpret_cast<const uint4 *>(krow + 16 * t);
+          score_block(kf, cb);
+        }
+      }
+      const float ov = __shfl_xor(best, 32, 64);  // lanes l and l ^ 32 hold the same pair
+      const int oi = __shfl_xor(best_i, 32, 64);
+      if (ov > best || (ov == best && oi < best_i)) {
+        best = ov;
+        best_i = oi;
+      }
+      if (lane < 32) {
+        red_v[wave][lane] = best;
+        red_i[wave][lane] = best_i;
+      }
+      __syncthreads();
+      if (wave == 0 && lane < 32 && j < c_m) {
+        float v = red_v[0][lane];
+        int bi = red_i[0][lane];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {  // waves hold interleaved blocks: ties go to the lower index
+          const float wv = red_v[w][lane];
+          const int wi = red_i[w][lane];
+          if (wv > v || (wv == v && wi < bi)) {
+            v = wv;
+            bi = wi;
+          }
+        }
+        const int64_t b = b0 + (int64_t)(p / (uint32_t)top_k);
+        const int s = (int)(p % (uint32_t)top_k);
+        const float thr = m == 0 ? thr_v : thr_t;
+        const bool hit = (cmp == TM_CMP_GE) ? (v >= thr) : (v > thr);
+        const int64_t o = b * os_b + s * os_s;
+        out_hit[o] = hit ? 1 : 0;
+        out_idx[o] = hit ? (int64_t)bi : 0;
+      }
+      __syncthreads();  // red_* are rewritten by the next block
+    }
+  }
+}
+
+// Tokens per workgroup chunk of gated_seg_kernel: about 512 workgroups over
+// the experts, at most kSegList / top_k tokens (the LDS pair list), at least
+// 64 tokens per chunk unless the batch is smaller.
+int64_t seg_tokens_per_wg(int64_t n, int64_t n_exp, int top_k) {
+  const int64_t cap = kSegList / top_k;
+  int64_t chunks = tm_cdiv(512, n_exp);
+  const int64_t by_size = tm_cdiv(n, 64);
+  chunks = chunks < by_size ? chunks : by_size;
+  if (chunks < 1) chunks = 1;
+  int64_t tok = tm_cdiv(n, chunks);
+  return tok < cap ? tok : cap;
+}
+
+// ---------------------------------------------------------------------------
+// Decode hybrid search, two launches.
+//  hybrid_partial_kernel: grid (token, slice): each workgroup stages the
+//    token's x in LDS, writes the fp32 projection partial of its slice of
+//    `hidden` (every column) and the online-window scores of its share of
+//    the window rows.
+//  hybrid_finish_kernel: one workgroup per token: q = dtype(sum of the slice
+//    partials in slice order + bias) (one rounding), the window arg-max and
+//    online hits, then the offline search of the remaining slots (one wave
+//    per slot) and every output.
+// Workspace: partials [n][G][dim] fp32, then window scores [n][kMaxOnline].
+// ---------------------------------------------------------------------------
+constexpr int kMaxOnline = 1024;
+constexpr int kHybRowsPerSlice = 128;
+constexpr int kHybMaxSlices = 16;
+
+inline int hybrid_slices(int hidden) {
+  int g = hidden / kHybRowsPerSlice;
+  return g < 1 ? 1 : (g > kHybMaxSlices ? kHybMaxSlices : g);
+}
+inline int hybrid_slice_rows(int hidden, int g) { return (int)(tm_cdiv(tm_cdiv(hidden, g), 8) * 8); }
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kThreads) void hybrid_partial_kernel(
+    const typename Elem<DT>::T *__restrict__ x, int hidden, int64_t ld_x, const uint8_t *__restrict__ is_vision,
+    const typename Elem<DT>::T *__restrict__ pv, const typename Elem<DT>::T *__restrict__ pt, int64_t ps_h,
+    int64_t ps_d, int dim, int slice_rows, int need_proj, const typename Elem<DT>::T *__restrict__ on_keys,
+    int64_t ld_on, int n_valid, float *__restrict__ partial, float *__restrict__ scores) {
+  using T = typename Elem<DT>::T;
+  extern __shared__ float xsh[];  // hidden floats
+  __shared__ float red[kThreads];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t b = blockIdx.x;
+  const int g = blockIdx.y, G = gridDim.y;
+  const T *xr = x + b * ld_x;
+  for (int h = tid; h < hidden; h += kThreads) xsh[h] = Elem<DT>::to_f(xr[h]);
+  __syncthreads();
+  // projection partial over rows [h0, h1) of this slice, every column
+  if (need_proj) {  // uniform
+    const bool vis = is_vision == nullptr || is_vision[b];
+    const T *P = vis ? pv : pt;
+    const int h0 = g * slice_rows;
+    const int h1 = h0 + slice_rows < hidden ? h0 + slice_rows : hidden;
+    const int parts = kThreads / dim;  // >= 1
+    const int col = tid % dim, part = tid / dim;
+    float acc = 0.f;
+    if (part < parts && h0 < h1) {
+      const int per = (h1 - h0 + parts - 1) / parts;
+      const int a0 = h0 + part * per;
+      const int a1 = a0 + per < h1 ? a0 + per : h1;
+      if (VEC && ps_h == 1) {  // k-contiguous copy: each thread's rows are one contiguous run
+        const T *src = P + (int64_t)col * ps_d;
+        int h = a0;
+        for (; h + 8 <= a1; h += 8) {
+          float v[8];
+          tm_load8<DT>(src + h, v);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc = fmaf(xsh[h + u], v[u], acc);
+        }
+        for (; h < a1; ++h) acc = fmaf(xsh[h], Elem<DT>::to_f(src[h]), acc);
+      } else {
+        for (int h = a0; h < a1; ++h)
+          acc = fmaf(xsh[h], Elem<DT>::to_f(P[(int64_t)h * ps_h + (int64_t)col * ps_d]), acc);
+      }
+    }
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < dim) {
+      float sum = 0.f;
+      for (int pp = 0; pp < parts; ++pp) sum += red[pp * dim + tid];  // parts in order
+      partial[((int64_t)b * G + g) * dim + tid] = sum;
+    }
+  }
+  // online scores of window rows g, g + G, ...: one wave per row
+  for (int j = g + G * wave; j < n_valid; j += G * (kThreads / 64)) {
+    const T *kr = on_keys + (int64_t)j * ld_on;
+    float acc = 0.f;
+    if (VEC) {
+      for (int h = 8 * lane; h + 8 <= hidden; h += 8 * 64) {
+        float v[8];
+        tm_load8<DT>(kr + h, v);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(xsh[h + u], v[u], acc);
+      }
+      for (int h = (hidden / 8) * 8 + lane; h < hidden; h += 64) acc = fmaf(xsh[h], Elem<DT>::to_f(kr[h]), acc);
+    } else {
+      for (int h = lane; h < hidden; h += 64) acc = fmaf(xsh[h], Elem<DT>::to_f(kr[h]), acc);
+    }
+    acc = tm_wave_sum(acc);
+    if (lane == 0) scores[(int64_t)b * kMaxOnline + j] = acc;
+  }
+}
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kThreads) void hybrid_finish_kernel(
+    const uint8_t *__restrict__ is_vision, const typename Elem<DT>::T *__restrict__ bv,
+    const typename Elem<DT>::T *__restrict__ bt, int dim, int n_slices, const float *__restrict__ partial,
+    const float *__restrict__ scores, int n_valid, const int64_t *__restrict__ on_ids, int on_topk,
+    int64_t ld_on_ids, const typename Elem<DT>::T *__restrict__ keys, int64_t n_exp, int64_t n_cent, int64_t ks_e,
+    int64_t ks_m, int64_t ks_c, const int64_t *__restrict__ sel, int top_k, int64_t ss_b, int64_t ss_s, int keep_k,
     uint8_t *__restrict__ on_hit, int64_t *__restrict__ on_idx, uint8_t *__restrict__ off_hit,
     int64_t *__restrict__ off_idx, int64_t *__restrict__ on_slot, int64_t os_b, int64_t os_s,
-    typename Elem<DT>::T *__restrict__ q_ws) {
-  using T = typename Elem<DT>::T;
-  extern __shared__ float xsh[];        // hidden floats
-  __shared__ float on_sc[1024];         // online scores
-  __shared__ float part[kThreads];      // projection partials
+    typename Elem<DT>::T *__restrict__ q_out, int64_t ld_q_out) {
   __shared__ float qsh[kMaxDim];
   __shared__ int s_jstar, s_valid_on;
   __shared__ uint8_t s_onhit[64];
   __shared__ int s_onslot[64];
-  __shared__ int s_need_offline;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t b = blockIdx.x;
   const bool vis = is_vision == nullptr || is_vision[b];
-  const T *xr = x + b * ld_x;
-  for (int h = tid; h < hidden; h += kThreads) xsh[h] = Elem<DT>::to_f(xr[h]);
-  if (tid == 0) s_need_offline = 0;
-  __syncthreads();
-
-  // 1) online window scores x . online_keys[j]
-  for (int j = wave; j < n_valid; j += kThreads / 64) {
-    const T *kr = on_keys + (int64_t)j * ld_on;
-    float acc = 0.f;
-    for (int h = lane; h < hidden; h += 64) acc = fmaf(xsh[h], Elem<DT>::to_f(kr[h]), acc);
-    acc = tm_wave_sum(acc);
-    if (lane == 0) on_sc[j] = acc;
+  const bool need_proj = keep_k < top_k;
+  // 1) q = dtype(sum of the slice partials + bias)
+  if (need_proj && tid < dim) {
+    float sum = 0.f;
+    for (int g = 0; g < n_slices; ++g) sum += partial[((int64_t)b * n_slices + g) * dim + tid];
+    const float v = tm_round<DT>(sum + Elem<DT>::to_f((vis ? bv : bt)[tid]));
+    qsh[tid] = v;
+    if (q_out != nullptr) q_out[b * ld_q_out + tid] = Elem<DT>::from_f(v);
   }
-  __syncthreads();
-  if (tid == 0) {
+  // 2) window arg-max (first index of the maximum), one wave
+  if (wave == 0) {
     float mx = -__builtin_huge_valf();
-    int js = -1;
-    for (int j = 0; j < n_valid; ++j)
-      if (on_sc[j] > mx) { mx = on_sc[j]; js = j; }
-    const int valid_on = (n_valid > 0 && mx > 0.f) ? 1 : 0;
-    s_jstar = js;
-    s_valid_on = valid_on;
-    on_idx[b] = valid_on ? js : -1;
+    int js = 0x7fffffff;
+    for (int j = lane; j < n_valid; j += 64) {
+      const float v = scores[(int64_t)b * kMaxOnline + j];
+      if (v > mx) { mx = v; js = j; }
+    }
+    tm_wave_argmax(mx, js);
+    if (lane == 0) {
+      const int valid_on = (n_valid > 0 && mx > 0.f) ? 1 : 0;
+      s_jstar = valid_on ? js : -1;
+      s_valid_on = valid_on;
+      on_idx[b] = valid_on ? js : -1;
+    }
   }
   __syncthreads();
-  // 2) online hits of the searched slots
+  // 3) online hits of the searched slots
   if (tid < top_k) {
     const int s = tid;
     uint8_t hit = 0;
@@ -145,59 +456,28 @@ __global__ __launch_bounds__(kThreads) void hybrid_kernel(
     }
     s_onhit[s] = hit;
     s_onslot[s] = slot;
-    if (s >= keep_k && !hit) atomicOr(&s_need_offline, 1);
   }
   __syncthreads();
-  // 3) raw projection q = dtype(x @ P_m + bias_m) (only if an offline search remains)
-  if (s_need_offline) {
-    const T *P = vis ? pv : pt;
-    const T *bias = vis ? bv : bt;
-    const int nparts = kThreads / dim;
-    const int col = tid % dim, p = tid / dim;
-    float acc = 0.f;
-    if (p < nparts) {
-      const int h0 = (int)(((int64_t)hidden * p) / nparts), h1 = (int)(((int64_t)hidden * (p + 1)) / nparts);
-      for (int h = h0; h < h1; ++h) acc = fmaf(xsh[h], Elem<DT>::to_f(P[(int64_t)h * ps_h + (int64_t)col * ps_d]), acc);
-    }
-    part[tid] = acc;
-    __syncthreads();
-    if (tid < dim) {
-      float sum = 0.f;
-      for (int pp = 0; pp < nparts; ++pp) sum += part[pp * dim + tid];
-      const float v = tm_round<DT>(sum + Elem<DT>::to_f(bias[tid]));
-      qsh[tid] = v;
-      q_ws[b * dim + tid] = Elem<DT>::from_f(v);
-    }
-    __syncthreads();
-    // 4) offline search of the remaining slots, one wave per slot
-    for (int s = keep_k + wave; s < top_k; s += kThreads / 64) {
-      if (s_onhit[s]) continue;
+  // 4) offline search of the remaining slots, one wave per slot; every output written
+  for (int s = wave; s < top_k; s += kThreads / 64) {
+    const int64_t o = b * os_b + s * os_s;
+    uint8_t hit = 0;
+    int64_t idx = 0;
+    if (s >= keep_k && !s_onhit[s]) {  // uniform per wave
       const int64_t e = sel[b * ss_b + s * ss_s];
-      uint8_t hit = 0;
-      int64_t idx = 0;
       if (e >= 0 && e < n_exp) {
         float best;
         int best_i;
-        wave_table_argmax<DT, VEC>(keys + e * ks_e + (vis ? 0 : 1) * ks_m, ks_c, n_cent, dim, qsh, best,
-                                   best_i);
+        wave_table_argmax<DT, VEC>(keys + e * ks_e + (vis ? 0 : 1) * ks_m, ks_c, n_cent, dim, qsh, best, best_i);
         hit = best >= 0.f;
         idx = hit ? best_i : 0;
       }
-      if (lane == 0) {
-        off_hit[b * os_b + s * os_s] = hit;
-        off_idx[b * os_b + s * os_s] = idx;
-      }
     }
-  }
-  // 5) the remaining outputs
-  if (tid < top_k) {
-    const int s = tid;
-    const int64_t o = b * os_b + s * os_s;
-    on_hit[o] = s_onhit[s];
-    on_slot[o] = s_onhit[s] ? s_onslot[s] : 0;
-    if (s < keep_k || s_onhit[s] || !s_need_offline) {
-      off_hit[o] = 0;
-      off_idx[o] = 0;
+    if (lane == 0) {
+      off_hit[o] = hit;
+      off_idx[o] = idx;
+      on_hit[o] = s_onhit[s];
+      on_slot[o] = s_onhit[s] ? s_onslot[s] : 0;
     }
   }
 }
@@ -223,6 +503,45 @@ extern "C" int tm_search_gated(int32_t dtype, const void *q_low, int64_t n_token
     const int E = Elem<DT>::kBytes;
     const bool vec = dim % 8 == 0 && tm_aligned16(keys) && (ks_e * E) % 16 == 0 && (ks_m * E) % 16 == 0 &&
                      (ks_c * E) % 16 == 0;
+    if constexpr (E == 2) {
+      const int64_t tok = top_k <= kSegList ? seg_tokens_per_wg(n_tokens, n_experts, top_k) : 0;
+      const int64_t chunks = tok > 0 ? tm_cdiv(n_tokens, tok) : 0;
+      const bool seg = vec && dim % 16 == 0 && tm_aligned16(q_low) && (ld_q * E) % 16 == 0 && tok > 0 &&
+                       chunks <= 65535 && n_experts <= 0x7fffffff && n_centroids < 0x7fffffff;
+      if (seg) {
+        const dim3 sgrid((unsigned)n_experts, (unsigned)chunks);
+        auto go = [&](auto dim_tag) {
+          constexpr int D = decltype(dim_tag)::value;
+          auto launch_seg = [&](auto reg_tag) {
+            constexpr bool R = decltype(reg_tag)::value;
+            hipLaunchKernelGGL((gated_seg_kernel<DT, D, R>), sgrid, dim3(kSegThreads), 0, tm_hip_stream(stream),
+                               static_cast<const T *>(q_low), n_tokens, ld_q, static_cast<const T *>(keys),
+                               n_experts, n_centroids, ks_e, ks_m, ks_c, sel, top_k, ss_b, ss_s, is_vision, reuse,
+                               rs_b, rs_s, col_offset, thr_vision, thr_text, cmp, out_hit, out_idx, os_b, os_s, tok);
+          };
+          if constexpr (D <= 128) {
+            if (n_centroids <= 256) {
+              launch_seg(std::true_type{});
+              return;
+            }
+          }
+          launch_seg(std::false_type{});
+        };
+        bool launched = true;
+        switch (dim) {
+          case 16: go(std::integral_constant<int, 16>{}); break;
+          case 32: go(std::integral_constant<int, 32>{}); break;
+          case 64: go(std::integral_constant<int, 64>{}); break;
+          case 128: go(std::integral_constant<int, 128>{}); break;
+          case 256: go(std::integral_constant<int, 256>{}); break;
+          default: launched = false;
+        }
+        if (launched) {
+          TM_LAUNCH_CHECK("tm_search_gated");
+          return TM_OK;
+        }
+      }
+    }
     dim3 grid((unsigned)tm_cdiv(pairs, kThreads / 64)), block(kThreads);
     auto launch = [&](auto vec_tag) {
       constexpr bool VEC = decltype(vec_tag)::value;
@@ -239,6 +558,11 @@ extern "C" int tm_search_gated(int32_t dtype, const void *q_low, int64_t n_token
   });
 }
 
+extern "C" size_t tm_search_hybrid_workspace_size(int64_t n_tokens, int32_t hidden, int32_t dim) {
+  if (n_tokens <= 0 || hidden <= 0 || dim <= 0) return 0;
+  return (size_t)n_tokens * ((size_t)hybrid_slices(hidden) * (size_t)dim + kMaxOnline) * sizeof(float);
+}
+
 extern "C" int tm_search_hybrid(int32_t dtype, const void *x, int64_t n_tokens, int32_t hidden, int64_t ld_x,
                                 const uint8_t *is_vision, const void *proj_vis, const void *bias_vis,
                                 const void *proj_txt, const void *bias_txt, int64_t ps_h, int64_t ps_d,
@@ -248,13 +572,15 @@ extern "C" int tm_search_hybrid(int32_t dtype, const void *x, int64_t n_tokens, 
                                 int64_t ks_m, int64_t ks_c, const int64_t *sel, int32_t top_k, int64_t ss_b,
                                 int64_t ss_s, int32_t keep_k, uint8_t *on_hit, int64_t *on_idx,
                                 uint8_t *off_hit, int64_t *off_idx, int64_t *on_slot, int64_t os_b,
-                                int64_t os_s, void *workspace, size_t workspace_bytes, tm_stream_t stream) {
+                                int64_t os_s, void *q_out, int64_t ld_q_out, void *workspace, size_t workspace_bytes,
+                                tm_stream_t stream) {
   TM_REQUIRE(n_tokens >= 0 && hidden >= 1 && hidden <= 16384 && ld_x >= hidden && dim >= 1 && dim <= kMaxDim &&
                  n_centroids >= 1 && n_centroids <= 65536 && n_experts >= 1 && top_k >= 0 && top_k <= 64,
              TM_EINVAL_SHAPE, "tm_search_hybrid: bad sizes");
-  TM_REQUIRE(n_online_valid >= 0 && n_online_valid <= 1024 && online_topk >= 0 && online_topk <= 64,
+  TM_REQUIRE(n_online_valid >= 0 && n_online_valid <= kMaxOnline && online_topk >= 0 && online_topk <= 64,
              TM_EINVAL_SHAPE, "tm_search_hybrid: online window too large");
   TM_REQUIRE(ps_h == 1 || ps_d == 1, TM_EINVAL_SHAPE, "tm_search_hybrid: projection needs a unit stride");
+  TM_REQUIRE(q_out == nullptr || ld_q_out >= dim, TM_EINVAL_SHAPE, "tm_search_hybrid: bad q_out stride");
   if (n_tokens == 0) return TM_OK;
   TM_REQUIRE(x && proj_vis && bias_vis && keys && sel && on_hit && on_idx && off_hit && off_idx && on_slot,
              TM_EINVAL_ARG, "tm_search_hybrid: null pointer");
@@ -262,31 +588,40 @@ extern "C" int tm_search_hybrid(int32_t dtype, const void *x, int64_t n_tokens, 
              "tm_search_hybrid: proj_txt and bias_txt must both be set or both be NULL");
   TM_REQUIRE(n_online_valid == 0 || (online_keys && online_ids), TM_EINVAL_ARG,
              "tm_search_hybrid: online window pointers missing");
-  TM_REQUIRE(n_tokens < (int64_t)0x7fffffff, TM_EINVAL_SHAPE, "tm_search_hybrid: too many tokens");
+  TM_REQUIRE(n_tokens < 65536 * 32768LL, TM_EINVAL_SHAPE, "tm_search_hybrid: too many tokens");
   if (keep_k < 0) keep_k = 0;
   if (keep_k > top_k) keep_k = top_k;
   // nothing searched: outputs are only cleared (on_idx = -1), no window lookup
   if (keep_k == top_k) n_online_valid = 0;
+  const size_t need = tm_search_hybrid_workspace_size(n_tokens, hidden, dim);
+  TM_REQUIRE(workspace != nullptr && workspace_bytes >= need && tm_aligned16(workspace), TM_EWORKSPACE,
+             "tm_search_hybrid: workspace %zu bytes < %zu", workspace_bytes, need);
   return TM_DISPATCH_DTYPE(dtype, DT, [&] {
     using T = typename Elem<DT>::T;
     const int E = Elem<DT>::kBytes;
-    const size_t need = (size_t)n_tokens * dim * E;
-    TM_REQUIRE(workspace && workspace_bytes >= need, TM_EWORKSPACE,
-               "tm_search_hybrid: workspace %zu bytes < %zu", workspace_bytes, need);
     const bool vec = dim % 8 == 0 && tm_aligned16(keys) && (ks_e * E) % 16 == 0 && (ks_m * E) % 16 == 0 &&
-                     (ks_c * E) % 16 == 0;
+                     (ks_c * E) % 16 == 0 && tm_aligned16(x) && (ld_x * E) % 16 == 0 &&
+                     (n_online_valid == 0 || (tm_aligned16(online_keys) && (ld_online * E) % 16 == 0)) &&
+                     (ps_h != 1 || (tm_aligned16(proj_vis) && (proj_txt == nullptr || tm_aligned16(proj_txt)) &&
+                                    (ps_d * E) % 16 == 0));
     const T *pt = static_cast<const T *>(proj_txt ? proj_txt : proj_vis);
     const T *bt = static_cast<const T *>(proj_txt ? bias_txt : bias_vis);
-    const size_t shmem = (size_t)hidden * sizeof(float);
+    const int G = hybrid_slices(hidden);
+    float *partial = static_cast<float *>(workspace);
+    float *scores = partial + (size_t)n_tokens * G * dim;
+    hipStream_t s = tm_hip_stream(stream);
     auto launch = [&](auto vec_tag) {
       constexpr bool VEC = decltype(vec_tag)::value;
-      hipLaunchKernelGGL((hybrid_kernel<DT, VEC>), dim3((unsigned)n_tokens), dim3(kThreads), shmem,
-                         tm_hip_stream(stream), static_cast<const T *>(x), hidden, ld_x, is_vision,
-                         static_cast<const T *>(proj_vis), static_cast<const T *>(bias_vis), pt, bt, ps_h, ps_d,
-                         dim, static_cast<const T *>(online_keys), ld_online, n_online_valid, online_ids,
-                         online_topk, ld_online_ids, static_cast<const T *>(keys), n_experts, n_centroids,
-                         ks_e, ks_m, ks_c, sel, top_k, ss_b, ss_s, keep_k, on_hit, on_idx, off_hit, off_idx,
-                         on_slot, os_b, os_s, static_cast<T *>(workspace));
+      hipLaunchKernelGGL((hybrid_partial_kernel<DT, VEC>), dim3((unsigned)n_tokens, (unsigned)G), dim3(kThreads),
+                         (size_t)hidden * sizeof(float), s, static_cast<const T *>(x), hidden, ld_x, is_vision,
+                         static_cast<const T *>(proj_vis), pt, ps_h, ps_d, dim, hybrid_slice_rows(hidden, G),
+                         keep_k < top_k ? 1 : 0, static_cast<const T *>(online_keys), ld_online, n_online_valid,
+                         partial, scores);
+      hipLaunchKernelGGL((hybrid_finish_kernel<DT, VEC>), dim3((unsigned)n_tokens), dim3(kThreads), 0, s, is_vision,
+                         static_cast<const T *>(bias_vis), bt, dim, G, partial, scores, n_online_valid, online_ids,
+                         online_topk, ld_online_ids, static_cast<const T *>(keys), n_experts, n_centroids, ks_e, ks_m,
+                         ks_c, sel, top_k, ss_b, ss_s, keep_k, on_hit, on_idx, off_hit, off_idx, on_slot, os_b, os_s,
+                         static_cast<T *>(q_out), ld_q_out);
     };
     if (vec) launch(std::true_type{});
     else launch(std::false_type{});

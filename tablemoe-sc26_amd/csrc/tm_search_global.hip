@@ -1334,23 +1334,25 @@ int dispatch_dim(int dim, int top_k, const void *q, int64_t n, int64_t ld_q, con
 }
 
 // ---------------------------------------------------------------------------
-// fp32 tables (the CPU-reference configuration): a lane per query, blocks of
-// kF32Block centroid rows staged in LDS and read as broadcasts (every lane
-// reads the same address), fp32 FMAs in dimension order, and the same
-// per-lane packed-key lists and split merge as the 16-bit forms.  The split
-// plan never uses more splits than the 16-bit plan of the same shape, so
-// tm_search_global_workspace_size covers it.
+// fp32 tables (the CPU-reference configuration): a workgroup owns 64
+// queries (lane = query, the query held in registers) and one centroid
+// range; the range is staged through LDS kF32Block rows at a time and the
+// four waves take every fourth row of it (rows are read as broadcasts: every
+// lane of a wave reads the same address).  Each row's dot product is fp32
+// FMAs in dimension order; each lane keeps a packed-key list (the 16-bit
+// forms' keys and order) and the four waves' lists are merged through LDS.
+// Per-split lists are merged by the same merge kernels as the 16-bit forms;
+// tm_search_global_workspace_size covers the larger of the two plans.
 // ---------------------------------------------------------------------------
-constexpr int kF32Block = 32;  // centroids per LDS block
+constexpr int kF32Block = 32;  // centroid rows per LDS stage
+constexpr int kF32Rows = 64;   // queries per workgroup
 
-SplitPlan plan_f32(int64_t n, int64_t c, int dim, int top_k) {
-  SplitPlan p = plan_split(n, c, dim, top_k);
-  const int64_t bound = p.nsplit;
-  p.stream = false;
-  p.wide = false;
-  p.row_blocks = tm_cdiv(n, kThreads);
-  int64_t want = tm_cdiv(512, p.row_blocks);
-  if (want > bound) want = bound;
+// About 1024 workgroups (one per 32-row stage at small n), so a small
+// batch still spreads over the chip.
+SplitPlan plan_f32(int64_t n, int64_t c) {
+  SplitPlan p{};
+  p.row_blocks = tm_cdiv(n, kF32Rows);
+  int64_t want = tm_cdiv(1024, p.row_blocks);
   if (want > tm_cdiv(c, kF32Block)) want = tm_cdiv(c, kF32Block);
   if (want < 1) want = 1;
   p.chunk = tm_cdiv(tm_cdiv(c, want), kF32Block) * kF32Block;
@@ -1363,63 +1365,62 @@ __global__ __launch_bounds__(kThreads) void search_f32_kernel(const float *__res
                                                               const float *__restrict__ cents, int64_t n_cent,
                                                               int64_t ld_c, const float *__restrict__ c_sqnorm,
                                                               int64_t chunk, uint64_t *__restrict__ ws) {
-  constexpr int QC = DIM <= 128 ? DIM : 64;  // query elements held in registers at a time
-  constexpr int V4 = DIM / 4;                // float4 per centroid row
+  constexpr int V4 = DIM / 4;  // float4 per centroid row
   __shared__ float4 cs[kF32Block * V4];
   __shared__ float pen_s[kF32Block];
-  const int tid = threadIdx.x;
-  const int64_t r = (int64_t)blockIdx.x * kThreads + tid;
-  const float *qrow = q + (r < n ? r : n - 1) * ld_q;
+  __shared__ uint64_t lists[3][K][kF32Rows];  // waves 1..3 hand their lists to wave 0
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t r = (int64_t)blockIdx.x * kF32Rows + lane;
+  const float4 *qrow = reinterpret_cast<const float4 *>(q + (r < n ? r : n - 1) * ld_q);
   const int64_t c0 = (int64_t)blockIdx.y * chunk;
   const int64_t c1 = c0 + chunk < n_cent ? c0 + chunk : n_cent;
-  float qv[QC];
-  auto load_q = [&](int kc) {
+  float4 qv[V4];
 #pragma unroll
-    for (int k = 0; k < QC; k += 4) {
-      const float4 v = *reinterpret_cast<const float4 *>(qrow + kc + k);
-      qv[k] = v.x; qv[k + 1] = v.y; qv[k + 2] = v.z; qv[k + 3] = v.w;
-    }
-  };
-  if constexpr (QC == DIM) load_q(0);
+  for (int k = 0; k < V4; ++k) qv[k] = qrow[k];
   Best<K> best;
   best.init();
   for (int64_t cb = c0; cb < c1; cb += kF32Block) {
-    __syncthreads();  // the previous block's reads are done
+    __syncthreads();  // the previous stage's reads are done
     for (int e = tid; e < kF32Block * V4; e += kThreads) {
       const int64_t c = cb + e / V4;
       cs[e] = c < c1 ? *reinterpret_cast<const float4 *>(cents + c * ld_c + 4 * (e % V4)) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (tid < kF32Block) pen_s[tid] = (METRIC == TM_METRIC_L2 && cb + tid < c1) ? c_sqnorm[cb + tid] : 0.f;
     __syncthreads();
-    float acc[kF32Block];
-#pragma unroll
-    for (int j = 0; j < kF32Block; ++j) acc[j] = 0.f;
-#pragma unroll
-    for (int kc = 0; kc < DIM; kc += QC) {
-      if constexpr (QC != DIM) load_q(kc);
-#pragma unroll
-      for (int j = 0; j < kF32Block; ++j)
-#pragma unroll
-        for (int k = 0; k < QC; k += 4) {
-          const float4 cv = cs[j * V4 + (kc + k) / 4];
-          acc[j] = fmaf(qv[k], cv.x, acc[j]);
-          acc[j] = fmaf(qv[k + 1], cv.y, acc[j]);
-          acc[j] = fmaf(qv[k + 2], cv.z, acc[j]);
-          acc[j] = fmaf(qv[k + 3], cv.w, acc[j]);
-        }
-    }
     const int valid = (int)(c1 - cb < kF32Block ? c1 - cb : kF32Block);  // uniform
+    for (int j = wave; j < valid; j += 4) {  // this wave's rows, ascending
+      const float4 *row = cs + j * V4;
+      float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < kF32Block; ++j)
-      if (j < valid) {
-        const float dp = (METRIC == TM_METRIC_L2) ? fmaf(-2.f, acc[j], pen_s[j]) : -acc[j];
-        best.push(dp, (int)(cb + j));
+      for (int k = 0; k < V4; ++k) {
+        const float4 cv = row[k];
+        acc = fmaf(qv[k].x, cv.x, acc);
+        acc = fmaf(qv[k].y, cv.y, acc);
+        acc = fmaf(qv[k].z, cv.z, acc);
+        acc = fmaf(qv[k].w, cv.w, acc);
       }
+      const float dp = (METRIC == TM_METRIC_L2) ? fmaf(-2.f, acc, pen_s[j]) : -acc;
+      best.push(dp, (int)(cb + j));
+    }
   }
   best.finalize();
-  if (r < n) {
+  if (wave > 0) {
 #pragma unroll
-    for (int j = 0; j < K; ++j) ws[((int64_t)blockIdx.y * n + r) * K + j] = best.l[j];
+    for (int i = 0; i < K; ++i) lists[wave - 1][i][lane] = best.l[i];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        const uint64_t key = lists[w][i][lane];
+        if (key < best.l[K - 1]) list_insert<K>(best.l, key);
+      }
+    if (r < n) {
+#pragma unroll
+      for (int i = 0; i < K; ++i) ws[((int64_t)blockIdx.y * n + r) * K + i] = best.l[i];
+    }
   }
 }
 
@@ -1427,7 +1428,7 @@ template <int DIM, int K, int METRIC>
 int launch_search_f32(int top_k, const void *q, int64_t n, int64_t ld_q, const float *q_sqnorm, const void *cents,
                       int64_t n_cent, int64_t ld_c, const float *c_sqnorm, float *out_dist, int64_t *out_idx,
                       uint64_t *ws, const tm_route_args *ra, hipStream_t stream) {
-  const SplitPlan p = plan_f32(n, n_cent, DIM, top_k);
+  const SplitPlan p = plan_f32(n, n_cent);
   const float *Q = static_cast<const float *>(q);
   hipLaunchKernelGGL((search_f32_kernel<DIM, K, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
                      dim3(kThreads), 0, stream, Q, n, ld_q, static_cast<const float *>(cents), n_cent, ld_c, c_sqnorm,
@@ -1484,8 +1485,9 @@ extern "C" int tm_centroid_sqnorms(int32_t dtype, const void *cents, int64_t n_c
 extern "C" size_t tm_search_global_workspace_size(int64_t n_tokens, int64_t n_cent, int32_t dim,
                                                   int32_t top_k) {
   if (n_tokens <= 0 || n_cent <= 0 || top_k <= 0 || (dim != 64 && dim != 128 && dim != 256)) return 0;
-  const SplitPlan p = plan_split(n_tokens, n_cent, dim, top_k);
-  return (size_t)p.nsplit * (size_t)n_tokens * (size_t)list_len(top_k) * sizeof(uint64_t);
+  const int64_t s16 = plan_split(n_tokens, n_cent, dim, top_k).nsplit;  // 16-bit tables
+  const int64_t s32 = plan_f32(n_tokens, n_cent).nsplit;                // fp32 tables
+  return (size_t)(s16 > s32 ? s16 : s32) * (size_t)n_tokens * (size_t)list_len(top_k) * sizeof(uint64_t);
 }
 
 static int search_impl(int32_t dtype, const void *q, int64_t n_tokens, int64_t ld_q, const float *q_sqnorm,

@@ -62,9 +62,10 @@ PROTOTYPES = {
                              vp]),
     "tm_search_gated": (C.c_int, [i32, vp, i64, i64, vp, i64, i64, i32, i64, i64, i64, vp, i32, i64, i64, vp, vp,
                                   i64, i64, i32, f32, f32, i32, vp, vp, i64, i64, vp]),
+    "tm_search_hybrid_workspace_size": (sz, [i64, i32, i32]),
     "tm_search_hybrid": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, vp, vp, i64, i64, i32, vp, i64, i32, vp, i32,
                                    i64, vp, i64, i64, i64, i64, i64, vp, i32, i64, i64, i32, vp, vp, vp, vp, vp, i64,
-                                   i64, vp, sz, vp]),
+                                   i64, vp, i64, vp, sz, vp]),
     "tm_fixed_keep_mask": (C.c_int, [i64, i32, i32, vp, vp]),
     "tm_expert_keep_mask_workspace_size": (sz, [i64, i32]),
     "tm_expert_keep_mask": (C.c_int, [vp, vp, vp, i64, i32, i32, f64, vp, vp, vp, sz, vp]),

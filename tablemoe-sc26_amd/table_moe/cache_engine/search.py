@@ -286,6 +286,7 @@ class VectorSearchEngine:
         keys = self.manager.keys_buffer
         isv = N.as_u8(is_vision_mask.reshape(-1).to(device=dev, dtype=torch.bool))
         q_ws = self._ensure_decode_query_workspace(n, dims["compressed_dim"])
+        ws = self._scratch("hybrid", N.lib().tm_search_hybrid_workspace_size(n, hidden, dims["compressed_dim"]))
         pv, pt = dims["pca_vis"], dims["pca_txt"]
         tv, tt = dims["proj_t"]
         N.call(
@@ -296,7 +297,7 @@ class VectorSearchEngine:
             N.ptr(keys), keys.shape[0], keys.shape[2], keys.stride(0), keys.stride(1), keys.stride(2),
             N.ptr(sel), top_k, sel.stride(0), sel.stride(1), int(keep_k), N.ptr(N.as_u8(on_hit)), N.ptr(on_idx),
             N.ptr(N.as_u8(off_hit)), N.ptr(off_idx), N.ptr(on_slot), on_hit.stride(0), on_hit.stride(1),
-            N.ptr(q_ws), q_ws.numel() * q_ws.element_size(), N.stream(dev),
+            N.ptr(q_ws), q_ws.stride(0), N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(dev),
         )
 
     def search_decode_hybrid(self, layer_idx, hidden_states, selected_experts, is_vision_mask, keep_k=None):

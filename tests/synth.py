@@ -147,3 +147,35 @@ def make_stack(n_layers: int = 48, *, n: int | None = None, device="cuda", gen_d
     router logits, slot outputs and residual, drawn on ``gen_device``."""
     return [make_workload(4, n=n, seed=CONFIGS[4]["seed"] + l, device=device, gen_device=gen_device, **overrides)
             for l in range(n_layers)]
+
+
+def make_mode_r_manager(dev, E=128, H=2048, d=64, K=256, seed=7):
+    """A HybridStorageManager of the reference's default shape (128 experts x
+    2 modalities x 256 centroids in 64-d, hidden 2048) filled on the device:
+    random keys (normalised copy as the loader makes it), cached outputs, PCA
+    pairs, a full 64-entry online window."""
+    from table_moe.cache_engine import CacheConfig, HybridStorageManager
+    from table_moe.cache_engine.table_file import normalize_last_dim
+
+    saved = {k: getattr(CacheConfig, k) for k in ("FIXED_K", "COMPRESSED_DIM", "MODEL_DTYPE", "ONLINE_CACHE_SIZE",
+                                                  "ONLINE_TOP_K")}
+    CacheConfig.FIXED_K, CacheConfig.COMPRESSED_DIM, CacheConfig.MODEL_DTYPE = K, d, torch.bfloat16
+    CacheConfig.ONLINE_CACHE_SIZE, CacheConfig.ONLINE_TOP_K = 64, 8
+    try:
+        mgr = HybridStorageManager(2, E, H, dev)
+    finally:
+        for k_, v in saved.items():
+            setattr(CacheConfig, k_, v)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    raw = torch.randn(E, 2, K, d, generator=g, device=dev)
+    mgr.raw_keys_buffer.copy_(raw.to(torch.bfloat16))
+    mgr.keys_buffer.copy_(normalize_last_dim(raw, 1e-6).to(torch.bfloat16))
+    mgr.values_buffer.copy_(torch.randn(E, 2, K, H, generator=g, device=dev).to(torch.bfloat16))
+    for mod in ("vision", "text"):
+        p = torch.linalg.qr(torch.randn(H, d, generator=g, device=dev, dtype=torch.float32))[0]
+        mgr.pca[mod] = {"proj": p.to(torch.bfloat16), "bias": (torch.randn(d, generator=g, device=dev) * 0.05)
+                        .to(torch.bfloat16)}
+    hist = torch.randn(64, H, generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, device=dev)[:8] for _ in range(64)])
+    mgr.update_online_cache(hist, ids, torch.randn(64, 8, H, generator=g, device=dev).to(torch.bfloat16))
+    return mgr

@@ -284,12 +284,14 @@ def test_search_hybrid_vs_oracle(hip_device, n_valid, keep_k, dtype):
     on_idx = torch.full((n,), -9, dtype=torch.long, device=dev)
     off_idx = torch.full((n, k), -9, dtype=torch.long, device=dev)
     on_slot = torch.full((n, k), -9, dtype=torch.long, device=dev)
-    ws = torch.zeros(n, d, dtype=dtype, device=dev)
+    ws = torch.zeros(n, d, dtype=dtype, device=dev)  # the projected queries
+    nbytes = N.lib().tm_search_hybrid_workspace_size(n, H, d)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     N.call("tm_search_hybrid", N.dtype_tag(dtype), xd.data_ptr(), n, H, H, N.as_u8(visd).data_ptr(), pvt.data_ptr(),
            bvd.data_ptr(), ptt.data_ptr(), btd.data_ptr(), 1, H, d, okd.data_ptr() if n_valid else None, H, n_valid,
            oid.data_ptr() if n_valid else None, wk, wk, kd.data_ptr(), E, K, kd.stride(0), kd.stride(1), kd.stride(2),
            seld.data_ptr(), k, k, 1, keep_k, on_hit.data_ptr(), on_idx.data_ptr(), off_hit.data_ptr(),
-           off_idx.data_ptr(), on_slot.data_ptr(), k, 1, ws.data_ptr(), ws.numel() * ws.element_size(), N.stream(dev))
+           off_idx.data_ptr(), on_slot.data_ptr(), k, 1, ws.data_ptr(), d, scratch.data_ptr(), nbytes, N.stream(dev))
     torch.cuda.synchronize()
     ref = O.search_hybrid(np64(x), vis.numpy(), (np64(pv), np64(bv)), (np64(pt), np64(bt)), ODT[dtype], np64(keys),
                           sel.numpy(), keep_k, np64(on_keys) if n_valid else None, on_ids.numpy() if n_valid else None,

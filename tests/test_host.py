@@ -43,6 +43,41 @@ def test_modality_context_mask():
     ModalityContext.clear()
 
 
+def test_modality_context_per_thread_and_reset():
+    """State is per thread (the reference's thread-local contract), a new
+    prompt drops the memoised masks, attention weights round-trip, and a
+    seq_len shorter than the prompt selects its last tokens."""
+    import threading
+
+    from table_moe.utils.modality import ModalityContext
+
+    ModalityContext.clear()
+    ids = torch.tensor([[151656, 3, 151655, 151655]])
+    ModalityContext.set_input_ids(ids)
+    w = torch.rand(4)
+    ModalityContext.set_attn_weights(w)
+    seen = {}
+
+    def other():
+        seen["ids"] = ModalityContext.get_input_ids()
+        seen["w"] = ModalityContext.get_attn_weights()
+        seen["mask"] = ModalityContext.get_modality_mask(torch.device("cpu"), 4)
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["ids"] is None and seen["w"] is None and not seen["mask"].any()
+    assert ModalityContext.get_attn_weights() is w
+    m4 = ModalityContext.get_modality_mask(torch.device("cpu"), 4)
+    np.testing.assert_array_equal(m4.numpy(), [[True, False, True, True]])
+    np.testing.assert_array_equal(ModalityContext.get_modality_mask(torch.device("cpu"), 2).numpy(), [[True, True]])
+    np.testing.assert_array_equal(ModalityContext.get_modality_mask(torch.device("cpu")).numpy(), m4.numpy())
+    ModalityContext.set_input_ids(torch.tensor([[1, 2, 3, 4]]))  # a new prompt: memo dropped
+    assert not ModalityContext.get_modality_mask(torch.device("cpu"), 4).any()
+    ModalityContext.clear()
+    assert ModalityContext.get_input_ids() is None and ModalityContext.get_attn_weights() is None
+
+
 def test_table_files_load_on_host(tmp_path):
     """The on-disk table format (step2/step3 .pt files) is parsed and installed;
     bad files are reported and skipped (reference manager.py:157-210)."""
