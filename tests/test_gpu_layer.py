@@ -8,7 +8,7 @@ import torch
 
 from oracle import tm_oracle as O
 from parity_util import (ODT, assert_bf16_output, assert_projection_close, assert_within_ulps, check_pick,
-                         check_topk_rows, np64, proj_abssum)
+                         check_topk_rows, np64, proj_abssum, ulp)
 from table_moe import _native as N
 
 pytestmark = pytest.mark.gpu
@@ -652,15 +652,17 @@ def test_layer_forward_decode_plan_matches_staged(hip_device, cfg, n, hidden, di
     assert int(ra["keep"].sum()) == O.keep_count(n, 0.6)
 
 
-def test_layer_forward_config3_decode_end_to_end(hip_device):
-    """Config 3 (decode, N=32 text tokens, C=16384, top-4 inverse-distance
-    blend) through the one-call layer, checked stage by stage against the
-    oracle: projection, top-4 lists on the device's queries, the keep set on
-    the device's distances, and the combined rows."""
+@pytest.mark.parametrize("n", [1, 8, 32])
+def test_layer_forward_config3_decode_end_to_end(hip_device, n):
+    """Config 3 (decode, N = 1, 8, 32 text tokens, C=16384, top-4
+    inverse-distance blend) through the one-call layer (the decode plan),
+    checked stage by stage against the oracle: router, projection, top-4
+    lists on the device's queries, the keep set on the device's distances,
+    and the combined rows."""
     from table_moe.cache_engine import GlobalTable
     from synth import make_workload
 
-    wl = make_workload(3)
+    wl = make_workload(3, n=n)
     d = wl.to(hip_device)
     tbl = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
     res = tbl.layer_forward(d.x, d.is_vision, d.logits, d.slot_out, d.residual, router_top_k=8, n_nearest=4,
@@ -677,10 +679,11 @@ def test_layer_forward_config3_decode_end_to_end(hip_device):
     gi = np64(res["idx"])
     check_topk_rows(exact, gi, want_idx, False, "search")
     gd = np64(res["dist"])
-    np.testing.assert_allclose(gd, exact[np.arange(32)[:, None], gi], rtol=1e-5, atol=1e-3)
+    np.testing.assert_allclose(gd, exact[np.arange(n)[:, None], gi], rtol=1e-5, atol=1e-3)
     keep = np64(res["keep"])
-    assert keep.sum() == O.keep_count(32, 0.6) == 19
-    np.testing.assert_array_equal(keep, O.keep_select(gd[:, 0].astype(np.float32).astype(np.float64), 19))
+    n_keep = O.keep_count(n, 0.6)
+    assert keep.sum() == n_keep == {1: 1, 8: 4, 32: 19}[n]
+    np.testing.assert_array_equal(keep, O.keep_select(gd[:, 0].astype(np.float32).astype(np.float64), n_keep))
     exact = O.gather_combine(keep, np64(wl.slot_out), np64(res["weights"]), np64(wl.values), gi, gd,
                              np64(wl.residual), O.F32)
     abssum = O.gather_combine(keep, np.abs(np64(wl.slot_out)), np64(res["weights"]), np.abs(np64(wl.values)), gi,
@@ -785,3 +788,73 @@ def test_decode_combine_update_matches_unfused(hip_device, hazard):
     for a, b_ in zip(fused, (mgr.online_keys, mgr.online_expert_ids, mgr.online_values)):
         assert torch.equal(a, b_)
     assert int(mgr.online_expert_ids[0, 7]) == -1 and torch.all(mgr.online_values[0, 7] == 0)
+
+
+@pytest.mark.parametrize("hazard", [True, False])
+@pytest.mark.parametrize("pattern", ["mixed", "all_survive", "none_survive"])
+def test_decode_combine_update_vs_oracle(hip_device, hazard, pattern):
+    """The fused decode tail against the reference's semantics restated in
+    numpy: the slot sources of _forward_decode_bs1
+    (models/qwen3_vl_moe/cached_layers.py:213-247: kept slots recomputed,
+    online hits from online_values[on_idx, on_slot], offline hits from
+    values[expert, modality, off_idx], other slots zero), the effective
+    weights and matmul (:141-159, :252-259) as O.slot_combine, and the ring
+    write of update_online_cache_bs1 (manager.py:89-106) as O.online_update
+    -- including an online source in the ring row being overwritten."""
+    dev = hip_device
+    mgr, g = _mode_r_manager(dev, seed=211)
+    H, k, W = 512, 8, 64
+    hist = torch.randn(W, H, generator=g).to(torch.bfloat16).to(dev)
+    hist_ids = torch.stack([torch.randperm(16, generator=g)[:k] for _ in range(W)]).to(dev)
+    mgr.update_online_cache(hist, hist_ids, torch.randn(W, k, H, generator=g).to(torch.bfloat16).to(dev))
+    ring_row = mgr.online_ptr
+    x = torch.randn(H, generator=g).to(torch.bfloat16).to(dev)
+    sel = torch.randperm(16, generator=g)[:k].to(dev)
+    w = torch.softmax(torch.randn(k, generator=g), 0).to(dev)
+    keep_k = 0 if pattern == "none_survive" else 3
+    compute = torch.zeros(k, dtype=torch.bool, device=dev)
+    compute[:keep_k] = True
+    computed = torch.randn(k, H, generator=g).to(torch.bfloat16).to(dev)
+    if pattern == "mixed":
+        on_hit = torch.tensor([0, 0, 0, 1, 0, 1, 0, 0], dtype=torch.bool, device=dev)
+        off_hit = torch.tensor([0, 0, 0, 0, 1, 0, 1, 0], dtype=torch.bool, device=dev)
+    elif pattern == "all_survive":
+        on_hit = torch.tensor([0, 0, 0, 1, 1, 0, 0, 0], dtype=torch.bool, device=dev)
+        off_hit = torch.tensor([0, 0, 0, 0, 0, 1, 1, 1], dtype=torch.bool, device=dev)
+    else:
+        on_hit = torch.zeros(k, dtype=torch.bool, device=dev)
+        off_hit = torch.zeros(k, dtype=torch.bool, device=dev)
+    on_idx = torch.tensor([ring_row if hazard else (ring_row + 17) % W], device=dev)
+    on_slot = torch.tensor([0, 0, 0, 2, 5, 7, 0, 0], device=dev)
+    off_idx = torch.tensor([0, 0, 0, 0, 41, 200, 7, 255], device=dev)
+    vis = torch.tensor(True, device=dev)
+    st0 = dict(keys=np64(mgr.online_keys), ids=np64(mgr.online_expert_ids), values=np64(mgr.online_values),
+               ptr=ring_row, full=True, size=W)
+    out = torch.empty(H, dtype=torch.bfloat16, device=dev)
+    mgr.combine_and_update_bs1(x, w, sel, vis, compute, computed, on_hit, on_idx, on_slot, off_hit, off_idx, out)
+    torch.cuda.synchronize()
+    # the reference's collected rows, from the state before the call
+    c, oh, fh = np64(compute).astype(bool), np64(on_hit).astype(bool), np64(off_hit).astype(bool)
+    collected = np.zeros((k, H))
+    vals = np64(mgr.values_buffer)
+    for s_ in range(k):
+        if c[s_]:
+            collected[s_] = np64(computed)[s_]
+        elif oh[s_]:
+            collected[s_] = st0["values"][int(on_idx[0]), int(on_slot[s_])]
+        elif fh[s_]:
+            collected[s_] = vals[int(sel[s_]), 0, int(off_idx[s_])]
+    survivor = c | oh | fh
+    want, _ = O.slot_combine(collected[None], np64(w)[None], survivor[None], O.BF16)
+    absw, _ = O.slot_combine(np.abs(collected)[None], np64(w)[None], survivor[None], O.F32)
+    got = np64(out)[None]
+    if not survivor.any():
+        assert (got == 0).all()
+    else:
+        tol = ulp(want, torch.bfloat16) + 2.0**-20 * absw
+        assert np.all(np.abs(got - want) <= tol), np.abs(got - want).max()
+    st1 = O.online_update(st0, np64(x)[None], np64(sel)[None], collected[None], survivor[None])
+    np.testing.assert_array_equal(np64(mgr.online_keys), st1["keys"])
+    np.testing.assert_array_equal(np64(mgr.online_expert_ids), st1["ids"])
+    np.testing.assert_array_equal(np64(mgr.online_values), st1["values"])
+    assert mgr.online_ptr == st1["ptr"]
