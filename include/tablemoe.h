@@ -405,8 +405,11 @@ int tm_last_query_importance(int32_t dtype, const void *q, int64_t qs_b, int64_t
  * fp16_epilogue_utils.h:51-125), y = dtype(f W2^T).  fp32 accumulation on
  * bf16/fp16 matrix cores.  Weights as nn.Linear stores them: W1, W3
  * [n_experts, inter, hidden], W2 [n_experts, hidden, inter], contiguous.
- * hidden and inter must be multiples of 128.  Workspace: the [rows, inter]
- * intermediate (tm_swiglu_workspace_size).
+ * hidden and inter must be multiples of 128, inter * hidden < 2^30; x,
+ * out, addend rows and the weights 16-byte aligned (row strides and
+ * tm_grouped_swiglu's row_out offsets multiples of 8 elements: rows are
+ * written in 16-byte pieces).  Workspace: the [rows, inter] intermediate
+ * (tm_swiglu_workspace_size).
  * ====================================================================== */
 size_t tm_swiglu_workspace_size(int64_t max_rows, int32_t inter, int32_t dtype);
 int tm_expert_swiglu(int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,

@@ -34,10 +34,10 @@ static inline int64_t tm_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 __device__ __forceinline__ float tm_bf16_to_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
 __device__ __forceinline__ uint16_t tm_f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);                                              // round half even
-  return (uint16_t)(u >> 16);
+  // v_cvt_pk_bf16_f32: round half to even; a NaN keeps its sign and upper
+  // payload bits with the quiet bit set, i.e. (bits >> 16) | 0x40.  Checked
+  // against that software rule over all 2^32 fp32 bit patterns on gfx950.
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 template <int DT>

@@ -19,26 +19,28 @@
 //
 // grouped_gemm_kernel computes one BM x BN tile C = A B^T of one expert:
 // A rows gathered (token rows of x, or the grouped rows of the intermediate),
-// B rows k-contiguous (nn.Linear weights [out, in]), K in BK-wide stages.
-// Stages move global -> LDS by direct loads, three in flight (16-byte chunks
-// XOR-swizzled by row, so the operand reads of 32 rows spread over the
-// banks); one barrier per stage.  Four waves own 128 x 64 quadrants (4 x 2
-// blocks of v_mfma_f32_32x32x16).  Up mode multiplies W1 and W3 against the same A
-// fragments and applies the SiLU-mul epilogue; down mode writes each row to
-// its slot of the output.
+// B rows k-contiguous (nn.Linear weights [out, in]), K in BK-wide stages
+// moved global -> LDS by direct loads (16-byte chunks XOR-swizzled by row, so
+// the operand reads of 32 rows spread over the banks), three in flight.
+// Four waves, one per SIMD, each software-pipelined so that the operand reads
+// of one k-step run under the MFMAs of the previous one.  Up mode multiplies
+// W1 and W3 against the same A fragments and applies the SiLU-mul epilogue;
+// down mode writes each row to its slot of the output.
 #include "tm_internal.h"
 #include "tm_dma.h"
 #include "tm_mfma.h"
 
 namespace {
 
-constexpr int BM = 256, BN = 128, BK = 32, kThreads = 256, kRing = 4;
-constexpr int kCPR = BK / 8;                 // 16-byte chunks per tile row
+constexpr int BM = 256, BK = 32, kThreads = 256;
+constexpr int kMinBN = 128;                  // column tile of the up GEMM (and of narrow down GEMMs)
+constexpr int kCPR = BK / 8;                 // 16-byte chunks per tile row and stage
 constexpr int kAStage = BM * kCPR;           // A slots (16 bytes) per stage
-constexpr int kBStage = BN * kCPR;           // slots of each B per stage
-constexpr int kADma = kAStage / 64 / 4;      // A loads per wave per stage (4)
-constexpr int kBDma = kBStage / 64 / 4;      // loads of each B per wave per stage (2)
-constexpr int kMI = 4, kNI = 2;              // 32 x 32 blocks per wave: 128 rows x 64 columns
+constexpr int kADma = kAStage / kThreads;    // A loads per thread per stage (4)
+constexpr int kMI = 4;                       // 32-row blocks per wave: 128 rows
+constexpr int kStageCols = 128;              // epilogue staging width (columns per pass)
+constexpr int kStageLd = kStageCols + 8;     // staging row stride in floats
+constexpr int kEpiFloats = BM * kStageLd;    // staging tile size in floats (139,264 bytes)
 
 enum { kModeUp = 0, kModeDown = 1 };
 
@@ -47,7 +49,6 @@ enum { kModeUp = 0, kModeDown = 1 };
 // puts the 8 rows of a line group on 8 distinct 16-byte bank groups, and an
 // operand read (one chunk of 32 consecutive rows) is conflict-free.
 __device__ __forceinline__ int swz_chunk(int row, int kc) { return kc ^ ((row >> 1) & (kCPR - 1)); }
-__device__ __forceinline__ int swz(int row, int kc) { return row * kCPR + swz_chunk(row, kc); }
 
 // Tile source: the grouped tile list (tiles != nullptr: [0] rows, [1] tiles,
 // then tile_expert[t_max], tile_row0[t_max]) or one dense expert of `rows`.
@@ -58,24 +59,48 @@ struct TileSrc {
   int32_t rows;
 };
 
-// One BM x BN tile, 4 waves in a 2 x 2 grid of 128 x 64 quadrants (one wave
-// per SIMD, accumulators in the AGPRs).  Operands move global -> LDS by
-// direct loads into a kRing-stage ring, kRing - 1 stages in flight: at step i
-// a wave waits for its own loads of stage i, the barrier makes every wave's
-// loads of stage i visible (and retires every wave's reads of stage i - 1),
-// then the loads of stage i + 3 go into that freed slot and stage i is
-// multiplied.  Lane l of a load fills slot p0 + l; it reads the global chunk
-// that belongs there (the inverse of the swizzle).
-template <int DT, int NB, int MODE>
+// One BM x BN tile C = A B^T of one expert (NB = 2: two B matrices against
+// the same A, the gate and up projections).  Four waves in a 2 x 2 grid of
+// 128 x BN/2 quadrants, one wave per SIMD, 16 accumulator blocks of
+// v_mfma_f32_32x32x16 per wave (all 256 AGPRs): 4 x 2 per B for the up GEMM
+// (BN = 128), 4 x 4 for the down GEMM (BN = 256), so every k-step reads 8
+// operand fragments from LDS for 16 MFMAs (a hidden size that is not a
+// multiple of 256 takes 128-column down tiles: 6 reads, 8 MFMAs).
+//
+// K moves in BK-wide stages through a 4-slot LDS ring filled by direct
+// global -> LDS loads (A rows gathered by 64-bit per-lane addresses, B rows
+// through a buffer resource whose scalar offset walks K), three stages in
+// flight.  Each wave is software-pipelined over half-stages (k-steps): while
+// the matrix core runs the 16 MFMAs of one k-step, the wave reads the next
+// k-step's 8 fragments into the other register set (sched_group_barrier
+// interleaves one read per two MFMAs).  The stage boundary sits between a
+// stage's two k-steps: wait for this wave's loads of the next stage, barrier
+// (every wave's loads of it are then visible and every wave has finished its
+// reads of the current stage's slot), and refill that slot with the stage
+// four ahead.  Stages past the last re-read the last one (never multiplied),
+// so the wait counts are the same in every iteration.
+template <int DT, int NB, int MODE, int BN>
 __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
     const typename Elem<DT>::T *__restrict__ A, int64_t lda, const int32_t *__restrict__ a_rows,
     const typename Elem<DT>::T *__restrict__ B0, const typename Elem<DT>::T *__restrict__ B1, int64_t b_expert,
     int K, int n_tiles, TileSrc ts, typename Elem<DT>::T *__restrict__ C, int64_t ldc,
     const int64_t *__restrict__ c_rows, const typename Elem<DT>::T *__restrict__ addend, int64_t ld_add) {
   using T = typename Elem<DT>::T;
+  constexpr int kNI = BN / 64;                   // 32-column blocks per wave and B
+  constexpr int kBStage = BN * kCPR;             // slots of each B per stage
+  constexpr int kBDma = kBStage / kThreads;      // loads of each B per thread per stage
   constexpr int kStage = kAStage + NB * kBStage;
-  constexpr int kDma = kADma + NB * kBDma;  // loads per wave per stage
-  __shared__ uint4 lds[kRing * kStage];
+  constexpr int kDma = kADma + NB * kBDma;       // loads per wave per stage
+  constexpr int kFrag = kMI + NB * kNI;          // operand fragments per k-step
+  constexpr int kMfma = NB * kMI * kNI;          // MFMAs per k-step (16; 8 for a 128-column down GEMM)
+  static_assert(kMfma <= 16, "accumulators fit the AGPRs");
+  static_assert(kBStage % kThreads == 0 && 3 * kDma < 64, "stage shape");
+  // One LDS array: the 4-slot ring during the K loop, then the fp32 staging
+  // tile of the epilogue (kStageCols columns, rows padded to kStageLd floats).
+  constexpr int kLdsSlots = 4 * kStage > kEpiFloats / 4 ? 4 * kStage : kEpiFloats / 4;
+  __shared__ uint4 lds_all[kLdsSlots];
+  uint4 *const ring0 = lds_all, *const ring1 = lds_all + kStage, *const ring2 = lds_all + 2 * kStage,
+               *const ring3 = lds_all + 3 * kStage;
 
   // Block b runs on XCD b % 8 (the dispatcher's round robin): the n_tiles
   // column tiles of row tile y get ids 8 apart, so they share one XCD and its
@@ -96,101 +121,183 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
     if (r0 >= ts.rows) return;
     r_end = ts.rows;
   }
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Global source of each of this lane's loads (stage 0); stage s adds s * BK.
+  // Loads: thread t fills slots t + 256 j of the A part and of each B part;
+  // slot p holds row p / kCPR, chunk swz_chunk(row, p % kCPR) (the swizzle is
+  // its own inverse).  A: 64-bit address of stage 0 (stage s adds s * BK).
   const T *a_src[kADma];
-  const T *b_src[NB][kBDma];
 #pragma unroll
   for (int j = 0; j < kADma; ++j) {
-    const int p = (wave * kADma + j) * 64 + lane;
-    const int row = p / kCPR, kc = swz_chunk(row, p % kCPR);  // the swizzle is its own inverse
+    const int p = tid + kThreads * j;
+    const int row = p / kCPR, kc = swz_chunk(row, p % kCPR);
     int gr = r0 + row;
     gr = gr < r_end ? gr : r_end - 1;  // rows past the expert re-read its last row; their results are dropped
     const int64_t ar = a_rows ? (int64_t)a_rows[gr] : (int64_t)gr;
     a_src[j] = A + ar * lda + kc * 8;
   }
+  // B: the expert's BN rows from n0 on, through a buffer; lane offsets fixed,
+  // the stage's K offset in the scalar offset.
+  tm_rsrc_t b_rs[NB];
+  b_rs[0] = tm_make_rsrc(B0 + (int64_t)e * b_expert + (int64_t)n0 * K, (uint64_t)BN * K * sizeof(T));
+  if constexpr (NB > 1) b_rs[1] = tm_make_rsrc(B1 + (int64_t)e * b_expert + (int64_t)n0 * K, (uint64_t)BN * K * sizeof(T));
+  uint32_t b_off[kBDma];
 #pragma unroll
   for (int j = 0; j < kBDma; ++j) {
-    const int p = (wave * kBDma + j) * 64 + lane;
+    const int p = tid + kThreads * j;
     const int row = p / kCPR, kc = swz_chunk(row, p % kCPR);
-    const int64_t br = (int64_t)e * b_expert + (int64_t)(n0 + row) * K + kc * 8;
-    b_src[0][j] = B0 + br;
-    if constexpr (NB > 1) b_src[1][j] = B1 + br;
+    b_off[j] = (uint32_t)row * (uint32_t)K * (uint32_t)sizeof(T) + (uint32_t)kc * 16u;
   }
-  const int KT = K / BK;
-  auto issue = [&](int stage) {  // stages past the last re-read it (their slot is never multiplied)
+  const int KT = K / BK;  // a multiple of 4 (the host checks)
+  // Load j (0 .. kDma-1) of stage `stage` into `ring`: A loads first, then
+  // each B's.  Stages past the last re-read the last one.
+  auto issue_one = [&](auto j_c, uint4 *ring, int stage) {
+    constexpr int j = decltype(j_c)::value;
     const int kt = stage < KT ? stage : KT - 1;
-    uint4 *s = lds + (stage % kRing) * kStage;
+    const uint32_t lds = (uint32_t)(uintptr_t)ring + (uint32_t)wave * 1024u;  // wave's 64 slots of load 0
+    if constexpr (j < kADma) {
+      tm_dma16_s(a_src[j] + (int64_t)kt * BK, lds + (uint32_t)(j * kThreads * 16));
+    } else {
+      constexpr int bb = (j - kADma) / kBDma, jb = (j - kADma) % kBDma;
+      tm_dma16_buf_so(b_rs[bb], b_off[jb], (uint32_t)kt * (uint32_t)(BK * sizeof(T)),
+                      lds + (uint32_t)((kAStage + bb * kBStage + jb * kThreads) * 16));
+    }
+  };
+  auto issue = [&](uint4 *ring, int stage) { tm_static_for<kDma>([&](auto j_c) { issue_one(j_c, ring, stage); }); };
+
+  // Fragment byte offsets within a slot: row R + (lane % 32) (R a multiple of
+  // 32) at chunk 2 ks + lane / 32 sits at R * 64 + off[ks], the same for every
+  // block, part and slot; opaque, so the rest stays an immediate offset.
+  uint32_t f_off[2];
 #pragma unroll
-    for (int j = 0; j < kADma; ++j) tm_dma16(a_src[j] + (int64_t)kt * BK, s + (wave * kADma + j) * 64);
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int j = 0; j < kBDma; ++j)
-        tm_dma16(b_src[b][j] + (int64_t)kt * BK, s + kAStage + b * kBStage + (wave * kBDma + j) * 64);
+  for (int ks = 0; ks < 2; ++ks) {
+    const int r = lane & 31;
+    f_off[ks] = (uint32_t)(r * kCPR + swz_chunk(r, 2 * ks + (lane >> 5))) * 16u;
+    asm volatile("" : "+v"(f_off[ks]));
+  }
+  uint4 fr[2][kFrag];  // two k-steps' operands: [0..kMI) A blocks, then B blocks
+  auto read_one = [&](auto g_c, uint4 (&f)[kFrag], const uint4 *ring, int ks) {
+    constexpr int g = decltype(g_c)::value;
+    const char *base = reinterpret_cast<const char *>(ring) + f_off[ks];
+    if constexpr (g < kMI) {
+      f[g] = *reinterpret_cast<const uint4 *>(base + (wm * 128 + g * 32) * 64);
+    } else {
+      constexpr int bb = (g - kMI) / kNI, ni = (g - kMI) % kNI;
+      f[g] = *reinterpret_cast<const uint4 *>(base + (kAStage + bb * kBStage) * 16 + (wn * (BN / 2) + ni * 32) * 64);
+    }
   };
 
   tm_f32x16 acc[NB][kMI][kNI];
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
     for (int mi = 0; mi < kMI; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < kNI; ++ni) acc[b][mi][ni] = tm_f32x16{};
+      for (int ni = 0; ni < kNI; ++ni) acc[bb][mi][ni] = tm_f32x16{};
+  auto mfma_one = [&](auto m_c, const uint4 (&f)[kFrag]) {
+    constexpr int m = decltype(m_c)::value;
+    constexpr int bb = m / (kMI * kNI), mi = (m / kNI) % kMI, ni = m % kNI;
+    acc[bb][mi][ni] = tm_mfma32x32x16<DT>(f[mi], f[kMI + bb * kNI + ni], acc[bb][mi][ni]);
+  };
+  // One k-step: its MFMAs on `f`, and between them (in fixed groups, so the
+  // waits of neither sit in front of the matrix core) the reads of `next`
+  // from `rd` at k-step ks and, with DMA, the kDma loads of stage `st` into
+  // `dst` (kDma == kFrag for every shape here).
+  static_assert(kDma == kFrag, "one load per operand read");
+  constexpr int kPer = kMfma / kFrag;
+  auto kstep = [&](auto dma_c, const uint4 (&f)[kFrag], uint4 (&next)[kFrag], const uint4 *rd, int ks, uint4 *dst,
+                   int st) {
+    tm_static_for<kFrag>([&](auto g_c) {
+      constexpr int g = decltype(g_c)::value;
+      tm_static_for<kPer>([&](auto q_c) { mfma_one(std::integral_constant<int, g * kPer + decltype(q_c)::value>{}, f); });
+      read_one(g_c, next, rd, ks);
+      if constexpr (decltype(dma_c)::value) issue_one(g_c, dst, st);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    tm_static_for<kMfma - kFrag * kPer>(
+        [&](auto q_c) { mfma_one(std::integral_constant<int, kFrag * kPer + decltype(q_c)::value>{}, f); });
+  };
 
-  issue(0);
-  issue(1);
-  issue(2);
-  for (int i = 0; i < KT; ++i) {
-    tm_wait_vm_lgkm0<2 * kDma>();  // this wave's loads of stage i are done (stages i+1, i+2 may fly)
-    __syncthreads();
-    issue(i + 3);
-    const uint4 *s = lds + (i % kRing) * kStage;
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int kc = ks * 2 + (lane >> 5);
-      uint4 fa[kMI], fb[NB][kNI];
-#pragma unroll
-      for (int mi = 0; mi < kMI; ++mi) fa[mi] = s[swz(wm * 128 + mi * 32 + (lane & 31), kc)];
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int ni = 0; ni < kNI; ++ni) fb[b][ni] = s[kAStage + b * kBStage + swz(wn * 64 + ni * 32 + (lane & 31), kc)];
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int mi = 0; mi < kMI; ++mi)
-#pragma unroll
-          for (int ni = 0; ni < kNI; ++ni) acc[b][mi][ni] = tm_mfma32x32x16<DT>(fa[mi], fb[b][ni], acc[b][mi][ni]);
-    }
+  issue(ring0, 0);
+  issue(ring1, 1);
+  issue(ring2, 2);
+  issue(ring3, 3);
+  tm_wait_vm_lgkm0<3 * kDma>();  // stage 0 of this wave landed
+  __builtin_amdgcn_s_barrier();
+  tm_static_for<kFrag>([&](auto g_c) { read_one(g_c, fr[0], ring0, 0); });
+
+  // stage i in ring slot `cur`, stage i + 1 in `nxt`
+  auto step = [&](uint4 *cur, const uint4 *nxt, int i) {
+    kstep(std::false_type{}, fr[0], fr[1], cur, 1, cur, 0);
+    tm_wait_vm_lgkm0<2 * kDma>();  // stage i + 1 of this wave landed (i + 2, i + 3 may fly); reads done
+    __builtin_amdgcn_s_barrier();  // ... in every wave; no wave reads slot `cur` any more
+    kstep(std::true_type{}, fr[1], fr[0], nxt, 0, cur, i + 4);
+  };
+  for (int i = 0; i < KT; i += 4) {
+    step(ring0, ring1, i);
+    step(ring1, ring2, i + 1);
+    step(ring2, ring3, i + 2);
+    step(ring3, ring0, i + 3);
   }
   tm_wait_vm_lgkm0<0>();  // no load may still target this workgroup's LDS when it exits
+  __syncthreads();         // ... and every wave is done with the ring
 
-  // Epilogue: lane owns column (lane % 32) of each block and its 16 rows.
+  // Epilogue through LDS, kStageCols columns at a time.  Each wave writes its
+  // fp32 results (up mode: silu(dtype(g)) * u, unrounded) to the staging tile
+  // [BM][kStageLd]: lane owns column (lane % 32) of each block and its 16 rows
+  // 8 (i / 4) + 4 (lane / 32) + i % 4 (the +8 float row padding puts the two
+  // row groups of one write on disjoint banks).  Then each thread rounds and
+  // stores 8-column chunks: 16 threads per 128-column row, so every store of a
+  // wave writes 4 whole rows (down mode adds the addend row chunk first, in
+  // fp32, one rounding).
+  float *const stage = reinterpret_cast<float *>(lds_all);
+  const int lrow = wm * 128 + 4 * (lane >> 5), lcol = wn * (BN / 2) + (lane & 31);
 #pragma unroll
-  for (int mi = 0; mi < kMI; ++mi)
+  for (int pass = 0; pass < BN / kStageCols; ++pass) {
+    if (pass > 0) __syncthreads();  // the previous pass's chunks are read
+    if (lcol - (lane & 31) >= pass * kStageCols && lcol - (lane & 31) < (pass + 1) * kStageCols) {  // uniform
+      float *w = stage + lrow * kStageLd + (lcol - pass * kStageCols);
 #pragma unroll
-    for (int ni = 0; ni < kNI; ++ni)
+      for (int mi = 0; mi < kMI; ++mi)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = wm * 128 + mi * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        const int col = n0 + wn * 64 + ni * 32 + (lane & 31);
-        const int gr = r0 + row;
-        if (gr >= r_end) continue;
-        float v;
-        if constexpr (MODE == kModeUp) {
-          const float g = tm_round<DT>(acc[0][mi][ni][i]);
-          const float u = acc[NB - 1][mi][ni][i];
-          v = (g / (1.f + __expf(-g))) * u;
-        } else {
-          v = acc[0][mi][ni][i];
-          if (addend != nullptr) v += Elem<DT>::to_f(addend[(int64_t)gr * ld_add + col]);  // dense rows only
+        for (int ni = 0; ni < kNI; ++ni)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            float v;
+            if constexpr (MODE == kModeUp) {
+              const float g = tm_round<DT>(acc[0][mi][ni][i]);
+              v = g * __builtin_amdgcn_rcpf(1.f + __expf(-g)) * acc[NB - 1][mi][ni][i];
+            } else {
+              v = acc[0][mi][ni][i];
+            }
+            w[(mi * 32 + 8 * (i >> 2) + (i & 3)) * kStageLd + ni * 32] = v;
+          }
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int k = 0; k < BM * kStageCols / 8 / kThreads; ++k) {
+      const int c = tid + k * kThreads;
+      const int row = c / (kStageCols / 8), col8 = (c % (kStageCols / 8)) * 8;
+      const int gr = r0 + row;
+      if (gr >= r_end) break;  // rows only grow with k
+      const int col = n0 + pass * kStageCols + col8;
+      float v[8];
+      const float4 *src = reinterpret_cast<const float4 *>(stage + row * kStageLd + col8);
+      const float4 lo = src[0], hi = src[1];
+      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w; v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+      if constexpr (MODE == kModeDown) {
+        if (addend != nullptr) {  // dense rows only
+          float a[8];
+          tm_load8<DT>(addend + (int64_t)gr * ld_add + col, a);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] += a[j];
         }
-        const int64_t dst = c_rows ? c_rows[gr] + col : (int64_t)gr * ldc + col;
-        C[dst] = Elem<DT>::from_f(v);
       }
+      tm_store8<DT>(C + (c_rows ? c_rows[gr] + col : (int64_t)gr * ldc + col), v);
+    }
+  }
 }
 
 // One workgroup of kGroupThreads: bucket the recomputed (token, slot) pairs
@@ -293,14 +400,14 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
   }
 }
 
-template <int DT, int NB, int MODE>
+template <int DT, int NB, int MODE, int BN>
 void launch_gemm(const void *A, int64_t lda, const int32_t *a_rows, const void *B0, const void *B1, int64_t b_expert,
                  int K, int N, const TileSrc &ts, int64_t grid_y, void *C, int64_t ldc, const int64_t *c_rows,
                  const void *addend, int64_t ld_add, hipStream_t s) {
   using T = typename Elem<DT>::T;
   const int n_tiles = N / BN;
   const int64_t blocks = tm_cdiv(grid_y, 8) * 8 * n_tiles;
-  hipLaunchKernelGGL((grouped_gemm_kernel<DT, NB, MODE>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
+  hipLaunchKernelGGL((grouped_gemm_kernel<DT, NB, MODE, BN>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
                      static_cast<const T *>(A), lda, a_rows, static_cast<const T *>(B0), static_cast<const T *>(B1),
                      b_expert, K, n_tiles, ts, static_cast<T *>(C), ldc, c_rows, static_cast<const T *>(addend),
                      ld_add);
@@ -317,11 +424,15 @@ int swiglu_impl(int32_t dtype, const void *x, int64_t ld_x, const int32_t *row_t
     if constexpr (DT == TM_DT_F32) {
       return tm_fail(TM_EINVAL_DTYPE, "tm_grouped_swiglu: dtype must be F16 or BF16");
     } else {
-      launch_gemm<DT, 2, kModeUp>(x, ld_x, row_token, w1, w3, (int64_t)inter * hidden, hidden, inter, ts, grid_y,
-                                  fused, inter, nullptr, nullptr, 0, s);
+      launch_gemm<DT, 2, kModeUp, kMinBN>(x, ld_x, row_token, w1, w3, (int64_t)inter * hidden, hidden, inter, ts,
+                                          grid_y, fused, inter, nullptr, nullptr, 0, s);
       TM_LAUNCH_CHECK("tm_grouped_swiglu(up)");
-      launch_gemm<DT, 1, kModeDown>(fused, inter, nullptr, w2, nullptr, (int64_t)hidden * inter, inter, hidden, ts,
-                                    grid_y, out, ld_out, row_out, addend, ld_add, s);
+      if (hidden % (2 * kMinBN) == 0)  // 256-column tiles: half the LDS reads per MFMA of 128-column ones
+        launch_gemm<DT, 1, kModeDown, 2 * kMinBN>(fused, inter, nullptr, w2, nullptr, (int64_t)hidden * inter, inter,
+                                                  hidden, ts, grid_y, out, ld_out, row_out, addend, ld_add, s);
+      else
+        launch_gemm<DT, 1, kModeDown, kMinBN>(fused, inter, nullptr, w2, nullptr, (int64_t)hidden * inter, inter,
+                                              hidden, ts, grid_y, out, ld_out, row_out, addend, ld_add, s);
       TM_LAUNCH_CHECK("tm_grouped_swiglu(down)");
       return TM_OK;
     }
@@ -329,8 +440,9 @@ int swiglu_impl(int32_t dtype, const void *x, int64_t ld_x, const int32_t *row_t
 }
 
 bool shapes_ok(int32_t hidden, int32_t inter) {
-  return hidden > 0 && inter > 0 && hidden % BN == 0 && inter % BN == 0 && hidden % BK == 0 && inter % BK == 0 &&
-         hidden / BK >= 1 && inter / BK >= 1;
+  // multiples of 128: whole column tiles, and K in whole rounds of the 4-slot ring (4 stages of BK)
+  return hidden > 0 && inter > 0 && hidden % kMinBN == 0 && inter % kMinBN == 0 && (int64_t)inter * hidden <
+         ((int64_t)1 << 30);
 }
 
 }  // namespace
@@ -368,14 +480,15 @@ extern "C" int tm_grouped_swiglu(int32_t dtype, const void *x, int64_t ld_x, int
                                  const int32_t *tiles, void *out, void *workspace, size_t workspace_bytes,
                                  tm_stream_t stream) {
   TM_REQUIRE(shapes_ok(hidden, inter), TM_EINVAL_SHAPE,
-             "tm_grouped_swiglu: hidden and inter must be positive multiples of %d", BN);
+             "tm_grouped_swiglu: hidden and inter must be positive multiples of %d", kMinBN);
   TM_REQUIRE(n_experts >= 1 && max_rows >= 0 && max_rows < ((int64_t)1 << 31) && ld_x >= hidden, TM_EINVAL_SHAPE,
              "tm_grouped_swiglu: bad sizes");
   if (max_rows == 0) return TM_OK;
   TM_REQUIRE(x && w1 && w3 && w2 && expert_offsets && row_token && row_out && tiles && out, TM_EINVAL_ARG,
              "tm_grouped_swiglu: null pointer");
-  TM_REQUIRE(tm_aligned16(x) && (ld_x * 2) % 16 == 0 && tm_aligned16(w1) && tm_aligned16(w3) && tm_aligned16(w2),
-             TM_EINVAL_SHAPE, "tm_grouped_swiglu: x rows and weights must be 16-byte aligned");
+  TM_REQUIRE(tm_aligned16(x) && (ld_x * 2) % 16 == 0 && tm_aligned16(w1) && tm_aligned16(w3) && tm_aligned16(w2) &&
+                 tm_aligned16(out),
+             TM_EINVAL_SHAPE, "tm_grouped_swiglu: x rows, weights and out must be 16-byte aligned");
   const size_t need = tm_swiglu_workspace_size(max_rows, inter, dtype);
   TM_REQUIRE(workspace != nullptr && workspace_bytes >= need && tm_aligned16(workspace), TM_EWORKSPACE,
              "tm_grouped_swiglu: workspace %zu bytes < %zu", workspace_bytes, need);
@@ -392,14 +505,16 @@ int expert_swiglu_impl(const char *name, int32_t dtype, const void *x, int64_t n
                        int64_t ld_add, void *out, int64_t ld_out, void *workspace, size_t workspace_bytes,
                        tm_stream_t stream) {
   TM_REQUIRE(shapes_ok(hidden, inter), TM_EINVAL_SHAPE, "%s: hidden and inter must be positive multiples of %d",
-             name, BN);
+             name, kMinBN);
   TM_REQUIRE(n_rows >= 0 && n_rows < ((int64_t)1 << 31) && ld_x >= hidden && ld_out >= hidden &&
                  (addend == nullptr || ld_add >= hidden),
              TM_EINVAL_SHAPE, "%s: bad sizes", name);
   if (n_rows == 0) return TM_OK;
   TM_REQUIRE(x && w1 && w3 && w2 && out, TM_EINVAL_ARG, "%s: null pointer", name);
-  TM_REQUIRE(tm_aligned16(x) && (ld_x * 2) % 16 == 0 && tm_aligned16(w1) && tm_aligned16(w3) && tm_aligned16(w2),
-             TM_EINVAL_SHAPE, "%s: x rows and weights must be 16-byte aligned", name);
+  TM_REQUIRE(tm_aligned16(x) && (ld_x * 2) % 16 == 0 && tm_aligned16(w1) && tm_aligned16(w3) && tm_aligned16(w2) &&
+                 tm_aligned16(out) && (ld_out * 2) % 16 == 0 &&
+                 (addend == nullptr || (tm_aligned16(addend) && (ld_add * 2) % 16 == 0)),
+             TM_EINVAL_SHAPE, "%s: x, out and addend rows and the weights must be 16-byte aligned", name);
   const size_t need = tm_swiglu_workspace_size(n_rows, inter, dtype);
   TM_REQUIRE(workspace != nullptr && workspace_bytes >= need && tm_aligned16(workspace), TM_EWORKSPACE,
              "%s: workspace %zu bytes < %zu", name, workspace_bytes, need);

@@ -13,6 +13,17 @@
 
 #include "tm_common.h"
 
+#include <type_traits>
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void tm_static_for(F &&f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    tm_static_for<N, I + 1>(f);
+  }
+}
+
 typedef __bf16 tm_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 tm_f16x8 __attribute__((ext_vector_type(8)));
 typedef float tm_f32x4 __attribute__((ext_vector_type(4)));

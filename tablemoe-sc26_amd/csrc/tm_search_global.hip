@@ -219,33 +219,6 @@ __device__ __forceinline__ void block_epilogue(const tm_f32x16 &acc, const float
 constexpr int kDmaBufs = 4;
 constexpr int kDmaStageBytes = 16384;
 
-// The same direct-to-LDS load through a buffer resource (4 SGPRs: base,
-// stride 0, size in bytes, raw 32-bit format): lanes whose byte offset is at
-// or past the size are range-checked by the hardware and read nothing, so a
-// stage that runs past the end of the table needs no clamping.
-typedef uint32_t tm_rsrc_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ tm_rsrc_t tm_make_rsrc(const void *base, uint64_t bytes) {
-  const uint64_t a = (uint64_t)(uintptr_t)base;
-  tm_rsrc_t r;
-  r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);  // stride 0
-  r.z = __builtin_amdgcn_readfirstlane((uint32_t)(bytes < 0xffffffffull ? bytes : 0xffffffffull));
-  r.w = 0x00020000u;  // raw buffer, 32-bit data format
-  return r;
-}
-
-__device__ __forceinline__ void tm_dma16_buf(tm_rsrc_t rsrc, uint32_t voff, uint32_t lds_base) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(voff), "s"(rsrc), "s"(lds_base)
-      : "memory");
-}
 
 
 template <int DT, int DIM, int K, int METRIC>
@@ -405,14 +378,6 @@ __global__ __launch_bounds__(kThreads, 2) void search_dma_kernel(
 // t+3.  The stage count is padded to whole rounds of the ring so the loop
 // body has no branch; padded stages meet -inf start values.
 // ---------------------------------------------------------------------------
-// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
-template <int N, int I = 0, typename F>
-__device__ __forceinline__ void tm_static_for(F &&f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    tm_static_for<N, I + 1>(f);
-  }
-}
 
 struct Top1Lane {
   float r;      // running maximum
