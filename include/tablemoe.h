@@ -517,12 +517,24 @@ typedef struct tm_layer_io {
 /* sizeof(tm_table_layer) for which == 0, sizeof(tm_layer_io) for which == 1
  * (lets a binding check its mirror of the two structs). */
 size_t tm_struct_size(int32_t which);
-/* Workspace of tm_table_forward.  Its first 256 bytes hold arrival counters
- * (batches of at most 64 tokens reduce the projection across workgroups;
- * larger top-1 batches decode each query tile's search result in the tile's
- * last workgroup): they must be zero before the first call on a workspace
- * (allocate it zero-filled) and every call leaves them zero.  Calls that
- * share one workspace must not overlap (one stream). */
+/* Workspace of tm_table_forward.  Its first TM_LAYER_SYNC_BYTES bytes hold
+ * arrival counters and flags (batches of at most 64 tokens hand the
+ * projection and the search results between workgroups; larger top-1 batches
+ * decode each query tile's search result in the tile's last workgroup): they
+ * must be zero before the first call on a workspace (allocate it
+ * zero-filled); every call leaves the counters zero and the flags at a
+ * generation the next call continues from.  Calls that share one workspace
+ * must not overlap (one stream).
+ *
+ * Batches of at most 64 tokens may run as one launch whose workgroups wait
+ * for each other (bounded waits; the launch assumes its 128 workgroups can
+ * be resident together, as on an otherwise idle device).  A wait that runs
+ * out (20 ms) adds one to the uint32 at byte TM_LAYER_SYNC_ERR_BYTE of the
+ * workspace; that call's outputs are then undefined (the row chunks the
+ * waiting workgroup writes are NaN).  The library never clears the word
+ * (zero = no wait ever ran out). */
+#define TM_LAYER_SYNC_BYTES 16384
+#define TM_LAYER_SYNC_ERR_BYTE 5760
 size_t tm_table_forward_workspace_size(const tm_table_layer *table, int64_t n_tokens, int32_t n_nearest);
 int tm_table_forward(const tm_table_layer *table, const tm_layer_io *io, void *workspace,
                      size_t workspace_bytes, void *const *stage_events, tm_stream_t stream);

@@ -37,6 +37,7 @@ constexpr int kRound = 16;     // k-steps of operand loads issued together per w
 constexpr int kKeyRep = 8;     // replicas of the best-key array (spreads the search's atomics)
 constexpr int kChunk = 512;    // row elements per finishing wave (64 lanes x 8)
 constexpr int kMaxLists = 4;   // split lists per lane in the finishing kernel (nsplit <= 256)
+constexpr int kStreamChunkD = 128;  // centroids per search split (tm_internal_stream_nsplit's split size)
 
 struct SliceRoute {
   tm_route_args a;
@@ -80,30 +81,39 @@ __global__ __launch_bounds__(64) void project_split_kernel(
   const int klast = ks_end - 1;  // >= 0 (an empty slice clamps to the last k-step and multiplies nothing)
   const int kq = 8 * (lane >> 4);
 
-  // modality of the tile's rows first: the operand loads depend on it
+  // modality of the tile's rows (which P each row multiplies)
   const uint8_t *vsrc = is_vision ? is_vision + (arow_ok ? arow : 0) : reinterpret_cast<const uint8_t *>(x);
   const uint8_t vis_byte = *vsrc;
   // the reducer's bias values, loaded now so their latency hides behind the slice
   const int col = cb * 16 + (lane & 15);
   const float bias_v = Elem<DT>::to_f(bv[col]);
   const float bias_t = Elem<DT>::to_f(bt[col]);
+
+  tm_f32x4 fin = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+  // whole-k-step slices: x and both modalities' P loaded at once, so no P
+  // load waits for the modality byte
+  constexpr int KA = KPW > 0 ? KPW : 1;
+  uint4 xa[KA], pva[KA], pta[KA];
+  if constexpr (KPW > 0) {
+    const uint4 *pvf = reinterpret_cast<const uint4 *>(pv) + lane;
+    const uint4 *ptf = reinterpret_cast<const uint4 *>(pt) + lane;
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) {
+      xa[j] = *reinterpret_cast<const uint4 *>(xrow + (ks_begin + j) * 32 + kq);
+      pva[j] = pvf[((int64_t)(ks_begin + j) * NCB + cb) * 64];
+      pta[j] = ptf[((int64_t)(ks_begin + j) * NCB + cb) * 64];
+    }
+  }
   const int amod = !arow_ok ? 2 : ((is_vision == nullptr || vis_byte) ? 0 : 1);
   const uint32_t vis_bits = (uint32_t)(__ballot(amod == 0) & 0xFFFFull);
   const uint32_t txt_bits = (uint32_t)(__ballot(amod == 1) & 0xFFFFull);
-
-  tm_f32x4 fin = tm_f32x4{0.f, 0.f, 0.f, 0.f};
   auto run_pass = [&](const T *P, uint32_t rows_of_pass) {
     const uint4 *pf = reinterpret_cast<const uint4 *>(P) + lane;
     tm_f32x4 acc = tm_f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (KPW > 0) {
-      uint4 ar[KPW], br[KPW];
+      const bool is_v = P == pv;  // uniform
 #pragma unroll
-      for (int j = 0; j < KPW; ++j) {
-        ar[j] = *reinterpret_cast<const uint4 *>(xrow + (ks_begin + j) * 32 + kq);
-        br[j] = pf[((int64_t)(ks_begin + j) * NCB + cb) * 64];
-      }
-#pragma unroll
-      for (int j = 0; j < KPW; ++j) acc = tm_mfma16x16x32<DT>(ar[j], br[j], acc);
+      for (int j = 0; j < KPW; ++j) acc = tm_mfma16x16x32<DT>(xa[j], is_v ? pva[j] : pta[j], acc);
     } else {
     for (int r0 = ks_begin; r0 < ks_end; r0 += kRound) {  // uniform; one round for hidden <= 32 * S * kRound
       uint4 ar[kRound], br[kRound];
@@ -366,6 +376,607 @@ __global__ __launch_bounds__(64) void decode_finish_kernel(
   if (h0 < hidden) tm_store8_nt<DT>(dst, acc);
 }
 
+// ---------------------------------------------------------------------------
+// One-launch decode plan (decode_fused_kernel): the three launches above as
+// three phases of one launch of kFusedWGs four-wave workgroups.  A phase
+// whose inputs come from other workgroups waits on a grid-wide flag.
+//   A  projection tasks (project_split_kernel's work; task t runs on wave
+//      t / G of workgroup t % G).  The last wave of a (tile, column block)
+//      group writes q and the block's |q|^2 and counts the group on q_cnt;
+//      the wave that completes q_cnt raises go_a.
+//   B  workgroup s < nsplit searches split s (search_stream_kernel's work) and
+//      publishes its lists and best keys; every workgroup then counts itself
+//      on one of kSubCnt sub-counters, the last arrival of each counts on
+//      s_top, and the last of those raises go_b.
+//   C  wave 3 - t / G of workgroup t % G finishes task t = (token, row
+//      chunk) (decode_finish_kernel's work, the same arithmetic); counting
+//      the waves from the other end keeps the routing these waves do off the
+//      projection waves.
+// What does not depend on another workgroup is loaded before the first wait:
+// the split's centroid rows and norms, the task's residual chunk and slot
+// rows, and the weights when the router ran in its own launch.  Otherwise each
+// finishing wave routes its own token (tm_route_compute, the router kernel's
+// routine, so the same bits) while the projection runs.
+//
+// Flags carry a generation: every wave reads gen at the start, a flag raised
+// in this call holds gen + 1 and the wave that raises go_b advances gen, so
+// no flag is ever cleared; each counter is cleared by the arrival that
+// completes it.  Data handed between workgroups moves through agent-scope
+// atomic loads and stores, which the hardware performs at one point of
+// coherence per address for every XCD (the loads bypass the non-coherent
+// per-XCD L2), and the counts through agent-scope atomics.  A producer's
+// s_waitcnt vmcnt(0) (gfx9 counts stores and returnless atomics in vmcnt)
+// returns only after its stores are acknowledged, and only then does it
+// count; a consumer loads only after it saw the flag.  Agent-scope
+// release/acquire fences would write back and invalidate whole L2s
+// instead (measured at microseconds per launch).  Every wait polls with a
+// bound of kSpinTicks ticks of the 100 MHz constant clock: a wait that runs
+// out counts on the err word, and that workgroup's output chunks are
+// written as NaN, so a launch whose workgroups could not all be resident at
+// once (another kernel filling the device) ends with flagged outputs instead
+// of hanging.
+// ---------------------------------------------------------------------------
+constexpr int kFusedWGs = 128;
+constexpr int kGoRep = 16;     // copies of each go flag (the pollers spread over them)
+constexpr int kSubCnt = 8;     // sub-counters of the search arrival
+constexpr int kLine = 32;      // words per 128-byte line: each hot word on a line of its own
+constexpr uint64_t kSpinTicks = 2000000;  // 20 ms
+static_assert(kFusedWGs % kSubCnt == 0, "whole sub-counter groups");
+// word offsets in the layer workspace's sync region (words 0 .. 63 belong to
+// the other plans' counters)
+constexpr int kWGen = 64;
+constexpr int kWQcnt = kWGen + kLine;
+constexpr int kWStop = kWQcnt + kLine;
+constexpr int kWSsub = kWStop + kLine;
+constexpr int kWGoA = kWSsub + kSubCnt * kLine;
+constexpr int kWGoB = kWGoA + kGoRep * kLine;
+constexpr int kWErr = kWGoB + kGoRep * kLine;
+constexpr int kWGrp = kWErr + kLine;  // the projection groups' counters, one line each
+constexpr int kMaxGroups = 64 / 16 * 128 / 16;  // (64 rows / 16) x (d 128 / 16)
+static_assert((kWGrp + kMaxGroups * kLine) * 4 <= TM_LAYER_SYNC_BYTES, "sync region");
+static_assert(kWErr * 4 == TM_LAYER_SYNC_ERR_BYTE, "documented err word");
+
+struct FusedArgs {
+  int64_t n, nsplit, n_cent, ld_c, n_keep, ld_x, ld_logits, so_b, so_s, ld_v, ld_r, ld_o;
+  int hidden, n_chunks, l2, routed, n_experts, has_res;
+  const void *x;
+  const uint8_t *is_vision;
+  const void *pv, *bv, *pt, *bt;
+  void *q;
+  float *qn_blk;
+  float4 *part;
+  const void *cents;
+  const float *c_sqnorm;
+  uint64_t *lists, *keys;
+  const float *logits;
+  float *w;      // router outputs (routed) or the router weights (input)
+  int64_t *ids;  // router outputs (routed)
+  const void *slot_out, *values, *residual;
+  void *out;
+  float *out_dist;
+  int64_t *out_idx;
+  float *out_qn;
+  uint8_t *out_keep;
+  uint32_t *sync;
+};
+
+__device__ __forceinline__ uint64_t coh_ld(const uint64_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_st(uint64_t *p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_st32(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t coh_add(uint32_t *p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Poll one flag until it holds `want`; false when kSpinTicks passed first.
+__device__ __forceinline__ bool wait_flag(const uint32_t *f, uint32_t want) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want) {
+    if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return true;
+}
+
+// Phase A of decode_fused_kernel: project_split_kernel's wave (hidden ==
+// 32 * kSlices * KPW).  fused_project_loads issues every operand load of
+// task `task` at once -- x, both modalities' P (so no load waits for the
+// modality byte) and the biases -- and fused_project_task multiplies,
+// publishes and, in the group's last wave, reduces; its hand-offs are
+// coherent stores, and the wave that completes q_cnt raises go_a.
+template <int DT, int KPW>
+struct ProjOps {
+  uint4 x[KPW], pv[KPW], pt[KPW];
+  typename Elem<DT>::T bias_v, bias_t;  // raw: converted where used
+  uint8_t vis;
+};
+
+template <int DT, int DIM, int KPW>
+__device__ __forceinline__ void fused_project_loads(const FusedArgs &a, int64_t task, int lane, ProjOps<DT, KPW> &o) {
+  using T = typename Elem<DT>::T;
+  constexpr int NCB = DIM / 16;
+  constexpr int S = kSlices;
+  const int64_t n = a.n;
+  const int sl = (int)(task % S);
+  const int64_t g = task / S;
+  const int cb = (int)(g % NCB);
+  const int64_t arow = (g / NCB) * 16 + (lane & 15);
+  const bool arow_ok = arow < n;
+  const T *x = static_cast<const T *>(a.x);
+  const T *xrow = x + (arow_ok ? arow : 0) * a.ld_x;
+  const int ks_begin = sl * KPW;
+  const int kq = 8 * (lane >> 4);
+  const uint8_t *vsrc = a.is_vision ? a.is_vision + (arow_ok ? arow : 0) : reinterpret_cast<const uint8_t *>(x);
+  o.vis = *vsrc;
+  const int col = cb * 16 + (lane & 15);
+  o.bias_v = static_cast<const T *>(a.bv)[col];
+  o.bias_t = static_cast<const T *>(a.bt)[col];
+  const uint4 *pvf = reinterpret_cast<const uint4 *>(a.pv) + lane;
+  const uint4 *ptf = reinterpret_cast<const uint4 *>(a.pt) + lane;
+#pragma unroll
+  for (int j = 0; j < KPW; ++j) {
+    o.x[j] = *reinterpret_cast<const uint4 *>(xrow + (ks_begin + j) * 32 + kq);
+    o.pv[j] = pvf[((int64_t)(ks_begin + j) * NCB + cb) * 64];
+    o.pt[j] = ptf[((int64_t)(ks_begin + j) * NCB + cb) * 64];
+  }
+}
+
+template <int DT, int DIM, int KPW>
+__device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t task, uint32_t g0v, int lane,
+                                                   const ProjOps<DT, KPW> &o) {
+  using T = typename Elem<DT>::T;
+  constexpr int NCB = DIM / 16;
+  constexpr int S = kSlices;
+  const int64_t n = a.n;
+  const int sl = (int)(task % S);
+  const int64_t g = task / S;
+  const int cb = (int)(g % NCB);
+  const int64_t row0 = (g / NCB) * 16;
+  const int64_t arow = row0 + (lane & 15);
+  const bool arow_ok = arow < n;
+  const int amod = !arow_ok ? 2 : ((a.is_vision == nullptr || o.vis) ? 0 : 1);
+  const uint32_t vis_bits = (uint32_t)(__ballot(amod == 0) & 0xFFFFull);
+  const uint32_t txt_bits = (uint32_t)(__ballot(amod == 1) & 0xFFFFull);
+  tm_f32x4 fin = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+  auto run_pass = [&](const uint4 (&br)[KPW], uint32_t rows_of_pass) {
+    tm_f32x4 acc = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) acc = tm_mfma16x16x32<DT>(o.x[j], br[j], acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if ((rows_of_pass >> (4 * (lane >> 4) + i)) & 1u) fin[i] = acc[i];
+  };
+  if (vis_bits) run_pass(o.pv, vis_bits);  // uniform branches
+  if (txt_bits) run_pass(o.pt, txt_bits);
+  const float bias_v = Elem<DT>::to_f(o.bias_v), bias_t = Elem<DT>::to_f(o.bias_t);
+
+  // reset the tile's best keys (every replica) for phase B
+  if (cb == 0 && lane < 16 && arow_ok)
+    for (int r = sl; r < kKeyRep; r += S) coh_st(a.keys + (int64_t)r * n + arow, ~0ull);
+
+  // publish this slice's partial, count it on the group
+  uint64_t *pp = reinterpret_cast<uint64_t *>(a.part) + ((g * S + sl) * 64 + lane) * 2;
+  coh_st(pp, ((uint64_t)__float_as_uint(fin[1]) << 32) | __float_as_uint(fin[0]));
+  coh_st(pp + 1, ((uint64_t)__float_as_uint(fin[3]) << 32) | __float_as_uint(fin[2]));
+  __builtin_amdgcn_s_waitcnt(0);
+  uint32_t ticket = 0;
+  if (lane == 0) ticket = coh_add(a.sync + kWGrp + g * kLine);
+  ticket = (uint32_t)__builtin_amdgcn_readfirstlane((int)ticket);
+  if (ticket != S - 1) return;  // uniform: not the group's last slice
+  if (lane == 0) coh_st32(a.sync + kWGrp + g * kLine, 0u);
+
+  // the group's last wave: the S partials added in slice order, bias, one rounding
+  uint64_t pv2[S][2];
+#pragma unroll
+  for (int s2 = 0; s2 < S; ++s2) {
+    const uint64_t *src = reinterpret_cast<const uint64_t *>(a.part) + ((g * S + s2) * 64 + lane) * 2;
+    pv2[s2][0] = coh_ld(src);
+    pv2[s2][1] = coh_ld(src + 1);
+  }
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s2 = 0; s2 < S; ++s2) {
+    v[0] += __uint_as_float((uint32_t)pv2[s2][0]);
+    v[1] += __uint_as_float((uint32_t)(pv2[s2][0] >> 32));
+    v[2] += __uint_as_float((uint32_t)pv2[s2][1]);
+    v[3] += __uint_as_float((uint32_t)(pv2[s2][1] >> 32));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * (lane >> 4) + i;
+    const bool vis = (vis_bits >> r) & 1u;
+    v[i] = tm_round<DT>(v[i] + (vis ? bias_v : bias_t));
+    float sq = v[i] * v[i];
+    sq += __shfl_xor(sq, 1, 64);
+    sq += __shfl_xor(sq, 2, 64);
+    sq += __shfl_xor(sq, 4, 64);
+    sq += __shfl_xor(sq, 8, 64);
+    const int64_t gr = row0 + r;
+    if (gr < n && (lane & 15) == 0) coh_st32(reinterpret_cast<uint32_t *>(a.qn_blk + gr * NCB + cb), __float_as_uint(sq));
+  }
+  // q in 8-byte pieces: lane l writes row 4 (l / 16) + l % 4, columns 4 ((l % 16) / 4) .. + 3 of the block
+  uint64_t piece = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float y = __shfl(v[i], (lane & ~3) + t, 64);
+      if (i == (lane & 3)) piece |= (uint64_t)__builtin_bit_cast(uint16_t, Elem<DT>::from_f(y)) << (16 * t);
+    }
+  const int64_t qrow = row0 + 4 * (lane >> 4) + (lane & 3);
+  if (qrow < n)
+    coh_st(reinterpret_cast<uint64_t *>(static_cast<T *>(a.q) + qrow * DIM + cb * 16 + 4 * ((lane & 15) >> 2)), piece);
+  __builtin_amdgcn_s_waitcnt(0);
+  uint32_t qt = 0;
+  if (lane == 0) qt = coh_add(a.sync + kWQcnt);
+  qt = (uint32_t)__builtin_amdgcn_readfirstlane((int)qt);
+  const uint32_t ngroups = (uint32_t)(((n + 15) / 16) * NCB);
+  if (qt == ngroups - 1) {  // uniform: q is complete
+    const uint32_t gen = (uint32_t)__builtin_amdgcn_readfirstlane((int)g0v);
+    if (lane == 0) coh_st32(a.sync + kWQcnt, 0u);
+    if (lane < kGoRep) coh_st32(a.sync + kWGoA + lane * kLine, gen + 1);
+  }
+}
+
+template <int DT, int DIM, int KPW, int K, int TK>
+__global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
+  using T = typename Elem<DT>::T;
+  constexpr int KS = DIM / 16;
+  constexpr int NCB = DIM / 16;
+  constexpr int S = kSlices;
+  constexpr int NN = K;
+  __shared__ uint64_t merge_buf[4][K][64];
+  __shared__ uint4 q_lds[64 * DIM / 8];
+  __shared__ uint32_t s_ok;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wg = (int)blockIdx.x;
+  const int G = (int)gridDim.x;
+  const int64_t n = a.n;
+  uint32_t *const sync = a.sync;
+
+  // Loads in the order they are needed (vmcnt retires them in order): the
+  // projection task's operands, the split's centroid block and norms, the
+  // finishing task's rows, then this call's generation.  Every one is
+  // unconditional (clamped or redirected addresses): a load under a branch
+  // makes the compiler wait for it, and for all loads before it, right there.
+  const int64_t ta = (int64_t)wave * G + wg;
+  const int64_t ta_n = ((n + 15) / 16) * NCB * S;
+  const bool has_a = ta < ta_n;  // uniform per wave
+  ProjOps<DT, KPW> po;
+  if (has_a) fused_project_loads<DT, DIM, KPW>(a, ta, lane, po);
+
+  const bool has_split = wg < a.nsplit;  // uniform
+  const int64_t c_begin = (int64_t)wg * kStreamChunkD;
+  const int64_t c_end = (c_begin + kStreamChunkD < a.n_cent) ? c_begin + kStreamChunkD : a.n_cent;
+  const int64_t c0 = c_begin + 32 * wave;
+  const T *cents = static_cast<const T *>(a.cents);
+  uint4 af[KS];
+  {
+    const int64_t cr = c0 + (lane & 31);
+    const int64_t crr = cr < a.n_cent ? cr : a.n_cent - 1;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      af[ks] = *reinterpret_cast<const uint4 *>(cents + crr * a.ld_c + ks * 16 + 8 * (lane >> 5));
+  }
+  float pen[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t cm = c0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    pen[i] = a.c_sqnorm[cm < a.n_cent ? cm : a.n_cent - 1];  // a readable stand-in for the dot metric
+  }
+
+  const int ntc = (int)n * a.n_chunks;
+  const int tc = (3 - wave) * G + wg;  // from the last wave down: the first waves take the projection
+  const bool has_c = tc < ntc;  // uniform per wave
+  const int b = has_c ? tc / a.n_chunks : 0;
+  const int ch = has_c ? tc % a.n_chunks : 0;
+  const int h0 = ch * kChunk + lane * 8;
+  const int hl = h0 < a.hidden ? h0 : a.hidden - 8;
+  // the finishing task's rows, kept raw (converting them here would make the
+  // compiler wait for them here)
+  tm_u32x4 rrow, srow[TK];
+  float wv[TK];
+  if (has_c) {
+    rrow = __builtin_nontemporal_load(
+        reinterpret_cast<const tm_u32x4 *>(static_cast<const T *>(a.residual) + (int64_t)b * a.ld_r + hl));
+    const T *src = static_cast<const T *>(a.slot_out) + (int64_t)b * a.so_b + hl;
+#pragma unroll
+    for (int s = 0; s < TK; ++s)
+      srow[s] = __builtin_nontemporal_load(reinterpret_cast<const tm_u32x4 *>(src + (int64_t)s * a.so_s));
+#pragma unroll
+    for (int s = 0; s < TK; ++s) wv[s] = a.w[(int64_t)b * TK + s];  // replaced by the routing below when routed
+  }
+
+  // this call's generation: moved to a scalar only where it is used, so no
+  // wait for it (and for every load before it) lands here
+  uint32_t g0v = 0;
+  if (lane == 0) g0v = __hip_atomic_load(sync + kWGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  auto g0 = [&] { return (uint32_t)__builtin_amdgcn_readfirstlane((int)g0v); };
+
+  // ---- phase A: projection task ----
+  if (has_a) fused_project_task<DT, DIM, KPW>(a, ta, g0v, lane, po);
+  if (!a.l2) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pen[i] = 0.f;
+  }
+  // the finishing wave routes its token
+  if (a.routed && has_c) {
+    float kw[8];
+    int ki[8];
+    float wsum;
+    if (a.n_experts == 64)
+      tm_route_compute<8, 8>(a.logits, n, a.ld_logits, TK, b, lane & 7, kw, ki, wsum);
+    else
+      tm_route_compute<16, 8>(a.logits, n, a.ld_logits, TK, b, lane & 7, kw, ki, wsum);
+#pragma unroll
+    for (int s = 0; s < TK; ++s) wv[s] = kw[s];
+    if (ch == 0 && lane == 0) {
+#pragma unroll
+      for (int s = 0; s < TK; ++s) {
+        a.w[(int64_t)b * TK + s] = kw[s];
+        a.ids[(int64_t)b * TK + s] = ki[s];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t cm = c0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+    pen[i] = cm < c_end ? pen[i] : __builtin_huge_valf();
+  }
+
+  // ---- wait for q ----
+  __syncthreads();
+  if (tid == 0) {
+    const bool ok = wait_flag(sync + kWGoA + (wg % kGoRep) * kLine, g0() + 1);
+    if (!ok) coh_add(sync + kWErr);
+    s_ok = ok ? 1u : 0u;
+  }
+  __syncthreads();
+  bool poison = s_ok == 0u;
+
+  // ---- phase B: search split wg ----
+  if (has_split) {  // uniform
+    const bool two = n > 32;
+    const T *q = static_cast<const T *>(a.q);
+    // q (32 or 64 rows) comes into LDS once per workgroup, 16-byte chunk j
+    // of row r at r * CH + (j ^ (r % CH)) (conflict-free fragment reads)
+    constexpr int CH = DIM / 8;
+    const int rows = two ? 64 : 32;
+    for (int c = tid; c < rows * CH; c += 256) {
+      const int r = c / CH, j = c % CH;
+      const int64_t rr = r < n ? r : n - 1;
+      const uint64_t *src = reinterpret_cast<const uint64_t *>(q + rr * DIM + j * 8);
+      const uint64_t lo = coh_ld(src), hi = coh_ld(src + 1);
+      q_lds[r * CH + (j ^ (r % CH))] = make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+    }
+    __syncthreads();
+    auto q_slab = [&](int sl, uint4 (&qf)[KS]) {
+      const int r = sl * 32 + (lane & 31);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qf[ks] = q_lds[r * CH + ((2 * ks + (lane >> 5)) ^ (r % CH))];
+    };
+    tm_f32x16 sacc[2];
+    sacc[0] = tm_f32x16{};
+    sacc[1] = tm_f32x16{};
+    {
+      uint4 qf[KS];
+      q_slab(0, qf);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) sacc[0] = tm_mfma32x32x16<DT>(af[ks], qf[ks], sacc[0]);
+    }
+    if (two) {  // uniform: rows 32 .. 63
+      uint4 qf[KS];
+      q_slab(1, qf);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) sacc[1] = tm_mfma32x32x16<DT>(af[ks], qf[ks], sacc[1]);
+    }
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      if (sl == 1 && !two) break;  // uniform
+      uint64_t l[K];
+#pragma unroll
+      for (int j = 0; j < K; ++j) l[j] = ~0ull;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int c = (int)c0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        const float dp = a.l2 ? fmaf(-2.f, sacc[sl][i], pen[i]) : (pen[i] - sacc[sl][i]);
+        uint64_t xk = dp == __builtin_huge_valf() ? ~0ull : (((uint64_t)tm_orderable(dp) << 32) | (uint32_t)c);
+#pragma unroll
+        for (int j = 0; j < K; ++j) {  // compare-swap chain (no branch)
+          const uint64_t lo = l[j] < xk ? l[j] : xk;
+          xk = l[j] < xk ? xk : l[j];
+          l[j] = lo;
+        }
+      }
+      uint64_t o[K];
+#pragma unroll
+      for (int j = 0; j < K; ++j) o[j] = __shfl_xor(l[j], 32, 64);
+      merge_min_k<K>(l, o);
+      if (lane < 32) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) merge_buf[wave][j][sl * 32 + lane] = l[j];
+      }
+    }
+    __syncthreads();
+    if (tid < (two ? 64 : 32)) {
+      const int r = tid;
+      uint64_t l[K];
+#pragma unroll
+      for (int j = 0; j < K; ++j) l[j] = merge_buf[0][j][r];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        uint64_t o[K];
+#pragma unroll
+        for (int j = 0; j < K; ++j) o[j] = merge_buf[w][j][r];
+        merge_min_k<K>(l, o);
+      }
+      if (r < n) {
+        if constexpr (K > 1) {
+          uint64_t *dst = a.lists + ((int64_t)wg * n + r) * K;
+#pragma unroll
+          for (int j = 0; j < K; ++j) coh_st(dst + j, l[j]);
+        }
+        atomicMin(reinterpret_cast<unsigned long long *>(a.keys + (int64_t)(wg % kKeyRep) * n + r),
+                  (unsigned long long)l[0]);
+      }
+    }
+  }
+  // ---- arrival, then wait for every split ----
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's list stores and key minima performed
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t t = coh_add(sync + kWSsub + (wg % kSubCnt) * kLine);
+    if (t == (uint32_t)(G / kSubCnt - 1)) {
+      coh_st32(sync + kWSsub + (wg % kSubCnt) * kLine, 0u);
+      const uint32_t u = coh_add(sync + kWStop);
+      if (u == kSubCnt - 1) {  // every workgroup arrived
+        coh_st32(sync + kWStop, 0u);
+        for (int i = 0; i < kGoRep; ++i) coh_st32(sync + kWGoB + i * kLine, g0() + 1);
+        coh_st32(sync + kWGen, g0() + 1);
+      }
+    }
+    const bool ok = wait_flag(sync + kWGoB + (wg % kGoRep) * kLine, g0() + 1);
+    if (!ok) coh_add(sync + kWErr);
+    s_ok = ok ? 1u : 0u;
+  }
+  __syncthreads();
+  poison = poison || s_ok == 0u;
+  if (!has_c) return;  // uniform per wave
+
+  // ---- phase C: token b, row chunk ch ----
+  const int jl = lane < n ? lane : (int)n - 1;
+  uint64_t kr[kKeyRep];
+#pragma unroll
+  for (int r = 0; r < kKeyRep; ++r) kr[r] = coh_ld(a.keys + (int64_t)r * n + jl);
+  float qb[NCB];
+#pragma unroll
+  for (int c = 0; c < NCB; c += 2) {
+    const uint64_t u = coh_ld(reinterpret_cast<const uint64_t *>(a.qn_blk + (int64_t)jl * NCB + c));
+    qb[c] = __uint_as_float((uint32_t)u);
+    qb[c + 1] = __uint_as_float((uint32_t)(u >> 32));
+  }
+  uint64_t lst[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) lst[j] = ~0ull;
+  if constexpr (K > 1) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      if (m == 1 && a.nsplit <= 64) break;  // uniform
+      const int64_t s = lane + 64 * m;
+      const uint64_t *src = a.lists + ((s < a.nsplit ? s : a.nsplit - 1) * n + b) * K;
+      uint64_t o[K];
+#pragma unroll
+      for (int j = 0; j < K; ++j) o[j] = s < a.nsplit ? coh_ld(src + j) : ~0ull;
+      merge_min_k<K>(lst, o);
+    }
+  }
+
+  // keep rank of token b among the n tokens' best distances
+  uint64_t kj = kr[0];
+#pragma unroll
+  for (int r = 1; r < kKeyRep; ++r) kj = kr[r] < kj ? kr[r] : kj;
+  const float qn_j = qn_tree<NCB>(qb);
+  int64_t ix_j;
+  const float d_j = tm_key_to_dist(kj, qn_j, a.l2 != 0, ix_j);
+  const uint32_t key_j = tm_orderable(d_j);
+  const uint32_t key_b = (uint32_t)__builtin_amdgcn_readlane((int)key_j, b);
+  const float qn_b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qn_j), b));
+  const bool ahead = lane < n && (key_j > key_b || (key_j == key_b && lane < b));
+  const int rank = __popcll(__ballot(ahead));
+  const int64_t n_keep = a.n_keep;
+  const bool kept = n_keep >= n ? true : (n_keep <= 0 ? false : rank < n_keep);
+
+  if constexpr (K > 1) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      uint64_t other[K];
+#pragma unroll
+      for (int j = 0; j < K; ++j) other[j] = __shfl_xor(lst[j], o, 64);
+      merge_min_k<K>(lst, other);
+    }
+  } else {
+    lst[0] = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kj, b) |
+             ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(kj >> 32), b) << 32);
+  }
+  float dn[NN];
+  int64_t cn[NN];
+#pragma unroll
+  for (int j = 0; j < NN; ++j) dn[j] = tm_key_to_dist(lst[j], qn_b, a.l2 != 0, cn[j]);
+
+  if (ch == 0 && lane == 0) {
+#pragma unroll
+    for (int j = 0; j < NN; ++j) {
+      a.out_dist[(int64_t)b * NN + j] = dn[j];
+      a.out_idx[(int64_t)b * NN + j] = cn[j];
+    }
+    a.out_keep[b] = kept ? 1 : 0;
+    a.out_qn[b] = qn_b;
+  }
+
+  float acc[8];
+  {
+    const T *e = reinterpret_cast<const T *>(&rrow);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = a.has_res ? Elem<DT>::to_f(e[i]) : 0.f;
+  }
+  T *dst = static_cast<T *>(a.out) + (int64_t)b * a.ld_o + hl;
+  if (kept) {  // uniform
+    float sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < TK; ++s) sum += wv[s];
+    const bool any = sum > 0.f;
+    float coef[TK];
+#pragma unroll
+    for (int s = 0; s < TK; ++s) coef[s] = wv[s] / sum;
+    if (any) {
+#pragma unroll
+      for (int s = 0; s < TK; ++s) {
+        const T *e = reinterpret_cast<const T *>(&srow[s]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], Elem<DT>::to_f(e[i]), acc[i]);
+      }
+    }
+  } else {
+    const T *values = static_cast<const T *>(a.values);
+    const T *src[NN];
+    float coef[NN];
+    bool okc[NN];
+    float inv_sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < NN; ++j) {
+      okc[j] = cn[j] >= 0 && cn[j] < a.n_cent;
+      src[j] = values + (okc[j] ? cn[j] : 0) * a.ld_v + hl;
+      coef[j] = okc[j] ? ((NN > 1) ? 1.f / (dn[j] + 1e-6f) : 1.f) : 0.f;
+      inv_sum += coef[j];
+    }
+    if (NN > 1) {
+#pragma unroll
+      for (int j = 0; j < NN; ++j) coef[j] = okc[j] ? coef[j] / inv_sum : 0.f;
+    }
+    float v[NN][8];
+#pragma unroll
+    for (int j = 0; j < NN; ++j) tm_load8<DT>(src[j], v[j]);
+#pragma unroll
+    for (int j = 0; j < NN; ++j)
+      if (okc[j]) {  // uniform; the loads above are already issued
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[j], v[j][i], acc[i]);
+      }
+  }
+  if (poison) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = __builtin_nanf("");
+  }
+  if (h0 < a.hidden) tm_store8_nt<DT>(dst, acc);
+}
+
 template <int DT, int DIM, int RVPL, int KPW>
 void launch_split(const tm_table_layer *t, const tm_layer_io *io, const tm_decode_ws &w, const tm_route_args *ra,
                   hipStream_t s) {
@@ -455,6 +1066,79 @@ void finish_tk(const tm_table_layer *t, const tm_layer_io *io, const tm_decode_w
     finish_nn<DT, 6, NCB>(t, io, w, nsplit, n_keep, s);
 }
 
+template <int DT, int KPW, int K, int TK>
+void launch_fused(const tm_table_layer *t, const tm_layer_io *io, const tm_decode_ws &w, const tm_route_args *ra,
+                  int64_t nsplit, int64_t n_keep, hipStream_t s) {
+  FusedArgs a{};
+  a.n = io->n_tokens;
+  a.nsplit = nsplit;
+  a.n_cent = t->n_cent;
+  a.ld_c = t->ld_c;
+  a.n_keep = n_keep;
+  a.ld_x = io->ld_x;
+  a.hidden = t->hidden;
+  a.n_chunks = (int)tm_cdiv(t->hidden, kChunk);
+  a.l2 = t->metric == TM_METRIC_L2 ? 1 : 0;
+  a.routed = ra != nullptr ? 1 : 0;
+  a.n_experts = ra != nullptr ? ra->n_experts : 0;
+  a.logits = ra != nullptr ? ra->logits : nullptr;
+  a.ld_logits = ra != nullptr ? ra->ld : 0;
+  a.x = io->x;
+  a.is_vision = io->is_vision;
+  a.pv = t->proj_vis;
+  a.bv = t->bias_vis;
+  a.pt = t->proj_txt ? t->proj_txt : t->proj_vis;
+  a.bt = t->proj_txt ? t->bias_txt : t->bias_vis;
+  a.q = io->q;
+  a.qn_blk = w.qn_blk;
+  a.part = reinterpret_cast<float4 *>(w.part);
+  a.cents = t->cents;
+  // stand-ins keep every prologue load unconditional: the norms (dot
+  // metric) read the centroid bytes, the residual (none) reads slot rows
+  a.c_sqnorm = t->c_sqnorm ? t->c_sqnorm : static_cast<const float *>(t->cents);
+  a.lists = w.lists;
+  a.keys = w.keys;
+  a.w = io->weights;
+  a.ids = io->expert_ids;
+  a.slot_out = io->slot_out;
+  a.so_b = io->so_b;
+  a.so_s = io->so_s;
+  a.values = t->values;
+  a.ld_v = t->ld_v;
+  a.has_res = io->residual != nullptr ? 1 : 0;
+  a.residual = io->residual ? io->residual : io->slot_out;
+  a.ld_r = io->residual ? io->ld_r : 0;
+  a.out = io->out;
+  a.ld_o = io->ld_o;
+  a.out_dist = io->dist;
+  a.out_idx = io->idx;
+  a.out_qn = io->q_sqnorm;
+  a.out_keep = io->keep;
+  a.sync = w.cnt;
+  hipLaunchKernelGGL((decode_fused_kernel<DT, 128, KPW, K, TK>), dim3(kFusedWGs), dim3(256), 0, s, a);
+}
+
+template <int DT, int KPW>
+void fused_nn_tk(const tm_table_layer *t, const tm_layer_io *io, const tm_decode_ws &w, const tm_route_args *ra,
+                 int64_t nsplit, int64_t n_keep, hipStream_t s) {
+  const bool tk8 = io->router_top_k == 8;
+  if (io->n_nearest == 1)
+    tk8 ? launch_fused<DT, KPW, 1, 8>(t, io, w, ra, nsplit, n_keep, s)
+        : launch_fused<DT, KPW, 1, 6>(t, io, w, ra, nsplit, n_keep, s);
+  else
+    tk8 ? launch_fused<DT, KPW, 4, 8>(t, io, w, ra, nsplit, n_keep, s)
+        : launch_fused<DT, KPW, 4, 6>(t, io, w, ra, nsplit, n_keep, s);
+}
+
+// The one-launch plan's shapes (on top of tm_internal_decode_ok): d = 128,
+// hidden 2048 or 2560, at most kFusedWGs search splits, a fused router of 64
+// or 128 experts (or weights from a router launch).
+bool fused_ok(const tm_table_layer *t, const tm_layer_io *io, const tm_route_args *ra, int64_t nsplit) {
+  return t->dim == 128 && (t->hidden == 2048 || t->hidden == 2560) && nsplit >= 1 && nsplit <= kFusedWGs &&
+         (ra == nullptr || ((ra->n_experts == 64 || ra->n_experts == 128) && ra->top_k == io->router_top_k)) &&
+         (t->metric == TM_METRIC_DOT || t->c_sqnorm != nullptr) && io->weights && io->expert_ids;
+}
+
 bool rows16(const void *base, int64_t ld) {
   return base == nullptr || (tm_aligned16(base) && (ld * 2) % 16 == 0);
 }
@@ -498,6 +1182,17 @@ int tm_internal_decode_forward(const tm_table_layer *t, const tm_layer_io *io, c
              "tm_table_forward: decode workspace missing");
   const int64_t n = io->n_tokens;
   const int64_t nsplit = tm_internal_stream_nsplit(n, t->n_cent, t->dim, io->n_nearest);
+  if (ev == nullptr && fused_ok(t, io, ra, nsplit)) {  // one launch
+    const int kpw = t->hidden / (32 * kSlices);
+    if (t->dtype == TM_DT_BF16)
+      kpw == 8 ? fused_nn_tk<TM_DT_BF16, 8>(t, io, w, ra, nsplit, n_keep, s)
+               : fused_nn_tk<TM_DT_BF16, 10>(t, io, w, ra, nsplit, n_keep, s);
+    else
+      kpw == 8 ? fused_nn_tk<TM_DT_F16, 8>(t, io, w, ra, nsplit, n_keep, s)
+               : fused_nn_tk<TM_DT_F16, 10>(t, io, w, ra, nsplit, n_keep, s);
+    TM_LAUNCH_CHECK("tm_table_forward(decode)");
+    return TM_OK;
+  }
   int st = TM_DISPATCH_DTYPE(t->dtype, DT, [&] {
     if constexpr (DT != TM_DT_F32) {
       switch (t->dim) {

@@ -23,14 +23,16 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // and the key reset, search merging by atomic minimum, keep select decoding
 // the keys; for up to 4096 tokens the search decodes the keys and the
 // combine ranks the keep set), and the decode plan (n <= 64: split
-// projection, stream search, one finishing launch).  The first kSync bytes hold the decode plan's
-// arrival counters at the same offset for every n and plan: zero before the
-// first call on a workspace, and left zero by every call.  The decode plan
-// uses counters 0 .. 31, the ranked top-1 plan one per query tile from
-// kTileCnt on.
-constexpr size_t kSync = 256;
+// projection, stream search, one finishing launch, or all three in one
+// launch).  The first kSync bytes hold the plans' arrival counters and flags
+// at the same offset for every n and plan: zero before the first call on a
+// workspace, and left zero (counters) or at this workspace's generation
+// (flags) by every call.  The decode plan's split projection uses counters
+// 0 .. 63, the ranked top-1 plan one per query tile from kTileCnt on, the
+// one-launch decode plan words 64 and up.
+constexpr size_t kSync = TM_LAYER_SYNC_BYTES;
 constexpr int kTileCnt = 32;
-constexpr int kMaxTiles = kSync / 4 - kTileCnt;
+constexpr int kMaxTiles = 64 - kTileCnt;  // words 64 on belong to the one-launch decode plan
 
 struct WsLayout {
   size_t sync, project, search, keep, keys, qn_part, part, total;
@@ -193,7 +195,7 @@ void *g_scratch_ptr[kMaxDevices];
 bool g_scratch_cleared[kMaxDevices];
 
 __global__ void clear_sync_kernel(uint32_t *p) {
-  if (threadIdx.x < kSync / 4) p[threadIdx.x] = 0u;
+  for (unsigned i = threadIdx.x; i < kSync / 4; i += blockDim.x) p[i] = 0u;
 }
 
 // The current device's scratch address; on a device's first call, looks it
@@ -215,7 +217,7 @@ int scratch_for_current_device(hipStream_t s, void **out) {
     g_scratch_ptr[dev] = p;
   }
   if (!g_scratch_cleared[dev]) {
-    hipLaunchKernelGGL(clear_sync_kernel, dim3(1), dim3(kSync / 4), 0, s, static_cast<uint32_t *>(g_scratch_ptr[dev]));
+    hipLaunchKernelGGL(clear_sync_kernel, dim3(1), dim3(256), 0, s, static_cast<uint32_t *>(g_scratch_ptr[dev]));
     TM_LAUNCH_CHECK("tm_table_forward_noalloc(clear)");
     g_scratch_cleared[dev] = true;
   }

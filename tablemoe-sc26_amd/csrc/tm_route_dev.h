@@ -25,10 +25,13 @@ constexpr int kG8Steps[3] = {0xB1, 0x4E, 0x141};
 // ties go to the lower expert id; the winner is masked out after each round.
 // The group's lane 0 keeps the winners (top_k <= KM) and writes them once.
 // Every lane of the wave must call this (the reductions are 8-lane DPP exchanges).
+// tm_route_compute leaves the winners in every lane of the group (kw, ki;
+// entries past top_k unset) and their sum in wsum; tm_route_token also writes
+// them.
 template <int VPL, int KM>
-__device__ __forceinline__ void tm_route_token(const float *__restrict__ logits, int64_t n, int64_t ld, int top_k,
-                                               int renorm, float *__restrict__ out_w,
-                                               int64_t *__restrict__ out_ids, int64_t row, int sub) {
+__device__ __forceinline__ void tm_route_compute(const float *__restrict__ logits, int64_t n, int64_t ld, int top_k,
+                                                 int64_t row, int sub, float (&kw)[KM], int (&ki)[KM],
+                                                 float &wsum) {
   static_assert(VPL % 4 == 0, "whole 16-byte loads");
   const bool valid = row < n;
   const float *lr = logits + (valid ? row : n - 1) * ld + sub * VPL;
@@ -55,9 +58,7 @@ __device__ __forceinline__ void tm_route_token(const float *__restrict__ logits,
   sum += tm_g8f<kG8Steps[2]>(sum);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) v[j] = v[j] / sum;
-  float kw[KM];
-  int ki[KM];
-  float wsum = 0.f;
+  wsum = 0.f;
   for (int k = 0; k < top_k; ++k) {
     float bv = -2.f;
     int bi = 0x7fffffff;
@@ -86,6 +87,17 @@ __device__ __forceinline__ void tm_route_token(const float *__restrict__ logits,
       if (u == k) { kw[u] = bv; ki[u] = bi; }
     wsum += bv;
   }
+}
+
+template <int VPL, int KM>
+__device__ __forceinline__ void tm_route_token(const float *__restrict__ logits, int64_t n, int64_t ld, int top_k,
+                                               int renorm, float *__restrict__ out_w,
+                                               int64_t *__restrict__ out_ids, int64_t row, int sub) {
+  float kw[KM];
+  int ki[KM];
+  float wsum;
+  tm_route_compute<VPL, KM>(logits, n, ld, top_k, row, sub, kw, ki, wsum);
+  const bool valid = row < n;
   if (sub == 0 && valid) {
     const float d = renorm ? fmaxf(wsum, 1e-20f) : 1.f;
     float *ow = out_w + row * top_k;

@@ -24,6 +24,10 @@ TM_METRIC_L2, TM_METRIC_DOT = 0, 1
 TM_TARGET_ONE, TM_TARGET_ORIG_SUM, TM_TARGET_GIVEN = 0, 1, 2
 TM_SCORE_MODEL, TM_SCORE_F32 = 0, 1
 TM_LAYER_NO_COMBINE = 1
+# tm_table_forward workspace: sync region size and the byte offset of the
+# count of bounded waits that ran out (include/tablemoe.h)
+TM_LAYER_SYNC_BYTES = 16384
+TM_LAYER_SYNC_ERR_BYTE = 5760
 
 _DTYPE_TAG = {torch.float32: TM_DT_F32, torch.float16: TM_DT_F16, torch.bfloat16: TM_DT_BF16}
 

@@ -250,6 +250,16 @@ class GlobalTable:
         res.pop("_inputs")
         return res
 
+    def wait_errors(self) -> int:
+        """Bounded cross-workgroup waits of the one-launch decode plan that ran
+        out on this table's workspace (zero unless the device was so busy that
+        the launch's workgroups could not all be resident); synchronises."""
+        ws = self._bufs.get("layer_ws")
+        if ws is None or ws.numel() < N.TM_LAYER_SYNC_BYTES:
+            return 0
+        e = N.TM_LAYER_SYNC_ERR_BYTE
+        return int(ws[e:e + 4].view(torch.int32).item())
+
     def layer_search(self, hidden, is_vision, router_logits, router_top_k: int = 8, n_nearest: int = 1,
                      keep_rate: float = 0.6):
         """The layer call up to the keep set (tm_table_forward with

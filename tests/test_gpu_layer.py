@@ -691,6 +691,71 @@ def test_layer_forward_config3_decode_end_to_end(hip_device, n):
     assert_bf16_output(np64(res["out"]), exact, abssum)
 
 
+def _gen_word(table):
+    """Generation word of the one-launch decode plan in a table's layer workspace
+    (byte 256 of the sync region): advanced once by every one-launch call."""
+    ws = table._bufs["layer_ws"]
+    return int(ws[256:260].view(torch.int32).item())
+
+
+@pytest.mark.parametrize("cfg,n,nn,variant", [
+    (3, 1, 4, "base"), (3, 8, 4, "base"), (3, 32, 4, "base"), (3, 33, 1, "mix"), (3, 64, 4, "mix"),
+    (5, 17, 4, "base"), (5, 64, 1, "nores"), (3, 24, 4, "fp16"), (3, 40, 4, "dot"), (3, 32, 4, "small_c"),
+    (5, 5, 1, "fp16")])
+def test_decode_one_launch_matches_three_launches(hip_device, cfg, n, nn, variant):
+    """Decode batches with d = 128, hidden 2048 or 2560 and at most 128
+    search splits run as one launch whose three phases hand q and the search
+    results between workgroups through flags; with stage events the same
+    call runs the three-launch plan.  Both give identical bits on three calls
+    in a row on one workspace (new tokens each call: the flags' generation
+    advances every call), the one-launch plan really ran (its generation word
+    counts the calls), and no bounded wait ran out.  Covers 1 to 64 tokens
+    (one and two query slabs), top-1 and top-4, 64 and 128 experts (top-6 and
+    top-8), mixed modalities, no residual, fp16, the dot metric and a table of
+    8 splits (most workgroups idle in the search phase)."""
+    from table_moe.cache_engine import GlobalTable
+    from synth import make_workload
+
+    dev = hip_device
+    over = {"n_cent": 1000} if variant == "small_c" else {}
+    dtype = torch.float16 if variant == "fp16" else None
+    wl = make_workload(cfg, n=n, dtype=dtype, bias_scale=0.3, **over)
+    d = wl.to(dev)
+    is_vision = d.is_vision
+    if variant == "mix":
+        is_vision = (torch.rand(n, generator=_gen(n)) < 0.5).to(dev)
+    residual = None if variant == "nores" else d.residual
+    metric = "dot" if variant == "dot" else "l2"
+    a = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt), metric=metric)
+    b = GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt), metric=metric)
+    evs = [torch.cuda.Event() for _ in range(6)]
+    topk = d.cfg["router_top_k"]
+    g = _gen(7 + n)
+    for rep in range(3):
+        x = d.x if rep == 0 else d.x[torch.randperm(n, generator=g).to(dev)].contiguous()
+        logits = d.logits if rep == 0 else torch.randn(d.logits.shape, generator=g).to(dev)
+        ra = a.layer_forward(x, is_vision, logits, d.slot_out, residual, topk, nn, 0.6)
+        rb = b.layer_forward(x, is_vision, logits, d.slot_out, residual, topk, nn, 0.6, stage_events=evs)
+        torch.cuda.synchronize()
+        for key in ("weights", "ids", "q", "qn", "dist", "idx", "keep", "out"):
+            if key == "out" and ra[key] is None:
+                continue
+            assert torch.equal(ra[key], rb[key]), (key, rep)
+        assert _gen_word(a) == rep + 1
+    assert _gen_word(b) == 0  # the staged calls never touch the one-launch words
+    assert a.wait_errors() == 0
+    assert torch.isfinite(ra["out"].float()).all()
+    # and the one-launch plan's stage outputs against the stage calls (as the three-launch plan's are)
+    check_decode_plan_stagewise(b, ra, _with(d, x, logits), is_vision, residual, _with(wl, x.cpu(), logits.cpu()), nn)
+
+
+def _with(wl, x, logits):
+    """A copy of a workload record with other tokens and router logits."""
+    kw = dict(wl.__dict__)
+    kw["x"], kw["logits"] = x, logits
+    return type(wl)(**kw)
+
+
 @pytest.mark.parametrize("cfg,n,nn", [(2, 768, 1), (2, 4096, 1), (3, 32, 4)])
 def test_layer_graph_replays_match_eager(hip_device, cfg, n, nn):
     """A captured tm_table_forward replays correctly: several replays with new
