@@ -433,7 +433,7 @@ constexpr int kWGoB = kWGoA + kGoRep * kLine;
 constexpr int kWErr = kWGoB + kGoRep * kLine;
 constexpr int kWGrp = kWErr + kLine;  // the projection groups' counters, one line each
 constexpr int kMaxGroups = 64 / 16 * 128 / 16;  // (64 rows / 16) x (d 128 / 16)
-static_assert((kWGrp + kMaxGroups * kLine) * 4 <= TM_LAYER_SYNC_BYTES, "sync region");
+static_assert((kWGrp + kMaxGroups * kLine) <= 2560, "the ranked top-1 plan's counters follow");
 static_assert(kWErr * 4 == TM_LAYER_SYNC_ERR_BYTE, "documented err word");
 
 struct FusedArgs {

@@ -53,9 +53,13 @@ __attribute__((visibility("hidden"))) int tm_internal_search_keys(
 // The same search for large n (wide kernel: 8-wave workgroups, one per CU):
 // the workgroup that finishes a 256-query tile last also decodes the tile's
 // keys into dist[i], idx[i] and q_sqnorm[i] (|q|^2 = the sum of `parts`
-// partial norms qn_part[p][i]).  `cnt` holds one arrival counter per tile,
-// zero before the call and left zero.  tm_internal_search_decode_tiles gives
+// partial norms qn_part[p][i]).  `cnt` holds one arrival counter per tile
+// (cnt[tile * kTmCntStride]), zero before the call and left zero.  tm_internal_search_decode_tiles gives
 // the tile count (0: shape not supported).
+// Arrival counters handed to tm_internal_search_decode sit kTmCntStride words
+// apart (one 128-byte line each: 256 workgroups count on 16 counters, and
+// counters sharing a line serialise one another).
+constexpr int kTmCntStride = 32;
 __attribute__((visibility("hidden"))) int64_t tm_internal_search_decode_tiles(int32_t dtype, int64_t n,
                                                                               int64_t n_cent, int64_t ld_q,
                                                                               int64_t ld_c, int32_t dim);

@@ -926,7 +926,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void search_top1_wide_kernel(
     tm_wait_vm_lgkm0<0>();
     __syncthreads();
     if (tid == 0) {
-      uint32_t *cnt = wd.cnt + blockIdx.y;
+      uint32_t *cnt = wd.cnt + blockIdx.y * kTmCntStride;
       const uint32_t ticket = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const bool last = ticket == gridDim.x - 1;
       if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
