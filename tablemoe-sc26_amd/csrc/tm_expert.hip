@@ -44,11 +44,12 @@ constexpr int kEpiFloats = BM * kStageLd;    // staging tile size in floats (139
 
 enum { kModeUp = 0, kModeDown = 1 };
 
-// Slot of (row, 16-byte chunk kc) in a stage.  A row is 64 bytes, so two
-// rows share one 128-byte line of banks; XOR-ing the chunk with (row / 2) % 4
-// puts the 8 rows of a line group on 8 distinct 16-byte bank groups, and an
-// operand read (one chunk of 32 consecutive rows) is conflict-free.
-__device__ __forceinline__ int swz_chunk(int row, int kc) { return kc ^ ((row >> 1) & (kCPR - 1)); }
+// Slot of (row, 16-byte chunk kc) in a stage.  A row is 64 bytes, so four
+// rows share one 256-byte line of the 64 banks, which a 16-byte read serves
+// 16 lanes at a time; XOR-ing the chunk with (row / 4) % 4 puts 16
+// consecutive rows on 16 distinct 16-byte bank groups, and an operand read
+// (one chunk of 32 consecutive rows) is conflict-free.
+__device__ __forceinline__ int swz_chunk(int row, int kc) { return kc ^ ((row >> 2) & (kCPR - 1)); }
 
 // Tile source: the grouped tile list (tiles != nullptr: [0] rows, [1] tiles,
 // then tile_expert[t_max], tile_row0[t_max]) or one dense expert of `rows`.
