@@ -534,7 +534,7 @@ size_t tm_struct_size(int32_t which);
  * waiting workgroup writes are NaN).  The library never clears the word
  * (zero = no wait ever ran out). */
 #define TM_LAYER_SYNC_BYTES 16384
-#define TM_LAYER_SYNC_ERR_BYTE 5760
+#define TM_LAYER_SYNC_ERR_BYTE 3584
 size_t tm_table_forward_workspace_size(const tm_table_layer *table, int64_t n_tokens, int32_t n_nearest);
 int tm_table_forward(const tm_table_layer *table, const tm_layer_io *io, void *workspace,
                      size_t workspace_bytes, void *const *stage_events, tm_stream_t stream);

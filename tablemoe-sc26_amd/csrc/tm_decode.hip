@@ -382,8 +382,8 @@ __global__ __launch_bounds__(64) void decode_finish_kernel(
 // whose inputs come from other workgroups waits on a grid-wide flag.
 //   A  projection tasks (project_split_kernel's work; task t runs on wave
 //      t / G of workgroup t % G).  The last wave of a (tile, column block)
-//      group writes q and the block's |q|^2 and counts the group on q_cnt;
-//      the wave that completes q_cnt raises go_a.
+//      group writes q and the block's |q|^2 and raises the group's flag; a
+//      workgroup goes on once one wave saw every group's flag.
 //   B  workgroup s < nsplit searches split s (search_stream_kernel's work) and
 //      publishes its lists and best keys; every workgroup then counts itself
 //      on one of kSubCnt sub-counters, the last arrival of each counts on
@@ -425,15 +425,14 @@ static_assert(kFusedWGs % kSubCnt == 0, "whole sub-counter groups");
 // word offsets in the layer workspace's sync region (words 0 .. 63 belong to
 // the other plans' counters)
 constexpr int kWGen = 64;
-constexpr int kWQcnt = kWGen + kLine;
-constexpr int kWStop = kWQcnt + kLine;
+constexpr int kWStop = kWGen + kLine;
 constexpr int kWSsub = kWStop + kLine;
-constexpr int kWGoA = kWSsub + kSubCnt * kLine;
-constexpr int kWGoB = kWGoA + kGoRep * kLine;
+constexpr int kWGoB = kWSsub + kSubCnt * kLine;
 constexpr int kWErr = kWGoB + kGoRep * kLine;
-constexpr int kWGrp = kWErr + kLine;  // the projection groups' counters, one line each
 constexpr int kMaxGroups = 64 / 16 * 128 / 16;  // (64 rows / 16) x (d 128 / 16)
-static_assert((kWGrp + kMaxGroups * kLine) <= 2560, "the ranked top-1 plan's counters follow");
+constexpr int kWGrp = kWErr + kLine;                   // the projection groups' counters, one line each
+constexpr int kWFlagA = kWGrp + kMaxGroups * kLine;    // the projection groups' q-ready flags, one line each
+static_assert(kWFlagA + kMaxGroups * kLine <= 3072, "the ranked top-1 plan's counters follow");
 static_assert(kWErr * 4 == TM_LAYER_SYNC_ERR_BYTE, "documented err word");
 
 struct FusedArgs {
@@ -488,7 +487,7 @@ __device__ __forceinline__ bool wait_flag(const uint32_t *f, uint32_t want) {
 // task `task` at once -- x, both modalities' P (so no load waits for the
 // modality byte) and the biases -- and fused_project_task multiplies,
 // publishes and, in the group's last wave, reduces; its hand-offs are
-// coherent stores, and the wave that completes q_cnt raises go_a.
+// coherent stores, and that wave raises the group's q-ready flag.
 template <int DT, int KPW>
 struct ProjOps {
   uint4 x[KPW], pv[KPW], pt[KPW];
@@ -611,16 +610,9 @@ __device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t t
   const int64_t qrow = row0 + 4 * (lane >> 4) + (lane & 3);
   if (qrow < n)
     coh_st(reinterpret_cast<uint64_t *>(static_cast<T *>(a.q) + qrow * DIM + cb * 16 + 4 * ((lane & 15) >> 2)), piece);
-  __builtin_amdgcn_s_waitcnt(0);
-  uint32_t qt = 0;
-  if (lane == 0) qt = coh_add(a.sync + kWQcnt);
-  qt = (uint32_t)__builtin_amdgcn_readfirstlane((int)qt);
-  const uint32_t ngroups = (uint32_t)(((n + 15) / 16) * NCB);
-  if (qt == ngroups - 1) {  // uniform: q is complete
-    const uint32_t gen = (uint32_t)__builtin_amdgcn_readfirstlane((int)g0v);
-    if (lane == 0) coh_st32(a.sync + kWQcnt, 0u);
-    if (lane < kGoRep) coh_st32(a.sync + kWGoA + lane * kLine, gen + 1);
-  }
+  __builtin_amdgcn_s_waitcnt(0);  // q and |q|^2 of the block acknowledged before its flag
+  const uint32_t gen = (uint32_t)__builtin_amdgcn_readfirstlane((int)g0v);
+  if (lane == 0) coh_st32(a.sync + kWFlagA + g * kLine, gen + 1);
 }
 
 template <int DT, int DIM, int KPW, int K, int TK>
@@ -731,12 +723,22 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
     pen[i] = cm < c_end ? pen[i] : __builtin_huge_valf();
   }
 
-  // ---- wait for q ----
+  // ---- wait for q: wave 0's lane g polls group g's flag ----
   __syncthreads();
-  if (tid == 0) {
-    const bool ok = wait_flag(sync + kWGoA + (wg % kGoRep) * kLine, g0() + 1);
-    if (!ok) coh_add(sync + kWErr);
-    s_ok = ok ? 1u : 0u;
+  if (wave == 0) {
+    const int ngroups = (int)((n + 15) / 16) * NCB;
+    const uint32_t want = g0() + 1;
+    const uint32_t *f = sync + kWFlagA + (lane < ngroups ? lane : 0) * kLine;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    bool ok = true;
+    while (__ballot(lane < ngroups && __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want) != 0) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) { ok = false; break; }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) {
+      if (!ok) coh_add(sync + kWErr);
+      s_ok = ok ? 1u : 0u;
+    }
   }
   __syncthreads();
   bool poison = s_ok == 0u;

@@ -28,10 +28,10 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // at the same offset for every n and plan: zero before the first call on a
 // workspace, and left zero (counters) or at this workspace's generation
 // (flags) by every call.  The decode plan's split projection uses counters
-// 0 .. 63, the one-launch decode plan words 64 .. 2559, the ranked top-1
+// 0 .. 63, the one-launch decode plan words 64 .. 3071, the ranked top-1
 // plan one per query tile, kTmCntStride words apart, from kTileCnt on.
 constexpr size_t kSync = TM_LAYER_SYNC_BYTES;
-constexpr int kTileCnt = 2560;  // past the one-launch decode plan's words
+constexpr int kTileCnt = 3072;  // past the one-launch decode plan's words
 constexpr int kMaxTiles = 32;
 static_assert((kTileCnt + kMaxTiles * kTmCntStride) * 4 <= (int)kSync, "sync region");
 

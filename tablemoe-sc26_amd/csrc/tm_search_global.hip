@@ -472,8 +472,11 @@ __global__ __launch_bounds__(kThreads, 2) void search_top1_kernel(
   }
   auto issue = [&](uint4 *buf, int s) {
     const uint32_t lds0 = (uint32_t)(uintptr_t)buf + (uint32_t)wave_u * 1024u;
-    const int64_t row0 = __builtin_elementwise_min(c_begin + (int64_t)s * ROWS, n_cent);
-    const tm_rsrc_t rs = tm_make_rsrc(cents + row0 * ld_c, (uint64_t)(n_cent - row0) * ldb);
+    // the resource ends with the workgroup's range: rows past it (the stages
+    // of the last ring round past the range, a partial last stage) read
+    // nothing instead of another range's centroids
+    const int64_t row0 = __builtin_elementwise_min(c_begin + (int64_t)s * ROWS, c_end);
+    const tm_rsrc_t rs = tm_make_rsrc(cents + row0 * ld_c, (uint64_t)(c_end - row0) * ldb);
 #pragma unroll
     for (int u = 0; u < NDMA; ++u) tm_dma16_buf(rs, voff[u], lds0 + (uint32_t)(u * kThreads * 16));
   };
@@ -726,8 +729,11 @@ __global__ __launch_bounds__(kWideThreads, 1) void search_top1_wide_kernel(
   }
   auto issue = [&](uint4 *buf, int s) {
     const uint32_t lds0 = (uint32_t)(uintptr_t)buf + (uint32_t)wave_u * 1024u;
-    const int64_t row0 = __builtin_elementwise_min(c_begin + (int64_t)s * ROWS, n_cent);
-    const tm_rsrc_t rs = tm_make_rsrc(cents + row0 * ld_c, (uint64_t)(n_cent - row0) * ldb);
+    // the resource ends with the workgroup's range: rows past it (the stages
+    // of the last ring round past the range, a partial last stage) read
+    // nothing instead of another range's centroids
+    const int64_t row0 = __builtin_elementwise_min(c_begin + (int64_t)s * ROWS, c_end);
+    const tm_rsrc_t rs = tm_make_rsrc(cents + row0 * ld_c, (uint64_t)(c_end - row0) * ldb);
 #pragma unroll
     for (int u = 0; u < NDMA; ++u) tm_dma16_buf(rs, voff[u], lds0 + (uint32_t)(u * kWideThreads * 16));
   };

@@ -27,7 +27,7 @@ TM_LAYER_NO_COMBINE = 1
 # tm_table_forward workspace: sync region size and the byte offset of the
 # count of bounded waits that ran out (include/tablemoe.h)
 TM_LAYER_SYNC_BYTES = 16384
-TM_LAYER_SYNC_ERR_BYTE = 5760
+TM_LAYER_SYNC_ERR_BYTE = 3584
 
 _DTYPE_TAG = {torch.float32: TM_DT_F32, torch.float16: TM_DT_F16, torch.bfloat16: TM_DT_BF16}
 
