@@ -55,6 +55,10 @@ constexpr int kWideThreads = 512;
 constexpr int kWideQ = 256;  // queries per workgroup
 constexpr int kWideStageBytes = 32768;
 constexpr int kWideMinGroups = 192;  // fewer leave too many of the 256 CUs idle
+// The layer call's ranked plan takes the wide kernel from 128 workgroups on:
+// its key decode and the ranked combine save the keep-select launch, which
+// outweighs the idle CUs (N = 2048 at C = 8192: 8 tiles x 16 ranges).
+constexpr int kWideDecMinGroups = 128;
 
 struct WidePlan {
   int64_t tiles, nsplit, chunk;
@@ -1609,7 +1613,7 @@ int64_t tm_internal_search_decode_tiles(int32_t dtype, int64_t n, int64_t n_cent
                                         int32_t dim) {
   if (!tm_internal_search_keys_ok(dtype, n, n_cent, ld_c, dim, 1) || ld_q < dim) return 0;
   const WidePlan p = plan_wide(n, n_cent, dim);
-  if (p.tiles * p.nsplit < kWideMinGroups || !wide_strides_ok(ld_q, ld_c, dim)) return 0;
+  if (p.tiles * p.nsplit < kWideDecMinGroups || !wide_strides_ok(ld_q, ld_c, dim)) return 0;
   return p.tiles;
 }
 
