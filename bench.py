@@ -447,6 +447,12 @@ def run_config5(replays=10):
     shared_flops = n * 6.0 * h * 2 * inter
     search_flops = 2.0 * n * h * cfg["dim"] + 2.0 * n * cfg["n_cent"] * cfg["dim"]
     total_flops = routed_flops + shared_flops + search_flops
+    # The routed GEMMs stream every expert's three weight matrices for ~rows/e
+    # rows each (~230 FLOP per weight byte at this shape, below the 312 FLOP/B
+    # ridge of the bf16 peak over HBM): their bound is HBM.  Bytes they must
+    # move: the weights, the gathered x rows, the intermediate written and
+    # read once, the slot rows written.
+    routed_bytes = 2.0 * (3 * e * inter * h + rows * h + 2 * rows * inter + rows * h)
     log(f"config 5 layer: {layer_us:.1f} us ({json.dumps({k_: round(v, 1) for k_, v in times.items()})})")
     return {
         "workload": "config 5: N=4096, hidden 2560 bf16, 64 routed experts top-6 (intermediate 1536) + shared experts "
@@ -456,6 +462,8 @@ def run_config5(replays=10):
         "us_per_layer": layer_us, "tokens_per_s": n / (layer_us * 1e-6), **times,
         "routed_rows": rows, "routed_tflops": routed_flops / (times["routed_recompute_us"] * 1e-6) / 1e12,
         "routed_mfma_frac": routed_flops / (times["routed_recompute_us"] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
+        "routed_algorithmic_bytes": routed_bytes,
+        "routed_hbm_frac": routed_bytes / (times["routed_recompute_us"] * 1e-6) / 1e9 / HBM_PEAK_GBPS,
         "shared_tflops": shared_flops / (times["shared_us"] * 1e-6) / 1e12,
         "shared_mfma_frac": shared_flops / (times["shared_us"] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
         "layer_tflops": total_flops / (layer_us * 1e-6) / 1e12,
