@@ -23,6 +23,7 @@
 // project_epilogue_kernel adds them in split order (deterministic), adds the
 // bias, rounds, normalises and stores q.  Without one, the same epilogue runs
 // inside the workgroup.
+#include "tm_dma.h"
 #include "tm_internal.h"
 #include "tm_mfma.h"
 #include "tm_route_dev.h"
@@ -494,6 +495,232 @@ __global__ __launch_bounds__(256, 2) void project_cols_kernel(
   for (int w = 0; w < 4; ++w) {  // wave order: deterministic
     const float4 a = *reinterpret_cast<const float4 *>(&red[w][erow][8 * part]);
     const float4 c = *reinterpret_cast<const float4 *>(&red[w][erow][8 * part + 4]);
+    v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+    v[4] += c.x; v[5] += c.y; v[6] += c.z; v[7] += c.w;
+  }
+  const bool vis = (vis_bits >> erow) & 1u;
+  const uint4 braw = vis ? braw_v : braw_t;
+  const T *be = reinterpret_cast<const T *>(&braw);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = tm_round<DT>(v[i] + Elem<DT>::to_f(be[i]));
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+  ss += __shfl_xor(ss, 1, 64);
+  ss += __shfl_xor(ss, 2, 64);
+  ss += __shfl_xor(ss, 4, 64);
+  if (ok) {
+    tm_store8<DT>(q + gr * ld_q + col, v);
+    if (part == 0) qn_part[(int64_t)g * n + gr] = ss;
+    if (keys != nullptr && g == 0 && part == 1) keys[gr] = ~0ull;
+  }
+}
+
+// project_cols_pipe_kernel: the column-split projection with every operand
+// load issued from inline asm and waited for with an exact count (DIM = 128,
+// hidden = 512 * NCH: each wave's slice is NCH whole chunks of 4 k-steps, so
+// the pipeline is straight-line code with compile-time wait counts).  Same
+// tiles, waves, k slices and MFMA sequence as project_cols_kernel, so the
+// same bits.
+//
+// Loads retire in order.  In the register kernel the P fragments of chunk
+// c + 1 are requested after the x of chunk c + 2, so waiting for them waits
+// for that x too, and every chunk costs one HBM round trip (~1.5 us under
+// load; P is as cold as x when each layer has its own table).  Here each wave
+// keeps two chunks of both operands in flight: a 2-slot ring of x chunks in
+// LDS (direct global -> LDS loads, 8 KiB a chunk) and two register buffers of
+// P chunks (16 KiB each).  While chunk c is multiplied, P(c + 2, t) is issued
+// into P(c, t)'s registers as soon as k-step t is done, then x(c + 2) into
+// chunk c's slot once its fragment reads are done, so every wait leaves the
+// next chunk's loads in flight.  The compiler does not see these loads, so it adds no waits of its own; the
+// values are tied to the waits by empty asm statements, which every path
+// reaches after the wait that retires them (no register that a load will
+// still write is read or reused before).  LDS per workgroup is
+// the ring (64 KiB), with the wave partials aliased onto it after the last
+// chunk, so two workgroups fit a CU (router workgroups of the same launch
+// included).  Tiles that mix modalities run the pipeline once per modality
+// (the second pass streams x again) and keep each row's own result.
+template <int DT, int DIM, int RVPL, int NCH>
+__global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
+    const typename Elem<DT>::T *__restrict__ x, int64_t n, int hidden, int64_t ld_x,
+    const uint8_t *__restrict__ is_vision, const typename Elem<DT>::T *__restrict__ pv,
+    const typename Elem<DT>::T *__restrict__ bv, const typename Elem<DT>::T *__restrict__ pt,
+    const typename Elem<DT>::T *__restrict__ bt, typename Elem<DT>::T *__restrict__ q, int64_t ld_q,
+    float *__restrict__ qn_part, uint64_t *__restrict__ keys, int64_t n_tiles, ColsRoute cr) {
+  using T = typename Elem<DT>::T;
+  constexpr int G = ColsCfg<DIM>::G;
+  constexpr int NCB = ColsCfg<DIM>::NCB;
+  static_assert(NCH >= 1 && NCH <= 8, "chunks per wave");
+  constexpr int kRowPad = 64 + 4;
+  static_assert(DIM == 128, "4 column blocks of 1 KiB per k-step and wave");
+  // per wave: 2 ring slots of 32 rows x 16 x 16 bytes; the wave partials
+  // (32 x kRowPad floats) reuse the wave's own slots after its last chunk
+  __shared__ uint4 ring[4][2 * 512];
+  static_assert(32 * kRowPad * 4 <= 2 * 512 * 16, "partials fit the wave's ring");
+
+  const int tid = threadIdx.x;
+  if constexpr (RVPL > 0) {
+    if ((int64_t)blockIdx.x >= cr.first) {  // uniform: router workgroup, 32 tokens
+      const int64_t tok = ((int64_t)blockIdx.x - cr.first) * 32 + (tid >> 3);
+      tm_route_token<RVPL, 8>(cr.a.logits, n, cr.a.ld, cr.a.top_k, 0, cr.a.out_w, cr.a.out_ids, tok, tid & 7);
+      return;
+    }
+  }
+  const int64_t b = blockIdx.x;
+  const int64_t tile = (b / (8 * G)) * 8 + (b % 8);
+  const int g = (int)((b / 8) % G);
+  if (tile >= n_tiles) return;  // uniform (the grid is padded to whole groups of 8 tiles)
+
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t row0 = tile * 32;
+
+  const int ks_begin = wave * 4 * NCH;  // hidden == 512 * NCH (checked by the launcher)
+
+  const int xslot = lane & 15;
+  const int xr0 = lane >> 4;
+  const int64_t rows_left = n - 1 - row0;
+  auto x_src = [&](int i, int c) {  // rows past n read the last row
+    const int r = 4 * i + xr0;
+    const int kk = (ks_begin + 4 * c) * 32 + 8 * (xslot ^ (r & 15));
+    return x + (row0 + (r < rows_left ? r : rows_left)) * ld_x + kk;
+  };
+  const uint32_t lds_w = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&ring[wave][0]);
+  auto issue_x = [&](int c) {  // chunk c into slot c & 1: load i brings rows 4i .. 4i + 3
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tm_dma16_s(x_src(i, c), lds_w + (uint32_t)(((c & 1) * 512 + 64 * i) * 16));
+  };
+  auto read_a = [&](int c, int rb, int t) {  // A fragment of k-step t of chunk c, rows 16*rb + lane%16
+    const int r = 16 * rb + (lane & 15);
+    return ring[wave][(c & 1) * 512 + r * 16 + ((4 * t + (lane >> 4)) ^ (r & 15))];
+  };
+
+  // modality byte of row (lane & 31), then the first two x chunks; the byte
+  // is in once at most 8 * X0 loads remain outstanding
+  const int64_t vr = row0 + (lane & 31);
+  const bool vr_ok = vr < n;
+  const uint8_t *vsrc = is_vision ? is_vision + (vr_ok ? vr : 0) : reinterpret_cast<const uint8_t *>(x);
+  uint32_t vb;
+  asm volatile("global_load_ubyte %0, %1, off" : "=v"(vb) : "v"(vsrc) : "memory");
+  constexpr int X0 = NCH > 1 ? 2 : 1;  // x chunks issued ahead of the loop
+  issue_x(0);
+  if constexpr (X0 > 1) issue_x(1);
+  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(vb) : "n"(8 * X0) : "memory");
+  const int amod = !vr_ok ? 2 : ((is_vision == nullptr || (vb & 0xffu)) ? 0 : 1);
+  const uint32_t vis_bits = (uint32_t)(__ballot(amod == 0) & 0xFFFFFFFFull);  // bit r: tile row r uses P_vis
+  const uint32_t txt_bits = (uint32_t)(__ballot(amod == 1) & 0xFFFFFFFFull);
+
+  const int erow = tid >> 3;
+  const int part = tid & 7;
+  const int col = 64 * g + 8 * part;
+  const uint4 braw_v = *reinterpret_cast<const uint4 *>(bv + col);
+  const uint4 braw_t = *reinterpret_cast<const uint4 *>(bt + col);
+
+  tm_u32x4 pb[2][4][4];  // P of two chunks: [c & 1][k-step][column block]
+  tm_f32x4 fin[2][4];    // each row's result from the pass of its modality
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) fin[rb][c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto run_pass = [&](const T *P, uint32_t rows_of_pass, bool first) {
+    const uint4 *pf = reinterpret_cast<const uint4 *>(P) + (int64_t)(4 * g) * 64 + lane;
+    auto issue_p = [&](int c, int t) {  // k-step t of chunk c
+      const uint4 *src = pf + (int64_t)(ks_begin + 4 * c + t) * NCB * 64;
+      asm volatile(
+          "global_load_dwordx4 %0, %4, off\n\t"
+          "global_load_dwordx4 %1, %4, off offset:1024\n\t"
+          "global_load_dwordx4 %2, %4, off offset:2048\n\t"
+          "global_load_dwordx4 %3, %4, off offset:3072"
+          : "=&v"(pb[c & 1][t][0]), "=&v"(pb[c & 1][t][1]), "=&v"(pb[c & 1][t][2]), "=&v"(pb[c & 1][t][3])
+          : "v"(src)
+          : "memory");
+    };
+    if (!first) {  // the first pass's x chunks were issued before the modality wait
+      issue_x(0);
+      if constexpr (X0 > 1) issue_x(1);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) issue_p(0, t);
+    if constexpr (NCH > 1) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) issue_p(1, t);
+    }
+    tm_f32x4 acc[2][4];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[rb][c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      // x(c) and P(c) are in once only the loads issued after both remain:
+      // P(1) for chunk 0 (x(1) precedes P(0)); for chunk c >= 1 the P and x of
+      // chunk c + 1, issued while chunk c - 1 was multiplied
+      constexpr int kAfter0 = NCH > 1 ? 16 : 0;
+      if (c == 0)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfter0) : "memory");
+      else if (c + 1 < NCH)
+        asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(pb[c & 1][t][u]));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          const uint4 a = read_a(c, rb, t);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const tm_u32x4 &bb = pb[c & 1][t][u];
+            acc[rb][u] = tm_mfma16x16x32<DT>(a, make_uint4(bb.x, bb.y, bb.z, bb.w), acc[rb][u]);
+          }
+        }
+        if (c + 2 < NCH) issue_p(c + 2, t);
+      }
+      if (c + 2 < NCH) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // chunk c's fragment reads are done
+        issue_x(c + 2);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // nothing of this pass still lands in the ring
+    // D row of acc[rb][u][i] is 16*rb + 4*(lane>>4) + i
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool mine = (rows_of_pass >> (16 * rb + 4 * (lane >> 4) + i)) & 1u;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) fin[rb][u][i] = mine ? acc[rb][u][i] : fin[rb][u][i];
+      }
+  };
+  if (vis_bits) run_pass(pv, vis_bits, true);  // uniform branches
+  if (txt_bits) run_pass(pt, txt_bits, vis_bits == 0);
+  if (!vis_bits && !txt_bits) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no row: drain the x loads
+
+  float *red = reinterpret_cast<float *>(&ring[0][0]);  // [4][32][kRowPad], wave w inside its own ring
+  auto red_at = [&](int w, int r, int c) { return red + w * (2 * 512 * 4) + r * kRowPad + c; };
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * rb + 4 * (lane >> 4) + i;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) *red_at(wave, r, 16 * u + (lane & 15)) = fin[rb][u][i];
+    }
+  __syncthreads();
+
+  const int64_t gr = row0 + erow;
+  const bool ok = gr < n;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {  // wave order: deterministic
+    const float4 a = *reinterpret_cast<const float4 *>(red_at(w, erow, 8 * part));
+    const float4 c = *reinterpret_cast<const float4 *>(red_at(w, erow, 8 * part + 4));
     v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
     v[4] += c.x; v[5] += c.y; v[6] += c.z; v[7] += c.w;
   }
@@ -1126,6 +1353,17 @@ void launch_cols(const void *x, int64_t n, int hidden, int64_t ld_x, const uint8
     cr.a = *ra;
     cr.first = blocks;
     blocks += tm_cdiv(n, 32);
+  }
+  if constexpr (DIM == 128) {
+    // hidden 2048 or 2560: every wave's slice is 4 or 5 whole chunks, the pipelined kernel
+    if (hidden == 2048 || hidden == 2560) {
+      auto kern = hidden == 2048 ? project_cols_pipe_kernel<DT, DIM, RVPL, 4> : project_cols_pipe_kernel<DT, DIM, RVPL, 5>;
+      hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, static_cast<const T *>(x), n, hidden,
+                         ld_x, is_vision, static_cast<const T *>(pv), static_cast<const T *>(bv),
+                         static_cast<const T *>(pt ? pt : pv), static_cast<const T *>(pt ? bt : bv),
+                         static_cast<T *>(q), ld_q, qn_part, keys, n_tiles, cr);
+      return;
+    }
   }
   hipLaunchKernelGGL((project_cols_kernel<DT, DIM, RVPL>), dim3((unsigned)blocks), dim3(256), 0, stream,
                      static_cast<const T *>(x), n, hidden, ld_x, is_vision, static_cast<const T *>(pv),

@@ -536,6 +536,10 @@ def test_layer_forward_one_call_matches_staged(hip_device):
 @pytest.mark.parametrize("n,hidden,dim,mix,n_cent,dup", [
     (300, 1000, 128, False, 1024, False), (515, 2080, 64, True, 1024, False), (96, 264, 128, True, 1024, False),
     (4096, 2048, 128, True, 1024, False),
+    # hidden 2048 / 2560 (pipelined projection: 4 / 5 chunks per wave) with a
+    # ragged row tile and mixed tiles; other multiples of 32 (register kernel)
+    (300, 2560, 128, True, 1024, False), (777, 2048, 128, True, 2048, False),
+    (200, 480, 128, True, 1024, False), (777, 1056, 128, True, 2048, False),
     # ranked form (wide search decoding the keys, keep set ranked in the
     # combine): config-2 shape, repeated tokens (tied distances at the keep
     # boundary), d = 64, a ragged last query tile and centroid range
