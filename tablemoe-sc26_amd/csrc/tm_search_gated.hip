@@ -125,6 +125,12 @@ __global__ __launch_bounds__(kThreads) void gated_kernel(
 // Segment-grouped gated search (16-bit tables, DIM % 16 == 0).
 // ---------------------------------------------------------------------------
 constexpr int kSegThreads = 256;
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load and store of the wave (its fence), which
+// would drain the next block's query prefetch and this block's result stores
+// at each barrier; the exchanges here go through LDS alone.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 constexpr int kSegList = 8192;  // pair slots per workgroup (LDS); tokens per chunk <= kSegList / top_k
 
 // REG: tables of at most 256 rows with DIM <= 128 -- each wave loads its
@@ -158,13 +164,19 @@ __global__ __launch_bounds__(kSegThreads) void gated_seg_kernel(
   // the loads are in flight together; pair p = token * top_k + slot.
   constexpr int kScanTok = 4, kScanSlots = 8;
   const int ntok = (int)(b1 - b0);
-  auto test_pair = [&](int bl, int s, int64_t ex) {
+  auto row_ptr = [&](int m, int64_t cb) {
+    int64_t c = cb + (lane & 31);
+    c = c < n_cent ? c : n_cent - 1;  // rows past the table re-read its last row (masked below)
+    return keys + e * ks_e + m * ks_m + c * ks_c + 8 * (lane >> 5);
+  };
+  // the pair's searched flag and modality, from values already loaded
+  auto test_pair = [&](int bl, int s, int64_t ex, bool rflag, bool vflag) {
     const bool valid = ex >= 0 && ex < n_exp;
     if (ex == e || (!valid && e == 0)) {
       const int64_t b = b0 + bl;
-      const bool searched = valid && s >= col_offset && (reuse == nullptr || reuse[b * rs_b + s * rs_s]);
+      const bool searched = valid && s >= col_offset && rflag;
       if (searched) {
-        const int m = (is_vision == nullptr || is_vision[b]) ? 0 : 1;
+        const int m = vflag ? 0 : 1;
         const int pos = atomicAdd(&cnt[m], 1);
         list[m == 0 ? pos : kSegList - 1 - pos] = (uint32_t)(bl * top_k + s);
       } else {
@@ -174,38 +186,128 @@ __global__ __launch_bounds__(kSegThreads) void gated_seg_kernel(
       }
     }
   };
-  for (int t0 = 0; t0 < ntok; t0 += kSegThreads * kScanTok) {
-    int64_t ex[kScanTok][kScanSlots];
+  const bool fast = top_k == kScanSlots && ss_s == 1 && ss_b == kScanSlots &&
+                    (reuse == nullptr || (rs_s == 1 && rs_b == kScanSlots)) &&
+                    (reinterpret_cast<uintptr_t>(sel) & 15) == 0 &&
+                    (reuse == nullptr || (reinterpret_cast<uintptr_t>(reuse) & 1) == 0);
+  if (fast) {  // uniform
+    // 1) coalesced scan of contiguous [n][8] ids: 4 lanes per token, 2 slots
+    // each (one 16-byte load of ids, one 2-byte load of reuse flags); a pass
+    // covers 64 tokens and every pass's loads are issued before any test.
+    constexpr int kPasses = 16;
+    const int q4 = lane & 3, s0 = 2 * q4;
+    for (int t0 = 0; t0 < ntok; t0 += kPasses * 64) {
+      uint4 idv[kPasses];
+      uint16_t rfv[kPasses];
+      uint8_t vfv[kPasses];
 #pragma unroll
-    for (int u = 0; u < kScanTok; ++u) {
-      const int bl = t0 + u * kSegThreads + tid;
-      const int blc = bl < ntok ? bl : ntok - 1;
+      for (int u = 0; u < kPasses; ++u) {
+        const int bl = t0 + u * 64 + (tid >> 2);
+        const int64_t b = b0 + (bl < ntok ? bl : ntok - 1);  // clamped: every load is in bounds
+        idv[u] = *reinterpret_cast<const uint4 *>(sel + b * kScanSlots + s0);
+        rfv[u] = reuse == nullptr ? (uint16_t)0x0101 : *reinterpret_cast<const uint16_t *>(reuse + b * kScanSlots + s0);
+        vfv[u] = is_vision == nullptr ? (uint8_t)1 : is_vision[b];
+      }
+      // Every pass's loads are issued before the first test: the values are
+      // inputs of these empty statements (without them the scheduler sinks
+      // loads toward their tests and their latencies add up: 31 vs 21 us).
 #pragma unroll
-      for (int s = 0; s < kScanSlots; ++s) {
-        const int sc = s < top_k ? s : top_k - 1;
-        ex[u][s] = sel[(b0 + blc) * ss_b + sc * ss_s];  // clamped: every load is in bounds
+      for (int u = 0; u < kPasses; ++u)
+        asm volatile("" ::"v"(idv[u].x), "v"(idv[u].z), "v"((uint32_t)rfv[u]), "v"((uint32_t)vfv[u]));
+      // test, branch-free: bit 2u + h of mv / mt marks a searched vision /
+      // text pair of expert e (token t0 + 64u + tid / 4, slot s0 + h); zmask
+      // marks e's pairs that are not searched (zero outputs, written below)
+      const uint32_t e32 = (uint32_t)e, nexp32 = (uint32_t)n_exp;
+      const int tl = tid >> 2;
+      uint32_t mv = 0, mt = 0, zmask = 0;
+#pragma unroll
+      for (int u = 0; u < kPasses; ++u) {
+        const bool in = t0 + u * 64 + tl < ntok;
+        const bool text = vfv[u] == 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t lo = h == 0 ? idv[u].x : idv[u].z, hi = h == 0 ? idv[u].y : idv[u].w;
+          const bool valid = hi == 0 && lo < nexp32;  // negative ids have hi != 0
+          const bool mine = in && (valid ? lo == e32 : e32 == 0);
+          const bool searched = mine && valid && s0 + h >= col_offset && ((rfv[u] >> (8 * h)) & 0xffu) != 0;
+          const uint32_t bit = 1u << (2 * u + h);
+          zmask |= (mine && !searched) ? bit : 0u;
+          mv |= (searched && !text) ? bit : 0u;
+          mt |= (searched && text) ? bit : 0u;
+        }
+      }
+      auto token_of = [&](int k) { return t0 + (k >> 1) * 64 + tl; };
+      while (zmask != 0) {  // rare: zero outputs of e's pairs that are not searched
+        const int k = __builtin_ctz(zmask);
+        zmask &= zmask - 1;
+        const int64_t o = (b0 + token_of(k)) * os_b + (int64_t)(s0 + (k & 1)) * os_s;
+        out_hit[o] = 0;
+        out_idx[o] = 0;
+      }
+      // append: one LDS atomic per wave and modality (positions from a wave
+      // prefix sum of the per-lane counts), then each lane writes its pairs
+      const uint32_t cv = (uint32_t)__builtin_popcount(mv), ct = (uint32_t)__builtin_popcount(mt);
+      const uint32_t iv = tm_wave_incl_scan(cv), it = tm_wave_incl_scan(ct);
+      const uint32_t tv = (uint32_t)__builtin_amdgcn_readlane((int)iv, 63);
+      const uint32_t tt = (uint32_t)__builtin_amdgcn_readlane((int)it, 63);
+      int bv = 0, bt = 0;
+      if (lane == 63) {
+        if (tv) bv = atomicAdd(&cnt[0], (int)tv);
+        if (tt) bt = atomicAdd(&cnt[1], (int)tt);
+      }
+      int pv = __builtin_amdgcn_readlane(bv, 63) + (int)(iv - cv);
+      int pt = __builtin_amdgcn_readlane(bt, 63) + (int)(it - ct);
+      while (mv != 0) {
+        const int k = __builtin_ctz(mv);
+        mv &= mv - 1;
+        list[pv++] = (uint32_t)(token_of(k) * kScanSlots + s0 + (k & 1));
+      }
+      while (mt != 0) {
+        const int k = __builtin_ctz(mt);
+        mt &= mt - 1;
+        list[kSegList - 1 - pt++] = (uint32_t)(token_of(k) * kScanSlots + s0 + (k & 1));
       }
     }
-#pragma unroll
-    for (int u = 0; u < kScanTok; ++u) {
-      const int bl = t0 + u * kSegThreads + tid;
-      if (bl >= ntok) continue;
-#pragma unroll
-      for (int s = 0; s < kScanSlots; ++s)
-        if (s < top_k) test_pair(bl, s, ex[u][s]);
-      for (int s = kScanSlots; s < top_k; ++s) test_pair(bl, s, sel[(b0 + bl) * ss_b + s * ss_s]);
+  } else {
+    // 1) scan: a thread takes tokens tid, tid + 256, ... and loads the slot
+    // ids, reuse flags and modality bytes of kScanTok of them (up to
+    // kScanSlots slots each) before testing any: every load is in flight
+    // together and no test waits on a load of its own.
+    for (int t0 = 0; t0 < ntok; t0 += kSegThreads * kScanTok) {
+      int64_t ex[kScanTok][kScanSlots];
+      uint8_t rf[kScanTok][kScanSlots];
+      uint8_t vf[kScanTok];
+  #pragma unroll
+      for (int u = 0; u < kScanTok; ++u) {
+        const int bl = t0 + u * kSegThreads + tid;
+        const int64_t b = b0 + (bl < ntok ? bl : ntok - 1);  // clamped: every load is in bounds
+  #pragma unroll
+        for (int s = 0; s < kScanSlots; ++s) {
+          const int sc = s < top_k ? s : top_k - 1;
+          ex[u][s] = sel[b * ss_b + sc * ss_s];
+          rf[u][s] = reuse == nullptr ? (uint8_t)1 : reuse[b * rs_b + sc * rs_s];
+        }
+        vf[u] = is_vision == nullptr ? (uint8_t)1 : is_vision[b];
+      }
+  #pragma unroll
+      for (int u = 0; u < kScanTok; ++u) {
+        const int bl = t0 + u * kSegThreads + tid;
+        if (bl >= ntok) continue;
+  #pragma unroll
+        for (int s = 0; s < kScanSlots; ++s)
+          if (s < top_k) test_pair(bl, s, ex[u][s], rf[u][s] != 0, vf[u] != 0);
+        for (int s = kScanSlots; s < top_k; ++s) {
+          const int64_t b = b0 + bl;
+          test_pair(bl, s, sel[b * ss_b + s * ss_s], reuse == nullptr || reuse[b * rs_b + s * rs_s],
+                    vf[u] != 0);
+        }
+      }
     }
   }
-  __syncthreads();
+  lds_barrier();  // the list and the counts are complete (the pair stores may still fly)
   const int counts[2] = {cnt[0], cnt[1]};
-  // 2) search, 32 pairs of one modality at a time
-  auto row_ptr = [&](int m, int64_t cb) {
-    int64_t c = cb + (lane & 31);
-    c = c < n_cent ? c : n_cent - 1;  // rows past the table re-read its last row (masked below)
-    return keys + e * ks_e + m * ks_m + c * ks_c + 8 * (lane >> 5);
-  };
   uint4 kreg[REG ? 2 : 1][REG ? 2 : 1][KS];
-  if constexpr (REG) {
+  if constexpr (REG) {  // the tables that have pairs, held in registers for every block
 #pragma unroll
     for (int m = 0; m < 2; ++m)
       if (counts[m] > 0)  // uniform
@@ -216,37 +318,73 @@ __global__ __launch_bounds__(kSegThreads) void gated_seg_kernel(
           for (int t = 0; t < KS; ++t) kreg[m][bi][t] = *reinterpret_cast<const uint4 *>(krow + 16 * t);
         }
   }
-  for (int m = 0; m < 2; ++m) {
+  // 2) search, 32 pairs of one modality at a time: the vision blocks, then
+  // the text blocks; each block's queries are loaded while the previous
+  // block is scored
+  const int nbv = (counts[0] + 31) >> 5, nb = nbv + ((counts[1] + 31) >> 5);
+  auto block_pair = [&](int i, int &m, int &j, int &jj, uint32_t &p) {
+    m = i < nbv ? 0 : 1;
     const int c_m = counts[m];
-    for (int blk = 0; blk < c_m; blk += 32) {  // uniform
-      const int j = blk + (lane & 31);
-      const int jj = j < c_m ? j : blk;  // past the end: the block's first pair (result dropped)
-      const uint32_t p = list[m == 0 ? jj : kSegList - 1 - jj];
-      const T *qrow = q + (b0 + (int64_t)(p / (uint32_t)top_k)) * ld_q + 8 * (lane >> 5);
-      uint4 qf[KS];
+    const int blk = (i < nbv ? i : i - nbv) * 32;
+    j = blk + (lane & 31);
+    jj = j < c_m ? j : blk;  // past the end: the block's first pair (result dropped)
+    p = list[m == 0 ? jj : kSegList - 1 - jj];
+  };
+  auto load_q = [&](uint32_t p, uint4 (&f)[KS]) {
+    const T *qrow = q + (b0 + (int64_t)(p / (uint32_t)top_k)) * ld_q + 8 * (lane >> 5);
 #pragma unroll
-      for (int t = 0; t < KS; ++t) qf[t] = *reinterpret_cast<const uint4 *>(qrow + 16 * t);
+    for (int t = 0; t < KS; ++t) f[t] = *reinterpret_cast<const uint4 *>(qrow + 16 * t);
+  };
+  uint4 qf[KS], qn[KS];
+  if (nb > 0) {  // uniform
+    int m0, j0, jj0;
+    uint32_t p0;
+    block_pair(0, m0, j0, jj0, p0);
+    load_q(p0, qn);
+  }
+  for (int i = 0; i < nb; ++i) {  // uniform
+    int m, j, jj;
+    uint32_t p;
+    block_pair(i, m, j, jj, p);
+    const int c_m = counts[m];
+#pragma unroll
+    for (int t = 0; t < KS; ++t) qf[t] = qn[t];
+    if (i + 1 < nb) {  // uniform: the next block's queries fly while this one is scored
+      int m1, j1, jj1;
+      uint32_t p1;
+      block_pair(i + 1, m1, j1, jj1, p1);
+      load_q(p1, qn);
+    }
+    {
       float best = -__builtin_huge_valf();
       int best_i = 0x7fffffff;
       auto score_block = [&](const uint4 (&kf)[KS], int64_t cb) {
         tm_f32x16 acc{};
 #pragma unroll
         for (int t = 0; t < KS; ++t) acc = tm_mfma32x32x16<DT>(kf[t], qf[t], acc);
-        // lane holds pair (lane % 32) against rows 8(i/4) + 4(lane/32) + i%4 of the block, ascending in i
+        // lane holds pair (lane % 32) against rows 8(i/4) + 4(lane/32) + i%4 of
+        // the block, ascending in i; selects, not branches (the first of equal
+        // maxima stays)
+        const int c0 = (int)cb + 4 * (lane >> 5), nc = (int)n_cent;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int64_t ci = cb + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-          if (ci < n_cent && acc[i] > best) {
-            best = acc[i];
-            best_i = (int)ci;
-          }
+          const int ci = c0 + 8 * (i >> 2) + (i & 3);
+          const float v = acc[i];
+          const bool take = (ci < nc) & (v > best);
+          best = take ? v : best;
+          best_i = take ? ci : best_i;
         }
       };
       if constexpr (REG) {
 #pragma unroll
         for (int bi = 0; bi < 2; ++bi) {
           const int64_t cb = (int64_t)wave * 32 + bi * 128;
-          if (cb < n_cent) score_block(kreg[m][bi], cb);  // uniform per wave
+          if (cb < n_cent) {  // uniform per wave
+            if (m == 0)  // uniform: constant register indices on both sides
+              score_block(kreg[0][bi], cb);
+            else
+              score_block(kreg[1][bi], cb);
+          }
         }
       } else {
         for (int64_t cb = (int64_t)wave * 32; cb < n_cent; cb += 4 * 32) {  // uniform per wave
@@ -267,7 +405,7 @@ __global__ __launch_bounds__(kSegThreads) void gated_seg_kernel(
         red_v[wave][lane] = best;
         red_i[wave][lane] = best_i;
       }
-      __syncthreads();
+      lds_barrier();
       if (wave == 0 && lane < 32 && j < c_m) {
         float v = red_v[0][lane];
         int bi = red_i[0][lane];
@@ -288,7 +426,7 @@ __global__ __launch_bounds__(kSegThreads) void gated_seg_kernel(
         out_hit[o] = hit ? 1 : 0;
         out_idx[o] = hit ? (int64_t)bi : 0;
       }
-      __syncthreads();  // red_* are rewritten by the next block
+      lds_barrier();  // red_* are rewritten by the next block
     }
   }
 }
