@@ -219,21 +219,40 @@ __global__ __launch_bounds__(kSegThreads) void gated_seg_kernel(
       // marks e's pairs that are not searched (zero outputs, written below)
       const uint32_t e32 = (uint32_t)e, nexp32 = (uint32_t)n_exp;
       const int tl = tid >> 2;
+      const bool col_ok[2] = {s0 >= col_offset, s0 + 1 >= col_offset};
       uint32_t mv = 0, mt = 0, zmask = 0;
+      if (e32 != 0) {  // uniform: a pair is e's exactly when its id equals e (e < n_exp: valid)
 #pragma unroll
-      for (int u = 0; u < kPasses; ++u) {
-        const bool in = t0 + u * 64 + tl < ntok;
-        const bool text = vfv[u] == 0;
+        for (int u = 0; u < kPasses; ++u) {
+          const uint32_t out = t0 + u * 64 + tl < ntok ? 0u : 1u;  // clamped rows past the chunk
+          const bool text = vfv[u] == 0;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t lo = h == 0 ? idv[u].x : idv[u].z, hi = h == 0 ? idv[u].y : idv[u].w;
-          const bool valid = hi == 0 && lo < nexp32;  // negative ids have hi != 0
-          const bool mine = in && (valid ? lo == e32 : e32 == 0);
-          const bool searched = mine && valid && s0 + h >= col_offset && ((rfv[u] >> (8 * h)) & 0xffu) != 0;
-          const uint32_t bit = 1u << (2 * u + h);
-          zmask |= (mine && !searched) ? bit : 0u;
-          mv |= (searched && !text) ? bit : 0u;
-          mt |= (searched && text) ? bit : 0u;
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t lo = h == 0 ? idv[u].x : idv[u].z, hi = h == 0 ? idv[u].y : idv[u].w;
+            const bool mine = ((lo ^ e32) | hi | out) == 0;
+            const bool searched = mine && col_ok[h] && ((rfv[u] >> (8 * h)) & 0xffu) != 0;
+            const uint32_t bit = 1u << (2 * u + h);
+            zmask |= (mine && !searched) ? bit : 0u;
+            mv |= (searched && !text) ? bit : 0u;
+            mt |= (searched && text) ? bit : 0u;
+          }
+        }
+      } else {  // expert 0 also takes the pairs whose id is out of range (zero outputs)
+#pragma unroll
+        for (int u = 0; u < kPasses; ++u) {
+          const bool in = t0 + u * 64 + tl < ntok;
+          const bool text = vfv[u] == 0;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t lo = h == 0 ? idv[u].x : idv[u].z, hi = h == 0 ? idv[u].y : idv[u].w;
+            const bool valid = hi == 0 && lo < nexp32;  // negative ids have hi != 0
+            const bool mine = in && (!valid || lo == 0);
+            const bool searched = mine && valid && col_ok[h] && ((rfv[u] >> (8 * h)) & 0xffu) != 0;
+            const uint32_t bit = 1u << (2 * u + h);
+            zmask |= (mine && !searched) ? bit : 0u;
+            mv |= (searched && !text) ? bit : 0u;
+            mt |= (searched && text) ? bit : 0u;
+          }
         }
       }
       auto token_of = [&](int k) { return t0 + (k >> 1) * 64 + tl; };
