@@ -478,6 +478,8 @@ int64_t seg_tokens_per_wg(int64_t n, int64_t n_exp, int top_k) {
 constexpr int kMaxOnline = 1024;
 constexpr int kHybRowsPerSlice = 128;
 constexpr int kHybMaxSlices = 16;
+constexpr int kHybMaxOnTopk = 16;  // window rows' ids compared from registers up to this many
+constexpr int kFinThreads = 512;   // hybrid_finish_kernel: q waves, the window wave, 8 search waves
 
 inline int hybrid_slices(int hidden) {
   int g = hidden / kHybRowsPerSlice;
@@ -557,7 +559,7 @@ __global__ __launch_bounds__(kThreads) void hybrid_partial_kernel(
 }
 
 template <int DT, bool VEC>
-__global__ __launch_bounds__(kThreads) void hybrid_finish_kernel(
+__global__ __launch_bounds__(kFinThreads) void hybrid_finish_kernel(
     const uint8_t *__restrict__ is_vision, const typename Elem<DT>::T *__restrict__ bv,
     const typename Elem<DT>::T *__restrict__ bt, int dim, int n_slices, const float *__restrict__ partial,
     const float *__restrict__ scores, int n_valid, const int64_t *__restrict__ on_ids, int on_topk,
@@ -574,16 +576,28 @@ __global__ __launch_bounds__(kThreads) void hybrid_finish_kernel(
   const int64_t b = blockIdx.x;
   const bool vis = is_vision == nullptr || is_vision[b];
   const bool need_proj = keep_k < top_k;
-  // 1) q = dtype(sum of the slice partials + bias)
+  // the slot's expert id, loaded first (used after the first barrier)
+  const int64_t my_e = tid < top_k ? sel[b * ss_b + tid * ss_s] : 0;
+  // 1) q = dtype(sum of the slice partials + bias): every slice's partial is
+  // requested before any is added (in slice order, as before)
   if (need_proj && tid < dim) {
+    float pv[kHybMaxSlices];
+#pragma unroll
+    for (int g = 0; g < kHybMaxSlices; ++g) {
+      const int gc = g < n_slices ? g : n_slices - 1;
+      pv[g] = partial[((int64_t)b * n_slices + gc) * dim + tid];
+    }
+    const float bias = Elem<DT>::to_f((vis ? bv : bt)[tid]);
     float sum = 0.f;
-    for (int g = 0; g < n_slices; ++g) sum += partial[((int64_t)b * n_slices + g) * dim + tid];
-    const float v = tm_round<DT>(sum + Elem<DT>::to_f((vis ? bv : bt)[tid]));
+#pragma unroll
+    for (int g = 0; g < kHybMaxSlices; ++g)
+      if (g < n_slices) sum += pv[g];
+    const float v = tm_round<DT>(sum + bias);
     qsh[tid] = v;
     if (q_out != nullptr) q_out[b * ld_q_out + tid] = Elem<DT>::from_f(v);
   }
-  // 2) window arg-max (first index of the maximum), one wave
-  if (wave == 0) {
+  // 2) window arg-max (first index of the maximum) on wave 4, beside the q waves
+  if (wave == 4) {
     float mx = -__builtin_huge_valf();
     int js = 0x7fffffff;
     for (int j = lane; j < n_valid; j += 64) {
@@ -599,24 +613,34 @@ __global__ __launch_bounds__(kThreads) void hybrid_finish_kernel(
     }
   }
   __syncthreads();
-  // 3) online hits of the searched slots
+  // 3) online hits of the searched slots: the window row's ids all requested
+  // at once, then the first match
   if (tid < top_k) {
     const int s = tid;
     uint8_t hit = 0;
     int slot = 0;
     if (s >= keep_k && s_valid_on) {
-      const int64_t e = sel[b * ss_b + s * ss_s];
       const int64_t *ids = on_ids + (int64_t)s_jstar * ld_on_ids;
-      for (int t = 0; t < on_topk; ++t) {
-        if (ids[t] == e) { hit = 1; slot = t; break; }
+      if (on_topk <= kHybMaxOnTopk) {
+        int64_t v[kHybMaxOnTopk];
+#pragma unroll
+        for (int t = 0; t < kHybMaxOnTopk; ++t) v[t] = ids[t < on_topk ? t : 0];
+#pragma unroll
+        for (int t = kHybMaxOnTopk - 1; t >= 0; --t)  // descending: the first match wins
+          if (t < on_topk && v[t] == my_e) { hit = 1; slot = t; }
+      } else {
+        for (int t = 0; t < on_topk; ++t) {
+          if (ids[t] == my_e) { hit = 1; slot = t; break; }
+        }
       }
     }
     s_onhit[s] = hit;
     s_onslot[s] = slot;
   }
   __syncthreads();
-  // 4) offline search of the remaining slots, one wave per slot; every output written
-  for (int s = wave; s < top_k; s += kThreads / 64) {
+  // 4) offline search of the remaining slots, one wave per slot (8 waves);
+  // every output written
+  for (int s = wave; s < top_k; s += kFinThreads / 64) {
     const int64_t o = b * os_b + s * os_s;
     uint8_t hit = 0;
     int64_t idx = 0;
@@ -774,7 +798,7 @@ extern "C" int tm_search_hybrid(int32_t dtype, const void *x, int64_t n_tokens, 
                          static_cast<const T *>(proj_vis), pt, ps_h, ps_d, dim, hybrid_slice_rows(hidden, G),
                          keep_k < top_k ? 1 : 0, static_cast<const T *>(online_keys), ld_online, n_online_valid,
                          partial, scores);
-      hipLaunchKernelGGL((hybrid_finish_kernel<DT, VEC>), dim3((unsigned)n_tokens), dim3(kThreads), 0, s, is_vision,
+      hipLaunchKernelGGL((hybrid_finish_kernel<DT, VEC>), dim3((unsigned)n_tokens), dim3(kFinThreads), 0, s, is_vision,
                          static_cast<const T *>(bias_vis), bt, dim, G, partial, scores, n_online_valid, online_ids,
                          online_topk, ld_online_ids, static_cast<const T *>(keys), n_experts, n_centroids, ks_e, ks_m,
                          ks_c, sel, top_k, ss_b, ss_s, keep_k, on_hit, on_idx, off_hit, off_idx, on_slot, os_b, os_s,
