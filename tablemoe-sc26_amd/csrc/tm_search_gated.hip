@@ -500,6 +500,8 @@ __global__ __launch_bounds__(kThreads) void hybrid_partial_kernel(
   const int64_t b = blockIdx.x;
   const int g = blockIdx.y, G = gridDim.y;
   const T *xr = x + b * ld_x;
+  // (unrolled loops below: several iterations' loads are in flight together)
+#pragma unroll 8
   for (int h = tid; h < hidden; h += kThreads) xsh[h] = Elem<DT>::to_f(xr[h]);
   __syncthreads();
   // projection partial over rows [h0, h1) of this slice, every column
@@ -518,6 +520,7 @@ __global__ __launch_bounds__(kThreads) void hybrid_partial_kernel(
       if (VEC && ps_h == 1) {  // k-contiguous copy: each thread's rows are one contiguous run
         const T *src = P + (int64_t)col * ps_d;
         int h = a0;
+#pragma unroll 4
         for (; h + 8 <= a1; h += 8) {
           float v[8];
           tm_load8<DT>(src + h, v);
@@ -543,6 +546,7 @@ __global__ __launch_bounds__(kThreads) void hybrid_partial_kernel(
     const T *kr = on_keys + (int64_t)j * ld_on;
     float acc = 0.f;
     if (VEC) {
+#pragma unroll 4
       for (int h = 8 * lane; h + 8 <= hidden; h += 8 * 64) {
         float v[8];
         tm_load8<DT>(kr + h, v);
