@@ -89,6 +89,14 @@ class GlobalTable:
             self._bufs[name] = t
         return t[:numel].view(shape)
 
+    def _side_stream(self) -> torch.cuda.Stream:
+        """The table's second stream on its device (default priority), made
+        on first use."""
+        s = getattr(self, "_side", None)
+        if s is None:
+            s = self._side = torch.cuda.Stream(self.device)
+        return s
+
     # ---------------------------------------------------------------- stages
     def project(self, hidden: torch.Tensor, is_vision: torch.Tensor | None = None):
         """q = dtype(x @ P_m + bias_m) and ||q||^2 (fp32)."""
@@ -287,23 +295,40 @@ class GlobalTable:
         gather + combine on top: out = dtype(dtype(residual + shared) + y),
         y = the renormalised routed slots (kept tokens) or the cached output
         of the nearest centroid (the others).  Top-1 table.  Returns the
-        stage outputs and ``slot_out``; buffers are reused by the next call."""
+        stage outputs and ``slot_out``; buffers are reused by the next call.
+
+        The shared experts depend on neither the search nor the routed
+        recompute, so they run on a second stream of the device (default
+        priority), forked from the caller's stream before the search and
+        joined before the combine: their workgroups fill the CUs that the
+        single-workgroup launches (keep select, slot grouping) and the last
+        partial rounds of the routed GEMMs leave idle.  The fork and join are
+        stream waits, so the call stays capturable in a HIP graph."""
         from ..ops import expert_swiglu
 
-        res = self.layer_search(hidden, is_vision, router_logits, router_top_k, 1, keep_rate)
         n = hidden.shape[0]
-        slot_out = self._buf("recompute_slots", (n, router_top_k, self.hidden), self.dtype)
-        experts.forward(hidden, res["ids"], res["keep"], slot_out)
+        main = torch.cuda.current_stream(self.device)
+        side = None
         base = residual
         if shared is not None:
             w1, w3, w2 = shared
+            # allocated on the caller's stream, which waits for the side
+            # stream at the join, before any later call can free them
             base = self._buf("shared_plus_residual", (n, self.hidden), self.dtype)
             nbytes = N.lib().tm_swiglu_workspace_size(n, w1.shape[0], N.dtype_tag(self.dtype))
             ws = self._buf("shared_ws", (max(nbytes, 1),), torch.uint8)
-            if residual is None:
-                expert_swiglu(hidden, w1, w3, w2, out=base, workspace=ws)
-            else:
-                expert_swiglu(hidden, w1, w3, w2, out=base, workspace=ws, addend=residual)
+            side = self._side_stream()
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                if residual is None:
+                    expert_swiglu(hidden, w1, w3, w2, out=base, workspace=ws)
+                else:
+                    expert_swiglu(hidden, w1, w3, w2, out=base, workspace=ws, addend=residual)
+        res = self.layer_search(hidden, is_vision, router_logits, router_top_k, 1, keep_rate)
+        slot_out = self._buf("recompute_slots", (n, router_top_k, self.hidden), self.dtype)
+        experts.forward(hidden, res["ids"], res["keep"], slot_out)
+        if side is not None:
+            main.wait_stream(side)
         out = self.gather_combine(res["keep"], slot_out, res["weights"], res["idx"], res["dist"], base, out)
         res["slot_out"] = slot_out
         res["out"] = out

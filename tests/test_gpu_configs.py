@@ -237,3 +237,55 @@ def test_config5_layer_end_to_end(hip_device):
                             torch.bfloat16, min_exact=0.9)
     _, want_idx, exact = O.global_search(q_h, np64(wl.centroids), 1)
     check_topk_rows(exact, np64(idx)[rows], want_idx, False, "config 5 search")
+
+
+def test_config5_layer_graph_replays(hip_device):
+    """The config-5 layer call runs its shared experts on a second stream
+    (forked from the caller's stream, joined before the combine).  Captured
+    in a HIP graph and replayed three times, with the output cleared and
+    other eager work on the caller's stream between replays, every replay
+    equals the eager call bit for bit (slot outputs of the kept tokens,
+    search outputs and combined rows)."""
+    from synth import make_workload
+    from table_moe.ops import GroupedExperts
+
+    dev = hip_device
+    wl = make_workload(5, with_slot_out=False, device=dev, gen_device=dev)
+    cfg = wl.cfg
+    n, h, e, k, inter = cfg["n"], cfg["hidden"], cfg["n_experts"], cfg["router_top_k"], 1536
+    g = torch.Generator(device=dev).manual_seed(56)
+    rnd = lambda *shape: (torch.randn(*shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)  # noqa: E731
+    ex = GroupedExperts(rnd(e, inter, h), rnd(e, inter, h), rnd(e, h, inter))
+    shared = (rnd(2 * inter, h), rnd(2 * inter, h), rnd(h, 2 * inter))
+    tbl = _table(wl)
+    out = torch.empty_like(wl.residual)
+
+    def layer():
+        return tbl.layer_forward_recompute(wl.x, wl.is_vision, wl.logits, ex, wl.residual, k, 0.6, shared=shared,
+                                           out=out)
+
+    res = layer()
+    torch.cuda.synchronize()
+    kb = res["keep"].bool()
+    want = {key: res[key].clone() for key in ("ids", "idx", "dist", "keep", "out")}
+    want_slot = res["slot_out"][kb].clone()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        layer()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        layer()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out.zero_()
+        res["slot_out"].zero_()
+        scratch = (wl.x.float() * (rep + 1)).sum()  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(scratch)
+        for key, val in want.items():
+            assert torch.equal(res[key], val), (rep, key)
+        assert torch.equal(res["slot_out"][kb], want_slot), rep
