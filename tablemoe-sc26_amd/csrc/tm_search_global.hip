@@ -57,7 +57,8 @@ constexpr int kWideStageBytes = 32768;
 constexpr int kWideMinGroups = 192;  // fewer leave too many of the 256 CUs idle
 // The layer call's ranked plan takes the wide kernel from 128 workgroups on:
 // its key decode and the ranked combine save the keep-select launch, which
-// outweighs the idle CUs (N = 2048 at C = 8192: 8 tiles x 16 ranges).
+// outweighs idle CUs (N = 2048 at C = 8192 fills the chip with half-round
+// ranges: 8 tiles x 32 ranges of 256 centroids).
 constexpr int kWideDecMinGroups = 128;
 
 struct WidePlan {
@@ -65,9 +66,12 @@ struct WidePlan {
 };
 
 inline int64_t wide_rows(int dim) { return kWideStageBytes / (dim * 2); }
+// Centroids of a half-round range (two stages).
+inline int64_t wide_half_rows(int dim) { return 2 * wide_rows(dim); }
 
 // One workgroup per CU where the shape allows: ranges of whole ring rounds
-// (4 stages), at most kDmaMaxChunk centroids (the start-value array).
+// (4 stages) or of half a round, at most kDmaMaxChunk centroids (the
+// start-value array).
 WidePlan plan_wide(int64_t n, int64_t c, int dim) {
   WidePlan p;
   p.tiles = tm_cdiv(n, kWideQ);
@@ -80,6 +84,17 @@ WidePlan plan_wide(int64_t n, int64_t c, int dim) {
   if (want < 1) want = 1;
   p.chunk = tm_cdiv(tm_cdiv(c, want), unit) * unit;
   p.nsplit = tm_cdiv(c, p.chunk);
+  // One round per range and still at most half the CUs busy: ranges of half
+  // a round (two stages, the kernel's HALF form, d = 128) double the
+  // workgroups, up to one per CU.
+  if (dim == 128 && p.chunk == unit && p.tiles * p.nsplit * 2 <= 256) {
+    const int64_t half = wide_half_rows(dim);
+    const int64_t ns = tm_cdiv(c, half);
+    if (p.tiles * ns <= 256) {
+      p.chunk = half;
+      p.nsplit = ns;
+    }
+  }
   return p;
 }
 
@@ -662,6 +677,9 @@ __global__ __launch_bounds__(kThreads, 2) void search_top1_kernel(
 // merge_top1_kernel) or one atomic minimum into keys[n] (DEC true: the layer
 // call).
 //
+// HALF: the range is at most two stages (half a ring round), run as two
+// steps without the round loop.
+//
 // With DEC, the workgroup that finishes a query tile last (one arrival
 // counter per tile, zero before the launch and left zero) decodes the
 // tile's finished keys into distance, centroid and |q|^2 (device-coherent
@@ -676,7 +694,7 @@ struct WideDecode {
   uint32_t *cnt;  // one per query tile
 };
 
-template <int DT, int DIM, int METRIC, bool DEC>
+template <int DT, int DIM, int METRIC, bool DEC, bool HALF>
 __global__ __launch_bounds__(kWideThreads, 1) void search_top1_wide_kernel(
     const typename Elem<DT>::T *__restrict__ q, int64_t n, int64_t ld_q,
     const typename Elem<DT>::T *__restrict__ cents, int64_t n_cent, int64_t ld_c,
@@ -880,11 +898,20 @@ __global__ __launch_bounds__(kWideThreads, 1) void search_top1_wide_kernel(
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  for (int s = 0; s < nstage4; s += 4) {
-    step(st0, st1, st3, s);
-    step(st1, st2, st0, s + 1);
-    step(st2, st3, st1, s + 2);
-    step(st3, st0, st2, s + 3);
+  if constexpr (HALF) {
+    // Half-round range (at most two stages): the two steps alone; the loads
+    // of the stages past the range read nothing, target this workgroup's
+    // ring and are waited for below, and the operands read ahead from slot
+    // 2 are never used.
+    step(st0, st1, st3, 0);
+    step(st1, st2, st0, 1);
+  } else {
+    for (int s = 0; s < nstage4; s += 4) {
+      step(st0, st1, st3, s);
+      step(st1, st2, st0, s + 1);
+      step(st2, st3, st1, s + 2);
+      step(st3, st0, st2, s + 3);
+    }
   }
 #pragma unroll
   for (int sl = 0; sl < 2; ++sl) top1_update(top[sl], accs[1][sl], cbs[1]);  // the last block is odd
@@ -959,6 +986,15 @@ __global__ __launch_bounds__(kWideThreads, 1) void search_top1_wide_kernel(
       wd.out_qn[r] = qn;
     }
   }
+}
+
+// The wide kernel for a plan's range length: the HALF form for half-round
+// ranges (d = 128 only: at d = 64 that form spills registers).
+template <int DT, int DIM, int METRIC, bool DEC>
+auto wide_kernel_for(int64_t chunk) {
+  if constexpr (DIM == 128)
+    if (chunk == wide_half_rows(DIM)) return search_top1_wide_kernel<DT, DIM, METRIC, DEC, true>;
+  return search_top1_wide_kernel<DT, DIM, METRIC, DEC, false>;
 }
 
 // The K smallest of two ascending K-lists, ascending: min(a[i], b[K-1-i]) is
@@ -1263,9 +1299,8 @@ int launch_search(int top_k, const void *q, int64_t n, int64_t ld_q, const float
       hipLaunchKernelGGL((search_stream_kernel<DT, DIM, K, 2, METRIC>), dim3((unsigned)p.nsplit), block, 0, stream,
                          Q, n, ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws, nullptr, 1);
   } else if (K == 1 && p.wide && wide_strides_ok(ld_q, ld_c, DIM)) {
-    hipLaunchKernelGGL((search_top1_wide_kernel<DT, DIM < 256 ? DIM : 128, METRIC, false>),
-                       dim3((unsigned)p.nsplit, (unsigned)p.row_blocks), dim3(kWideThreads), 0, stream, Q, n, ld_q, C,
-                       n_cent, ld_c, c_sqnorm, p.chunk, ws, WideDecode{});
+    hipLaunchKernelGGL((wide_kernel_for<DT, DIM < 256 ? DIM : 128, METRIC, false>(p.chunk)), dim3((unsigned)p.nsplit, (unsigned)p.row_blocks), dim3(kWideThreads), 0, stream, Q, n,
+                       ld_q, C, n_cent, ld_c, c_sqnorm, p.chunk, ws, WideDecode{});
   } else if (K == 1 && DIM <= 128 && ld_c * dma_rows(DIM) * (int64_t)sizeof(T) < ((int64_t)1 << 31)) {
     // (d = 256 would not fit two waves per SIMD; the stage byte offsets must fit 31 bits)
     hipLaunchKernelGGL((search_top1_kernel<DT, DIM < 256 ? DIM : 128, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
@@ -1592,7 +1627,7 @@ void launch_search_decode(const WidePlan &p, const void *q, int64_t n, int64_t l
                           int64_t n_cent, int64_t ld_c, const float *c_sqnorm, uint64_t *keys, const WideDecode &wd,
                           hipStream_t stream) {
   using T = typename Elem<DT>::T;
-  hipLaunchKernelGGL((search_top1_wide_kernel<DT, DIM, METRIC, true>), dim3((unsigned)p.nsplit, (unsigned)p.tiles),
+  hipLaunchKernelGGL((wide_kernel_for<DT, DIM, METRIC, true>(p.chunk)), dim3((unsigned)p.nsplit, (unsigned)p.tiles),
                      dim3(kWideThreads), 0, stream, static_cast<const T *>(q), n, ld_q, static_cast<const T *>(cents),
                      n_cent, ld_c, c_sqnorm, p.chunk, keys, wd);
 }
