@@ -448,6 +448,27 @@ int tm_grouped_swiglu(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden
                       const int32_t *expert_offsets, const int32_t *row_token, const int64_t *row_out,
                       const int32_t *tiles, void *out, void *workspace, size_t workspace_bytes,
                       tm_stream_t stream);
+/* Packed expert weights (no counterpart in the reference: a device layout
+ * of the same weights for tm_grouped_swiglu_packed).  Each tile of rows
+ * that one GEMM workgroup multiplies keeps its place in the nn.Linear
+ * layout but is reordered by 32-column stage, so a stage of the tile is one
+ * contiguous block in the order the GEMM stages it through LDS (the plain
+ * layout reads a 64-byte piece of each of the tile's rows per stage).
+ * role TM_PACK_GATE_UP: w is W1 or W3 [n_experts, inter, hidden]; role
+ * TM_PACK_DOWN: w is W2 [n_experts, hidden, inter].  out has w's size and
+ * must not overlap it; pack once per weight set.  F16/BF16. */
+#define TM_PACK_GATE_UP 0
+#define TM_PACK_DOWN 1
+int tm_expert_pack_weights(int32_t dtype, const void *w, int32_t n_experts, int32_t hidden, int32_t inter,
+                           int32_t role, void *out, tm_stream_t stream);
+/* tm_grouped_swiglu on weights packed by tm_expert_pack_weights (w1p and
+ * w3p with TM_PACK_GATE_UP, w2p with TM_PACK_DOWN); the same results bit for
+ * bit. */
+int tm_grouped_swiglu_packed(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden, int32_t inter,
+                             int32_t n_experts, const void *w1p, const void *w3p, const void *w2p, int64_t max_rows,
+                             const int32_t *expert_offsets, const int32_t *row_token, const int64_t *row_out,
+                             const int32_t *tiles, void *out, void *workspace, size_t workspace_bytes,
+                             tm_stream_t stream);
 
 /* ======================================================================
  * Mode G -- one MoE layer of the table path in ONE call.

@@ -80,7 +80,7 @@ struct TileSrc {
 // reads of the current stage's slot), and refill that slot with the stage
 // four ahead.  Stages past the last re-read the last one (never multiplied),
 // so the wait counts are the same in every iteration.
-template <int DT, int NB, int MODE, int BN>
+template <int DT, int NB, int MODE, int BN, bool PB>
 __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
     const typename Elem<DT>::T *__restrict__ A, int64_t lda, const int32_t *__restrict__ a_rows,
     const typename Elem<DT>::T *__restrict__ B0, const typename Elem<DT>::T *__restrict__ B1, int64_t b_expert,
@@ -140,7 +140,9 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
     a_src[j] = A + ar * lda + kc * 8;
   }
   // B: the expert's BN rows from n0 on, through a buffer; lane offsets fixed,
-  // the stage's K offset in the scalar offset.
+  // the stage's K offset in the scalar offset.  Packed weights (PB) hold each
+  // stage of the tile as one contiguous block in slot order, so slot p is at
+  // byte 16 p of the stage's block.
   tm_rsrc_t b_rs[NB];
   b_rs[0] = tm_make_rsrc(B0 + (int64_t)e * b_expert + (int64_t)n0 * K, (uint64_t)BN * K * sizeof(T));
   if constexpr (NB > 1) b_rs[1] = tm_make_rsrc(B1 + (int64_t)e * b_expert + (int64_t)n0 * K, (uint64_t)BN * K * sizeof(T));
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
   for (int j = 0; j < kBDma; ++j) {
     const int p = tid + kThreads * j;
     const int row = p / kCPR, kc = swz_chunk(row, p % kCPR);
-    b_off[j] = (uint32_t)row * (uint32_t)K * (uint32_t)sizeof(T) + (uint32_t)kc * 16u;
+    b_off[j] = PB ? (uint32_t)p * 16u : (uint32_t)row * (uint32_t)K * (uint32_t)sizeof(T) + (uint32_t)kc * 16u;
   }
   const int KT = K / BK;  // a multiple of 4 (the host checks)
   // Load j (0 .. kDma-1) of stage `stage` into `ring`: A loads first, then
@@ -162,7 +164,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
       tm_dma16_s(a_src[j] + (int64_t)kt * BK, lds + (uint32_t)(j * kThreads * 16));
     } else {
       constexpr int bb = (j - kADma) / kBDma, jb = (j - kADma) % kBDma;
-      tm_dma16_buf_so(b_rs[bb], b_off[jb], (uint32_t)kt * (uint32_t)(BK * sizeof(T)),
+      tm_dma16_buf_so(b_rs[bb], b_off[jb], (uint32_t)kt * (uint32_t)(PB ? kBStage * 16 : BK * sizeof(T)),
                       lds + (uint32_t)((kAStage + bb * kBStage + jb * kThreads) * 16));
     }
   };
@@ -401,14 +403,14 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
   }
 }
 
-template <int DT, int NB, int MODE, int BN>
+template <int DT, int NB, int MODE, int BN, bool PB>
 void launch_gemm(const void *A, int64_t lda, const int32_t *a_rows, const void *B0, const void *B1, int64_t b_expert,
                  int K, int N, const TileSrc &ts, int64_t grid_y, void *C, int64_t ldc, const int64_t *c_rows,
                  const void *addend, int64_t ld_add, hipStream_t s) {
   using T = typename Elem<DT>::T;
   const int n_tiles = N / BN;
   const int64_t blocks = tm_cdiv(grid_y, 8) * 8 * n_tiles;
-  hipLaunchKernelGGL((grouped_gemm_kernel<DT, NB, MODE, BN>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
+  hipLaunchKernelGGL((grouped_gemm_kernel<DT, NB, MODE, BN, PB>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
                      static_cast<const T *>(A), lda, a_rows, static_cast<const T *>(B0), static_cast<const T *>(B1),
                      b_expert, K, n_tiles, ts, static_cast<T *>(C), ldc, c_rows, static_cast<const T *>(addend),
                      ld_add);
@@ -417,27 +419,69 @@ void launch_gemm(const void *A, int64_t lda, const int32_t *a_rows, const void *
 // The two GEMMs of the MLP over the rows the tile source names; `addend`
 // (dense rows only, nullable) is added to the down projection before its
 // rounding.
+// Column tile of the down GEMM: 256 columns when hidden allows (half the LDS
+// reads per MFMA of 128-column tiles).
+inline int down_bn(int32_t hidden) { return hidden % (2 * kMinBN) == 0 ? 2 * kMinBN : kMinBN; }
+
+template <int DT, bool PB>
+void swiglu_launch(const void *x, int64_t ld_x, const int32_t *row_token, int32_t hidden, int32_t inter,
+                   const void *w1, const void *w3, const void *w2, const TileSrc &ts, int64_t grid_y, void *out,
+                   int64_t ld_out, const int64_t *row_out, void *fused, const void *addend, int64_t ld_add,
+                   hipStream_t s) {
+  launch_gemm<DT, 2, kModeUp, kMinBN, PB>(x, ld_x, row_token, w1, w3, (int64_t)inter * hidden, hidden, inter, ts,
+                                          grid_y, fused, inter, nullptr, nullptr, 0, s);
+  if (down_bn(hidden) == 2 * kMinBN)
+    launch_gemm<DT, 1, kModeDown, 2 * kMinBN, PB>(fused, inter, nullptr, w2, nullptr, (int64_t)hidden * inter, inter,
+                                                  hidden, ts, grid_y, out, ld_out, row_out, addend, ld_add, s);
+  else
+    launch_gemm<DT, 1, kModeDown, kMinBN, PB>(fused, inter, nullptr, w2, nullptr, (int64_t)hidden * inter, inter,
+                                              hidden, ts, grid_y, out, ld_out, row_out, addend, ld_add, s);
+}
+
+// The two GEMMs of the MLP over the rows the tile source names; `addend`
+// (dense rows only, nullable) is added to the down projection before its
+// rounding; `packed`: the weights are in tm_expert_pack_weights's layout.
 int swiglu_impl(int32_t dtype, const void *x, int64_t ld_x, const int32_t *row_token, int32_t hidden,
                 int32_t inter, const void *w1, const void *w3, const void *w2, const TileSrc &ts, int64_t grid_y,
                 void *out, int64_t ld_out, const int64_t *row_out, void *fused, const void *addend, int64_t ld_add,
-                hipStream_t s) {
+                bool packed, hipStream_t s) {
   return TM_DISPATCH_DTYPE(dtype, DT, [&] {
     if constexpr (DT == TM_DT_F32) {
       return tm_fail(TM_EINVAL_DTYPE, "tm_grouped_swiglu: dtype must be F16 or BF16");
     } else {
-      launch_gemm<DT, 2, kModeUp, kMinBN>(x, ld_x, row_token, w1, w3, (int64_t)inter * hidden, hidden, inter, ts,
-                                          grid_y, fused, inter, nullptr, nullptr, 0, s);
-      TM_LAUNCH_CHECK("tm_grouped_swiglu(up)");
-      if (hidden % (2 * kMinBN) == 0)  // 256-column tiles: half the LDS reads per MFMA of 128-column ones
-        launch_gemm<DT, 1, kModeDown, 2 * kMinBN>(fused, inter, nullptr, w2, nullptr, (int64_t)hidden * inter, inter,
-                                                  hidden, ts, grid_y, out, ld_out, row_out, addend, ld_add, s);
+      if (packed)
+        swiglu_launch<DT, true>(x, ld_x, row_token, hidden, inter, w1, w3, w2, ts, grid_y, out, ld_out, row_out,
+                                fused, addend, ld_add, s);
       else
-        launch_gemm<DT, 1, kModeDown, kMinBN>(fused, inter, nullptr, w2, nullptr, (int64_t)hidden * inter, inter,
-                                              hidden, ts, grid_y, out, ld_out, row_out, addend, ld_add, s);
-      TM_LAUNCH_CHECK("tm_grouped_swiglu(down)");
+        swiglu_launch<DT, false>(x, ld_x, row_token, hidden, inter, w1, w3, w2, ts, grid_y, out, ld_out, row_out,
+                                 fused, addend, ld_add, s);
+      TM_LAUNCH_CHECK("tm_grouped_swiglu");
       return TM_OK;
     }
   });
+}
+
+// Packed weights: tile t of BN rows of expert e (rows n0 = t BN ..) keeps
+// its place [e][n0 .. n0 + BN) x K of the nn.Linear layout, reordered by
+// stage: stage kt (columns kt BK .. + BK) is one contiguous block of BN x BK
+// elements holding slot p = 16 bytes (row p / kCPR, chunk swz_chunk(row,
+// p % kCPR)) at element 8 p -- the order the GEMM's LDS ring holds a stage
+// in, so a stage's weight tile is one contiguous read.  One workgroup per
+// stage of one tile.
+template <typename T, int BN>
+__global__ __launch_bounds__(kThreads) void pack_weights_kernel(const T *__restrict__ w, int64_t K, int64_t KT,
+                                                                 T *__restrict__ out) {
+  const int64_t b = blockIdx.x;  // (tile of every expert) * KT + kt
+  const int64_t tile = b / KT, kt = b % KT;
+  const T *src = w + tile * BN * K + kt * BK;
+  T *dst = out + tile * BN * K + kt * (BN * BK);
+#pragma unroll
+  for (int j = 0; j < BN * kCPR / kThreads; ++j) {
+    const int p = threadIdx.x + kThreads * j;
+    const int row = p / kCPR, kc = swz_chunk(row, p % kCPR);
+    *reinterpret_cast<uint4 *>(dst + (int64_t)p * 8) =
+        *reinterpret_cast<const uint4 *>(src + (int64_t)row * K + kc * 8);
+  }
 }
 
 bool shapes_ok(int32_t hidden, int32_t inter) {
@@ -475,11 +519,13 @@ extern "C" size_t tm_swiglu_workspace_size(int64_t max_rows, int32_t inter, int3
   return (size_t)max_rows * (size_t)inter * (dtype == TM_DT_F32 ? 4 : 2);
 }
 
-extern "C" int tm_grouped_swiglu(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden, int32_t inter,
-                                 int32_t n_experts, const void *w1, const void *w3, const void *w2, int64_t max_rows,
-                                 const int32_t *expert_offsets, const int32_t *row_token, const int64_t *row_out,
-                                 const int32_t *tiles, void *out, void *workspace, size_t workspace_bytes,
-                                 tm_stream_t stream) {
+namespace {
+
+int grouped_swiglu_impl(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden, int32_t inter,
+                        int32_t n_experts, const void *w1, const void *w3, const void *w2, int64_t max_rows,
+                        const int32_t *expert_offsets, const int32_t *row_token, const int64_t *row_out,
+                        const int32_t *tiles, void *out, void *workspace, size_t workspace_bytes, bool packed,
+                        tm_stream_t stream) {
   TM_REQUIRE(shapes_ok(hidden, inter), TM_EINVAL_SHAPE,
              "tm_grouped_swiglu: hidden and inter must be positive multiples of %d", kMinBN);
   TM_REQUIRE(n_experts >= 1 && max_rows >= 0 && max_rows < ((int64_t)1 << 31) && ld_x >= hidden, TM_EINVAL_SHAPE,
@@ -496,7 +542,64 @@ extern "C" int tm_grouped_swiglu(int32_t dtype, const void *x, int64_t ld_x, int
   const int64_t t_max = tm_group_slots_tiles(max_rows, n_experts);
   const TileSrc ts{tiles, expert_offsets, t_max, 0};
   return swiglu_impl(dtype, x, ld_x, row_token, hidden, inter, w1, w3, w2, ts, t_max, out, 0, row_out, workspace,
-                     nullptr, 0, tm_hip_stream(stream));
+                     nullptr, 0, packed, tm_hip_stream(stream));
+}
+
+}  // namespace
+
+extern "C" int tm_grouped_swiglu(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden, int32_t inter,
+                                 int32_t n_experts, const void *w1, const void *w3, const void *w2, int64_t max_rows,
+                                 const int32_t *expert_offsets, const int32_t *row_token, const int64_t *row_out,
+                                 const int32_t *tiles, void *out, void *workspace, size_t workspace_bytes,
+                                 tm_stream_t stream) {
+  return grouped_swiglu_impl(dtype, x, ld_x, hidden, inter, n_experts, w1, w3, w2, max_rows, expert_offsets,
+                             row_token, row_out, tiles, out, workspace, workspace_bytes, false, stream);
+}
+
+extern "C" int tm_grouped_swiglu_packed(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden, int32_t inter,
+                                        int32_t n_experts, const void *w1p, const void *w3p, const void *w2p,
+                                        int64_t max_rows, const int32_t *expert_offsets, const int32_t *row_token,
+                                        const int64_t *row_out, const int32_t *tiles, void *out, void *workspace,
+                                        size_t workspace_bytes, tm_stream_t stream) {
+  return grouped_swiglu_impl(dtype, x, ld_x, hidden, inter, n_experts, w1p, w3p, w2p, max_rows, expert_offsets,
+                             row_token, row_out, tiles, out, workspace, workspace_bytes, true, stream);
+}
+
+extern "C" int tm_expert_pack_weights(int32_t dtype, const void *w, int32_t n_experts, int32_t hidden, int32_t inter,
+                                      int32_t role, void *out, tm_stream_t stream) {
+  TM_REQUIRE(shapes_ok(hidden, inter) && n_experts >= 1, TM_EINVAL_SHAPE,
+             "tm_expert_pack_weights: hidden and inter must be positive multiples of %d", kMinBN);
+  TM_REQUIRE(role == TM_PACK_GATE_UP || role == TM_PACK_DOWN, TM_EINVAL_ARG, "tm_expert_pack_weights: bad role");
+  TM_REQUIRE(w && out, TM_EINVAL_ARG, "tm_expert_pack_weights: null pointer");
+  TM_REQUIRE(tm_aligned16(w) && tm_aligned16(out), TM_EINVAL_SHAPE,
+             "tm_expert_pack_weights: weights must be 16-byte aligned");
+  // W1 / W3: [n_experts, inter, hidden] in 128-row tiles; W2: [n_experts, hidden, inter] in down_bn rows
+  const int64_t rows = role == TM_PACK_GATE_UP ? inter : hidden;
+  const int64_t K = role == TM_PACK_GATE_UP ? hidden : inter;
+  const int bn = role == TM_PACK_GATE_UP ? kMinBN : down_bn(hidden);
+  const int64_t esz = dtype == TM_DT_F32 ? 4 : 2;
+  const char *wb = static_cast<const char *>(w);
+  char *ob = static_cast<char *>(out);
+  const int64_t bytes = (int64_t)n_experts * rows * K * esz;
+  TM_REQUIRE(ob + bytes <= wb || wb + bytes <= ob, TM_EINVAL_ARG, "tm_expert_pack_weights: out overlaps the weights");
+  const int64_t KT = K / BK;
+  const int64_t blocks = (int64_t)n_experts * (rows / bn) * KT;
+  hipStream_t s = tm_hip_stream(stream);
+  return TM_DISPATCH_DTYPE(dtype, DT, [&] {
+    if constexpr (DT == TM_DT_F32) {
+      return tm_fail(TM_EINVAL_DTYPE, "tm_expert_pack_weights: dtype must be F16 or BF16");
+    } else {
+      using T = typename Elem<DT>::T;
+      if (bn == kMinBN)
+        hipLaunchKernelGGL((pack_weights_kernel<T, kMinBN>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
+                           static_cast<const T *>(w), K, KT, static_cast<T *>(out));
+      else
+        hipLaunchKernelGGL((pack_weights_kernel<T, 2 * kMinBN>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
+                           static_cast<const T *>(w), K, KT, static_cast<T *>(out));
+      TM_LAUNCH_CHECK("tm_expert_pack_weights");
+      return TM_OK;
+    }
+  });
 }
 
 namespace {
@@ -521,7 +624,7 @@ int expert_swiglu_impl(const char *name, int32_t dtype, const void *x, int64_t n
              "%s: workspace %zu bytes < %zu", name, workspace_bytes, need);
   const TileSrc ts{nullptr, nullptr, 0, (int32_t)n_rows};
   return swiglu_impl(dtype, x, ld_x, nullptr, hidden, inter, w1, w3, w2, ts, tm_cdiv(n_rows, BM), out, ld_out,
-                     nullptr, workspace, addend, ld_add, tm_hip_stream(stream));
+                     nullptr, workspace, addend, ld_add, false, tm_hip_stream(stream));
 }
 
 }  // namespace

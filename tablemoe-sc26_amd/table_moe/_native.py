@@ -24,6 +24,7 @@ TM_METRIC_L2, TM_METRIC_DOT = 0, 1
 TM_TARGET_ONE, TM_TARGET_ORIG_SUM, TM_TARGET_GIVEN = 0, 1, 2
 TM_SCORE_MODEL, TM_SCORE_F32 = 0, 1
 TM_LAYER_NO_COMBINE = 1
+TM_PACK_GATE_UP, TM_PACK_DOWN = 0, 1
 # tm_table_forward workspace: sync region size and the byte offset of the
 # count of bounded waits that ran out (include/tablemoe.h)
 TM_LAYER_SYNC_BYTES = 16384
@@ -100,6 +101,9 @@ PROTOTYPES = {
     "tm_group_slots_tiles": (i64, [i64, i32]),
     "tm_group_slots": (C.c_int, [vp, i64, i32, i64, vp, i64, i64, i32, i64, i64, vp, vp, vp, vp, vp]),
     "tm_grouped_swiglu": (C.c_int, [i32, vp, i64, i32, i32, i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]),
+    "tm_grouped_swiglu_packed": (C.c_int, [i32, vp, i64, i32, i32, i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, sz,
+                                           vp]),
+    "tm_expert_pack_weights": (C.c_int, [i32, vp, i32, i32, i32, i32, vp, vp]),
     "tm_struct_size": (sz, [i32]),
     "tm_table_forward_workspace_size": (sz, [C.POINTER(TableLayer), i64, i32]),
     "tm_table_forward": (C.c_int, [C.POINTER(TableLayer), C.POINTER(LayerIO), vp, sz, vp, vp]),

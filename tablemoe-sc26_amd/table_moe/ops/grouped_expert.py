@@ -5,7 +5,10 @@ fills one expert at a time (models/qwen3_vl_moe/cached_layers.py:431-437)
 and the combine consumes.  Two C-ABI calls: tm_group_slots (bucket the pairs
 by expert on the device, no host sync) and tm_grouped_swiglu (two grouped
 GEMMs on the matrix cores).  Weights are stacked per expert as nn.Linear
-keeps them: w1, w3 [E, I, H], w2 [E, H, I].
+keeps them: w1, w3 [E, I, H], w2 [E, H, I]; by default a packed copy of
+them (tm_expert_pack_weights: each GEMM tile's 32-column stages stored
+contiguously, in the order the GEMM stages them) is made once and
+tm_grouped_swiglu_packed runs on it, with the same results bit for bit.
 """
 
 from __future__ import annotations
@@ -18,7 +21,7 @@ from .. import _native as N
 class GroupedExperts:
     """Stacked expert weights plus the reusable grouping buffers."""
 
-    def __init__(self, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor):
+    def __init__(self, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor, packed: bool = True):
         dev = N.require_hip(w1, w3, w2)
         e, inter, h = w1.shape
         if w3.shape != (e, inter, h) or w2.shape != (e, h, inter):
@@ -29,6 +32,15 @@ class GroupedExperts:
         self.n_experts, self.inter, self.hidden = e, inter, h
         self.dtype, self.device = w1.dtype, dev
         self._bufs: dict = {}
+        self.packed = None
+        if packed and h % 128 == 0 and inter % 128 == 0:
+            tag = N.dtype_tag(self.dtype)
+            ws = []
+            for w, role in ((self.w1, N.TM_PACK_GATE_UP), (self.w3, N.TM_PACK_GATE_UP), (self.w2, N.TM_PACK_DOWN)):
+                out = torch.empty_like(w)
+                N.call("tm_expert_pack_weights", tag, N.ptr(w), e, h, inter, role, N.ptr(out), N.stream(dev))
+                ws.append(out)
+            self.packed = tuple(ws)
 
     def _buf(self, name, numel, dtype):
         t = self._bufs.get(name)
@@ -68,7 +80,9 @@ class GroupedExperts:
         offs, row_token, row_out, tiles = self.group(ids, mask, slot_out)
         nbytes = N.lib().tm_swiglu_workspace_size(n * k, self.inter, N.dtype_tag(self.dtype))
         ws = self._buf("fused", nbytes, torch.uint8)
-        N.call("tm_grouped_swiglu", N.dtype_tag(self.dtype), N.ptr(x), x.stride(0), self.hidden, self.inter,
-               self.n_experts, N.ptr(self.w1), N.ptr(self.w3), N.ptr(self.w2), n * k, N.ptr(offs), N.ptr(row_token),
-               N.ptr(row_out), N.ptr(tiles), N.ptr(slot_out), N.ptr(ws), ws.numel(), N.stream(self.device))
+        fn, (w1, w3, w2) = (("tm_grouped_swiglu_packed", self.packed) if self.packed is not None
+                            else ("tm_grouped_swiglu", (self.w1, self.w3, self.w2)))
+        N.call(fn, N.dtype_tag(self.dtype), N.ptr(x), x.stride(0), self.hidden, self.inter, self.n_experts, N.ptr(w1),
+               N.ptr(w3), N.ptr(w2), n * k, N.ptr(offs), N.ptr(row_token), N.ptr(row_out), N.ptr(tiles),
+               N.ptr(slot_out), N.ptr(ws), ws.numel(), N.stream(self.device))
         return slot_out

@@ -107,6 +107,18 @@ def test_argument_validation_without_device(lib):
                                None) == N.TM_EWORKSPACE
     assert lib.tm_project_pack(N.TM_DT_F32, C.c_void_p(16), 2048, 128, 128, 1, C.c_void_p(16), 1 << 20,
                                None) == N.TM_EINVAL_DTYPE
+    # packed expert weights: role, shape, overlap and dtype are checked before any launch
+    assert lib.tm_expert_pack_weights(N.TM_DT_BF16, C.c_void_p(16), 4, 2560, 1536, 2, C.c_void_p(1 << 40),
+                                      None) == N.TM_EINVAL_ARG
+    assert lib.tm_expert_pack_weights(N.TM_DT_BF16, C.c_void_p(16), 4, 2500, 1536, N.TM_PACK_DOWN,
+                                      C.c_void_p(1 << 40), None) == N.TM_EINVAL_SHAPE
+    assert lib.tm_expert_pack_weights(N.TM_DT_BF16, C.c_void_p(1 << 20), 4, 256, 128, N.TM_PACK_GATE_UP,
+                                      C.c_void_p((1 << 20) + 4096), None) == N.TM_EINVAL_ARG
+    assert b"overlaps" in lib.tm_last_error()
+    assert lib.tm_expert_pack_weights(N.TM_DT_F32, C.c_void_p(16), 4, 256, 128, N.TM_PACK_GATE_UP,
+                                      C.c_void_p(1 << 40), None) == N.TM_EINVAL_DTYPE
+    assert lib.tm_grouped_swiglu_packed(N.TM_DT_BF16, None, 2560, 2560, 1536, 64, None, None, None, 0, None, None,
+                                        None, None, None, None, 0, None) == N.TM_OK  # no rows: no-op
 
 
 

@@ -193,3 +193,60 @@ def test_maybe_run_fp16_fused_expert_contract(hip_device, monkeypatch):
     monkeypatch.delenv("TABLEMOE_USE_FP16_FUSED_EXPERT")
     owner.w2 = Wrap(torch.nn.Linear(inter, h, bias=True).to(dev, torch.float16))
     assert maybe_run_fp16_fused_expert(owner, x1) is None
+
+
+def _pack_reference(w, bn):
+    """The packed layout restated on the host: tile t of bn rows, stage kt of
+    32 columns is one block of bn x 32 elements; its 16-byte slot p holds
+    row p // 4, 8-column chunk (p % 4) ^ ((row // 4) % 4) of the stage."""
+    e, rows, k = w.shape
+    src = w.reshape(e * rows // bn, bn, k // 32, 4, 8)  # [tile, row, stage, chunk, 8]
+    p = np.arange(bn * 4)
+    row, kc = p // 4, (p % 4) ^ ((p // 4 // 4) % 4)
+    out = src[:, row, :, kc, :]  # [slot, tile, stage, 8]: the indexed axes come first
+    return np.ascontiguousarray(out.transpose(1, 2, 0, 3)).reshape(w.shape)
+
+
+@pytest.mark.parametrize("h,inter", [(2560, 1536), (384, 256)])
+def test_pack_weights_layout(hip_device, h, inter):
+    """tm_expert_pack_weights against the host restatement of the layout:
+    gate/up weights in 128-row tiles, down weights in 256-row tiles when
+    hidden is a multiple of 256 (else 128), each 32-column stage of a tile
+    one contiguous block in the GEMM's LDS slot order."""
+    dev = hip_device
+    g = torch.Generator().manual_seed(23)
+    e = 3
+    w13 = torch.arange(e * inter * h, dtype=torch.int32).reshape(e, inter, h)
+    w2 = torch.randint(-30000, 30000, (e, h, inter), generator=g, dtype=torch.int32)
+    for w, role, bn in ((w13, N.TM_PACK_GATE_UP, 128), (w2, N.TM_PACK_DOWN, 256 if h % 256 == 0 else 128)):
+        src = w.to(torch.int16).view(torch.bfloat16).to(dev)
+        out = torch.empty_like(src)
+        N.call("tm_expert_pack_weights", N.TM_DT_BF16, N.ptr(src), e, h, inter, role, N.ptr(out), N.stream(dev))
+        torch.cuda.synchronize()
+        want = _pack_reference(src.view(torch.int16).cpu().numpy(), bn)
+        np.testing.assert_array_equal(out.view(torch.int16).cpu().numpy(), want)
+
+
+def test_grouped_swiglu_packed_equals_plain(hip_device):
+    """Config-5 shapes on 2048 tokens (experts with more than one 256-row
+    tile): the packed-weight GEMMs write the same slot rows, bit for bit, as
+    the plain-layout ones."""
+    from table_moe.ops import GroupedExperts
+
+    dev = hip_device
+    g = torch.Generator().manual_seed(29)
+    n, k, e, h, inter, dtype = 2048, 6, 64, 2560, 1536, torch.bfloat16
+    x = torch.randn(n, h, generator=g).to(dtype).to(dev)
+    w1, w3, w2 = (w.to(dev) for w in _weights(g, e, h, inter, dtype))
+    ids = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)]).to(dev)
+    mask = (torch.rand(n, k, generator=g) < 0.7).to(dev)
+    packed, plain = GroupedExperts(w1, w3, w2), GroupedExperts(w1, w3, w2, packed=False)
+    assert packed.packed is not None and plain.packed is None
+    a = torch.full((n, k, h), 3.0, dtype=dtype, device=dev)
+    b = torch.full((n, k, h), 3.0, dtype=dtype, device=dev)
+    for _ in range(2):
+        packed.forward(x, ids, mask, a)
+        plain.forward(x, ids, mask, b)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert float((a != 3.0).float().mean()) > 0.5
