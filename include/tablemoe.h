@@ -463,7 +463,10 @@ int tm_expert_pack_weights(int32_t dtype, const void *w, int32_t n_experts, int3
                            int32_t role, void *out, tm_stream_t stream);
 /* tm_grouped_swiglu on weights packed by tm_expert_pack_weights (w1p and
  * w3p with TM_PACK_GATE_UP, w2p with TM_PACK_DOWN); the same results bit for
- * bit. */
+ * bit.  Its workspace holds the intermediate as whole 256-row tiles, each
+ * stored stage by stage like the packed weights:
+ * tm_grouped_swiglu_packed_workspace_size bytes. */
+size_t tm_grouped_swiglu_packed_workspace_size(int64_t max_rows, int32_t inter, int32_t n_experts, int32_t dtype);
 int tm_grouped_swiglu_packed(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden, int32_t inter,
                              int32_t n_experts, const void *w1p, const void *w3p, const void *w2p, int64_t max_rows,
                              const int32_t *expert_offsets, const int32_t *row_token, const int64_t *row_out,

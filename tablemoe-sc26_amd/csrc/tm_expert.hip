@@ -129,15 +129,25 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
   // Loads: thread t fills slots t + 256 j of the A part and of each B part;
   // slot p holds row p / kCPR, chunk swz_chunk(row, p % kCPR) (the swizzle is
   // its own inverse).  A: 64-bit address of stage 0 (stage s adds s * BK).
+  // The packed down GEMM reads the intermediate tile y as the up GEMM wrote
+  // it, stage by stage in slot order: stage s of the tile is the contiguous
+  // block s * BM * BK (rows past the expert hold whatever was there; their
+  // results are dropped).
+  constexpr bool kTiledA = PB && MODE == kModeDown;
+  constexpr int64_t kAStep = kTiledA ? BM * BK : BK;  // elements from one stage to the next
   const T *a_src[kADma];
 #pragma unroll
   for (int j = 0; j < kADma; ++j) {
     const int p = tid + kThreads * j;
     const int row = p / kCPR, kc = swz_chunk(row, p % kCPR);
-    int gr = r0 + row;
-    gr = gr < r_end ? gr : r_end - 1;  // rows past the expert re-read its last row; their results are dropped
-    const int64_t ar = a_rows ? (int64_t)a_rows[gr] : (int64_t)gr;
-    a_src[j] = A + ar * lda + kc * 8;
+    if constexpr (kTiledA) {
+      a_src[j] = A + y * (int64_t)BM * lda + (int64_t)p * 8;
+    } else {
+      int gr = r0 + row;
+      gr = gr < r_end ? gr : r_end - 1;  // rows past the expert re-read its last row; their results are dropped
+      const int64_t ar = a_rows ? (int64_t)a_rows[gr] : (int64_t)gr;
+      a_src[j] = A + ar * lda + kc * 8;
+    }
   }
   // B: the expert's BN rows from n0 on, through a buffer; lane offsets fixed,
   // the stage's K offset in the scalar offset.  Packed weights (PB) hold each
@@ -161,7 +171,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
     const int kt = stage < KT ? stage : KT - 1;
     const uint32_t lds = (uint32_t)(uintptr_t)ring + (uint32_t)wave * 1024u;  // wave's 64 slots of load 0
     if constexpr (j < kADma) {
-      tm_dma16_s(a_src[j] + (int64_t)kt * BK, lds + (uint32_t)(j * kThreads * 16));
+      tm_dma16_s(a_src[j] + (int64_t)kt * kAStep, lds + (uint32_t)(j * kThreads * 16));
     } else {
       constexpr int bb = (j - kADma) / kBDma, jb = (j - kADma) % kBDma;
       tm_dma16_buf_so(b_rs[bb], b_off[jb], (uint32_t)kt * (uint32_t)(PB ? kBStage * 16 : BK * sizeof(T)),
@@ -298,7 +308,12 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
           for (int j = 0; j < 8; ++j) v[j] += a[j];
         }
       }
-      tm_store8<DT>(C + (c_rows ? c_rows[gr] + col : (int64_t)gr * ldc + col), v);
+      if constexpr (PB && MODE == kModeUp)  // tile y of the intermediate in the down GEMM's stage order
+        tm_store8<DT>(C + y * (int64_t)BM * ldc + (col / BK) * (BM * BK) +
+                          (row * kCPR + swz_chunk(row, (col % BK) / 8)) * 8,
+                      v);
+      else
+        tm_store8<DT>(C + (c_rows ? c_rows[gr] + col : (int64_t)gr * ldc + col), v);
     }
   }
 }
@@ -519,6 +534,14 @@ extern "C" size_t tm_swiglu_workspace_size(int64_t max_rows, int32_t inter, int3
   return (size_t)max_rows * (size_t)inter * (dtype == TM_DT_F32 ? 4 : 2);
 }
 
+// The packed path keeps the intermediate as whole 256-row tiles (one per
+// entry of the tile list).
+extern "C" size_t tm_grouped_swiglu_packed_workspace_size(int64_t max_rows, int32_t inter, int32_t n_experts,
+                                                          int32_t dtype) {
+  if (max_rows <= 0 || inter <= 0 || n_experts <= 0) return 0;
+  return (size_t)tm_group_slots_tiles(max_rows, n_experts) * BM * (size_t)inter * (dtype == TM_DT_F32 ? 4 : 2);
+}
+
 namespace {
 
 int grouped_swiglu_impl(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden, int32_t inter,
@@ -536,7 +559,8 @@ int grouped_swiglu_impl(int32_t dtype, const void *x, int64_t ld_x, int32_t hidd
   TM_REQUIRE(tm_aligned16(x) && (ld_x * 2) % 16 == 0 && tm_aligned16(w1) && tm_aligned16(w3) && tm_aligned16(w2) &&
                  tm_aligned16(out),
              TM_EINVAL_SHAPE, "tm_grouped_swiglu: x rows, weights and out must be 16-byte aligned");
-  const size_t need = tm_swiglu_workspace_size(max_rows, inter, dtype);
+  const size_t need = packed ? tm_grouped_swiglu_packed_workspace_size(max_rows, inter, n_experts, dtype)
+                              : tm_swiglu_workspace_size(max_rows, inter, dtype);
   TM_REQUIRE(workspace != nullptr && workspace_bytes >= need && tm_aligned16(workspace), TM_EWORKSPACE,
              "tm_grouped_swiglu: workspace %zu bytes < %zu", workspace_bytes, need);
   const int64_t t_max = tm_group_slots_tiles(max_rows, n_experts);

@@ -78,7 +78,9 @@ class GroupedExperts:
             raise ValueError(f"slot_out must be [N, {k}, {self.hidden}] with unit stride along hidden")
         x = hidden if hidden.stride(-1) == 1 else hidden.contiguous()
         offs, row_token, row_out, tiles = self.group(ids, mask, slot_out)
-        nbytes = N.lib().tm_swiglu_workspace_size(n * k, self.inter, N.dtype_tag(self.dtype))
+        tag = N.dtype_tag(self.dtype)
+        nbytes = (N.lib().tm_grouped_swiglu_packed_workspace_size(n * k, self.inter, self.n_experts, tag)
+                  if self.packed is not None else N.lib().tm_swiglu_workspace_size(n * k, self.inter, tag))
         ws = self._buf("fused", nbytes, torch.uint8)
         fn, (w1, w3, w2) = (("tm_grouped_swiglu_packed", self.packed) if self.packed is not None
                             else ("tm_grouped_swiglu", (self.w1, self.w3, self.w2)))

@@ -119,6 +119,9 @@ def test_argument_validation_without_device(lib):
                                       C.c_void_p(1 << 40), None) == N.TM_EINVAL_DTYPE
     assert lib.tm_grouped_swiglu_packed(N.TM_DT_BF16, None, 2560, 2560, 1536, 64, None, None, None, 0, None, None,
                                         None, None, None, None, 0, None) == N.TM_OK  # no rows: no-op
+    # the packed path's intermediate is whole 256-row tiles of the tile list
+    assert lib.tm_grouped_swiglu_packed_workspace_size(24576, 1536, 64, N.TM_DT_BF16) == (96 + 64) * 256 * 1536 * 2
+    assert lib.tm_swiglu_workspace_size(24576, 1536, N.TM_DT_BF16) == 24576 * 1536 * 2
 
 
 
