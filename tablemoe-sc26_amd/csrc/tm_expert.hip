@@ -325,6 +325,7 @@ constexpr int kGroupThreads = 1024;
 constexpr int kMaxExperts = 1024;
 constexpr int kGroupTok = 4;    // tokens per thread on the register path (n <= 4096)
 constexpr int kGroupSlots = 8;  // slots per token on the register path (top_k <= 8)
+static_assert(kGroupTok * kGroupThreads * 8 <= 65536, "a placed row (token << 3 | slot) fits 16 bits");
 
 __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
     const int64_t *__restrict__ ids, int64_t n, int top_k, int64_t ld_ids, const uint8_t *__restrict__ mask,
@@ -333,6 +334,11 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
   __shared__ int32_t hist[kMaxExperts];
   __shared__ int32_t cursor[kMaxExperts];
   __shared__ int32_t tile_base[kMaxExperts + 1];
+  // register path: each placed row as (token << 3 | slot), written out in row
+  // order afterwards (scattered 4- and 8-byte stores cost ~10 us; in row
+  // order they are a few coalesced passes)
+  __shared__ uint16_t placed[kGroupTok * kGroupThreads * kGroupSlots];
+  __shared__ int32_t s_rows;
   const int tid = threadIdx.x;
   for (int e = tid; e < n_experts; e += kGroupThreads) hist[e] = 0;
   // Each thread keeps the experts of its tokens (b = tid + 1024 j, j < kGroupTok)
@@ -383,6 +389,7 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
     tile_base[n_experts] = tr;
     tiles[0] = run;
     tiles[1] = tr;
+    s_rows = run;
   }
   __syncthreads();
   for (int e = tid; e < n_experts; e += kGroupThreads) {
@@ -400,11 +407,18 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
 #pragma unroll
       for (int s = 0; s < kGroupSlots; ++s)
         if (ex[j][s] >= 0) {
-          const int64_t b = tid + (int64_t)kGroupThreads * j;
+          const int b = tid + kGroupThreads * j;  // < 4096
           const int32_t pos = atomicAdd(&cursor[ex[j][s]], 1);
-          row_token[pos] = (int32_t)b;
-          row_out[pos] = b * so_b + (int64_t)s * so_s;
+          placed[pos] = (uint16_t)((b << 3) | s);
         }
+    __syncthreads();
+    const int32_t rows = s_rows;
+    for (int32_t i = tid; i < rows; i += kGroupThreads) {
+      const int v = placed[i];
+      const int64_t b = v >> 3;
+      row_token[i] = (int32_t)b;
+      row_out[i] = b * so_b + (int64_t)(v & 7) * so_s;
+    }
   } else {
     for (int64_t b = tid; b < n; b += kGroupThreads)
       for (int s = 0; s < top_k; ++s) {
