@@ -416,7 +416,7 @@ def run_config5(replays=10):
     import torch
 
     from synth import make_workload
-    from table_moe.ops import GroupedExperts, expert_swiglu
+    from table_moe.ops import GroupedExperts, SharedExperts
 
     dev = torch.device("cuda:0")
     wl = make_workload(5, with_slot_out=False, device=dev, gen_device=dev)
@@ -425,7 +425,7 @@ def run_config5(replays=10):
     g = torch.Generator(device=dev).manual_seed(55)
     rnd = lambda *shape: (torch.randn(*shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)  # noqa: E731
     ex = GroupedExperts(rnd(e, inter, h), rnd(e, inter, h), rnd(e, h, inter))
-    shared = (rnd(2 * inter, h), rnd(2 * inter, h), rnd(h, 2 * inter))
+    shared = SharedExperts(rnd(2 * inter, h), rnd(2 * inter, h), rnd(h, 2 * inter))
     tbl = _tables([wl])[0]
     out = torch.empty_like(wl.residual)
 
@@ -440,11 +440,10 @@ def run_config5(replays=10):
     w, idx, dist = res["weights"].clone(), res["idx"].clone(), res["dist"].clone()
     slot = res["slot_out"]
     base = torch.empty_like(wl.residual)
-    ws = torch.empty(n * 2 * inter * 2, dtype=torch.uint8, device=dev)
     parts = {
         "search_us": lambda: tbl.layer_search(wl.x, wl.is_vision, wl.logits, k, 1, 0.6),
         "routed_recompute_us": lambda: ex.forward(wl.x, ids, keep, slot),
-        "shared_us": lambda: expert_swiglu(wl.x, *shared, out=base, workspace=ws, addend=wl.residual),
+        "shared_us": lambda: shared.forward(wl.x, out=base, addend=wl.residual),
         "combine_us": lambda: tbl.gather_combine(keep, slot, w, idx, dist, base, out),
     }
     times = {}

@@ -467,6 +467,14 @@ int tm_expert_pack_weights(int32_t dtype, const void *w, int32_t n_experts, int3
  * stored stage by stage like the packed weights:
  * tm_grouped_swiglu_packed_workspace_size bytes. */
 size_t tm_grouped_swiglu_packed_workspace_size(int64_t max_rows, int32_t inter, int32_t n_experts, int32_t dtype);
+/* tm_expert_swiglu / tm_expert_swiglu_add (addend nullable) on one expert's
+ * weights packed by tm_expert_pack_weights with n_experts = 1 (a DeepSeek
+ * layer's shared experts); the same results bit for bit.  Workspace:
+ * tm_grouped_swiglu_packed_workspace_size(n_rows, inter, 1, dtype). */
+int tm_expert_swiglu_packed(int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
+                            const void *w1p, const void *w3p, const void *w2p, int32_t inter, const void *addend,
+                            int64_t ld_add, void *out, int64_t ld_out, void *workspace, size_t workspace_bytes,
+                            tm_stream_t stream);
 int tm_grouped_swiglu_packed(int32_t dtype, const void *x, int64_t ld_x, int32_t hidden, int32_t inter,
                              int32_t n_experts, const void *w1p, const void *w3p, const void *w2p, int64_t max_rows,
                              const int32_t *expert_offsets, const int32_t *row_token, const int64_t *row_out,

@@ -645,7 +645,7 @@ namespace {
 int expert_swiglu_impl(const char *name, int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
                        const void *w1, const void *w3, const void *w2, int32_t inter, const void *addend,
                        int64_t ld_add, void *out, int64_t ld_out, void *workspace, size_t workspace_bytes,
-                       tm_stream_t stream) {
+                       bool packed, tm_stream_t stream) {
   TM_REQUIRE(shapes_ok(hidden, inter), TM_EINVAL_SHAPE, "%s: hidden and inter must be positive multiples of %d",
              name, kMinBN);
   TM_REQUIRE(n_rows >= 0 && n_rows < ((int64_t)1 << 31) && ld_x >= hidden && ld_out >= hidden &&
@@ -657,12 +657,13 @@ int expert_swiglu_impl(const char *name, int32_t dtype, const void *x, int64_t n
                  tm_aligned16(out) && (ld_out * 2) % 16 == 0 &&
                  (addend == nullptr || (tm_aligned16(addend) && (ld_add * 2) % 16 == 0)),
              TM_EINVAL_SHAPE, "%s: x, out and addend rows and the weights must be 16-byte aligned", name);
-  const size_t need = tm_swiglu_workspace_size(n_rows, inter, dtype);
+  const size_t need = packed ? tm_grouped_swiglu_packed_workspace_size(n_rows, inter, 1, dtype)
+                              : tm_swiglu_workspace_size(n_rows, inter, dtype);
   TM_REQUIRE(workspace != nullptr && workspace_bytes >= need && tm_aligned16(workspace), TM_EWORKSPACE,
              "%s: workspace %zu bytes < %zu", name, workspace_bytes, need);
   const TileSrc ts{nullptr, nullptr, 0, (int32_t)n_rows};
   return swiglu_impl(dtype, x, ld_x, nullptr, hidden, inter, w1, w3, w2, ts, tm_cdiv(n_rows, BM), out, ld_out,
-                     nullptr, workspace, addend, ld_add, false, tm_hip_stream(stream));
+                     nullptr, workspace, addend, ld_add, packed, tm_hip_stream(stream));
 }
 
 }  // namespace
@@ -671,7 +672,7 @@ extern "C" int tm_expert_swiglu(int32_t dtype, const void *x, int64_t n_rows, in
                                 const void *w1, const void *w3, const void *w2, int32_t inter, void *out,
                                 int64_t ld_out, void *workspace, size_t workspace_bytes, tm_stream_t stream) {
   return expert_swiglu_impl("tm_expert_swiglu", dtype, x, n_rows, hidden, ld_x, w1, w3, w2, inter, nullptr, 0, out,
-                            ld_out, workspace, workspace_bytes, stream);
+                            ld_out, workspace, workspace_bytes, false, stream);
 }
 
 extern "C" int tm_expert_swiglu_add(int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
@@ -680,5 +681,13 @@ extern "C" int tm_expert_swiglu_add(int32_t dtype, const void *x, int64_t n_rows
                                     size_t workspace_bytes, tm_stream_t stream) {
   TM_REQUIRE(addend != nullptr, TM_EINVAL_ARG, "tm_expert_swiglu_add: null addend");
   return expert_swiglu_impl("tm_expert_swiglu_add", dtype, x, n_rows, hidden, ld_x, w1, w3, w2, inter, addend, ld_add,
-                            out, ld_out, workspace, workspace_bytes, stream);
+                            out, ld_out, workspace, workspace_bytes, false, stream);
+}
+
+extern "C" int tm_expert_swiglu_packed(int32_t dtype, const void *x, int64_t n_rows, int32_t hidden, int64_t ld_x,
+                                       const void *w1p, const void *w3p, const void *w2p, int32_t inter,
+                                       const void *addend, int64_t ld_add, void *out, int64_t ld_out,
+                                       void *workspace, size_t workspace_bytes, tm_stream_t stream) {
+  return expert_swiglu_impl("tm_expert_swiglu_packed", dtype, x, n_rows, hidden, ld_x, w1p, w3p, w2p, inter, addend,
+                            ld_add, out, ld_out, workspace, workspace_bytes, true, stream);
 }

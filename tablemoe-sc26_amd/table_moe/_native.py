@@ -105,6 +105,7 @@ PROTOTYPES = {
                                            vp]),
     "tm_expert_pack_weights": (C.c_int, [i32, vp, i32, i32, i32, i32, vp, vp]),
     "tm_grouped_swiglu_packed_workspace_size": (sz, [i64, i32, i32, i32]),
+    "tm_expert_swiglu_packed": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, i32, vp, i64, vp, i64, vp, sz, vp]),
     "tm_struct_size": (sz, [i32]),
     "tm_table_forward_workspace_size": (sz, [C.POINTER(TableLayer), i64, i32]),
     "tm_table_forward": (C.c_int, [C.POINTER(TableLayer), C.POINTER(LayerIO), vp, sz, vp, vp]),

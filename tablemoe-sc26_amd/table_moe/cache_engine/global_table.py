@@ -290,8 +290,9 @@ class GlobalTable:
         deepseek_layers.py:569-745 shape): the layer call up to the keep set,
         the kept tokens' routed slots recomputed by ``experts``
         (GroupedExperts, on the device, no host sync), the shared experts
-        ``shared`` = (w1, w3, w2) run over every token with the residual folded
-        into their down projection (dtype(residual + shared)), then the
+        ``shared`` = (w1, w3, w2) or a ``SharedExperts`` (packed weights, same
+        bits) run over every token with the residual folded into their down
+        projection (dtype(residual + shared)), then the
         gather + combine on top: out = dtype(dtype(residual + shared) + y),
         y = the renormalised routed slots (kept tokens) or the cached output
         of the nearest centroid (the others).  Top-1 table.  Returns the
@@ -304,26 +305,30 @@ class GlobalTable:
         single-workgroup launches (keep select, slot grouping) and the last
         partial rounds of the routed GEMMs leave idle.  The fork and join are
         stream waits, so the call stays capturable in a HIP graph."""
-        from ..ops import expert_swiglu
+        from ..ops import SharedExperts, expert_swiglu
 
         n = hidden.shape[0]
         main = torch.cuda.current_stream(self.device)
         side = None
         base = residual
         if shared is not None:
-            w1, w3, w2 = shared
             # allocated on the caller's stream, which waits for the side
             # stream at the join, before any later call can free them
             base = self._buf("shared_plus_residual", (n, self.hidden), self.dtype)
-            nbytes = N.lib().tm_swiglu_workspace_size(n, w1.shape[0], N.dtype_tag(self.dtype))
-            ws = self._buf("shared_ws", (max(nbytes, 1),), torch.uint8)
+            if isinstance(shared, SharedExperts):
+                nbytes = N.lib().tm_grouped_swiglu_packed_workspace_size(n, shared.inter, 1, N.dtype_tag(self.dtype))
+                if shared._ws is None or shared._ws.numel() < nbytes:
+                    shared._ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=self.device)
+                run = lambda: shared.forward(hidden, out=base, addend=residual)  # noqa: E731
+            else:
+                w1, w3, w2 = shared
+                nbytes = N.lib().tm_swiglu_workspace_size(n, w1.shape[0], N.dtype_tag(self.dtype))
+                ws = self._buf("shared_ws", (max(nbytes, 1),), torch.uint8)
+                run = lambda: expert_swiglu(hidden, w1, w3, w2, out=base, workspace=ws, addend=residual)  # noqa: E731
             side = self._side_stream()
             side.wait_stream(main)
             with torch.cuda.stream(side):
-                if residual is None:
-                    expert_swiglu(hidden, w1, w3, w2, out=base, workspace=ws)
-                else:
-                    expert_swiglu(hidden, w1, w3, w2, out=base, workspace=ws, addend=residual)
+                run()
         res = self.layer_search(hidden, is_vision, router_logits, router_top_k, 1, keep_rate)
         slot_out = self._buf("recompute_slots", (n, router_top_k, self.hidden), self.dtype)
         experts.forward(hidden, res["ids"], res["keep"], slot_out)

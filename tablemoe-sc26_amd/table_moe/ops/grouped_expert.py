@@ -88,3 +88,55 @@ class GroupedExperts:
                N.ptr(w3), N.ptr(w2), n * k, N.ptr(offs), N.ptr(row_token), N.ptr(row_out), N.ptr(tiles),
                N.ptr(slot_out), N.ptr(ws), ws.numel(), N.stream(self.device))
         return slot_out
+
+
+class SharedExperts:
+    """One dense SwiGLU MLP run over every row — a DeepSeek layer's shared
+    experts (models/deepseek_vl2/deepseek_layers.py:743) — on a packed copy of
+    its nn.Linear weights w1, w3 [I, H] and w2 [H, I] (tm_expert_pack_weights
+    with one expert; tm_expert_swiglu_packed), with the same results bit for
+    bit as ``expert_swiglu`` on the plain weights."""
+
+    def __init__(self, w1: torch.Tensor, w3: torch.Tensor, w2: torch.Tensor):
+        dev = N.require_hip(w1, w3, w2)
+        inter, h = w1.shape
+        if w3.shape != (inter, h) or w2.shape != (h, inter):
+            raise ValueError("w1/w3 must be [I, H] and w2 [H, I]")
+        if not (w1.dtype == w3.dtype == w2.dtype) or w1.dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError("shared expert weights must share dtype float16 or bfloat16")
+        if h % 128 or inter % 128:
+            raise ValueError("hidden and intermediate sizes must be multiples of 128")
+        self.inter, self.hidden, self.dtype, self.device = inter, h, w1.dtype, dev
+        tag = N.dtype_tag(self.dtype)
+        packed = []
+        for w, role in ((w1, N.TM_PACK_GATE_UP), (w3, N.TM_PACK_GATE_UP), (w2, N.TM_PACK_DOWN)):
+            w = w.contiguous()
+            out = torch.empty_like(w)
+            N.call("tm_expert_pack_weights", tag, N.ptr(w), 1, h, inter, role, N.ptr(out), N.stream(dev))
+            packed.append(out)
+        self.packed = tuple(packed)
+        self._ws = None
+
+    def forward(self, hidden: torch.Tensor, out: torch.Tensor | None = None,
+                addend: torch.Tensor | None = None) -> torch.Tensor:
+        """y = MLP(hidden) [M, H], or dtype(addend + MLP) with ``addend`` [M, H]
+        (not overlapping ``out``) in one rounding."""
+        N.require_hip(hidden)
+        m, h = hidden.shape
+        if h != self.hidden or hidden.dtype != self.dtype or hidden.stride(-1) != 1:
+            raise ValueError(f"hidden must be [M, {self.hidden}] {self.dtype} with unit stride")
+        if out is None:
+            out = torch.empty((m, h), dtype=self.dtype, device=self.device)
+        if addend is not None:
+            N.require_hip(addend)
+            if addend.shape != (m, h) or addend.dtype != self.dtype or addend.stride(-1) != 1:
+                raise ValueError(f"addend must be [{m}, {h}] {self.dtype} with unit stride along hidden")
+        tag = N.dtype_tag(self.dtype)
+        nbytes = N.lib().tm_grouped_swiglu_packed_workspace_size(m, self.inter, 1, tag)
+        if self._ws is None or self._ws.numel() < nbytes:
+            self._ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=self.device)
+        w1, w3, w2 = self.packed
+        N.call("tm_expert_swiglu_packed", tag, N.ptr(hidden), m, h, hidden.stride(0), N.ptr(w1), N.ptr(w3), N.ptr(w2),
+               self.inter, N.ptr(addend), 0 if addend is None else addend.stride(0), N.ptr(out), out.stride(0),
+               N.ptr(self._ws), self._ws.numel(), N.stream(self.device))
+        return out

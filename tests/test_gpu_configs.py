@@ -241,13 +241,15 @@ def test_config5_layer_end_to_end(hip_device):
 
 def test_config5_layer_graph_replays(hip_device):
     """The config-5 layer call runs its shared experts on a second stream
-    (forked from the caller's stream, joined before the combine).  Captured
-    in a HIP graph and replayed three times, with the output cleared and
-    other eager work on the caller's stream between replays, every replay
-    equals the eager call bit for bit (slot outputs of the kept tokens,
-    search outputs and combined rows)."""
+    (forked from the caller's stream, joined before the combine).  With the
+    shared experts as a SharedExperts (packed weights) the eager call equals
+    the call with the plain weight tuple bit for bit; captured in a HIP graph
+    and replayed three times, with the output cleared and other eager work on
+    the caller's stream between replays, every replay equals the eager call
+    bit for bit (slot outputs of the kept tokens, search outputs and combined
+    rows)."""
     from synth import make_workload
-    from table_moe.ops import GroupedExperts
+    from table_moe.ops import GroupedExperts, SharedExperts
 
     dev = hip_device
     wl = make_workload(5, with_slot_out=False, device=dev, gen_device=dev)
@@ -256,9 +258,12 @@ def test_config5_layer_graph_replays(hip_device):
     g = torch.Generator(device=dev).manual_seed(56)
     rnd = lambda *shape: (torch.randn(*shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)  # noqa: E731
     ex = GroupedExperts(rnd(e, inter, h), rnd(e, inter, h), rnd(e, h, inter))
-    shared = (rnd(2 * inter, h), rnd(2 * inter, h), rnd(h, 2 * inter))
+    shared_plain = (rnd(2 * inter, h), rnd(2 * inter, h), rnd(h, 2 * inter))
+    shared = SharedExperts(*shared_plain)
     tbl = _table(wl)
     out = torch.empty_like(wl.residual)
+    want_plain = tbl.layer_forward_recompute(wl.x, wl.is_vision, wl.logits, ex, wl.residual, k, 0.6,
+                                             shared=shared_plain, out=torch.empty_like(wl.residual))["out"].clone()
 
     def layer():
         return tbl.layer_forward_recompute(wl.x, wl.is_vision, wl.logits, ex, wl.residual, k, 0.6, shared=shared,
@@ -268,6 +273,7 @@ def test_config5_layer_graph_replays(hip_device):
     torch.cuda.synchronize()
     kb = res["keep"].bool()
     want = {key: res[key].clone() for key in ("ids", "idx", "dist", "keep", "out")}
+    assert torch.equal(want["out"], want_plain)
     want_slot = res["slot_out"][kb].clone()
     side = torch.cuda.Stream(dev)
     side.wait_stream(torch.cuda.current_stream(dev))

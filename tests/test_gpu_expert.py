@@ -250,3 +250,24 @@ def test_grouped_swiglu_packed_equals_plain(hip_device):
     torch.cuda.synchronize()
     assert torch.equal(a, b)
     assert float((a != 3.0).float().mean()) > 0.5
+
+
+@pytest.mark.parametrize("m,addend", [(300, True), (4096, True), (129, False)])
+def test_shared_experts_packed_equals_plain(hip_device, m, addend):
+    """SharedExperts (one expert's packed weights, tm_expert_swiglu_packed)
+    against expert_swiglu on the plain weights: the same rows bit for bit, at
+    the config-5 shared shape (intermediate 3072, hidden 2560), with and
+    without the residual addend, partial last tiles included."""
+    from table_moe.ops import SharedExperts, expert_swiglu
+
+    dev = hip_device
+    g = torch.Generator().manual_seed(31 + m)
+    h, inter, dtype = 2560, 3072, torch.bfloat16
+    x = torch.randn(m, h, generator=g).to(dtype).to(dev)
+    w1, w3, w2 = (w[0].to(dev) for w in _weights(g, 1, h, inter, dtype))
+    add = torch.randn(m, h, generator=g).to(dtype).to(dev) if addend else None
+    sh = SharedExperts(w1, w3, w2)
+    got = sh.forward(x, addend=add)
+    want = expert_swiglu(x, w1, w3, w2, addend=add)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
