@@ -26,6 +26,13 @@
 // of one k-step run under the MFMAs of the previous one.  Up mode multiplies
 // W1 and W3 against the same A fragments and applies the SiLU-mul epilogue;
 // down mode writes each row to its slot of the output.
+//
+// Packed path (tm_expert_pack_weights, tm_grouped_swiglu_packed,
+// tm_expert_swiglu_packed): each weight tile is stored stage by stage in the
+// LDS slot order, so a stage's weight tile is one contiguous read; the up
+// GEMM then writes the intermediate in the same stage order (whole 256-row
+// tiles) and the down GEMM reads its A stages contiguously.  Same arithmetic,
+// same bits.
 #include "tm_internal.h"
 #include "tm_dma.h"
 #include "tm_mfma.h"
@@ -445,9 +452,6 @@ void launch_gemm(const void *A, int64_t lda, const int32_t *a_rows, const void *
                      ld_add);
 }
 
-// The two GEMMs of the MLP over the rows the tile source names; `addend`
-// (dense rows only, nullable) is added to the down projection before its
-// rounding.
 // Column tile of the down GEMM: 256 columns when hidden allows (half the LDS
 // reads per MFMA of 128-column tiles).
 inline int down_bn(int32_t hidden) { return hidden % (2 * kMinBN) == 0 ? 2 * kMinBN : kMinBN; }
