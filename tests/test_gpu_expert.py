@@ -227,15 +227,17 @@ def test_pack_weights_layout(hip_device, h, inter):
         np.testing.assert_array_equal(out.view(torch.int16).cpu().numpy(), want)
 
 
-def test_grouped_swiglu_packed_equals_plain(hip_device):
+@pytest.mark.parametrize("n,k,e,h,inter,dtype", [(2048, 6, 64, 2560, 1536, torch.bfloat16),
+                                                 (700, 8, 16, 384, 256, torch.float16)])
+def test_grouped_swiglu_packed_equals_plain(hip_device, n, k, e, h, inter, dtype):
     """Config-5 shapes on 2048 tokens (experts with more than one 256-row
-    tile): the packed-weight GEMMs write the same slot rows, bit for bit, as
-    the plain-layout ones."""
+    tile), and fp16 with a hidden size that takes 128-column down tiles: the
+    packed-weight GEMMs write the same slot rows, bit for bit, as the
+    plain-layout ones."""
     from table_moe.ops import GroupedExperts
 
     dev = hip_device
-    g = torch.Generator().manual_seed(29)
-    n, k, e, h, inter, dtype = 2048, 6, 64, 2560, 1536, torch.bfloat16
+    g = torch.Generator().manual_seed(29 + n)
     x = torch.randn(n, h, generator=g).to(dtype).to(dev)
     w1, w3, w2 = (w.to(dev) for w in _weights(g, e, h, inter, dtype))
     ids = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)]).to(dev)
@@ -252,8 +254,9 @@ def test_grouped_swiglu_packed_equals_plain(hip_device):
     assert float((a != 3.0).float().mean()) > 0.5
 
 
-@pytest.mark.parametrize("m,addend", [(300, True), (4096, True), (129, False)])
-def test_shared_experts_packed_equals_plain(hip_device, m, addend):
+@pytest.mark.parametrize("m,addend,dtype", [(300, True, torch.bfloat16), (4096, True, torch.bfloat16),
+                                            (129, False, torch.bfloat16), (257, True, torch.float16)])
+def test_shared_experts_packed_equals_plain(hip_device, m, addend, dtype):
     """SharedExperts (one expert's packed weights, tm_expert_swiglu_packed)
     against expert_swiglu on the plain weights: the same rows bit for bit, at
     the config-5 shared shape (intermediate 3072, hidden 2560), with and
@@ -262,7 +265,7 @@ def test_shared_experts_packed_equals_plain(hip_device, m, addend):
 
     dev = hip_device
     g = torch.Generator().manual_seed(31 + m)
-    h, inter, dtype = 2560, 3072, torch.bfloat16
+    h, inter = 2560, 3072
     x = torch.randn(m, h, generator=g).to(dtype).to(dev)
     w1, w3, w2 = (w[0].to(dev) for w in _weights(g, 1, h, inter, dtype))
     add = torch.randn(m, h, generator=g).to(dtype).to(dev) if addend else None
