@@ -1,7 +1,8 @@
 """The drop-in boundary on the host: every name the reference's unchanged
 modules import from the files this package replaces exists here, and the
 replacement files only import each other (plus torch/numpy), so they can be
-copied over the reference's table_moe/ tree as INTEGRATION.md describes.
+copied over the reference's table_moe/ tree as an overlay (cache_engine/,
+skip/, ops/, utils/modality.py and utils/importance.py, _native.py, _lib/).
 
 The import list is transcribed from the reference:
   models/qwen3_vl_moe/cached_layers.py:5-13, hybrid_attention.py:11,
