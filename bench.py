@@ -464,8 +464,9 @@ def run_config5(replays=10):
     return {
         "workload": "config 5: N=4096, hidden 2560 bf16, 64 routed experts top-6 (intermediate 1536) + shared experts "
                     "(intermediate 2 x 1536), C=8192 x 128, keep_rate 0.6 (2457 kept tokens: 14742 recomputed slot "
-                    "rows), random-init N(0, 0.02) bf16 weights; table search -> grouped recompute -> shared experts "
-                    "folded into the residual -> gather + combine",
+                    "rows), random-init N(0, 0.02) bf16 weights; table search -> grouped recompute (packed expert "
+                    "weights) -> gather + combine, the shared experts (packed, folded into the residual) on a "
+                    "second stream beside the search and the recompute",
         "us_per_layer": layer_us, "tokens_per_s": n / (layer_us * 1e-6), **times,
         "routed_rows": rows, "routed_tflops": routed_flops / (times["routed_recompute_us"] * 1e-6) / 1e12,
         "routed_mfma_frac": routed_flops / (times["routed_recompute_us"] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
