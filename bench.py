@@ -335,6 +335,12 @@ def run_decode(replicas=DECODE_REPLICAS, replays=5):
             "search_bytes": by["search"] + cfg["hidden"] * cfg["dim"] * 2,
         }
         log(f"decode N={n}: {us:.2f} us/layer (median of {replays} replays of {replicas} layers)")
+    # the one-launch decode plan's bounded waits: a wait that ran out leaves
+    # undefined rows, so a timing it took part in is not a valid measurement
+    wait_errors = sum(t.wait_errors() for t in tables)
+    if wait_errors:
+        raise RuntimeError(f"decode: {wait_errors} cross-workgroup wait(s) ran out during the timed layers")
+    res["wait_errors"] = wait_errors
     del reps, tables
     torch.cuda.empty_cache()
     return {"workload": f"config 3: N in {{1, 8, 32}} text tokens, C=16384 x 128 bf16, cached outputs 16384x2048, "

@@ -434,7 +434,9 @@ int tm_expert_swiglu_add(int32_t dtype, const void *x, int64_t n_rows, int32_t h
  * row_out = b*so_b + s*so_s: the element offset of its output row), and
  * tiles [2 + 2*tm_group_slots_tiles(n_tokens*top_k, n_experts)]: row count,
  * tile count, then each 256-row tile's expert and first row.  The order of
- * rows inside an expert is unspecified; results do not depend on it. */
+ * rows inside an expert is unspecified; results do not depend on it.
+ * so_b and so_s must be multiples of 8 elements (TM_EINVAL_SHAPE
+ * otherwise). */
 int64_t tm_group_slots_tiles(int64_t max_rows, int32_t n_experts);
 int tm_group_slots(const int64_t *ids, int64_t n_tokens, int32_t top_k, int64_t ld_ids, const uint8_t *mask,
                    int64_t ms_b, int64_t ms_s, int32_t n_experts, int64_t so_b, int64_t so_s,
@@ -564,7 +566,10 @@ size_t tm_struct_size(int32_t which);
  * out (20 ms) adds one to the uint32 at byte TM_LAYER_SYNC_ERR_BYTE of the
  * workspace; that call's outputs are then undefined (the row chunks the
  * waiting workgroup writes are NaN).  The library never clears the word
- * (zero = no wait ever ran out). */
+ * (zero = no wait ever ran out).  The return code cannot report such a
+ * failure (the call returns before the kernels run): a caller that shares
+ * the device with other work must read the word after the calls complete
+ * and discard the outputs of any call during which it grew. */
 #define TM_LAYER_SYNC_BYTES 16384
 #define TM_LAYER_SYNC_ERR_BYTE 3584
 size_t tm_table_forward_workspace_size(const tm_table_layer *table, int64_t n_tokens, int32_t n_nearest);
@@ -575,9 +580,13 @@ int tm_table_forward(const tm_table_layer *table, const tm_layer_io *io, void *w
  * tm_table_forward without a workspace argument: no counterpart in the
  * reference.  For callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * Same semantics and results as tm_table_forward (no stage events); the
- * workspace is a static device array of TM_NOALLOC_SCRATCH_BYTES inside the
- * library (one per GPU, held until the process ends; looked up, and its
+ * Same semantics and results as tm_table_forward (no stage events), except
+ * that it never takes a plan whose workgroups wait for each other (batches
+ * of at most 64 tokens run the decode plan as three launches): its results
+ * do not depend on the device being otherwise idle, and there is no error
+ * word to read.  The workspace is a static device array of
+ * TM_NOALLOC_SCRATCH_BYTES inside the library (one per GPU, held until the
+ * process ends; looked up, and its
  * arrival counters cleared by a kernel on `stream`, on the first call on
  * each device).  A layer whose tm_table_forward_workspace_size exceeds
  * TM_NOALLOC_SCRATCH_BYTES is rejected with TM_EWORKSPACE.  Allocates

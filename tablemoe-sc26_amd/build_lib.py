@@ -51,6 +51,45 @@ HIP_FLAGS = [
 ]
 
 
+# Kernels that issue loads from inline asm into registers (the compiler does
+# not know those loads are in flight until the explicit s_waitcnt that
+# retires them): their results are right only while the register allocator
+# never spills, copies or reuses those registers before the wait.  The build
+# fails if such a kernel uses scratch, spills, or needs more VGPRs than the
+# budget its launch bounds give (256 at two waves per SIMD).  The pattern was
+# checked on the generated ISA (no read or reuse of an in-flight destination
+# register) with the compiler VALIDATED_CLANG names; another compiler only
+# draws a warning, since the resource check still runs.
+ASM_LOAD_KERNELS = {"tm_project.hip": (("project_cols_pipe_kernel", 256),)}
+VALIDATED_CLANG = "roc-7.2.0 26014"
+
+
+def _check_asm_load_kernels(src: Path, remarks: str) -> None:
+    import re
+
+    budget = dict(ASM_LOAD_KERNELS[src.name])
+    seen = 0
+    for block in re.split(r"remark: Function Name: ", remarks)[1:]:
+        name = block.split()[0]
+        limit = next((v for k, v in budget.items() if k in name), None)
+        if limit is None:
+            continue
+        seen += 1
+        def field(label):
+            m = re.search(re.escape(label) + r":\s*(\d+)", block)
+            if m is None:
+                raise RuntimeError(f"{src.name}: no '{label}' remark for {name}")
+            return int(m.group(1))
+        bad = {k: field(k) for k in ("ScratchSize [bytes/lane]", "VGPRs Spill", "SGPRs Spill") if field(k)}
+        if field("VGPRs") > limit:
+            bad["VGPRs"] = field("VGPRs")
+        if bad:
+            raise RuntimeError(f"{src.name}: {name} issues loads from inline asm and must not spill or exceed "
+                               f"{limit} VGPRs: {bad}")
+    if seen == 0:
+        raise RuntimeError(f"{src.name}: no resource remarks for {sorted(budget)}")
+
+
 def torch_lib_dir() -> Path:
     import importlib.util
 
@@ -62,12 +101,20 @@ def torch_lib_dir() -> Path:
 
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [str(HIPCC), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    checked = src.name in ASM_LOAD_KERNELS
+    extra = ["-Rpass-analysis=kernel-resource-usage"] if checked else []
+    cmd = [str(HIPCC), *HIP_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in (res.stderr or "").splitlines() if noise not in l)
+    lines = [l for l in (res.stderr or "").splitlines() if noise not in l]
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
+        raise RuntimeError(f"hipcc failed for {src.name}:\n" + "\n".join(lines))
+    if checked:
+        _check_asm_load_kernels(src, "\n".join(lines))
+        # keep only diagnostics that are not the resource remarks
+        lines = [l for l in lines if "kernel-resource-usage" not in l and not l.lstrip().startswith(("|", "^"))
+                 and not l.strip().split("|")[0].strip().isdigit()]
+    err = "\n".join(lines)
     if err.strip():
         print(err, file=sys.stderr)
     return obj
@@ -93,6 +140,10 @@ def build(jobs: int | None = None, verbose: bool = True, incremental: bool = Fal
     jobs = jobs or min(len(sources), max(1, os.cpu_count() or 1), 8)
     if verbose:
         print(f"[build_lib] compiling {len(sources)} sources for {ARCH} with {jobs} jobs", flush=True)
+    ver = subprocess.run([str(CLANGXX), "--version"], capture_output=True, text=True).stdout
+    if VALIDATED_CLANG not in ver:
+        print(f"[build_lib] warning: the inline-asm load kernels were validated with {VALIDATED_CLANG}, this "
+              f"compiler is: {ver.splitlines()[0] if ver else '?'}", file=sys.stderr)
     stale = [s for s in sources if not (incremental and _up_to_date(s))]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_compile, stale))

@@ -1171,7 +1171,8 @@ bool tm_internal_decode_ok(const tm_table_layer *t, const tm_layer_io *io) {
 }
 
 int tm_internal_decode_forward(const tm_table_layer *t, const tm_layer_io *io, const tm_decode_ws &w,
-                               const tm_route_args *ra, int64_t n_keep, void *const *ev, hipStream_t s) {
+                               const tm_route_args *ra, int64_t n_keep, void *const *ev, bool one_launch,
+                               hipStream_t s) {
   auto record = [&](int i) -> int {
     if (ev == nullptr || ev[i] == nullptr) return TM_OK;
     const hipError_t e = hipEventRecord(reinterpret_cast<hipEvent_t>(ev[i]), s);
@@ -1184,7 +1185,7 @@ int tm_internal_decode_forward(const tm_table_layer *t, const tm_layer_io *io, c
              "tm_table_forward: decode workspace missing");
   const int64_t n = io->n_tokens;
   const int64_t nsplit = tm_internal_stream_nsplit(n, t->n_cent, t->dim, io->n_nearest);
-  if (ev == nullptr && fused_ok(t, io, ra, nsplit)) {  // one launch
+  if (one_launch && ev == nullptr && fused_ok(t, io, ra, nsplit)) {  // one launch
     const int kpw = t->hidden / (32 * kSlices);
     if (t->dtype == TM_DT_BF16)
       kpw == 8 ? fused_nn_tk<TM_DT_BF16, 8>(t, io, w, ra, nsplit, n_keep, s)

@@ -539,6 +539,10 @@ extern "C" int tm_group_slots(const int64_t *ids, int64_t n_tokens, int32_t top_
   TM_REQUIRE(n_tokens * top_k < ((int64_t)1 << 31), TM_EINVAL_SHAPE, "tm_group_slots: too many slots");
   TM_REQUIRE(expert_offsets && tiles && (n_tokens == 0 || (ids && mask && row_token && row_out)), TM_EINVAL_ARG,
              "tm_group_slots: null pointer");
+  // tm_grouped_swiglu writes each row in 16-byte pieces from row_out
+  TM_REQUIRE(so_b % 8 == 0 && so_s % 8 == 0, TM_EINVAL_SHAPE,
+             "tm_group_slots: output strides (%lld, %lld) must be multiples of 8 elements", (long long)so_b,
+             (long long)so_s);
   const int64_t t_max = tm_group_slots_tiles(n_tokens * top_k, n_experts);
   hipLaunchKernelGGL(group_slots_kernel, dim3(1), dim3(kGroupThreads), 0, tm_hip_stream(stream), ids, n_tokens,
                      top_k, ld_ids, mask, ms_b, ms_s, n_experts, so_b, so_s, expert_offsets, row_token, row_out,

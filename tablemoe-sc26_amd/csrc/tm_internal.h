@@ -114,7 +114,10 @@ __attribute__((visibility("hidden"))) int tm_internal_search_stream(
 // row chunk).  With stage events, events 2 / 3 / 4 are recorded after the
 // projection / search / search (the keep select rides in the finishing
 // launch).  `cnt` holds one arrival counter per (16-row tile, 16-column
-// block): zero before the first call, left zero by every call.
+// block): zero before the first call, left zero by every call.  With
+// `one_launch` false the plan never takes its one-launch form (whose
+// workgroups wait for each other and need to be resident together): the
+// three launches hand data on only through the last arrival of each group.
 struct tm_decode_ws {
   uint64_t *lists;  // search lists [nsplit][n][list_len]
   uint64_t *keys;   // best keys [tm_internal_decode_keys(n)]
@@ -129,4 +132,4 @@ __attribute__((visibility("hidden"))) size_t tm_internal_decode_part_bytes(int64
 __attribute__((visibility("hidden"))) int tm_internal_decode_forward(const tm_table_layer *t, const tm_layer_io *io,
                                                                      const tm_decode_ws &w, const tm_route_args *ra,
                                                                      int64_t n_keep, void *const *stage_events,
-                                                                     hipStream_t stream);
+                                                                     bool one_launch, hipStream_t stream);

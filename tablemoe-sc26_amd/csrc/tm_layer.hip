@@ -141,7 +141,8 @@ int fused_top1_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLa
 // set and combines; events 3 and 4 coincide (the keep select rides in the
 // finishing launch), event 5 is recorded by the caller.
 int decode_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout &w, char *ws,
-                  const tm_route_args &ra, bool route_fused, int64_t n_keep, void *const *ev, hipStream_t s) {
+                  const tm_route_args &ra, bool route_fused, int64_t n_keep, void *const *ev, bool wait_plans,
+                  hipStream_t s) {
   const int64_t n = io->n_tokens;
   const WsPtrs p = ptrs(w, ws);
   const tm_decode_ws dw{reinterpret_cast<uint64_t *>(p.search), reinterpret_cast<uint64_t *>(p.keys),
@@ -152,7 +153,7 @@ int decode_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout
                                             0, io->weights, io->expert_ids, s)) != TM_OK)
     return st;
   if ((st = record(ev, 1, s)) != TM_OK) return st;
-  return tm_internal_decode_forward(t, io, dw, route_fused ? &ra : nullptr, n_keep, ev, s);
+  return tm_internal_decode_forward(t, io, dw, route_fused ? &ra : nullptr, n_keep, ev, wait_plans, s);
 }
 
 // Stages 0-4 of the general plan: the exported entry points; the router rides
@@ -237,8 +238,13 @@ extern "C" size_t tm_table_forward_workspace_size(const tm_table_layer *table, i
   return layout(table, n_tokens, n_nearest).total;
 }
 
-extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, void *workspace,
-                                size_t workspace_bytes, void *const *stage_events, tm_stream_t stream) {
+namespace {
+
+// tm_table_forward; `wait_plans` false keeps every launch free of waits on
+// other workgroups (the decode plan runs as three launches), so no result
+// depends on all of a launch's workgroups being resident together.
+int table_forward(const tm_table_layer *t, const tm_layer_io *io, void *workspace, size_t workspace_bytes,
+                  void *const *stage_events, bool wait_plans, tm_stream_t stream) {
   TM_REQUIRE(t && io, TM_EINVAL_ARG, "tm_table_forward: null descriptor");
   const int64_t n = io->n_tokens;
   TM_REQUIRE(n >= 0, TM_EINVAL_SHAPE, "tm_table_forward: negative token count");
@@ -264,7 +270,8 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
   const bool combine = (io->flags & TM_LAYER_NO_COMBINE) == 0;
   int st;
   if (combine && tm_internal_decode_ok(t, io)) {  // the finishing launch also combines
-    if ((st = decode_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s)) != TM_OK) return st;
+    if ((st = decode_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, wait_plans, s)) != TM_OK)
+      return st;
     return record(stage_events, 5, s);
   }
   const bool fused = fused_top1_ok(t, io);
@@ -286,6 +293,13 @@ extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, 
   return record(stage_events, 5, s);
 }
 
+}  // namespace
+
+extern "C" int tm_table_forward(const tm_table_layer *t, const tm_layer_io *io, void *workspace,
+                                size_t workspace_bytes, void *const *stage_events, tm_stream_t stream) {
+  return table_forward(t, io, workspace, workspace_bytes, stage_events, true, stream);
+}
+
 extern "C" int tm_table_forward_noalloc(const tm_table_layer *t, const tm_layer_io *io, tm_stream_t stream) {
   TM_REQUIRE(t && io, TM_EINVAL_ARG, "tm_table_forward_noalloc: null descriptor");
   TM_REQUIRE(io->n_tokens >= 0, TM_EINVAL_SHAPE, "tm_table_forward_noalloc: negative token count");
@@ -297,5 +311,8 @@ extern "C" int tm_table_forward_noalloc(const tm_table_layer *t, const tm_layer_
   void *ws = nullptr;
   const int st = scratch_for_current_device(tm_hip_stream(stream), &ws);
   if (st != TM_OK) return st;
-  return tm_table_forward(t, io, ws, (size_t)TM_NOALLOC_SCRATCH_BYTES, nullptr, stream);
+  // No plan whose workgroups wait for each other: such a wait that runs out
+  // is reported only in the workspace's error word, which a caller of this
+  // entry point cannot read.
+  return table_forward(t, io, ws, (size_t)TM_NOALLOC_SCRATCH_BYTES, nullptr, false, stream);
 }

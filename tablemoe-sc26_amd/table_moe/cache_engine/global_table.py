@@ -19,6 +19,7 @@ The reference counterparts it generalises: the projection
 from __future__ import annotations
 
 import ctypes as C
+import os
 
 import torch
 
@@ -28,6 +29,12 @@ _METRICS = {"l2": N.TM_METRIC_L2, "dot": N.TM_METRIC_DOT}
 
 
 class GlobalTable:
+    #: After every tm_table_forward call, synchronise and raise when one of the
+    #: launch's bounded cross-workgroup waits ran out (the workspace's error
+    #: word grew): a debugging aid for devices shared with other work, on by
+    #: TABLEMOE_CHECK_WAITS=1 or per table.
+    check_waits = os.environ.get("TABLEMOE_CHECK_WAITS", "0") not in ("", "0")
+
     def __init__(self, centroids: torch.Tensor, values: torch.Tensor, pca_vis, pca_txt=None, metric: str = "l2"):
         """centroids [C, d] and values [C, H] in bf16/fp16 (matrix-core
         search) or fp32 on a HIP device; pca_vis / pca_txt = (proj [H, d],
@@ -255,8 +262,20 @@ class GlobalTable:
             evs = (C.c_void_p * 6)(*[e.cuda_event for e in stage_events])
         N.check(N.lib().tm_table_forward(C.byref(self._desc), C.byref(io), N.ptr(ws), ws.numel(), evs,
                                          N.stream(self.device)), "tm_table_forward")
+        if self.check_waits:
+            self._raise_on_wait_errors()
         res.pop("_inputs")
         return res
+
+    def _raise_on_wait_errors(self):
+        if torch.cuda.is_current_stream_capturing():
+            return  # nothing ran yet: read wait_errors() after the replays
+        seen = getattr(self, "_wait_errors_seen", 0)
+        now = self.wait_errors()
+        self._wait_errors_seen = now
+        if now != seen:
+            raise RuntimeError(f"tm_table_forward: {now - seen} cross-workgroup wait(s) ran out; the call's outputs "
+                               "are undefined (the launch's workgroups could not all be resident together)")
 
     def wait_errors(self) -> int:
         """Bounded cross-workgroup waits of the one-launch decode plan that ran
@@ -280,6 +299,8 @@ class GlobalTable:
         ws = self._buf("layer_ws", (max(nbytes, 1),), torch.uint8)
         N.check(N.lib().tm_table_forward(C.byref(self._desc), C.byref(io), N.ptr(ws), ws.numel(), None,
                                          N.stream(self.device)), "tm_table_forward")
+        if self.check_waits:
+            self._raise_on_wait_errors()
         res.pop("_inputs")
         del res["out"]
         return res
@@ -343,7 +364,8 @@ class GlobalTable:
                               n_nearest: int = 1, keep_rate: float = 0.6, out=None):
         """layer_forward through tm_table_forward_noalloc: the library's static
         scratch instead of a workspace (at most TM_NOALLOC_SCRATCH_BYTES; calls
-        overlapping on one GPU race for it)."""
+        overlapping on one GPU race for it).  It takes no plan whose
+        workgroups wait for each other, so there is no error word to check."""
         io, res = self._layer_io(hidden, is_vision, router_logits, slot_out, residual, router_top_k, n_nearest,
                                  keep_rate, out)
         N.check(N.lib().tm_table_forward_noalloc(C.byref(self._desc), C.byref(io), N.stream(self.device)),

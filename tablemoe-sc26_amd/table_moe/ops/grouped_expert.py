@@ -76,6 +76,8 @@ class GroupedExperts:
         n, k = ids.shape
         if slot_out.shape != (n, k, self.hidden) or slot_out.stride(-1) != 1:
             raise ValueError(f"slot_out must be [N, {k}, {self.hidden}] with unit stride along hidden")
+        if slot_out.stride(0) % 8 or slot_out.stride(1) % 8 or slot_out.data_ptr() % 16:
+            raise ValueError("slot_out rows must start on 16-byte boundaries (strides multiples of 8 elements)")
         x = hidden if hidden.stride(-1) == 1 else hidden.contiguous()
         offs, row_token, row_out, tiles = self.group(ids, mask, slot_out)
         tag = N.dtype_tag(self.dtype)

@@ -25,6 +25,11 @@ def hip_device():
     from table_moe import _native
 
     _native.load()  # raise if the library is not built: no fallback path exists
+    from table_moe.cache_engine import GlobalTable
+
+    # every layer call of the GPU tests checks the workspace's error word: a
+    # bounded cross-workgroup wait that ran out fails the test that made it
+    GlobalTable.check_waits = True
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     return dev

@@ -122,6 +122,11 @@ def test_argument_validation_without_device(lib):
     # the packed path's intermediate is whole 256-row tiles of the tile list
     assert lib.tm_grouped_swiglu_packed_workspace_size(24576, 1536, 64, N.TM_DT_BF16) == (96 + 64) * 256 * 1536 * 2
     assert lib.tm_swiglu_workspace_size(24576, 1536, N.TM_DT_BF16) == 24576 * 1536 * 2
+    # grouped rows are written in 16-byte pieces: output strides off a multiple of 8 elements are rejected
+    p = C.c_void_p(256)
+    assert lib.tm_group_slots(p, 16, 6, 6, p, 6, 1, 64, 6 * 2564, 2564, p, p, p, p, None) == N.TM_EINVAL_SHAPE
+    assert b"multiples of 8" in lib.tm_last_error()
+    assert lib.tm_group_slots(p, 16, 6, 6, p, 6, 1, 64, 6 * 2560 + 4, 2560, p, p, p, p, None) == N.TM_EINVAL_SHAPE
 
 
 

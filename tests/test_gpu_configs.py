@@ -10,7 +10,8 @@ import pytest
 import torch
 
 from oracle import tm_oracle as O
-from parity_util import assert_bf16_output, assert_projection_close, check_topk_rows, np64, proj_abssum, ulp
+from parity_util import (assert_bf16_output, assert_projection_close, check_end_to_end_keep, check_end_to_end_topk,
+                         check_topk_rows, np64, proj_abssum, ulp)
 
 pytestmark = pytest.mark.gpu
 
@@ -53,6 +54,9 @@ def check_layer_vs_oracle(res, wl, dt, residual, topk, what, proj_min_exact=0.95
     keep = np64(res["keep"])
     n = q.shape[0]
     np.testing.assert_array_equal(keep, O.keep_select(gd[:, 0], int(keep.sum())), err_msg=f"{what} keep")
+    # end to end from x: the oracle's search and keep set on its own queries
+    vals_o, _, _ = check_end_to_end_topk(q, ref_q, np64(wl.centroids), gi, f"{what} search")
+    check_end_to_end_keep(gd[:, 0], vals_o[:, 0], keep, int(keep.sum()), f"{what} keep")
     want = O.gather_combine(keep, np64(wl.slot_out), np64(res["weights"]), np64(wl.values), gi, gd,
                             np64(residual), O.F32)
     absw = O.gather_combine(keep, np.abs(np64(wl.slot_out)), np64(res["weights"]), np.abs(np64(wl.values)), gi, gd,
@@ -229,6 +233,29 @@ def test_config5_layer_end_to_end(hip_device):
     absw = O.gather_combine(keep_s, np.abs(slot_h), np64(w)[rows], np.abs(np64(wl.values)), np64(idx)[rows],
                             np64(dist)[rows], np.abs(got_base), O.F32)
     assert_bf16_output(np64(out)[rows][sel], want, absw)
+    # The reference rounds in another order: the shared MLP output and the
+    # routed combine are each rounded, added and rounded
+    # (deepseek_layers.py:743), and the decoder layer adds the residual:
+    # ref = bf16(R + bf16(bf16(S) + bf16(Y))).  This layer computes
+    # bf16(bf16(R + S) + Y).  With u = 2^-8 (bf16 unit roundoff) both are
+    # within u-multiples of the exact R + S + Y, so they differ by at most
+    # u * (|R + S| + |S| + |Y| + |S + Y| + 2 |R + S + Y|) (+ the fp32 sums).
+    _, f_s = O.swiglu_expert(x, np64(s1), np64(s3), np64(s2), O.BF16)
+    big_s = f_s @ np64(s2).T  # the shared experts' down projection, unrounded
+    resid = np64(wl.residual)[rows]
+    big_y = O.gather_combine(keep_s, slot_h, np64(w)[rows], np64(wl.values), np64(idx)[rows], np64(dist)[rows],
+                             np.zeros_like(resid), O.F32)
+    bf = lambda v: O.round_to(v, O.BF16)  # noqa: E731
+    ref_order = bf(resid + bf(bf(big_s) + bf(big_y)))
+    exact = resid + big_s + big_y
+    u = 2.0 ** -8
+    bound = u * (np.abs(resid + big_s) + np.abs(big_s) + np.abs(big_y) + np.abs(big_s + big_y) + 2 * np.abs(exact))
+    got = np64(out)[rows]
+    diff = np.abs(got - ref_order)
+    assert np.all(diff <= bound * 1.001 + 1e-6), float(np.max(diff - bound))
+    same = float(np.mean(got == ref_order))
+    print(f"[config5] rounding order: {same:.4f} of subset elements equal the reference order's bits, "
+          f"max |diff| {float(diff.max()):.3g} (bound {float(bound.max()):.3g})", flush=True)
     # the subset's search and projection against the oracle
     q_h = np64(q)[rows]
     ref_q = O.project_queries(x, isv[rows], (np64(wl.proj_vis), np64(wl.bias_vis)),
@@ -237,6 +264,12 @@ def test_config5_layer_end_to_end(hip_device):
                             torch.bfloat16, min_exact=0.9)
     _, want_idx, exact = O.global_search(q_h, np64(wl.centroids), 1)
     check_topk_rows(exact, np64(idx)[rows], want_idx, False, "config 5 search")
+    # end to end from x on every token: the oracle's search and keep set on its own queries
+    isv_all = np64(wl.is_vision).astype(bool)
+    ref_q_all = O.project_queries(np64(wl.x), isv_all, (np64(wl.proj_vis), np64(wl.bias_vis)),
+                                  (np64(wl.proj_txt), np64(wl.bias_txt)), False, O.BF16)
+    vals_o, _, _ = check_end_to_end_topk(np64(q), ref_q_all, np64(wl.centroids), np64(idx), "config 5 search")
+    check_end_to_end_keep(np64(dist)[:, 0], vals_o[:, 0], kp, 2457, "config 5 keep")
 
 
 def test_config5_layer_graph_replays(hip_device):

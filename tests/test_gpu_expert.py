@@ -122,6 +122,35 @@ def test_group_slots_empty_batch(hip_device):
     assert out.shape == (0, k, h)
 
 
+def test_grouped_forward_rejects_misaligned_slot_rows(hip_device):
+    """Grouped rows are written in 16-byte pieces: a slot_out view whose rows
+    do not start on 16-byte boundaries (stride hidden + 4) is rejected before
+    any launch, by GroupedExperts.forward and by tm_group_slots itself."""
+    from table_moe.ops import GroupedExperts
+
+    dev = hip_device
+    e, h, k, n = 8, 128, 6, 4
+    w = torch.zeros(e, 128, h, dtype=torch.bfloat16, device=dev)
+    ge = GroupedExperts(w, w.clone(), torch.zeros(e, h, 128, dtype=torch.bfloat16, device=dev))
+    ids = torch.zeros(n, k, dtype=torch.long, device=dev)
+    keep = torch.ones(n, dtype=torch.bool, device=dev)
+    hidden = torch.zeros(n, h, dtype=torch.bfloat16, device=dev)
+    wide = torch.zeros(n, k, h + 4, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="16-byte"):
+        ge.forward(hidden, ids, keep, wide[..., :h])
+    t_max = N.lib().tm_group_slots_tiles(n * k, e)
+    offs = torch.zeros(e + 1, dtype=torch.int32, device=dev)
+    tiles = torch.zeros(2 + 2 * t_max, dtype=torch.int32, device=dev)
+    rows = torch.zeros(n * k, dtype=torch.int32, device=dev)
+    outs = torch.zeros(n * k, dtype=torch.long, device=dev)
+    st = N.lib().tm_group_slots(N.ptr(ids), n, k, k, N.ptr(keep), 1, 0, e, k * (h + 4), h + 4, N.ptr(offs),
+                                N.ptr(rows), N.ptr(outs), N.ptr(tiles), N.stream(dev))
+    assert st == N.TM_EINVAL_SHAPE
+    out = ge.forward(hidden, ids, keep, wide[..., :h].contiguous())  # aligned copy: accepted
+    torch.cuda.synchronize()
+    assert out.shape == (n, k, h)
+
+
 @pytest.mark.parametrize("mask_kind", ["token", "slot"])
 def test_grouped_swiglu_vs_oracle_and_single_expert(hip_device, mask_kind):
     """Config-5 shapes (64 experts, top-6, hidden 2560, intermediate 1536) on

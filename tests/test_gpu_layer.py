@@ -7,8 +7,8 @@ import pytest
 import torch
 
 from oracle import tm_oracle as O
-from parity_util import (ODT, assert_bf16_output, assert_projection_close, assert_within_ulps, check_pick,
-                         check_topk_rows, np64, proj_abssum, ulp)
+from parity_util import (ODT, assert_bf16_output, assert_projection_close, assert_within_ulps, check_end_to_end_keep,
+                         check_end_to_end_topk, check_pick, check_topk_rows, np64, proj_abssum, ulp)
 from table_moe import _native as N
 
 pytestmark = pytest.mark.gpu
@@ -472,6 +472,9 @@ def test_layer_forward_config2_end_to_end(hip_device):
     keep = np64(res["keep"])
     assert keep.sum() == O.keep_count(4096, 0.6) == 2457
     np.testing.assert_array_equal(keep, O.keep_select(gd[:, 0].astype(np.float32).astype(np.float64), 2457))
+    # end to end from x: the oracle's search and keep set on its own queries
+    vals_o, _, _ = check_end_to_end_topk(q, ref_q, np64(wl.centroids), gi, "config 2 search")
+    check_end_to_end_keep(gd[:, 0], vals_o[:, 0], keep, 2457, "config 2 keep")
     # combine on the device's selections
     exact = O.gather_combine(keep, np64(wl.slot_out), np64(res["weights"]), np64(wl.values), gi, gd,
                              np64(wl.residual), O.F32)
@@ -688,6 +691,9 @@ def test_layer_forward_config3_decode_end_to_end(hip_device, n):
     n_keep = O.keep_count(n, 0.6)
     assert keep.sum() == n_keep == {1: 1, 8: 4, 32: 19}[n]
     np.testing.assert_array_equal(keep, O.keep_select(gd[:, 0].astype(np.float32).astype(np.float64), n_keep))
+    # end to end from x: the oracle's top-4 lists and keep set on its own queries
+    vals_o, _, _ = check_end_to_end_topk(q, ref_q, np64(wl.centroids), gi, f"config 3 N={n} search")
+    check_end_to_end_keep(gd[:, 0], vals_o[:, 0], keep, n_keep, f"config 3 N={n} keep")
     exact = O.gather_combine(keep, np64(wl.slot_out), np64(res["weights"]), np64(wl.values), gi, gd,
                              np64(wl.residual), O.F32)
     abssum = O.gather_combine(keep, np.abs(np64(wl.slot_out)), np64(res["weights"]), np.abs(np64(wl.values)), gi,
@@ -797,6 +803,7 @@ def test_layer_graph_replays_match_eager(hip_device, cfg, n, nn):
         assert torch.isfinite(junk)
         for key in ("weights", "ids", "q", "dist", "idx", "keep", "out"):
             assert torch.equal(res[key], ref[key]), (rep, key)
+        assert tg.wait_errors() == 0, rep
 
 
 @pytest.mark.parametrize("hazard", [True, False])

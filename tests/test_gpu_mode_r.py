@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import tm_oracle as O
-from parity_util import ODT, check_pick, np64, proj_abssum, ulp
+from parity_util import ODT, check_gated_end_to_end, check_pick, np64, proj_abssum, ulp
 from table_moe import _native as N
 
 pytestmark = pytest.mark.gpu
@@ -119,6 +119,10 @@ def test_prefill_offline_qwen_shape_vs_oracle(hip_device, qwen):
     thr_v, thr_t = CacheConfig.OFFLINE_COSINE_THRESHOLD_VISION, CacheConfig.OFFLINE_COSINE_THRESHOLD_TEXT
     check_gated(q, mgr.keys_buffer, sel, wl.is_vision, reuse, hit, idx, thr_v, thr_t, O.CMP_GE, rows=rows,
                 min_hits=50)
+    # end to end from x: the oracle's search on its own normalised queries
+    check_gated_end_to_end(got_q, ref_q, np64(mgr.keys_buffer), np64(sel)[rows], np64(wl.is_vision)[rows],
+                           np64(reuse)[rows], np64(hit)[rows], np64(idx)[rows], thr_v, thr_t, O.CMP_GE,
+                           what="prefill offline (Qwen shape)")
     rs = np64(reuse)
     assert not np64(hit)[~rs].any() and (np64(idx)[~rs] == 0).all()
     assert np64(hit).sum() > 200
@@ -150,10 +154,14 @@ def test_decode_offline_entry_points_qwen_shape(hip_device, qwen):
     abssum = proj_abssum(np64(x), np64(vis), np64(pca["vision"]["proj"]), np64(pca["text"]["proj"]))
     assert np.all(np.abs(np64(q) - ref_q) <= ulp(ref_q, torch.bfloat16) + 2.0**-18 * abssum)
     check_gated(q, mgr.keys_buffer, sel, vis, reuse, hit, idx, 0.0, 0.0, O.CMP_GE, min_hits=5)
+    check_gated_end_to_end(np64(q), ref_q, np64(mgr.keys_buffer), np64(sel), np64(vis), np64(reuse), np64(hit),
+                           np64(idx), 0.0, 0.0, O.CMP_GE, what="decode offline")
     hit2, idx2 = eng.search_decode_offline_dot(0, x, sel, vis, reuse)
     torch.cuda.synchronize()
     thr = float(CacheConfig.OFFLINE_DOT_THRESHOLD)
     check_gated(q, mgr.raw_keys_buffer, sel, vis, reuse, hit2, idx2, thr, thr, O.CMP_GT, min_hits=5)
+    check_gated_end_to_end(np64(q), ref_q, np64(mgr.raw_keys_buffer), np64(sel), np64(vis), np64(reuse),
+                           np64(hit2), np64(idx2), thr, thr, O.CMP_GT, what="decode offline dot")
     keep_k = 4
     for b in range(n):
         oh = torch.full((k,), True, device=dev)

@@ -42,6 +42,7 @@ def test_noalloc_matches_workspace_call(hip_device):
         for key in KEYS:
             assert torch.equal(ra[key], rb[key]), (cfg, n, key)
         assert int(rb["keep"].sum()) == b.keep_count(n, 0.6)
+        assert a.wait_errors() == 0, (cfg, n)
 
 
 @pytest.mark.gpu
