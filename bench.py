@@ -555,6 +555,133 @@ def run_mode_r(replays=20):
     }
 
 
+def run_mode_r_layer(layers=24):
+    """The mode-R prefill layer (Qwen shapes, N=4096) as a drop-in user gets
+    it: the table path of QwenMoeWrapperCached.forward in the unchanged
+    hook's op order (cached_layers.py:282-465 -- router, the collected
+    buffer's zero-fill, keep mask, offline search, torch.where + .cpu() +
+    gather_values, the recomputed slots' and the gathered rows' scatters,
+    renormalise, bmm) on this package's entry points, with the routed
+    experts' outputs given (synthetic, like slot_out in mode G); and the same
+    layer with HybridStorageManager.combine_slots (tm_slot_combine) in place
+    of :302 and :437-465.  The hook is timed eagerly (its .cpu() syncs the
+    host; wall clock per layer, median); the edited layer eagerly and as a
+    graph of 16 layers (device time)."""
+    import torch
+
+    from synth import make_mode_r_manager, make_workload
+    from table_moe.cache_engine import VectorSearchEngine
+    from table_moe.ops import qwen_topk_softmax
+    from table_moe.skip import build_prefill_keep_mask, renormalize_surviving_weights
+
+    dev = torch.device("cuda:0")
+    mgr = make_mode_r_manager(dev)
+    eng = VectorSearchEngine(mgr)
+    wl = make_workload(2, with_slot_out=False, device=dev, gen_device=dev)
+    n, k, H = wl.x.shape[0], 8, wl.x.shape[1]
+    g = torch.Generator(device=dev).manual_seed(21)
+    logits = wl.logits.to(torch.bfloat16)  # the gate's output in the model dtype
+    attn = torch.rand(n, device=dev, generator=g)
+    isv = wl.is_vision
+    # half the tokens near a key of their first routed expert, so the search hits
+    w0, sel0 = qwen_topk_softmax(logits, k)
+    kb = mgr.keys_buffer
+    near = torch.rand(n, device=dev, generator=g) < 0.5
+    src = kb[sel0[:, 0], (~isv).long(), torch.randint(0, 256, (n,), device=dev, generator=g)].float()
+    p_v, p_t = mgr.pca["vision"]["proj"].float(), mgr.pca["text"]["proj"].float()
+    lift = torch.where(isv[:, None], src @ p_v.T, src @ p_t.T) * 4.0
+    x = torch.where(near[:, None], wl.x.float() * 0.2 + lift, wl.x.float()).to(torch.bfloat16)
+    expert_out = (torch.randn(n, k, H, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+
+    def hook_layer():
+        w, sel = qwen_topk_softmax(logits, k)  # :282
+        collected = torch.zeros((n, k, H), dtype=torch.bfloat16, device=dev)  # :302
+        compute = build_prefill_keep_mask(sel, w, attn, 128, 0.6)  # :336
+        search = ~compute
+        off_hit, off_idx = eng.search_prefill_offline(0, x, sel, isv, search)  # :387
+        rows, cols = torch.where(off_hit)  # :345-352 perform_value_fetch
+        eids = sel[rows, cols].cpu()
+        cids = off_idx[rows, cols].cpu()
+        mids = torch.where(isv[rows], 0, 1).cpu()
+        vals = mgr.gather_values(eids, mids, cids).to(dev, non_blocking=True)
+        c_rows, c_cols = torch.where(compute)  # :400, the expert loop's targets (:437)
+        collected[c_rows, c_cols] = expert_out[c_rows, c_cols]
+        collected[rows, cols] = vals  # :461
+        survivor = compute | off_hit
+        ew = renormalize_surviving_weights(w, survivor).to(logits.dtype)  # :462
+        return torch.bmm(ew.unsqueeze(1), collected).squeeze(1)  # :463
+
+    out_e = torch.empty(n, H, dtype=torch.bfloat16, device=dev)
+
+    def edited_layer():
+        w, sel = qwen_topk_softmax(logits, k)
+        compute = build_prefill_keep_mask(sel, w, attn, 128, 0.6)
+        off_hit, off_idx = eng.search_prefill_offline(0, x, sel, isv, ~compute)
+        return mgr.combine_slots(w, sel, isv, compute, expert_out, off_hit, off_idx, out=out_e)
+
+    def wall_us(fn, reps):
+        times = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            times.append((time.perf_counter() - t0) * 1e6)
+        return statistics.median(times)
+
+    a = hook_layer()
+    b = edited_layer()
+    torch.cuda.synchronize()
+    # the two orders give the same rows up to the combine's rounding (bmm in
+    # bf16 vs one fp32 sum): report the largest difference
+    max_diff = float((a.float() - b.float()).abs().max())
+    for _ in range(3):
+        hook_layer()
+        edited_layer()
+    hook_us = wall_us(hook_layer, layers)
+    edited_us = wall_us(edited_layer, layers)
+    edited_dev_us = per_call_us(edited_layer, 16, 10)
+    # the hook's table-path torch ops alone (device time): zero-fill, scatters, renormalise + bmm
+    w, sel = qwen_topk_softmax(logits, k)
+    compute = build_prefill_keep_mask(sel, w, attn, 128, 0.6)
+    off_hit, off_idx = eng.search_prefill_offline(0, x, sel, isv, ~compute)
+    rows, cols = torch.where(off_hit)
+    vals = mgr.gather_values(sel[rows, cols], torch.where(isv[rows], 0, 1), off_idx[rows, cols])
+    c_rows, c_cols = torch.where(compute)
+    collected = torch.empty((n, k, H), dtype=torch.bfloat16, device=dev)
+
+    def hook_torch():
+        collected.zero_()
+        collected[c_rows, c_cols] = expert_out[c_rows, c_cols]
+        collected[rows, cols] = vals
+        ew = renormalize_surviving_weights(w, compute | off_hit).to(logits.dtype)
+        return torch.bmm(ew.unsqueeze(1), collected).squeeze(1)
+
+    torch_dev_us = per_call_us(hook_torch, 8, 10)
+    combine_dev_us = per_call_us(lambda: mgr.combine_slots(w, sel, isv, compute, expert_out, off_hit, off_idx,
+                                                           out=out_e), 16, 10)
+    hits = int(off_hit.sum())
+    log(f"mode R layer (hook op order) {hook_us:.1f} us wall; edited (tm_slot_combine) {edited_us:.1f} us wall, "
+        f"{edited_dev_us:.1f} us device; hook torch ops {torch_dev_us:.1f} us vs combine_slots {combine_dev_us:.1f} us")
+    return {
+        "workload": "mode R prefill layer, Qwen3-VL-30B-A3B shapes (E=128 x 2 x K=256, d=64, hidden 2048 bf16, "
+                    "N=4096, top-8, keep 0.6 by importance), the routed experts' outputs given",
+        "hook_us": hook_us,
+        "edited_us": edited_us,
+        "edited_device_us": edited_dev_us,
+        "hook_torch_ops_device_us": torch_dev_us,
+        "combine_slots_device_us": combine_dev_us,
+        "hook_torch_share": (hook_us - edited_us) / hook_us,
+        "offline_hits": hits,
+        "max_abs_diff_hook_vs_edited": max_diff,
+        "tokens_per_s_hook": n / (hook_us * 1e-6),
+        "tokens_per_s_edited": n / (edited_dev_us * 1e-6),
+        "timing": "hook: eager, host wall clock per layer (its .cpu() syncs), median of "
+                  f"{layers}; edited: eager wall clock, and device time from graphs of 16 layers; torch ops / "
+                  "combine_slots: graphs of 8 / 16 calls",
+    }
+
+
 # --------------------------------------------------------------------------- CPU baseline
 def cpu_model():
     try:
@@ -750,6 +877,9 @@ def main() -> int:
         if name in sections:
             result[name] = fn()
             torch.cuda.empty_cache()
+    if "mode_r" in sections:
+        result["mode_r"]["layer"] = run_mode_r_layer()
+        torch.cuda.empty_cache()
     copy_calibration()
     if "cpu" in sections:
         log("timing the CPU baseline")

@@ -55,11 +55,12 @@ HIP_FLAGS = [
 # not know those loads are in flight until the explicit s_waitcnt that
 # retires them): their results are right only while the register allocator
 # never spills, copies or reuses those registers before the wait.  The build
-# fails if such a kernel uses scratch, spills, or needs more VGPRs than the
-# budget its launch bounds give (256 at two waves per SIMD).  The pattern was
-# checked on the generated ISA (no read or reuse of an in-flight destination
-# register) with the compiler VALIDATED_CLANG names; another compiler only
-# draws a warning, since the resource check still runs.
+# fails if such a kernel uses scratch, spills VGPRs, or needs more VGPRs than
+# the budget its launch bounds give (256 at two waves per SIMD), and if the
+# dataflow check of its gfx950 assembly (isa_check.py) finds an instruction
+# that reads or overwrites a register an outstanding load may still write.
+# The pattern was first validated with the compiler VALIDATED_CLANG names;
+# another compiler draws a warning (both checks still run).
 ASM_LOAD_KERNELS = {"tm_project.hip": (("project_cols_pipe_kernel", 256),)}
 VALIDATED_CLANG = "roc-7.2.0 26014"
 
@@ -80,7 +81,9 @@ def _check_asm_load_kernels(src: Path, remarks: str) -> None:
             if m is None:
                 raise RuntimeError(f"{src.name}: no '{label}' remark for {name}")
             return int(m.group(1))
-        bad = {k: field(k) for k in ("ScratchSize [bytes/lane]", "VGPRs Spill", "SGPRs Spill") if field(k)}
+        # SGPR spills go to lanes of compiler-allocated VGPRs (no scratch), and
+        # the dataflow check sees every VGPR they write
+        bad = {k: field(k) for k in ("ScratchSize [bytes/lane]", "VGPRs Spill") if field(k)}
         if field("VGPRs") > limit:
             bad["VGPRs"] = field("VGPRs")
         if bad:
@@ -88,6 +91,31 @@ def _check_asm_load_kernels(src: Path, remarks: str) -> None:
                                f"{limit} VGPRs: {bad}")
     if seen == 0:
         raise RuntimeError(f"{src.name}: no resource remarks for {sorted(budget)}")
+
+
+def _device_asm(src: Path) -> Path:
+    """gfx950 assembly of a source (for the dataflow check), in the build folder."""
+    out = BUILD_DIR / (src.stem + ".s")
+    cmd = [str(HIPCC), *HIP_FLAGS, "--cuda-device-only", "-S", str(src), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for {src.name}:\n{res.stderr}")
+    return out
+
+
+def _check_asm_dataflow(src: Path, asm_path: Path) -> None:
+    import isa_check
+
+    asm = asm_path.read_text()
+    for kernel, _ in ASM_LOAD_KERNELS[src.name]:
+        names = isa_check.functions_named(asm, kernel)
+        if not names:
+            raise RuntimeError(f"{src.name}: no function named *{kernel}* in the device assembly")
+        for name in names:
+            issues = isa_check.check_function(asm, name)
+            if issues:
+                shown = "\n".join(f"  line {k}: {kind}: {line}" for k, kind, line in issues[:8])
+                raise RuntimeError(f"{src.name}: {name} reads or overwrites registers of an in-flight load:\n{shown}")
 
 
 def torch_lib_dir() -> Path:
@@ -145,8 +173,12 @@ def build(jobs: int | None = None, verbose: bool = True, incremental: bool = Fal
         print(f"[build_lib] warning: the inline-asm load kernels were validated with {VALIDATED_CLANG}, this "
               f"compiler is: {ver.splitlines()[0] if ver else '?'}", file=sys.stderr)
     stale = [s for s in sources if not (incremental and _up_to_date(s))]
+    checked = [s for s in stale if s.name in ASM_LOAD_KERNELS]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        asm_jobs = {s: ex.submit(_device_asm, s) for s in checked}
         list(ex.map(_compile, stale))
+        for src, job in asm_jobs.items():
+            _check_asm_dataflow(src, job.result())
     objs = [BUILD_DIR / (s.stem + ".o") for s in sources]
     tlib = torch_lib_dir()
     if not (tlib / "libamdhip64.so").exists():

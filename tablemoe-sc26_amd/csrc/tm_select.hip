@@ -175,36 +175,53 @@ __global__ void fixed_keep_kernel(int64_t total, int top_k, int keep_k, uint8_t 
 
 // ---------------------------------------------------------------------------
 // a3: build_prefill_keep_mask (pruning.py:18-48), deterministic.
-// Pass 1: per token chunk, each expert's partial score sum (fixed entry
-// order) and selection count.  Pass 2 (one workgroup): chunk sums in chunk
-// order, ranking, mask.
+// Pass 1: per chunk of kEntries (token, slot) entries, each expert's partial
+// score sum (entries in order) and selection count.  Pass 2 (one
+// workgroup): each expert's chunk sums in a fixed order, ranking, mask.
+// Every loop issues its loads ahead of their use: a loop that loads and
+// uses one value per iteration waits a memory (or LDS) round trip each time.
 // ---------------------------------------------------------------------------
-constexpr int kEntries = 2048;  // (token, slot) entries per chunk
+constexpr int kEntries = 256;  // (token, slot) entries per chunk
 
 __global__ __launch_bounds__(256) void expert_partial_kernel(
     const int64_t *__restrict__ sel, const float *__restrict__ w, const float *__restrict__ attn,
     int64_t n, int top_k, int n_experts, int64_t tok_per_chunk, float *__restrict__ part_sum,
     uint32_t *__restrict__ part_cnt) {
-  __shared__ int s_sel[kEntries];
-  __shared__ float s_val[kEntries];
+  __shared__ int4 s_sel[kEntries / 4];
+  __shared__ float4 s_val[kEntries / 4];
   const int64_t t0 = (int64_t)blockIdx.x * tok_per_chunk;
   const int64_t t1 = (t0 + tok_per_chunk < n) ? t0 + tok_per_chunk : n;
   const int ne = (int)((t1 - t0) * top_k);
   const float nf = (float)n;
-  for (int j = threadIdx.x; j < ne; j += blockDim.x) {
-    const int64_t b = t0 + j / top_k;
-    const int s = j % top_k;
-    const int64_t e = sel[b * top_k + s];
-    s_sel[j] = (e >= 0 && e < n_experts) ? (int)e : -1;
-    const float wv = w[b * top_k + s];
-    s_val[j] = attn ? attn[b] * wv : wv / nf;
+  int *ss = reinterpret_cast<int *>(s_sel);
+  float *sv = reinterpret_cast<float *>(s_val);
+  for (int j = threadIdx.x; j < kEntries; j += blockDim.x) {
+    int ev = -1;
+    float v = 0.f;
+    if (j < ne) {
+      const int64_t b = t0 + j / top_k;
+      const int64_t e = sel[t0 * top_k + j];
+      ev = (e >= 0 && e < n_experts) ? (int)e : -1;
+      const float wv = w[t0 * top_k + j];
+      v = attn ? attn[b] * wv : wv / nf;
+    }
+    ss[j] = ev;  // entries past the chunk match no expert
+    sv[j] = v;
   }
   __syncthreads();
+  const int nq = (ne + 3) / 4;
   for (int e = threadIdx.x; e < n_experts; e += blockDim.x) {
     float acc = 0.f;
     uint32_t cnt = 0;
-    for (int j = 0; j < ne; ++j) {
-      if (s_sel[j] == e) { acc += s_val[j]; ++cnt; }
+#pragma unroll 8
+    for (int q = 0; q < nq; ++q) {  // broadcast reads, entries in order
+      const int4 s4 = s_sel[q];
+      const float4 v4 = s_val[q];
+      acc = s4.x == e ? acc + v4.x : acc;
+      acc = s4.y == e ? acc + v4.y : acc;
+      acc = s4.z == e ? acc + v4.z : acc;
+      acc = s4.w == e ? acc + v4.w : acc;
+      cnt += (uint32_t)(s4.x == e) + (uint32_t)(s4.y == e) + (uint32_t)(s4.z == e) + (uint32_t)(s4.w == e);
     }
     part_sum[(int64_t)blockIdx.x * n_experts + e] = acc;
     part_cnt[(int64_t)blockIdx.x * n_experts + e] = cnt;
@@ -213,6 +230,9 @@ __global__ __launch_bounds__(256) void expert_partial_kernel(
 
 constexpr int kRankThreads = 1024;
 constexpr int kMaxExperts = 1024;
+constexpr int kRankPass = 128;                         // experts per pass
+constexpr int kRankShares = kRankThreads / kRankPass;  // threads per expert (8)
+constexpr int kRankBatch = 16;                         // loads issued before any is used
 
 __global__ __launch_bounds__(kRankThreads) void expert_rank_kernel(
     const int64_t *__restrict__ sel, int64_t n, int top_k, int n_experts, int64_t nchunk,
@@ -221,42 +241,108 @@ __global__ __launch_bounds__(kRankThreads) void expert_rank_kernel(
   __shared__ float score[kMaxExperts];
   __shared__ uint8_t active[kMaxExperts];
   __shared__ uint8_t kept[kMaxExperts];
+  __shared__ float sh_sum[kRankShares][kRankPass];
+  __shared__ uint32_t sh_cnt[kRankShares][kRankPass];
   __shared__ __align__(16) uint32_t wave_tot[kRankThreads / 64 + 1];
   const int tid = threadIdx.x;
-  uint32_t my_active = 0;
-  for (int e = tid; e < n_experts; e += kRankThreads) {
+  const int sub = tid / kRankPass;  // share of the chunks / experts this thread takes
+  const int el = tid % kRankPass;   // expert within the pass: a wave reads consecutive experts
+  // Expert e's score: share sub adds chunks sub, sub + 8, ... in increasing
+  // order; the 8 shares are then added in share order.
+  for (int e0 = 0; e0 < n_experts; e0 += kRankPass) {
+    const int e = e0 + el;
+    const int ee = e < n_experts ? e : n_experts - 1;
     float s = 0.f;
     uint32_t c = 0;
-    for (int64_t k = 0; k < nchunk; ++k) {
-      s += part_sum[k * n_experts + e];
-      c += part_cnt[k * n_experts + e];
+    for (int64_t k0 = sub; k0 < nchunk; k0 += (int64_t)kRankShares * kRankBatch) {
+      float v[kRankBatch];
+      uint32_t cc[kRankBatch];
+#pragma unroll
+      for (int u = 0; u < kRankBatch; ++u) {
+        const int64_t k = k0 + (int64_t)u * kRankShares;
+        const int64_t kk = k < nchunk ? k : nchunk - 1;
+        v[u] = part_sum[kk * n_experts + ee];
+        cc[u] = part_cnt[kk * n_experts + ee];
+      }
+#pragma unroll
+      for (int u = 0; u < kRankBatch; ++u) {
+        const bool in = k0 + (int64_t)u * kRankShares < nchunk;
+        s = in ? s + v[u] : s;
+        c += in ? cc[u] : 0u;
+      }
     }
-    score[e] = s;
-    active[e] = c > 0;
-    my_active += (c > 0);
-    if (out_scores) out_scores[e] = s;
+    sh_sum[sub][el] = s;
+    sh_cnt[sub][el] = c;
+    __syncthreads();
+    if (sub == 0 && e < n_experts) {
+      float t = 0.f;
+      uint32_t tc = 0;
+#pragma unroll
+      for (int q = 0; q < kRankShares; ++q) {
+        t += sh_sum[q][el];
+        tc += sh_cnt[q][el];
+      }
+      score[e] = t;
+      active[e] = tc > 0;
+      if (out_scores) out_scores[e] = t;
+    }
+    __syncthreads();
   }
+  uint32_t my_active = 0;
+  for (int e = tid; e < n_experts; e += kRankThreads) my_active += active[e];
   uint32_t n_active;
   (void)block_exclusive_scan<kRankThreads>(my_active, wave_tot, n_active);
   int64_t num_keep = (int64_t)((double)n_active * keep_rate);
   if (num_keep < 1) num_keep = 1;
   if (num_keep > (int64_t)n_active) num_keep = n_active;
-  for (int e = tid; e < n_experts; e += kRankThreads) {
-    uint8_t k = 0;
-    if (active[e]) {
-      const float se = score[e];
-      int64_t rank = 0;
-      for (int o = 0; o < n_experts; ++o)
-        rank += (active[o] && (score[o] > se || (score[o] == se && o < e)));
-      k = rank < num_keep;
+  // Rank of each active expert among the active ones (higher score first,
+  // ties to the lower id): share sub counts the experts o = sub, sub + 8, ...
+  // ahead of e, branch-free, reading 8 of them before using any.
+  for (int e0 = 0; e0 < n_experts; e0 += kRankPass) {
+    const int e = e0 + el;
+    const int ee = e < n_experts ? e : n_experts - 1;
+    const float se = score[ee];
+    uint32_t r = 0;
+    for (int o0 = sub; o0 < n_experts; o0 += kRankShares * 8) {
+      float so[8];
+      uint32_t ao[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int o = o0 + u * kRankShares;
+        const int oo = o < n_experts ? o : 0;
+        so[u] = score[oo];
+        ao[u] = (o < n_experts) ? active[oo] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int o = o0 + u * kRankShares;
+        r += (ao[u] != 0u && (so[u] > se || (so[u] == se && o < e))) ? 1u : 0u;
+      }
     }
-    kept[e] = k;
+    sh_cnt[sub][el] = r;
+    __syncthreads();
+    if (sub == 0 && e < n_experts) {
+      uint32_t rank = 0;
+#pragma unroll
+      for (int q = 0; q < kRankShares; ++q) rank += sh_cnt[q][el];
+      kept[e] = (active[e] && (int64_t)rank < num_keep) ? 1 : 0;
+    }
+    __syncthreads();
   }
-  __syncthreads();
   const int64_t total = n * top_k;
-  for (int64_t i = tid; i < total; i += kRankThreads) {
-    const int64_t e = sel[i];
-    out_mask[i] = (e >= 0 && e < n_experts) ? kept[e] : 0;
+  constexpr int kMaskBatch = 16;  // ids loaded before any is used
+  for (int64_t i0 = tid; i0 < total; i0 += (int64_t)kRankThreads * kMaskBatch) {
+    int64_t ev[kMaskBatch];
+#pragma unroll
+    for (int u = 0; u < kMaskBatch; ++u) {
+      const int64_t i = i0 + (int64_t)u * kRankThreads;
+      ev[u] = sel[i < total ? i : total - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < kMaskBatch; ++u) {
+      const int64_t i = i0 + (int64_t)u * kRankThreads;
+      if (i < total) out_mask[i] = (ev[u] >= 0 && ev[u] < n_experts) ? kept[ev[u]] : 0;
+    }
   }
 }
 

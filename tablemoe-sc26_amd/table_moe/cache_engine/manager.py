@@ -239,6 +239,45 @@ class HybridStorageManager:
                    self.hidden_dim, N.stream(dev))
         return out
 
+    @torch.no_grad()
+    def combine_slots(self, routing_weights, selected_experts, is_vision, compute_mask, computed, off_hit, off_idx,
+                      on_hit=None, on_idx=None, on_slot=None, out=None, residual=None, target: str = "one"):
+        """The slot combine of a prefill/decode batch in one launch
+        (tm_slot_combine), for a hook that calls it instead of filling the
+        [N, k, H] collected buffer (cached_layers.py:302 zero-fill, :441-461
+        scatters, :462-465 renormalise + bmm): out[b] = sum over the surviving
+        slots s of w~[b, s] * source(b, s), source = computed[b, s] where
+        compute_mask, else the online window row (on_idx[b], on_slot[b, s])
+        where on_hit, else the table row values[sel[b, s], m(b), off_idx[b, s]]
+        where off_hit; w~ = the routing weights renormalised over the
+        survivors (target "one": rounded to the model dtype, as the hook's
+        .to(dtype); "orig_sum").  No host sync: the hit indices stay on the
+        device.  residual (optional) is added before the one rounding."""
+        dev = N.require_hip(routing_weights, selected_experts, compute_mask)
+        n, k = selected_experts.shape
+        mode = N.TM_TARGET_ORIG_SUM if target == "orig_sum" else N.TM_TARGET_ONE
+        w = routing_weights.to(torch.float32).contiguous()
+        sel = selected_experts.to(torch.long).contiguous()
+        u8 = lambda t: None if t is None else N.as_u8(t.to(device=dev, dtype=torch.bool).contiguous())  # noqa: E731
+        ix = lambda t: None if t is None else t.to(device=dev, dtype=torch.long).contiguous()  # noqa: E731
+        cm, fh, oh = u8(compute_mask), u8(off_hit), u8(on_hit)
+        isv = None if is_vision is None else u8(is_vision.reshape(-1))
+        fi, oi, osl = ix(off_idx), ix(None if on_idx is None else on_idx.reshape(-1)), ix(on_slot)
+        if computed is not None and (computed.stride(-1) != 1 or computed.dtype != self.dtype):
+            raise ValueError(f"computed must be [N, k, H] {self.dtype} with unit stride along hidden")
+        if out is None:
+            out = torch.empty((n, self.hidden_dim), dtype=self.dtype, device=dev)
+        v = self.values_buffer
+        ov = self.online_values if (oh is not None and self.enable_online) else None
+        N.call("tm_slot_combine", N.dtype_tag(self.dtype), n, k, self.hidden_dim, N.ptr(w), w.stride(0), N.ptr(cm),
+               N.ptr(computed), 0 if computed is None else computed.stride(0),
+               0 if computed is None else computed.stride(1), N.ptr(fh), N.ptr(fi), N.ptr(sel), k, N.ptr(isv),
+               N.ptr(v), v.shape[0], v.shape[2], v.stride(0), v.stride(1), v.stride(2), N.ptr(oh), N.ptr(oi),
+               N.ptr(osl), N.ptr(ov), 0 if ov is None else self.online_size, 1 if ov is None else ov.shape[1],
+               0 if ov is None else ov.stride(0), 0 if ov is None else ov.stride(1), mode, N.ptr(residual),
+               0 if residual is None else residual.stride(0), N.ptr(out), out.stride(0), N.stream(dev))
+        return out
+
     # ---------------------------------------------------------------- gather
     def _gather_into(self, expert_ids, modality_ids, modality, cluster_ids, dst_rows, out):
         dev = out.device

@@ -708,6 +708,7 @@ def _gen_word(table):
     return int(ws[256:260].view(torch.int32).item())
 
 
+
 @pytest.mark.parametrize("cfg,n,nn,variant", [
     (3, 1, 4, "base"), (3, 8, 4, "base"), (3, 32, 4, "base"), (3, 33, 1, "mix"), (3, 64, 4, "mix"),
     (5, 17, 4, "base"), (5, 64, 1, "nores"), (3, 24, 4, "fp16"), (3, 40, 4, "dot"), (3, 32, 4, "small_c"),
