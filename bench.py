@@ -538,10 +538,21 @@ def run_mode_r(replays=20):
     g = graph_of(decode)
     dec_us = statistics.median(replay_times_us(g, replays)) / 64
     del g
+    # the decode step's tail for one token (the slot combine with the online
+    # window, offline table and recomputed slots, then the ring write:
+    # tm_decode_combine_update), after the hybrid search of that token
+    eng.search_decode_hybrid_bs1_into(xs[0], sel[0], wl.is_vision[0], 4, *outs)
+    comp_rows = (torch.randn(k, x.shape[1], device=dev) * 0.05).to(torch.bfloat16)
+    keep_row = torch.zeros(k, dtype=torch.bool, device=dev)
+    keep_row[:4] = True
+    out_row = torch.empty(x.shape[1], dtype=torch.bfloat16, device=dev)
+    step_us = per_call_us(lambda: mgr.combine_and_update_bs1(xs[0], w[0], sel[0], wl.is_vision[0], keep_row,
+                                                             comp_rows, outs[0], outs[1], outs[4], outs[2],
+                                                             outs[3], out_row), 16, replays)
     pairs = int(reuse.sum().item())
     table_bytes = 128 * 2 * 256 * 64 * 2
     log(f"mode R: search_prefill_offline {prefill_us:.1f} us (gated search {gated_us:.1f} us, {pairs} pairs), "
-        f"decode bs1 hybrid {dec_us:.2f} us")
+        f"decode bs1 hybrid {dec_us:.2f} us, decode step combine + ring write {step_us:.2f} us")
     return {
         "workload": "mode R (the reference's per-(expert, modality) tables) at Qwen3-VL-30B-A3B shapes: E=128 x 2 "
                     "modalities x K=256 centroids, d=64, hidden 2048 bf16, N=4096 (3584 vision + 512 text), top-8; "
@@ -552,6 +563,7 @@ def run_mode_r(replays=20):
         "gated_pairs_per_s": pairs / (gated_us * 1e-6),
         "gated_table_GBps": table_bytes / (gated_us * 1e-6) / 1e9,
         "search_decode_hybrid_bs1_us": dec_us,
+        "decode_combine_update_bs1_us": step_us,
     }
 
 

@@ -440,6 +440,50 @@ __global__ __launch_bounds__(kThreads) void gather_combine_kernel(
 // a10+a11 reference-semantics slot combine (cached_layers.py:439-465,
 // deepseek_layers.py:695-729).
 // ---------------------------------------------------------------------------
+// combine_row for at most kSlotSrc sources (16-byte rows): every source load
+// of a chunk is issued before the first is used (the sources past nsrc read
+// the output row itself and are not added), so a token's rows stream in one
+// round trip instead of one per source.
+constexpr int kSlotSrc = 8;
+
+template <int DT>
+__device__ __forceinline__ void combine_row_few(const typename Elem<DT>::T *const *src, const float *coef, int nsrc,
+                                                const typename Elem<DT>::T *residual, typename Elem<DT>::T *dst,
+                                                int hidden) {
+  using T = typename Elem<DT>::T;
+  const T *p[kSlotSrc];
+  float c[kSlotSrc];
+#pragma unroll
+  for (int j = 0; j < kSlotSrc; ++j) {
+    p[j] = j < nsrc ? src[j] : dst;
+    c[j] = j < nsrc ? coef[j] : 0.f;
+  }
+  for (int h0 = threadIdx.x * 8; h0 < hidden; h0 += kThreads * 8) {
+    float acc[8];
+    if (residual) {
+      tm_load8<DT>(residual + h0, acc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+    }
+    uint4 raw[kSlotSrc];
+#pragma unroll
+    for (int j = 0; j < kSlotSrc; ++j) raw[j] = *reinterpret_cast<const uint4 *>(p[j] + h0);
+#pragma unroll
+    for (int j = 0; j < kSlotSrc; ++j) {
+      const T *e = reinterpret_cast<const T *>(&raw[j]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = j < nsrc ? fmaf(c[j], Elem<DT>::to_f(e[i]), acc[i]) : acc[i];
+    }
+    tm_store8<DT>(dst + h0, acc);
+  }
+}
+
+// a10+a11: one workgroup per token.  Lane s < top_k loads slot s's flags,
+// ids and weight (every load issued at once, whatever the flags say); the
+// source of the slot is the table row (off_hit), else the online window row
+// (on_hit), else the recomputed row (compute_mask), else none.  Thread 0
+// then forms the renormalised coefficients in slot order from LDS.
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void slot_combine_kernel(
     int top_k, int hidden, const float *__restrict__ w, int64_t ld_w,
@@ -455,48 +499,63 @@ __global__ __launch_bounds__(kThreads) void slot_combine_kernel(
   using T = typename Elem<DT>::T;
   __shared__ const T *s_src[kMaxSrc];
   __shared__ float s_coef[kMaxSrc];
+  __shared__ const T *s_p[kMaxSrc];
+  __shared__ float s_w[kMaxSrc];
   __shared__ int s_nsrc;
   const int64_t b = blockIdx.x;
-  if (threadIdx.x == 0) {
-    const T *src[kMaxSrc];
-    float wv[kMaxSrc];
-    float kept = 0.f, full = 0.f;
+  const int t = threadIdx.x;
+  if (t < top_k) {
+    const int64_t mi = b * ld_m + t;
+    const uint8_t fh = off_hit ? off_hit[mi] : 0;
+    const uint8_t oh = on_hit ? on_hit[mi] : 0;
+    const uint8_t cm = compute_mask ? compute_mask[mi] : 0;
+    const int64_t e = off_hit ? sel[mi] : -1;
+    const int64_t c = off_hit ? off_idx[mi] : -1;
+    const int64_t r = on_hit ? on_idx[b] : -1;
+    const int64_t jo = on_hit ? on_slot[mi] : -1;
+    const float ws = w[b * ld_w + t];
     const int m = (is_vision == nullptr || is_vision[b]) ? 0 : 1;
+    const T *p = nullptr;
+    if (fh) {
+      if (e >= 0 && e < n_exp && c >= 0 && c < n_cent) p = values + e * vs_e + m * vs_m + c * vs_c;
+    } else if (oh) {
+      if (r >= 0 && r < n_online && jo >= 0 && jo < online_topk) p = online_values + r * ov_w + jo * ov_s;
+    } else if (cm) {
+      p = computed + b * cs_b + t * cs_s;
+    }
+    s_p[t] = p;
+    s_w[t] = ws;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float kept = 0.f, full = 0.f;
     for (int s = 0; s < top_k; ++s) {
-      const int64_t mi = b * ld_m + s;
-      const T *p = nullptr;
-      if (off_hit && off_hit[mi]) {
-        const int64_t e = sel[mi], c = off_idx[mi];
-        if (e >= 0 && e < n_exp && c >= 0 && c < n_cent) p = values + e * vs_e + m * vs_m + c * vs_c;
-      } else if (on_hit && on_hit[mi]) {
-        const int64_t r = on_idx[b], j = on_slot[mi];
-        if (r >= 0 && r < n_online && j >= 0 && j < online_topk) p = online_values + r * ov_w + j * ov_s;
-      } else if (compute_mask && compute_mask[mi]) {
-        p = computed + b * cs_b + s * cs_s;
-      }
-      const float ws = w[b * ld_w + s];
-      full += ws;
-      src[s] = p;
-      wv[s] = ws;
-      if (p) kept += ws;
+      full += s_w[s];
+      if (s_p[s]) kept += s_w[s];
     }
     int ns = 0;
     if (kept > 0.f) {
       for (int s = 0; s < top_k; ++s) {
-        if (!src[s]) continue;
-        float c = wv[s] / kept;
-        if (target_mode == TM_TARGET_ORIG_SUM) c = c * full;
-        else c = tm_round<DT>(c);
-        s_src[ns] = src[s];
-        s_coef[ns] = c;
+        if (!s_p[s]) continue;
+        float cf = s_w[s] / kept;
+        if (target_mode == TM_TARGET_ORIG_SUM) cf = cf * full;
+        else cf = tm_round<DT>(cf);
+        s_src[ns] = s_p[s];
+        s_coef[ns] = cf;
         ++ns;
       }
     }
     s_nsrc = ns;
   }
   __syncthreads();
-  combine_row<DT, VEC>(s_src, s_coef, s_nsrc, residual ? residual + b * ld_r : nullptr, out + b * ld_o,
-                       hidden);
+  const T *res = residual ? residual + b * ld_r : nullptr;
+  if constexpr (VEC) {
+    if (top_k <= kSlotSrc) {  // uniform
+      combine_row_few<DT>(s_src, s_coef, s_nsrc, res, out + b * ld_o, hidden);
+      return;
+    }
+  }
+  combine_row<DT, VEC>(s_src, s_coef, s_nsrc, res, out + b * ld_o, hidden);
 }
 
 // ---------------------------------------------------------------------------
@@ -525,48 +584,60 @@ __global__ __launch_bounds__(kThreads) void slot_combine_update_kernel(
   using T = typename Elem<DT>::T;
   __shared__ const T *s_src[kDecodeSlots];
   __shared__ float s_coef[kDecodeSlots];
-  if (threadIdx.x == 0) {  // the source and coefficient of each slot, as slot_combine_kernel forms them
-    float wv[kDecodeSlots];
-    float kept = 0.f, full = 0.f;
+  __shared__ float s_w[kDecodeSlots];
+  const int t = threadIdx.x;
+  if (t < top_k) {  // lane s: slot s's flags, ids and weight, every load issued at once
+    const uint8_t fh = off_hit ? off_hit[t] : 0;
+    const uint8_t oh = on_hit ? on_hit[t] : 0;
+    const uint8_t cm = compute_mask ? compute_mask[t] : 0;
+    const int64_t e = sel[t];
+    const int64_t c = off_hit ? off_idx[t] : -1;
+    const int64_t rr = on_hit ? on_idx[0] : -1;
+    const int64_t j = on_hit ? on_slot[t] : -1;
+    const float ws = w[t];
     const int m = (is_vision == nullptr || is_vision[0]) ? 0 : 1;
+    const T *p = nullptr;
+    if (fh) {
+      if (e >= 0 && e < n_exp && c >= 0 && c < n_cent) p = values + e * vs_e + m * vs_m + c * vs_c;
+    } else if (oh) {
+      if (rr >= 0 && rr < n_online && j >= 0 && j < online_topk) p = online_values + rr * ov_w + j * ov_s;
+    } else if (cm) {
+      p = computed + t * cs_s;
+    }
+    s_src[t] = p;
+    s_w[t] = ws;
+    ring_ids[r * online_topk + t] = p ? e : -1;
+  }
+  __syncthreads();
+  if (t == 0) {  // the coefficients as slot_combine_kernel forms them (sums in slot order)
+    float kept = 0.f, full = 0.f;
     for (int s = 0; s < top_k; ++s) {
-      const T *p = nullptr;
-      if (off_hit && off_hit[s]) {
-        const int64_t e = sel[s], c = off_idx[s];
-        if (e >= 0 && e < n_exp && c >= 0 && c < n_cent) p = values + e * vs_e + m * vs_m + c * vs_c;
-      } else if (on_hit && on_hit[s]) {
-        const int64_t rr = on_idx[0], j = on_slot[s];
-        if (rr >= 0 && rr < n_online && j >= 0 && j < online_topk) p = online_values + rr * ov_w + j * ov_s;
-      } else if (compute_mask && compute_mask[s]) {
-        p = computed + s * cs_s;
-      }
-      wv[s] = w[s];
-      full += wv[s];
-      s_src[s] = p;
-      if (p) kept += wv[s];
+      full += s_w[s];
+      if (s_src[s]) kept += s_w[s];
     }
     for (int s = 0; s < top_k; ++s) {
       float c = 0.f;
       if (s_src[s] && kept > 0.f) {
-        c = wv[s] / kept;
+        c = s_w[s] / kept;
         c = (target_mode == TM_TARGET_ORIG_SUM) ? c * full : tm_round<DT>(c);
       }
       s_coef[s] = c;
-      ring_ids[r * online_topk + s] = s_src[s] ? sel[s] : -1;
     }
   }
   __syncthreads();
-  for (int h0 = threadIdx.x * 8; h0 < hidden; h0 += kThreads * 8) {
-    float v[kDecodeSlots][8];
+  const T *src[kDecodeSlots];
+  bool use[kDecodeSlots];
+  float cf[kDecodeSlots];
 #pragma unroll
-    for (int s = 0; s < kDecodeSlots; ++s) {
-      if (s < top_k && s_src[s]) {  // uniform
-        tm_load8<DT>(s_src[s] + h0, v[s]);
-      } else {
+  for (int s = 0; s < kDecodeSlots; ++s) {
+    use[s] = s < top_k && s_src[s] != nullptr;
+    src[s] = use[s] ? s_src[s] : x;  // dropped slots read the token's own row and store zeros
+    cf[s] = s < top_k ? s_coef[s] : 0.f;
+  }
+  for (int h0 = t * 8; h0 < hidden; h0 += kThreads * 8) {
+    tm_u32x4 raw[kDecodeSlots];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[s][i] = 0.f;
-      }
-    }
+    for (int s = 0; s < kDecodeSlots; ++s) raw[s] = *reinterpret_cast<const tm_u32x4 *>(src[s] + h0);
     float xin[8], acc[8];
     tm_load8<DT>(x + h0, xin);
     if (residual) {
@@ -575,12 +646,21 @@ __global__ __launch_bounds__(kThreads) void slot_combine_update_kernel(
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] = 0.f;
     }
+    // every source row of the chunk is loaded before any is used (the
+    // compiler would otherwise move a load into the branch of its use)
 #pragma unroll
-    for (int s = 0; s < kDecodeSlots; ++s)
-      if (s < top_k && s_src[s]) {  // sources in slot order, as combine_row adds them
+    for (int s = 0; s < kDecodeSlots; ++s) asm volatile("" : "+v"(raw[s]));
+    float v[kDecodeSlots][8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = fmaf(s_coef[s], v[s][i], acc[i]);
-      }
+    for (int s = 0; s < kDecodeSlots; ++s) {
+      const T *ev = reinterpret_cast<const T *>(&raw[s]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[s][i] = use[s] ? Elem<DT>::to_f(ev[i]) : 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < kDecodeSlots; ++s)  // sources in slot order, as combine_row adds them
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = use[s] ? fmaf(cf[s], v[s][i], acc[i]) : acc[i];
     tm_store8<DT>(out + h0, acc);
     tm_store8<DT>(ring_keys + r * (int64_t)hidden + h0, xin);
 #pragma unroll
