@@ -751,12 +751,27 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
     // of row r at r * CH + (j ^ (r % CH)) (conflict-free fragment reads)
     constexpr int CH = DIM / 8;
     const int rows = two ? 64 : 32;
-    for (int c = tid; c < rows * CH; c += 256) {
+    // every chunk's loads are issued before the first is written (a loop that
+    // loads and writes one chunk per iteration waits a round trip each time);
+    // rows past n read row n - 1
+    constexpr int kQIt = 64 * CH / 256;
+    uint64_t qlo[kQIt], qhi[kQIt];
+#pragma unroll
+    for (int it = 0; it < kQIt; ++it) {
+      const int c = tid + it * 256;
       const int r = c / CH, j = c % CH;
       const int64_t rr = r < n ? r : n - 1;
       const uint64_t *src = reinterpret_cast<const uint64_t *>(q + rr * DIM + j * 8);
-      const uint64_t lo = coh_ld(src), hi = coh_ld(src + 1);
-      q_lds[r * CH + (j ^ (r % CH))] = make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+      qlo[it] = coh_ld(src);
+      qhi[it] = coh_ld(src + 1);
+    }
+#pragma unroll
+    for (int it = 0; it < kQIt; ++it) {
+      const int c = tid + it * 256;
+      const int r = c / CH, j = c % CH;
+      if (c < rows * CH)
+        q_lds[r * CH + (j ^ (r % CH))] = make_uint4((uint32_t)qlo[it], (uint32_t)(qlo[it] >> 32), (uint32_t)qhi[it],
+                                                    (uint32_t)(qhi[it] >> 32));
     }
     __syncthreads();
     auto q_slab = [&](int sl, uint4 (&qf)[KS]) {
@@ -868,16 +883,21 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
 #pragma unroll
   for (int j = 0; j < K; ++j) lst[j] = ~0ull;
   if constexpr (K > 1) {
+    // both halves of the split lists are loaded before either is merged
+    // (unconditional loads of clamped addresses, masked afterwards)
+    uint64_t o[2][K];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      if (m == 1 && a.nsplit <= 64) break;  // uniform
       const int64_t s = lane + 64 * m;
       const uint64_t *src = a.lists + ((s < a.nsplit ? s : a.nsplit - 1) * n + b) * K;
-      uint64_t o[K];
 #pragma unroll
-      for (int j = 0; j < K; ++j) o[j] = s < a.nsplit ? coh_ld(src + j) : ~0ull;
-      merge_min_k<K>(lst, o);
+      for (int j = 0; j < K; ++j) {
+        const uint64_t v = coh_ld(src + j);
+        o[m][j] = s < a.nsplit ? v : ~0ull;
+      }
     }
+    merge_min_k<K>(lst, o[0]);
+    if (a.nsplit > 64) merge_min_k<K>(lst, o[1]);  // uniform
   }
 
   // keep rank of token b among the n tokens' best distances
