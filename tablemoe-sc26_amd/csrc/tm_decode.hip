@@ -386,8 +386,9 @@ __global__ __launch_bounds__(64) void decode_finish_kernel(
 //      workgroup goes on once one wave saw every group's flag.
 //   B  workgroup s < nsplit searches split s (search_stream_kernel's work) and
 //      publishes its lists and best keys; every workgroup then counts itself
-//      on one of kSubCnt sub-counters, the last arrival of each counts on
-//      s_top, and the last of those raises go_b.
+//      on one of kSubCnt sub-counters, the last arrival of each raises that
+//      sub-group's done flag, and a workgroup goes on once one wave saw every
+//      sub-group's flag.
 //   C  wave 3 - t / G of workgroup t % G finishes task t = (token, row
 //      chunk) (decode_finish_kernel's work, the same arithmetic); counting
 //      the waves from the other end keeps the routing these waves do off the
@@ -399,8 +400,9 @@ __global__ __launch_bounds__(64) void decode_finish_kernel(
 // routine, so the same bits) while the projection runs.
 //
 // Flags carry a generation: every wave reads gen at the start, a flag raised
-// in this call holds gen + 1 and the wave that raises go_b advances gen, so
-// no flag is ever cleared; each counter is cleared by the arrival that
+// in this call holds gen + 1 and workgroup 0 advances gen once it saw every
+// sub-group's done flag (every workgroup has read gen by then), so no flag is
+// ever cleared; each counter is cleared by the arrival that
 // completes it.  Data handed between workgroups moves through agent-scope
 // atomic loads and stores, which the hardware performs at one point of
 // coherence per address for every XCD (the loads bypass the non-coherent
@@ -417,18 +419,18 @@ __global__ __launch_bounds__(64) void decode_finish_kernel(
 // of hanging.
 // ---------------------------------------------------------------------------
 constexpr int kFusedWGs = 128;
-constexpr int kGoRep = 16;     // copies of each go flag (the pollers spread over them)
 constexpr int kSubCnt = 8;     // sub-counters of the search arrival
+constexpr int kSubRep = 2;     // copies of each sub-group's done flag (the pollers spread over them)
 constexpr int kLine = 32;      // words per 128-byte line: each hot word on a line of its own
 constexpr uint64_t kSpinTicks = 2000000;  // 20 ms
 static_assert(kFusedWGs % kSubCnt == 0, "whole sub-counter groups");
+static_assert(kSubCnt <= 64, "one polling lane per sub-group");
 // word offsets in the layer workspace's sync region (words 0 .. 63 belong to
 // the other plans' counters)
 constexpr int kWGen = 64;
-constexpr int kWStop = kWGen + kLine;
-constexpr int kWSsub = kWStop + kLine;
-constexpr int kWGoB = kWSsub + kSubCnt * kLine;
-constexpr int kWErr = kWGoB + kGoRep * kLine;
+constexpr int kWSsub = kWGen + 2 * kLine;                  // (one spare line after the generation)
+constexpr int kWDone = kWSsub + kSubCnt * kLine;           // the sub-groups' done flags, one line each
+constexpr int kWErr = kWDone + kSubCnt * kSubRep * kLine;
 constexpr int kMaxGroups = 64 / 16 * 128 / 16;  // (64 rows / 16) x (d 128 / 16)
 constexpr int kWGrp = kWErr + kLine;                   // the projection groups' counters, one line each
 constexpr int kWFlagA = kWGrp + kMaxGroups * kLine;    // the projection groups' q-ready flags, one line each
@@ -470,16 +472,6 @@ __device__ __forceinline__ void coh_st32(uint32_t *p, uint32_t v) {
 }
 __device__ __forceinline__ uint32_t coh_add(uint32_t *p) {
   return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Poll one flag until it holds `want`; false when kSpinTicks passed first.
-__device__ __forceinline__ bool wait_flag(const uint32_t *f, uint32_t want) {
-  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want) {
-    if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) return false;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  return true;
 }
 
 // Phase A of decode_fused_kernel: project_split_kernel's wave (hidden ==
@@ -850,18 +842,30 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   __syncthreads();
   if (tid == 0) {
     const uint32_t t = coh_add(sync + kWSsub + (wg % kSubCnt) * kLine);
-    if (t == (uint32_t)(G / kSubCnt - 1)) {
+    if (t == (uint32_t)(G / kSubCnt - 1)) {  // the sub-group's last arrival raises its done flags
       coh_st32(sync + kWSsub + (wg % kSubCnt) * kLine, 0u);
-      const uint32_t u = coh_add(sync + kWStop);
-      if (u == kSubCnt - 1) {  // every workgroup arrived
-        coh_st32(sync + kWStop, 0u);
-        for (int i = 0; i < kGoRep; ++i) coh_st32(sync + kWGoB + i * kLine, g0() + 1);
-        coh_st32(sync + kWGen, g0() + 1);
-      }
+      for (int r = 0; r < kSubRep; ++r) coh_st32(sync + kWDone + ((wg % kSubCnt) * kSubRep + r) * kLine, g0() + 1);
     }
-    const bool ok = wait_flag(sync + kWGoB + (wg % kGoRep) * kLine, g0() + 1);
-    if (!ok) coh_add(sync + kWErr);
-    s_ok = ok ? 1u : 0u;
+  }
+  if (wave == 0) {  // lane i polls sub-group i's done flag (replica wg % kSubRep)
+    const uint32_t *f = sync + kWDone + ((lane % kSubCnt) * kSubRep + wg % kSubRep) * kLine;
+    const uint32_t want = g0() + 1;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    bool ok = true;
+    for (;;) {
+      uint32_t v = want;
+      if (lane < kSubCnt) v = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__ballot(v != want) == 0) break;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) { ok = false; break; }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) {
+      if (!ok) coh_add(sync + kWErr);
+      // every workgroup arrived: workgroup 0 advances the generation (the
+      // next call's flags want gen + 2; no wave of this call reads gen again)
+      if (ok && wg == 0) coh_st32(sync + kWGen, g0() + 1);
+      s_ok = ok ? 1u : 0u;
+    }
   }
   __syncthreads();
   poison = poison || s_ok == 0u;
