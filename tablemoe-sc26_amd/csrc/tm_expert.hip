@@ -329,7 +329,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(
 // by expert.  mask[b * ms_b + s * ms_s] != 0 selects a pair (ms_s = 0: a
 // per-token flag); ids outside [0, n_experts) are skipped.
 constexpr int kGroupThreads = 1024;
-constexpr int kMaxExperts = 1024;
+constexpr int kMaxExperts = 1024;  // one scanning thread per expert
+static_assert(kMaxExperts <= kGroupThreads, "one expert per thread");
 constexpr int kGroupTok = 4;    // tokens per thread on the register path (n <= 4096)
 constexpr int kGroupSlots = 8;  // slots per token on the register path (top_k <= 8)
 static_assert(kGroupTok * kGroupThreads * 8 <= 65536, "a placed row (token << 3 | slot) fits 16 bits");
@@ -346,10 +347,13 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
   // order they are a few coalesced passes)
   __shared__ uint16_t placed[kGroupTok * kGroupThreads * kGroupSlots];
   __shared__ int32_t s_rows;
+  __shared__ int32_t wave_rows[kGroupThreads / 64], wave_tiles[kGroupThreads / 64];
   const int tid = threadIdx.x;
   for (int e = tid; e < n_experts; e += kGroupThreads) hist[e] = 0;
   // Each thread keeps the experts of its tokens (b = tid + 1024 j, j < kGroupTok)
   // in registers: all of their loads are issued before the first count.
+  // (Reading the id array as consecutive elements per wave load instead
+  // measured slower: 16.4 / 24.9 us against 15.2 / 21.7 us hot / cold.)
   int32_t ex[kGroupTok][kGroupSlots];
   // n == 0 takes the loop path, whose loops run no iteration: the register
   // path clamps to token n - 1 and would read below `ids` and `mask`.
@@ -383,20 +387,45 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
       }
   }
   __syncthreads();
-  if (tid == 0) {  // offsets and tile bases (n_experts <= 1024: a short serial scan)
-    int32_t run = 0, tr = 0;
-    for (int e = 0; e < n_experts; ++e) {
-      offsets[e] = run;
-      cursor[e] = run;
-      tile_base[e] = tr;
-      run += hist[e];
-      tr += (hist[e] + BM - 1) / BM;
+  {
+    // offsets and tile bases: exclusive scans over the experts, thread e
+    // owning expert e (n_experts <= kGroupThreads): wave scans, then the
+    // waves' totals in wave order (a serial loop over the experts cost ~4 us)
+    const int lane = tid & 63, wave = tid >> 6;
+    const int32_t h = tid < n_experts ? hist[tid] : 0;
+    const int32_t tc = (h + BM - 1) / BM;
+    int32_t ih = h, it = tc;  // inclusive within the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int32_t oh = __shfl_up(ih, d, 64), ot = __shfl_up(it, d, 64);
+      if (lane >= d) {
+        ih += oh;
+        it += ot;
+      }
     }
-    offsets[n_experts] = run;
-    tile_base[n_experts] = tr;
-    tiles[0] = run;
-    tiles[1] = tr;
-    s_rows = run;
+    if (lane == 63) {
+      wave_rows[wave] = ih;
+      wave_tiles[wave] = it;
+    }
+    __syncthreads();
+    int32_t bh = 0, bt = 0;
+    for (int w = 0; w < wave; ++w) {
+      bh += wave_rows[w];
+      bt += wave_tiles[w];
+    }
+    const int32_t eh = bh + ih - h, et = bt + it - tc;  // exclusive
+    if (tid < n_experts) {
+      offsets[tid] = eh;
+      cursor[tid] = eh;
+      tile_base[tid] = et;
+    }
+    if (tid == n_experts - 1) {
+      offsets[n_experts] = eh + h;
+      tile_base[n_experts] = et + tc;
+      tiles[0] = eh + h;
+      tiles[1] = et + tc;
+      s_rows = eh + h;
+    }
   }
   __syncthreads();
   for (int e = tid; e < n_experts; e += kGroupThreads) {
