@@ -34,7 +34,7 @@ __attribute__((visibility("hidden"))) int tm_internal_search_route(
 __attribute__((visibility("hidden"))) bool tm_internal_project_cols_ok(
     int32_t dtype, const void *x, int64_t n, int32_t hidden, int64_t ld_x, const void *pv, const void *bv,
     const void *pt, const void *bt, int64_t ps_h, int64_t ps_d, int32_t dim, const void *q, int64_t ld_q);
-__attribute__((visibility("hidden"))) size_t tm_internal_project_cols_parts(int32_t dim);
+__attribute__((visibility("hidden"))) size_t tm_internal_project_cols_parts(int32_t dim, int64_t n, int32_t hidden);
 __attribute__((visibility("hidden"))) int tm_internal_project_cols(
     int32_t dtype, const void *x, int64_t n, int32_t hidden, int64_t ld_x, const uint8_t *is_vision,
     const void *pv, const void *bv, const void *pt, const void *bt, int64_t ps_h, int64_t ps_d, int32_t dim,

@@ -120,7 +120,7 @@ int fused_top1_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLa
                                      qn_part, keys, route_fused ? &ra : nullptr, s)) != TM_OK)
     return st;
   if ((st = record(ev, 2, s)) != TM_OK) return st;
-  const int32_t parts = (int32_t)tm_internal_project_cols_parts(t->dim);
+  const int32_t parts = (int32_t)tm_internal_project_cols_parts(t->dim, n, t->hidden);
   if (ranked) {  // the search decodes the keys; the keep set is ranked in the combine
     if ((st = tm_internal_search_decode(t->dtype, io->q, n, t->dim, t->cents, t->n_cent, t->ld_c, t->c_sqnorm,
                                         t->dim, t->metric, keys, qn_part, parts, io->dist, io->idx, io->q_sqnorm,

@@ -540,7 +540,15 @@ __global__ __launch_bounds__(256, 2) void project_cols_kernel(
 // chunk, so two workgroups fit a CU (router workgroups of the same launch
 // included).  Tiles that mix modalities run the pipeline once per modality
 // (the second pass streams x again) and keep each row's own result.
-template <int DT, int DIM, int RVPL, int NCH>
+//
+// CB: 16-column blocks per workgroup.  4 (64 columns, two groups at d = 128)
+// keeps a CU's bytes smallest once the grid fills the chip; 2 (32 columns,
+// four groups) doubles the workgroups for batches whose 64-column grid
+// leaves half the CUs idle (a workgroup then streams 256 KiB instead of
+// 384 KiB).  The groups' partial |q|^2 are subtrees of the direct kernel's
+// lane tree either way (8 or 4 lanes of 8 columns), so qn_sum adds them to
+// the same bits.
+template <int DT, int DIM, int RVPL, int NCH, int CB>
 __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
     const typename Elem<DT>::T *__restrict__ x, int64_t n, int hidden, int64_t ld_x,
     const uint8_t *__restrict__ is_vision, const typename Elem<DT>::T *__restrict__ pv,
@@ -548,11 +556,12 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
     const typename Elem<DT>::T *__restrict__ bt, typename Elem<DT>::T *__restrict__ q, int64_t ld_q,
     float *__restrict__ qn_part, uint64_t *__restrict__ keys, int64_t n_tiles, ColsRoute cr) {
   using T = typename Elem<DT>::T;
-  constexpr int G = ColsCfg<DIM>::G;
+  constexpr int G = DIM / (16 * CB);  // column groups
   constexpr int NCB = ColsCfg<DIM>::NCB;
   static_assert(NCH >= 1 && NCH <= 8, "chunks per wave");
   constexpr int kRowPad = 64 + 4;
-  static_assert(DIM == 128, "4 column blocks of 1 KiB per k-step and wave");
+  static_assert(DIM == 128 && (CB == 4 || CB == 2), "CB column blocks of 1 KiB per k-step and wave");
+  constexpr int TPRW = 2 * CB;  // epilogue threads per row (8 columns each)
   // per wave: 2 ring slots of 32 rows x 16 x 16 bytes; the wave partials
   // (32 x kRowPad floats) reuse the wave's own slots after its last chunk
   __shared__ uint4 ring[4][2 * 512];
@@ -610,31 +619,39 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
   const uint32_t vis_bits = (uint32_t)(__ballot(amod == 0) & 0xFFFFFFFFull);  // bit r: tile row r uses P_vis
   const uint32_t txt_bits = (uint32_t)(__ballot(amod == 1) & 0xFFFFFFFFull);
 
-  const int erow = tid >> 3;
-  const int part = tid & 7;
-  const int col = 64 * g + 8 * part;
+  const int erow = tid / TPRW;  // rows past 31 (CB = 2: threads 128 ..) only load
+  const int part = tid % TPRW;
+  const int col = 16 * CB * g + 8 * part;
   const uint4 braw_v = *reinterpret_cast<const uint4 *>(bv + col);
   const uint4 braw_t = *reinterpret_cast<const uint4 *>(bt + col);
 
-  tm_u32x4 pb[2][4][4];  // P of two chunks: [c & 1][k-step][column block]
-  tm_f32x4 fin[2][4];    // each row's result from the pass of its modality
+  tm_u32x4 pb[2][4][CB];  // P of two chunks: [c & 1][k-step][column block]
+  tm_f32x4 fin[2][CB];    // each row's result from the pass of its modality
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) fin[rb][c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < CB; ++c) fin[rb][c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto run_pass = [&](const T *P, uint32_t rows_of_pass, bool first) {
-    const uint4 *pf = reinterpret_cast<const uint4 *>(P) + (int64_t)(4 * g) * 64 + lane;
+    const uint4 *pf = reinterpret_cast<const uint4 *>(P) + (int64_t)(CB * g) * 64 + lane;
     auto issue_p = [&](int c, int t) {  // k-step t of chunk c
       const uint4 *src = pf + (int64_t)(ks_begin + 4 * c + t) * NCB * 64;
-      asm volatile(
-          "global_load_dwordx4 %0, %4, off\n\t"
-          "global_load_dwordx4 %1, %4, off offset:1024\n\t"
-          "global_load_dwordx4 %2, %4, off offset:2048\n\t"
-          "global_load_dwordx4 %3, %4, off offset:3072"
-          : "=&v"(pb[c & 1][t][0]), "=&v"(pb[c & 1][t][1]), "=&v"(pb[c & 1][t][2]), "=&v"(pb[c & 1][t][3])
-          : "v"(src)
-          : "memory");
+      if constexpr (CB == 4)
+        asm volatile(
+            "global_load_dwordx4 %0, %4, off\n\t"
+            "global_load_dwordx4 %1, %4, off offset:1024\n\t"
+            "global_load_dwordx4 %2, %4, off offset:2048\n\t"
+            "global_load_dwordx4 %3, %4, off offset:3072"
+            : "=&v"(pb[c & 1][t][0]), "=&v"(pb[c & 1][t][1]), "=&v"(pb[c & 1][t][2]), "=&v"(pb[c & 1][t][3])
+            : "v"(src)
+            : "memory");
+      else
+        asm volatile(
+            "global_load_dwordx4 %0, %2, off\n\t"
+            "global_load_dwordx4 %1, %2, off offset:1024"
+            : "=&v"(pb[c & 1][t][0]), "=&v"(pb[c & 1][t][1])
+            : "v"(src)
+            : "memory");
     };
     if (!first) {  // the first pass's x chunks were issued before the modality wait
       issue_x(0);
@@ -646,34 +663,36 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t) issue_p(1, t);
     }
-    tm_f32x4 acc[2][4];
+    tm_f32x4 acc[2][CB];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) acc[rb][c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < CB; ++c) acc[rb][c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       // x(c) and P(c) are in once only the loads issued after both remain:
       // P(1) for chunk 0 (x(1) precedes P(0)); for chunk c >= 1 the P and x of
-      // chunk c + 1, issued while chunk c - 1 was multiplied
-      constexpr int kAfter0 = NCH > 1 ? 16 : 0;
+      // chunk c + 1, issued while chunk c - 1 was multiplied (4 k-steps of CB
+      // P loads, 8 x loads a chunk)
+      constexpr int kAfter0 = NCH > 1 ? 4 * CB : 0;
+      constexpr int kAfterMid = 4 * CB + 8;
       if (c == 0)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfter0) : "memory");
       else if (c + 1 < NCH)
-        asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterMid) : "memory");
       else
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(pb[c & 1][t][u]));
+        for (int u = 0; u < CB; ++u) asm volatile("" : "+v"(pb[c & 1][t][u]));
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
           const uint4 a = read_a(c, rb, t);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
+          for (int u = 0; u < CB; ++u) {
             const tm_u32x4 &bb = pb[c & 1][t][u];
             acc[rb][u] = tm_mfma16x16x32<DT>(a, make_uint4(bb.x, bb.y, bb.z, bb.w), acc[rb][u]);
           }
@@ -693,7 +712,7 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
       for (int i = 0; i < 4; ++i) {
         const bool mine = (rows_of_pass >> (16 * rb + 4 * (lane >> 4) + i)) & 1u;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) fin[rb][u][i] = mine ? acc[rb][u][i] : fin[rb][u][i];
+        for (int u = 0; u < CB; ++u) fin[rb][u][i] = mine ? acc[rb][u][i] : fin[rb][u][i];
       }
   };
   if (vis_bits) run_pass(pv, vis_bits, true);  // uniform branches
@@ -708,9 +727,10 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + 4 * (lane >> 4) + i;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) *red_at(wave, r, 16 * u + (lane & 15)) = fin[rb][u][i];
+      for (int u = 0; u < CB; ++u) *red_at(wave, r, 16 * u + (lane & 15)) = fin[rb][u][i];
     }
   __syncthreads();
+  if (erow >= 32) return;  // CB = 2: waves 2 and 3 have no row (no barrier follows)
 
   const int64_t gr = row0 + erow;
   const bool ok = gr < n;
@@ -732,9 +752,8 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
-  ss += __shfl_xor(ss, 1, 64);
-  ss += __shfl_xor(ss, 2, 64);
-  ss += __shfl_xor(ss, 4, 64);
+#pragma unroll
+  for (int o = 1; o < TPRW; o <<= 1) ss += __shfl_xor(ss, o, 64);
   if (ok) {
     tm_store8<DT>(q + gr * ld_q + col, v);
     if (part == 0) qn_part[(int64_t)g * n + gr] = ss;
@@ -1348,7 +1367,8 @@ void launch_cols(const void *x, int64_t n, int hidden, int64_t ld_x, const uint8
   using T = typename Elem<DT>::T;
   const int64_t n_tiles = tm_cdiv(n, 32);
   ColsRoute cr{};
-  int64_t blocks = tm_cdiv(n_tiles, 8) * 8 * ColsCfg<DIM>::G;
+  const int64_t groups = (int64_t)tm_internal_project_cols_parts(DIM, n, hidden);
+  int64_t blocks = tm_cdiv(n_tiles, 8) * 8 * groups;
   if (RVPL > 0) {
     cr.a = *ra;
     cr.first = blocks;
@@ -1357,7 +1377,11 @@ void launch_cols(const void *x, int64_t n, int hidden, int64_t ld_x, const uint8
   if constexpr (DIM == 128) {
     // hidden 2048 or 2560: every wave's slice is 4 or 5 whole chunks, the pipelined kernel
     if (hidden == 2048 || hidden == 2560) {
-      auto kern = hidden == 2048 ? project_cols_pipe_kernel<DT, DIM, RVPL, 4> : project_cols_pipe_kernel<DT, DIM, RVPL, 5>;
+      const bool narrow = groups == 4;  // 32-column groups
+      auto kern = hidden == 2048 ? (narrow ? project_cols_pipe_kernel<DT, DIM, RVPL, 4, 2>
+                                           : project_cols_pipe_kernel<DT, DIM, RVPL, 4, 4>)
+                                 : (narrow ? project_cols_pipe_kernel<DT, DIM, RVPL, 5, 2>
+                                           : project_cols_pipe_kernel<DT, DIM, RVPL, 5, 4>);
       hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, static_cast<const T *>(x), n, hidden,
                          ld_x, is_vision, static_cast<const T *>(pv), static_cast<const T *>(bv),
                          static_cast<const T *>(pt ? pt : pv), static_cast<const T *>(pt ? bt : bv),
@@ -1396,7 +1420,15 @@ bool tm_internal_project_cols_ok(int32_t dtype, const void *x, int64_t n, int32_
          (bt == nullptr || tm_aligned16(bt)) && tm_aligned16(q) && (ld_q * 2) % 16 == 0;
 }
 
-size_t tm_internal_project_cols_parts(int32_t dim) { return dim >= 64 ? (size_t)dim / 64 : 0; }
+// Column groups of the column-split projection, which is also the number of
+// partial |q|^2 per row: 64-column groups, or 32-column groups at d = 128 on
+// the pipelined kernel's hidden sizes when the 64-column grid would keep at
+// most half of the 256 CUs busy (n <= 2048).
+size_t tm_internal_project_cols_parts(int32_t dim, int64_t n, int32_t hidden) {
+  if (dim < 64) return 0;
+  const bool narrow = dim == 128 && (hidden == 2048 || hidden == 2560) && tm_cdiv(n, 32) * 2 <= 128;
+  return narrow ? 4 : (size_t)dim / 64;
+}
 
 int tm_internal_project_cols(int32_t dtype, const void *x, int64_t n, int32_t hidden, int64_t ld_x,
                              const uint8_t *is_vision, const void *pv, const void *bv, const void *pt,
