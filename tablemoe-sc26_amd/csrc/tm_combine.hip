@@ -366,14 +366,25 @@ __global__ __launch_bounds__(TPB * kThreads, 8) void gather_combine_rank_kernel(
 #pragma unroll
       for (int s = 0; s < TK; ++s) coef[s] = coef[s] / sum;
       const T *src = slot_out + b * so_b + h0;
-      tm_u32x4 raw[TK];  // 16-bit values until used: 4 registers per slot instead of 8
+      if constexpr (sizeof(T) == 2) {
+        tm_u32x4 raw[TK];  // 16-bit values until used: 4 registers per slot instead of 8
 #pragma unroll
-      for (int s = 0; s < TK; ++s) raw[s] = __builtin_nontemporal_load(reinterpret_cast<const tm_u32x4 *>(src + (int64_t)s * so_s));
+        for (int s = 0; s < TK; ++s)
+          raw[s] = __builtin_nontemporal_load(reinterpret_cast<const tm_u32x4 *>(src + (int64_t)s * so_s));
 #pragma unroll
-      for (int s = 0; s < TK; ++s) {
-        const T *e = reinterpret_cast<const T *>(&raw[s]);
+        for (int s = 0; s < TK; ++s) {
+          const T *e = reinterpret_cast<const T *>(&raw[s]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], Elem<DT>::to_f(e[i]), acc[i]);
+          for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], Elem<DT>::to_f(e[i]), acc[i]);
+        }
+      } else {  // fp32 rows: every slot's 8 values requested before the first is used
+        float sv[TK][8];
+#pragma unroll
+        for (int s = 0; s < TK; ++s) tm_load8_nt<DT>(src + (int64_t)s * so_s, sv[s]);
+#pragma unroll
+        for (int s = 0; s < TK; ++s)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], sv[s][i], acc[i]);
       }
     }
   } else {
@@ -834,11 +845,12 @@ extern "C" int tm_gather_combine_ranked(int32_t dtype, int64_t n_tokens, int32_t
 bool tm_internal_combine_rank_ok(int32_t dtype, int32_t hidden, const void *slot_out, int64_t so_b, int64_t so_s,
                                  int32_t top_k, const void *values, int64_t ld_v, const float *dist,
                                  const void *residual, int64_t ld_r, const void *out, int64_t ld_o) {
-  if (!(dtype == TM_DT_BF16 || dtype == TM_DT_F16) || !(top_k == 6 || top_k == 8) || hidden <= 0 ||
-      hidden > kThreads * 8)
+  if (!(dtype == TM_DT_BF16 || dtype == TM_DT_F16 || dtype == TM_DT_F32) || !(top_k == 6 || top_k == 8) ||
+      hidden <= 0 || hidden > kThreads * 8)
     return false;
-  return hidden % 8 == 0 && tm_aligned16(slot_out) && (so_b * 2) % 16 == 0 && (so_s * 2) % 16 == 0 &&
-         rows_aligned(values, ld_v, 2) && rows_aligned(residual, ld_r, 2) && rows_aligned(out, ld_o, 2) &&
+  const int E = dtype == TM_DT_F32 ? 4 : 2;
+  return hidden % 8 == 0 && tm_aligned16(slot_out) && (so_b * E) % 16 == 0 && (so_s * E) % 16 == 0 &&
+         rows_aligned(values, ld_v, E) && rows_aligned(residual, ld_r, E) && rows_aligned(out, ld_o, E) &&
          ld_o >= hidden && ld_v >= hidden && dist != nullptr && tm_aligned16(dist);
 }
 
@@ -865,12 +877,15 @@ int tm_internal_combine_rank(int32_t dtype, int64_t n_tokens, int32_t hidden, co
   };
   using BF = std::integral_constant<int, TM_DT_BF16>;
   using HF = std::integral_constant<int, TM_DT_F16>;
+  using F32 = std::integral_constant<int, TM_DT_F32>;
   using K8 = std::integral_constant<int, 8>;
   using K6 = std::integral_constant<int, 6>;
   if (dtype == TM_DT_BF16)
     top_k == 8 ? launch(BF{}, K8{}) : launch(BF{}, K6{});
-  else
+  else if (dtype == TM_DT_F16)
     top_k == 8 ? launch(HF{}, K8{}) : launch(HF{}, K6{});
+  else
+    top_k == 8 ? launch(F32{}, K8{}) : launch(F32{}, K6{});
   TM_LAUNCH_CHECK("tm_table_forward(combine)");
   return TM_OK;
 }

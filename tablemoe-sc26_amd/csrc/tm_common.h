@@ -105,27 +105,39 @@ __device__ __forceinline__ void tm_store8(typename Elem<DT>::T *p, const float (
   }
 }
 
-// Streaming variants for 2-byte types: non-temporal 16-byte accesses for data
-// read or written once (kept out of the caches' working set).
+// Streaming variants: non-temporal 16-byte accesses for data read or
+// written once (kept out of the caches' working set); fp32 moves 8 elements
+// as two of them.
 typedef unsigned int tm_u32x4 __attribute__((ext_vector_type(4)));
+typedef float tm_f32x4_nt __attribute__((ext_vector_type(4)));
 
 template <int DT>
 __device__ __forceinline__ void tm_load8_nt(const typename Elem<DT>::T *p, float (&v)[8]) {
-  static_assert(Elem<DT>::kBytes == 2, "2-byte types only");
-  const tm_u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const tm_u32x4 *>(p));
-  const typename Elem<DT>::T *e = reinterpret_cast<const typename Elem<DT>::T *>(&r);
+  if constexpr (Elem<DT>::kBytes == 2) {
+    const tm_u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const tm_u32x4 *>(p));
+    const typename Elem<DT>::T *e = reinterpret_cast<const typename Elem<DT>::T *>(&r);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = Elem<DT>::to_f(e[i]);
+    for (int i = 0; i < 8; ++i) v[i] = Elem<DT>::to_f(e[i]);
+  } else {
+    const tm_f32x4_nt a = __builtin_nontemporal_load(reinterpret_cast<const tm_f32x4_nt *>(p));
+    const tm_f32x4_nt b = __builtin_nontemporal_load(reinterpret_cast<const tm_f32x4_nt *>(p + 4));
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
 }
 
 template <int DT>
 __device__ __forceinline__ void tm_store8_nt(typename Elem<DT>::T *p, const float (&v)[8]) {
-  static_assert(Elem<DT>::kBytes == 2, "2-byte types only");
-  tm_u32x4 r;
-  typename Elem<DT>::T *e = reinterpret_cast<typename Elem<DT>::T *>(&r);
+  if constexpr (Elem<DT>::kBytes == 2) {
+    tm_u32x4 r;
+    typename Elem<DT>::T *e = reinterpret_cast<typename Elem<DT>::T *>(&r);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) e[i] = Elem<DT>::from_f(v[i]);
-  __builtin_nontemporal_store(r, reinterpret_cast<tm_u32x4 *>(p));
+    for (int i = 0; i < 8; ++i) e[i] = Elem<DT>::from_f(v[i]);
+    __builtin_nontemporal_store(r, reinterpret_cast<tm_u32x4 *>(p));
+  } else {
+    __builtin_nontemporal_store(tm_f32x4_nt{v[0], v[1], v[2], v[3]}, reinterpret_cast<tm_f32x4_nt *>(p));
+    __builtin_nontemporal_store(tm_f32x4_nt{v[4], v[5], v[6], v[7]}, reinterpret_cast<tm_f32x4_nt *>(p + 4));
+  }
 }
 
 // True when a pointer is aligned for tm_load8/tm_store8 of this type.

@@ -83,6 +83,16 @@ bool ranked_ok(const tm_table_layer *t, const tm_layer_io *io) {
                                      t->values, t->ld_v, io->dist, io->residual, io->ld_r, io->out, io->ld_o);
 }
 
+// The general plan's ranked form: a top-1 layer of at most 4096 tokens skips
+// the keep-select launch and ranks the keep set in the combine (its
+// search writes the distances the combine reads).
+bool general_ranked_ok(const tm_table_layer *t, const tm_layer_io *io) {
+  const int64_t n = io->n_tokens;
+  return io->n_nearest == 1 && n > 0 && n <= 4096 &&
+         tm_internal_combine_rank_ok(t->dtype, t->hidden, io->slot_out, io->so_b, io->so_s, io->router_top_k,
+                                     t->values, t->ld_v, io->dist, io->residual, io->ld_r, io->out, io->ld_o);
+}
+
 bool fused_top1_ok(const tm_table_layer *t, const tm_layer_io *io) {
   const int64_t n = io->n_tokens;
   return io->n_nearest == 1 &&
@@ -157,9 +167,11 @@ int decode_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout
 }
 
 // Stages 0-4 of the general plan: the exported entry points; the router rides
-// in the search's split-merge launch when it can.
+// in the search's split-merge launch when it can.  Ranked: no keep-select
+// launch (events 3 and 4 coincide; the combine ranks the keep set).
 int general_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayout &w, char *ws,
-                   const tm_route_args &ra, bool route_fused, int64_t n_keep, void *const *ev, hipStream_t s) {
+                   const tm_route_args &ra, bool route_fused, bool ranked, int64_t n_keep, void *const *ev,
+                   hipStream_t s) {
   const int64_t n = io->n_tokens;
   int st;
   if ((st = record(ev, 0, s)) != TM_OK) return st;
@@ -181,7 +193,7 @@ int general_stages(const tm_table_layer *t, const tm_layer_io *io, const WsLayou
     st = tm_search_global(t->dtype, io->q, n, t->dim, io->q_sqnorm, t->cents, t->n_cent, t->ld_c, t->c_sqnorm,
                           t->dim, io->n_nearest, t->metric, io->dist, io->idx, p.search, w.search, s);
   if (st != TM_OK) return st;
-  if ((st = record(ev, 3, s)) != TM_OK) return st;
+  if ((st = record(ev, 3, s)) != TM_OK || ranked) return st;
   return tm_keep_select(io->dist, n, io->n_nearest, n_keep, io->keep, w.keep ? p.keep : nullptr, w.keep, s);
 }
 
@@ -275,9 +287,10 @@ int table_forward(const tm_table_layer *t, const tm_layer_io *io, void *workspac
     return record(stage_events, 5, s);
   }
   const bool fused = fused_top1_ok(t, io);
-  const bool ranked = combine && fused && ranked_ok(t, io);  // the ranked plan decides the keep set in the combine
+  // ranked plans decide the keep set in the combine
+  const bool ranked = combine && (fused ? ranked_ok(t, io) : general_ranked_ok(t, io));
   st = fused ? fused_top1_stages(t, io, w, ws, ra, route_fused, ranked, n_keep, stage_events, s)
-             : general_stages(t, io, w, ws, ra, route_fused, n_keep, stage_events, s);
+             : general_stages(t, io, w, ws, ra, route_fused, ranked, n_keep, stage_events, s);
   if (st != TM_OK) return st;
   if ((st = record(stage_events, 4, s)) != TM_OK) return st;
   if (!combine) return record(stage_events, 5, s);
