@@ -548,6 +548,11 @@ def test_layer_forward_one_call_matches_staged(hip_device):
     # boundary), d = 64, a ragged last query tile and centroid range
     (4096, 2048, 128, True, 8192, False), (4096, 2048, 128, False, 8192, True), (4096, 1000, 64, False, 16384, False),
     (4000, 2080, 128, True, 12000, False),
+    # either side of the projection's switch to 32-column groups (n <= 2048):
+    # 32-column groups at hidden 2560 with tied tokens (one modality, so a
+    # repeated token's distance equals its original's), 64-column groups from
+    # n = 2049 (a ragged last row tile, mixed tiles)
+    (2048, 2560, 128, False, 4096, True), (2049, 2048, 128, True, 4096, False),
     # above the ranked form's token limit: keep select launch
     (8192, 1024, 128, False, 8192, False)])
 def test_layer_forward_fused_shapes_match_staged(hip_device, n, hidden, dim, mix, n_cent, dup):
@@ -594,6 +599,42 @@ def test_layer_forward_fused_shapes_match_staged(hip_device, n, hidden, dim, mix
         keep = ra["keep"].bool()
         kept_d = dist[keep]
         assert (dist[~keep] <= kept_d.min()).all()
+
+
+@pytest.mark.parametrize("dtype,n", [(torch.bfloat16, 1000), (torch.float16, 4096), (torch.bfloat16, 4096)])
+def test_layer_forward_general_ranked_matches_staged(hip_device, dtype, n):
+    """A projection bias that does not start on a 16-byte boundary keeps the
+    table's P in the strided layout (no packed copy), so a top-1 layer takes
+    the general plan (tm_project, the split search and its merge); for up to
+    4096 tokens the combine ranks the keep set itself (no keep-select
+    launch).  The result must equal the stage calls bit for bit, on two calls
+    in a row."""
+    from table_moe.cache_engine import GlobalTable
+    from synth import make_workload
+
+    dev = hip_device
+    wl = make_workload(2, n=n, dim=64, n_cent=2048, dtype=dtype)
+    d = wl.to(dev)
+    g = torch.Generator().manual_seed(n)
+    is_vision = (torch.rand(n, generator=g) < 0.5).to(dev)
+
+    def unaligned(b):  # the same values, 2 bytes past a 16-byte boundary
+        t = torch.empty(b.numel() + 1, dtype=b.dtype, device=dev)[1:]
+        t.copy_(b)
+        assert t.data_ptr() % 16 != 0
+        return t
+
+    bv, bt = unaligned(d.bias_vis), unaligned(d.bias_txt)
+    a = GlobalTable(d.centroids, d.values, (d.proj_vis, bv), (d.proj_txt, bt))
+    b = GlobalTable(d.centroids, d.values, (d.proj_vis, bv), (d.proj_txt, bt))
+    assert a.ps != (0, 0), "the table kept a packed projection: the fused plan would run"
+    rb = b.layer_forward_staged(d.x, is_vision, d.logits, d.slot_out, d.residual, 8, 1, 0.6)
+    for rep in range(2):
+        ra = a.layer_forward(d.x, is_vision, d.logits, d.slot_out, d.residual, 8, 1, 0.6)
+        torch.cuda.synchronize()
+        for key in ("weights", "ids", "q", "qn", "dist", "idx", "keep", "out"):
+            assert torch.equal(ra[key], rb[key]), (key, rep)
+    assert int(ra["keep"].sum()) == O.keep_count(n, 0.6)
 
 
 @pytest.mark.parametrize("dtype,metric", [(torch.float16, "l2"), (torch.bfloat16, "dot"), (torch.float16, "dot")])
