@@ -569,7 +569,11 @@ size_t tm_struct_size(int32_t which);
  * (zero = no wait ever ran out).  The return code cannot report such a
  * failure (the call returns before the kernels run): a caller that shares
  * the device with other work must read the word after the calls complete
- * and discard the outputs of any call during which it grew. */
+ * and discard the outputs of any call during which it grew.  A workgroup of
+ * such a call that started late may leave flags that a later call would
+ * take for its own: after the word grew, zero the first
+ * TM_LAYER_SYNC_BYTES of the workspace (the word included) before the next
+ * call on it. */
 #define TM_LAYER_SYNC_BYTES 16384
 #define TM_LAYER_SYNC_ERR_BYTE 3584
 size_t tm_table_forward_workspace_size(const tm_table_layer *table, int64_t n_tokens, int32_t n_nearest);

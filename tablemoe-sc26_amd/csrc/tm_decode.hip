@@ -861,9 +861,11 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
     }
     if (lane == 0) {
       if (!ok) coh_add(sync + kWErr);
-      // every workgroup arrived: workgroup 0 advances the generation (the
-      // next call's flags want gen + 2; no wave of this call reads gen again)
-      if (ok && wg == 0) coh_st32(sync + kWGen, g0() + 1);
+      // workgroup 0 advances the generation (the next call's flags want
+      // gen + 2; every wave of this call read gen at its start, and the next
+      // launch starts after this one ends), also after a wait that ran out,
+      // so flags this call raised are never taken for the next call's
+      if (wg == 0) coh_st32(sync + kWGen, g0() + 1);
       s_ok = ok ? 1u : 0u;
     }
   }

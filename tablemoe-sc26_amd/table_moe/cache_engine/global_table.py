@@ -274,8 +274,14 @@ class GlobalTable:
         now = self.wait_errors()
         self._wait_errors_seen = now
         if now != seen:
+            # a late workgroup of the failed call may have left flags the next
+            # call would take for its own: clear the sync region (the error
+            # word with it) before the workspace is used again
+            self._bufs["layer_ws"][:N.TM_LAYER_SYNC_BYTES].zero_()
+            self._wait_errors_seen = 0
             raise RuntimeError(f"tm_table_forward: {now - seen} cross-workgroup wait(s) ran out; the call's outputs "
-                               "are undefined (the launch's workgroups could not all be resident together)")
+                               "are undefined (the launch's workgroups could not all be resident together); the "
+                               "workspace's sync region was cleared")
 
     def wait_errors(self) -> int:
         """Bounded cross-workgroup waits of the one-launch decode plan that ran

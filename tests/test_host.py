@@ -144,3 +144,30 @@ def test_synthetic_workload_properties():
     assert float(err.median()) < 0.2 * np.sqrt(128) * 1.3
     w3 = make_workload(3, n=8)
     assert w3.centroids.shape == (16384, 128) and not w3.is_vision.any()
+
+
+def test_wait_error_clears_the_sync_region(monkeypatch):
+    """A grown error word makes the layer call raise, and the workspace's sync
+    region (flags, counters, the word) is cleared before the next call, so no
+    flag a late workgroup of the failed call left can pass for the next
+    call's; a later check with the word at zero passes.  Host logic only: the
+    workspace is a host tensor standing in for the device one (and no stream
+    is being captured)."""
+    from table_moe import _native as N
+    from table_moe.cache_engine import GlobalTable
+
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+
+    t = object.__new__(GlobalTable)
+    ws = torch.zeros(N.TM_LAYER_SYNC_BYTES + 256, dtype=torch.uint8)
+    ws[:N.TM_LAYER_SYNC_BYTES] = 7  # stale flags and counters
+    e = N.TM_LAYER_SYNC_ERR_BYTE
+    ws[e:e + 4].view(torch.int32)[0] = 1
+    ws[N.TM_LAYER_SYNC_BYTES:] = 5  # past the sync region: untouched
+    t._bufs = {"layer_ws": ws}
+    with pytest.raises(RuntimeError, match="ran out"):
+        t._raise_on_wait_errors()
+    assert int(ws[:N.TM_LAYER_SYNC_BYTES].count_nonzero()) == 0
+    assert bool((ws[N.TM_LAYER_SYNC_BYTES:] == 5).all())
+    assert t.wait_errors() == 0
+    t._raise_on_wait_errors()  # nothing new: no error
