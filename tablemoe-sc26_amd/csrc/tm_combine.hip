@@ -190,8 +190,9 @@ __global__ __launch_bounds__(kThreads) void gather_combine_fast_kernel(
 // wave-uniform branches, and inside each every source load is unconditional,
 // so all of a chunk's loads are in flight together (a load behind a per-source
 // branch makes the compiler wait for everything outstanding at the join).
-// Slot outputs, the residual and the output are streamed once: non-temporal
-// accesses; gathered value rows use ordinary loads (centroids repeat).
+// Slot outputs and the output are streamed once: non-temporal accesses;
+// gathered value rows (centroids repeat) and the residual use ordinary loads
+// (a non-temporal residual made the ranked combine ~0.7 us slower).
 // Same arithmetic as gather_combine_fast_kernel: fp32 accumulation starting
 // from the residual, sources added in order with fmaf, one rounding.
 // Keep decisions when the keep set is ranked in the combine: token b is
@@ -270,7 +271,7 @@ __global__ __launch_bounds__(kThreads, 8) void gather_combine_tk_kernel(
     for (int h0 = threadIdx.x * 8; h0 < hidden; h0 += kThreads * 8) {
       float acc[8];
       if (res_row) {
-        tm_load8_nt<DT>(res_row + h0, acc);
+        tm_load8<DT>(res_row + h0, acc);
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = 0.f;
@@ -309,7 +310,7 @@ __global__ __launch_bounds__(kThreads, 8) void gather_combine_tk_kernel(
     for (int h0 = threadIdx.x * 8; h0 < hidden; h0 += kThreads * 8) {
       float acc[8];
       if (res_row) {
-        tm_load8_nt<DT>(res_row + h0, acc);
+        tm_load8<DT>(res_row + h0, acc);
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] = 0.f;
@@ -350,7 +351,7 @@ __global__ __launch_bounds__(TPB * kThreads, 8) void gather_combine_rank_kernel(
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  if (residual != nullptr && act) tm_load8_nt<DT>(residual + b * ld_r + h0, acc);
+  if (residual != nullptr && act) tm_load8<DT>(residual + b * ld_r + h0, acc);
   const bool kept = rank_keep<TPB>(dist, rk.n, rk.n_keep, b0, g);
   if (!act) return;
   if (h0 == 0) rk.keep_out[b] = kept ? 1 : 0;

@@ -280,7 +280,7 @@ __global__ __launch_bounds__(64) void decode_finish_kernel(
   for (int s = 0; s < TK; ++s) wv[s] = w[(int64_t)b * TK + s];
   float acc[8];
   if (residual) {
-    tm_load8_nt<DT>(residual + (int64_t)b * ld_r + hl, acc);
+    tm_load8<DT>(residual + (int64_t)b * ld_r + hl, acc);
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
@@ -668,8 +668,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   tm_u32x4 rrow, srow[TK];
   float wv[TK];
   if (has_c) {
-    rrow = __builtin_nontemporal_load(
-        reinterpret_cast<const tm_u32x4 *>(static_cast<const T *>(a.residual) + (int64_t)b * a.ld_r + hl));
+    rrow = *reinterpret_cast<const tm_u32x4 *>(static_cast<const T *>(a.residual) + (int64_t)b * a.ld_r + hl);
     const T *src = static_cast<const T *>(a.slot_out) + (int64_t)b * a.so_b + hl;
 #pragma unroll
     for (int s = 0; s < TK; ++s)
