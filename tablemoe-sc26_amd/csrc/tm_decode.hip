@@ -630,8 +630,16 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   // finishing task's rows, then this call's generation.  Every one is
   // unconditional (clamped or redirected addresses): a load under a branch
   // makes the compiler wait for it, and for all loads before it, right there.
-  const int64_t ta = (int64_t)wave * G + wg;
+  // Task of (wave, workgroup): position L = wave * G + wg holds group
+  // 8 (L / 64) + L % 8, slice (L / 8) % 8, so a group's S slices run on
+  // workgroups congruent mod 8 (one XCD under the dispatcher's round robin).
+  // Measured against consecutive slices on 8 XCDs: 0.1 us faster at N = 1,
+  // the same at N = 8 and 32 -- the hand-offs' coherent accesses go to the
+  // point of coherence from any XCD.
+  const int64_t la = (int64_t)wave * G + wg;
+  const int64_t ta = (8 * (la / 64) + la % 8) * S + (la / 8) % 8;
   const int64_t ta_n = ((n + 15) / 16) * NCB * S;
+  static_assert(S == 8 && NCB == 8, "64 tasks per row tile");
   const bool has_a = ta < ta_n;  // uniform per wave
   ProjOps<DT, KPW> po;
   if (has_a) fused_project_loads<DT, DIM, KPW>(a, ta, lane, po);
