@@ -206,9 +206,47 @@ struct RankKeep {
   uint8_t *keep_out;
 };
 
+// The distances, kRankVec 16-byte vectors per thread and pass, plus (first
+// pass) one scalar per thread for the n % 4 last: every load uses a clamped
+// index (no load is conditional, so none makes the wave wait where it is
+// issued) and a pass's loads are in flight together; values past n are
+// loaded but count as a key no token is behind.  With n < 4 the vectors come
+// from a zero vector of their own.  n <= kRankOnePass: one pass, straight-
+// line code (the layer's sizes).
+constexpr int kRankVec = 4;
+__device__ float4 g_rank_pad;
+
 template <int TPB>
+constexpr int64_t kRankOnePass = 4LL * kRankVec * TPB * kThreads;
+
+struct RankPass {
+  float4 v[kRankVec];
+  float tail;
+};
+
+template <int TPB>
+__device__ __forceinline__ RankPass rank_load(const float *__restrict__ dist, int64_t n, int64_t base) {
+  constexpr int NT = TPB * kThreads;
+  const int64_t n4 = n >> 2;
+  const float4 *d4 = n4 > 0 ? reinterpret_cast<const float4 *>(dist) : &g_rank_pad;
+  const int64_t last = n4 > 0 ? n4 - 1 : 0;
+  RankPass r;
+#pragma unroll
+  for (int u = 0; u < kRankVec; ++u) {
+    const int64_t i = base + threadIdx.x + (int64_t)u * NT;
+    r.v[u] = d4[i < last ? i : last];
+  }
+  const int64_t j = 4 * n4 + threadIdx.x;
+  r.tail = dist[j < n ? j : n - 1];
+  return r;
+}
+
+// Keep decision of token b0 + g: dist_first is the first pass (rank_load at
+// base 0), loaded by the caller before its other loads so that it retires
+// first; ONE: n <= kRankOnePass<TPB>, no further pass.
+template <int TPB, bool ONE>
 __device__ __forceinline__ bool rank_keep(const float *__restrict__ dist, int64_t n, int64_t n_keep, int64_t b0,
-                                          int g) {
+                                          int g, const RankPass &dist_first) {
   constexpr int NT = TPB * kThreads;
   constexpr int NW = NT / 64;
   __shared__ uint32_t s_ahead[NW][TPB];
@@ -218,20 +256,32 @@ __device__ __forceinline__ bool rank_keep(const float *__restrict__ dist, int64_
   uint32_t ahead[TPB];
 #pragma unroll
   for (int t = 0; t < TPB; ++t) ahead[t] = 0;
+  // every key of a real distance is >= orderable(-inf) > 0: key 0 is ahead of
+  // no token and ties with none
   auto count = [&](uint32_t k, int64_t j) {
 #pragma unroll
-    for (int t = 0; t < TPB; ++t) ahead[t] += (k > kb[t] || (k == kb[t] && j < b0 + t)) ? 1u : 0u;
+    for (int t = 0; t < TPB; ++t)
+      ahead[t] += (uint32_t)(k > kb[t]) | ((uint32_t)(k == kb[t]) & (uint32_t)(j < b0 + t));
   };
-  const float4 *d4 = reinterpret_cast<const float4 *>(dist);
   const int64_t n4 = n >> 2;
-  for (int64_t i = threadIdx.x; i < n4; i += NT) {
-    const float4 v = d4[i];
-    count(tm_orderable(v.x), 4 * i);
-    count(tm_orderable(v.y), 4 * i + 1);
-    count(tm_orderable(v.z), 4 * i + 2);
-    count(tm_orderable(v.w), 4 * i + 3);
+  auto count_pass = [&](const RankPass &r, int64_t base) {
+#pragma unroll
+    for (int u = 0; u < kRankVec; ++u) {
+      const int64_t i = base + threadIdx.x + (int64_t)u * NT;
+      const bool in = i < n4;
+      count(in ? tm_orderable(r.v[u].x) : 0u, 4 * i);
+      count(in ? tm_orderable(r.v[u].y) : 0u, 4 * i + 1);
+      count(in ? tm_orderable(r.v[u].z) : 0u, 4 * i + 2);
+      count(in ? tm_orderable(r.v[u].w) : 0u, 4 * i + 3);
+    }
+  };
+  count_pass(dist_first, 0);
+  const int64_t jt = 4 * n4 + threadIdx.x;
+  count(jt < n ? tm_orderable(dist_first.tail) : 0u, jt);
+  if constexpr (!ONE) {
+    for (int64_t base = (int64_t)kRankVec * NT; base < n4; base += (int64_t)kRankVec * NT)
+      count_pass(rank_load<TPB>(dist, n, base), base);
   }
-  for (int64_t j = 4 * n4 + threadIdx.x; j < n; j += NT) count(tm_orderable(dist[j]), j);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int t = 0; t < TPB; ++t) {
@@ -330,12 +380,40 @@ __global__ __launch_bounds__(kThreads, 8) void gather_combine_tk_kernel(
   }
 }
 
+// 8 consecutive elements as loaded: 16-bit values stay packed (one 16-byte
+// vector), fp32 takes two vectors; converted where they are used.
+template <int DT>
+struct Raw8 {
+  tm_u32x4 w[Elem<DT>::kBytes / 2];
+  __device__ __forceinline__ float at(int i) const {
+    return Elem<DT>::to_f(reinterpret_cast<const typename Elem<DT>::T *>(&w[0])[i]);
+  }
+};
+
+template <int DT, bool NT>
+__device__ __forceinline__ Raw8<DT> raw_load8(const typename Elem<DT>::T *p) {
+  Raw8<DT> r;
+  const tm_u32x4 *v = reinterpret_cast<const tm_u32x4 *>(p);
+#pragma unroll
+  for (int k = 0; k < Elem<DT>::kBytes / 2; ++k) r.w[k] = NT ? __builtin_nontemporal_load(v + k) : v[k];
+  return r;
+}
+
 // Top-1 combine that also decides the keep set (rank_keep), TPB tokens per
 // workgroup (256 threads each, one 8-element chunk per thread: hidden <=
-// 2048), so the distances are read once per TPB tokens.  The residual chunk
-// (needed either way) is loaded before the ranking.  The arithmetic is
+// 2048), so the distances are read once per TPB tokens.  The arithmetic is
 // gather_combine_tk_kernel's (NN = 1).
-template <int DT, int TK, int TPB>
+//
+// Two dependent memory round trips per workgroup: every load whose address
+// is known at entry goes out first -- the first pass of distances, then the
+// residual chunk, the token's router weights and its centroid id -- with
+// clamped addresses, so no load is conditional and none makes the wave wait
+// where it is issued (loads retire in order: the distances, issued first,
+// are counted while the others are still in flight).  Once the ranking
+// decided, the token's TK slot chunks (kept) or its value chunk (replaced)
+// are loaded, all before the first is used; sources a token does not take
+// are loaded and masked out by a select, not skipped by a branch.
+template <int DT, int TK, int TPB, bool ONE>
 __global__ __launch_bounds__(TPB * kThreads, 8) void gather_combine_rank_kernel(
     int hidden, const typename Elem<DT>::T *__restrict__ slot_out, int64_t so_b, int64_t so_s,
     const float *__restrict__ w, int64_t ld_w, const typename Elem<DT>::T *__restrict__ values, int64_t n_cent,
@@ -343,59 +421,60 @@ __global__ __launch_bounds__(TPB * kThreads, 8) void gather_combine_rank_kernel(
     const typename Elem<DT>::T *__restrict__ residual, int64_t ld_r, typename Elem<DT>::T *__restrict__ out,
     int64_t ld_o, RankKeep rk) {
   using T = typename Elem<DT>::T;
-  const int g = threadIdx.x / kThreads;
+  // one token per workgroup: its index, row addresses, weights and centroid
+  // are wave-uniform (scalar registers and loads)
+  const int g = TPB == 1 ? 0 : threadIdx.x / kThreads;
   const int64_t b0 = (int64_t)blockIdx.x * TPB;
   const int64_t b = b0 + g;
   const int h0 = (threadIdx.x % kThreads) * 8;
   const bool act = h0 < hidden && b < rk.n;
-  float acc[8];
+  const int64_t bc = b < rk.n ? b : rk.n - 1;
+  const int hc = h0 < hidden ? h0 : hidden - 8;
+  const RankPass d0 = rank_load<TPB>(dist, rk.n, 0);
+  __builtin_amdgcn_sched_barrier(0);  // the distances first: they are needed first
+  // without a residual the output row stands in as a valid address (not used)
+  const Raw8<DT> res = raw_load8<DT, false>(residual ? residual + bc * ld_r + hc : out + bc * ld_o + hc);
+  float wt[TK];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  if (residual != nullptr && act) tm_load8<DT>(residual + b * ld_r + h0, acc);
-  const bool kept = rank_keep<TPB>(dist, rk.n, rk.n_keep, b0, g);
+  for (int s = 0; s < TK; ++s) wt[s] = w[bc * ld_w + s];
+  const int64_t c = idx[bc];
+  // every load above is issued before the counting starts (the compiler
+  // barrier keeps the weights' and centroid's loads from sinking into the
+  // branches that use them)
+  asm volatile("" ::: "memory");
+  const bool kept = rank_keep<TPB, ONE>(dist, rk.n, rk.n_keep, b0, g, d0);
   if (!act) return;
   if (h0 == 0) rk.keep_out[b] = kept ? 1 : 0;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = residual ? res.at(i) : 0.f;
   if (kept) {  // uniform over the token's 256 threads
-    float coef[TK];
+    const T *src = slot_out + b * so_b + h0;
     float sum = 0.f;
 #pragma unroll
-    for (int s = 0; s < TK; ++s) {
-      coef[s] = w[b * ld_w + s];
-      sum += coef[s];
-    }
-    if (sum > 0.f) {  // rows whose weights sum to 0 contribute nothing
+    for (int s = 0; s < TK; ++s) sum += wt[s];
+    const bool any = sum > 0.f;  // rows whose weights sum to 0 contribute nothing
+    // 16-bit rows: all TK chunks in flight before the first is used; fp32
+    // rows (8 registers a chunk) in two halves
+    constexpr int GRP = sizeof(T) == 2 ? TK : TK / 2;
 #pragma unroll
-      for (int s = 0; s < TK; ++s) coef[s] = coef[s] / sum;
-      const T *src = slot_out + b * so_b + h0;
-      if constexpr (sizeof(T) == 2) {
-        tm_u32x4 raw[TK];  // 16-bit values until used: 4 registers per slot instead of 8
+    for (int s0 = 0; s0 < TK; s0 += GRP) {
+      Raw8<DT> sv[GRP];
 #pragma unroll
-        for (int s = 0; s < TK; ++s)
-          raw[s] = __builtin_nontemporal_load(reinterpret_cast<const tm_u32x4 *>(src + (int64_t)s * so_s));
+      for (int s = 0; s < GRP; ++s) sv[s] = raw_load8<DT, true>(src + (int64_t)(s0 + s) * so_s);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < TK; ++s) {
-          const T *e = reinterpret_cast<const T *>(&raw[s]);
+      for (int s = 0; s < GRP; ++s) {
+        const float coef = wt[s0 + s] / sum;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], Elem<DT>::to_f(e[i]), acc[i]);
-        }
-      } else {  // fp32 rows: every slot's 8 values requested before the first is used
-        float sv[TK][8];
-#pragma unroll
-        for (int s = 0; s < TK; ++s) tm_load8_nt<DT>(src + (int64_t)s * so_s, sv[s]);
-#pragma unroll
-        for (int s = 0; s < TK; ++s)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], sv[s][i], acc[i]);
+        for (int i = 0; i < 8; ++i) acc[i] = any ? fmaf(coef, sv[s].at(i), acc[i]) : acc[i];
       }
     }
   } else {
-    const int64_t c = idx[b];
-    if (c >= 0 && c < n_cent) {
-      float val[8];
-      tm_load8<DT>(values + c * ld_v + h0, val);
+    const bool ok = c >= 0 && c < n_cent;
+    const Raw8<DT> val = raw_load8<DT, false>(values + (ok ? c : 0) * ld_v + h0);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = fmaf(1.f, val[i], acc[i]);
-    }
+    for (int i = 0; i < 8; ++i) acc[i] = ok ? fmaf(1.f, val.at(i), acc[i]) : acc[i];
   }
   tm_store8_nt<DT>(out + b * ld_o + h0, acc);
 }
@@ -871,10 +950,12 @@ int tm_internal_combine_rank(int32_t dtype, int64_t n_tokens, int32_t hidden, co
     constexpr int DT = decltype(dt_tag)::value;
     constexpr int TK = decltype(tk_tag)::value;
     using T = typename Elem<DT>::T;
-    hipLaunchKernelGGL((gather_combine_rank_kernel<DT, TK, kRankTokens>), dim3((unsigned)tm_cdiv(n_tokens, kRankTokens)),
-                       dim3(kRankTokens * kThreads), 0, s, hidden, static_cast<const T *>(slot_out), so_b, so_s,
-                       weights, ld_w, static_cast<const T *>(values), n_cent, ld_v, idx, dist,
-                       static_cast<const T *>(residual), ld_r, static_cast<T *>(out), ld_o, rk);
+    auto kern = n_tokens <= kRankOnePass<kRankTokens> ? gather_combine_rank_kernel<DT, TK, kRankTokens, true>
+                                                        : gather_combine_rank_kernel<DT, TK, kRankTokens, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tm_cdiv(n_tokens, kRankTokens)), dim3(kRankTokens * kThreads), 0, s,
+                       hidden, static_cast<const T *>(slot_out), so_b, so_s, weights, ld_w,
+                       static_cast<const T *>(values), n_cent, ld_v, idx, dist, static_cast<const T *>(residual),
+                       ld_r, static_cast<T *>(out), ld_o, rk);
   };
   using BF = std::integral_constant<int, TM_DT_BF16>;
   using HF = std::integral_constant<int, TM_DT_F16>;
