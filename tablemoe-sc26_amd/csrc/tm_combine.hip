@@ -479,6 +479,106 @@ __global__ __launch_bounds__(TPB * kThreads, 8) void gather_combine_rank_kernel(
   tm_store8_nt<DT>(out + b * ld_o + h0, acc);
 }
 
+// gather_combine_tk_kernel with one 8-element chunk per thread (hidden <=
+// 8 * kTk1MaxThreads, a block of round64(hidden / 8) threads), in two
+// dependent memory round trips: the keep byte first, then every other load
+// whose address is known at entry (the residual chunk with a clamped
+// address, the router weights, centroid ids and distances as scalar loads),
+// and once the keep byte is in, all of the branch's source chunks before the
+// first is used (sources a row does not take are loaded and masked out by a
+// select).  The loop kernel walks a chunk at a time, each behind a residual
+// load the compiler waits for where it is issued.  Same arithmetic.
+constexpr int kTk1MaxThreads = 1024;
+
+template <int DT, int TK, int NN>
+__global__ __launch_bounds__(kTk1MaxThreads, 8) void gather_combine_tk1_kernel(
+    int hidden, const uint8_t *__restrict__ keep, const typename Elem<DT>::T *__restrict__ slot_out, int64_t so_b,
+    int64_t so_s, const float *__restrict__ w, int64_t ld_w, const typename Elem<DT>::T *__restrict__ values,
+    int64_t n_cent, int64_t ld_v, const int64_t *__restrict__ idx, const float *__restrict__ dist, int64_t ld_idx,
+    const typename Elem<DT>::T *__restrict__ residual, int64_t ld_r, typename Elem<DT>::T *__restrict__ out,
+    int64_t ld_o) {
+  using T = typename Elem<DT>::T;
+  const int64_t b = blockIdx.x;
+  const int h0 = threadIdx.x * 8;
+  const bool act = h0 < hidden;
+  const int hc = act ? h0 : hidden - 8;
+  const uint8_t kp = keep[b];
+  __builtin_amdgcn_sched_barrier(0);  // the keep byte first: it is needed first
+  // without a residual the output row stands in as a valid address (not used)
+  Raw8<DT> res = raw_load8<DT, false>(residual ? residual + b * ld_r + hc : out + b * ld_o + hc);
+  float wt[TK];
+#pragma unroll
+  for (int s = 0; s < TK; ++s) wt[s] = w[b * ld_w + s];
+  int64_t c[NN];
+  float dj[NN];
+#pragma unroll
+  for (int j = 0; j < NN; ++j) {
+    c[j] = idx[b * ld_idx + j];
+    dj[j] = NN > 1 ? dist[b * ld_idx + j] : 0.f;
+  }
+  // The weights, ids and distances (scalar loads) are taken here, where the
+  // branch waits for the keep byte anyway: left to itself the compiler moves
+  // them into the branch, in front of its source loads.
+#pragma unroll
+  for (int s = 0; s < TK; ++s) asm volatile("" : "+s"(wt[s]));
+#pragma unroll
+  for (int j = 0; j < NN; ++j) asm volatile("" : "+s"(c[j]), "+s"(dj[j]));
+  float acc[8];
+  // The residual is converted only after the branch's source loads are
+  // issued (the empty asm keeps the conversion, common to both branches,
+  // from being hoisted above the branch).
+  auto take_res = [&] {
+#pragma unroll
+    for (int k = 0; k < Elem<DT>::kBytes / 2; ++k) asm volatile("" : "+v"(res.w[k]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = residual ? res.at(i) : 0.f;
+  };
+  if (kp) {  // uniform
+    const T *src = slot_out + b * so_b + hc;
+    Raw8<DT> sv[TK];
+#pragma unroll
+    for (int s = 0; s < TK; ++s) sv[s] = raw_load8<DT, true>(src + (int64_t)s * so_s);
+    __builtin_amdgcn_sched_barrier(0);  // all TK chunks in flight before the residual or any of them is used
+    take_res();
+    float sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < TK; ++s) sum += wt[s];
+    const bool any = sum > 0.f;  // rows whose weights sum to 0 contribute nothing
+#pragma unroll
+    for (int s = 0; s < TK; ++s) {
+      const float coef = wt[s] / sum;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = any ? fmaf(coef, sv[s].at(i), acc[i]) : acc[i];
+    }
+  } else {
+    bool ok[NN];
+    Raw8<DT> v[NN];
+#pragma unroll
+    for (int j = 0; j < NN; ++j) {
+      ok[j] = c[j] >= 0 && c[j] < n_cent;
+      v[j] = raw_load8<DT, false>(values + (ok[j] ? c[j] : 0) * ld_v + hc);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    take_res();
+    float coef[NN];
+    float inv_sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < NN; ++j) {
+      coef[j] = ok[j] ? ((NN > 1) ? 1.f / (dj[j] + 1e-6f) : 1.f) : 0.f;
+      inv_sum += coef[j];
+    }
+    if (NN > 1) {
+#pragma unroll
+      for (int j = 0; j < NN; ++j) coef[j] = ok[j] ? coef[j] / inv_sum : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < NN; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = ok[j] ? fmaf(coef[j], v[j].at(i), acc[i]) : acc[i];
+  }
+  if (act) tm_store8_nt<DT>(out + b * ld_o + h0, acc);
+}
+
 // General path (more than 8 sources): sources staged through LDS.
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void gather_combine_kernel(
@@ -832,10 +932,16 @@ extern "C" int tm_gather_rows(int32_t dtype, const void *values, int64_t n_exper
 // Launch of the shape-specialised combine when (top_k, n_nearest) matches.
 #define TM_GC_TK(TK_, NN_)                                                                                     \
   if (top_k == TK_ && n_nearest == NN_) {                                                                      \
-    hipLaunchKernelGGL((gather_combine_tk_kernel<DT, TK_, NN_>), grid, block, 0, s, hidden, keep,              \
-                       static_cast<const T *>(slot_out), so_b, so_s, weights, ld_w, static_cast<const T *>(values), \
-                       n_cent, ld_v, idx, dist, ld_idx, static_cast<const T *>(residual), ld_r, static_cast<T *>(out), \
-                       ld_o);                                                                                  \
+    if (hidden <= 8 * kTk1MaxThreads)                                                                          \
+      hipLaunchKernelGGL((gather_combine_tk1_kernel<DT, TK_, NN_>), grid, dim3(tk1_threads), 0, s, hidden,    \
+                         keep, static_cast<const T *>(slot_out), so_b, so_s, weights, ld_w,                    \
+                         static_cast<const T *>(values), n_cent, ld_v, idx, dist, ld_idx,                       \
+                         static_cast<const T *>(residual), ld_r, static_cast<T *>(out), ld_o);                  \
+    else                                                                                                       \
+      hipLaunchKernelGGL((gather_combine_tk_kernel<DT, TK_, NN_>), grid, block, 0, s, hidden, keep,            \
+                         static_cast<const T *>(slot_out), so_b, so_s, weights, ld_w,                           \
+                         static_cast<const T *>(values), n_cent, ld_v, idx, dist, ld_idx,                       \
+                         static_cast<const T *>(residual), ld_r, static_cast<T *>(out), ld_o);                  \
     TM_LAUNCH_CHECK("tm_gather_combine");                                                                      \
     return TM_OK;                                                                                              \
   }
@@ -864,6 +970,7 @@ extern "C" int tm_gather_combine(int32_t dtype, int64_t n_tokens, int32_t hidden
     if constexpr (Elem<DT>::kBytes == 2) {
       if (vec) {
         const dim3 grid((unsigned)n_tokens), block(kThreads);
+        const unsigned tk1_threads = (unsigned)((hidden / 8 + 63) / 64 * 64);  // one chunk per thread
         hipStream_t s = tm_hip_stream(stream);
         TM_GC_TK(8, 1)
         TM_GC_TK(8, 4)
