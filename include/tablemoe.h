@@ -442,6 +442,21 @@ int tm_group_slots(const int64_t *ids, int64_t n_tokens, int32_t top_k, int64_t 
                    int64_t ms_b, int64_t ms_s, int32_t n_experts, int64_t so_b, int64_t so_s,
                    int32_t *expert_offsets, int32_t *row_token, int64_t *row_out, int32_t *tiles,
                    tm_stream_t stream);
+/* tm_group_slots over several workgroups (no counterpart in the reference:
+ * the same outputs, with the ids read by many CUs instead of one): for
+ * 1 <= n_tokens <= 8192, 1 <= top_k <= 8 and 1 <= n_experts <= 256 two
+ * launches -- per-workgroup expert counts into `workspace`
+ * (tm_group_slots_workspace_size bytes, 16-byte aligned; TM_EWORKSPACE if
+ * smaller), then the placement of each workgroup's rows after those of the
+ * workgroups before it; other shapes run tm_group_slots (the workspace is
+ * not used, and tm_group_slots_workspace_size returns 0).  Same contract as
+ * tm_group_slots: the offsets, tile list and the set of rows of each expert
+ * are the same; the order of rows inside an expert is unspecified. */
+size_t tm_group_slots_workspace_size(int64_t n_tokens, int32_t top_k, int32_t n_experts);
+int tm_group_slots_ws(const int64_t *ids, int64_t n_tokens, int32_t top_k, int64_t ld_ids, const uint8_t *mask,
+                      int64_t ms_b, int64_t ms_s, int32_t n_experts, int64_t so_b, int64_t so_s,
+                      int32_t *expert_offsets, int32_t *row_token, int64_t *row_out, int32_t *tiles,
+                      void *workspace, size_t workspace_bytes, tm_stream_t stream);
 /* The MLP of every grouped row: row r (expert e by expert_offsets) reads
  * x[row_token[r]] and writes out[row_out[r] .. + hidden).  max_rows bounds
  * the row count (n_tokens * top_k of the tm_group_slots call). */

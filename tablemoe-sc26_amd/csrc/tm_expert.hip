@@ -468,6 +468,159 @@ __global__ __launch_bounds__(kGroupThreads) void group_slots_kernel(
   }
 }
 
+// Multi-workgroup grouping (tm_group_slots_ws): kGrpTok tokens per
+// workgroup, in two launches.  group_count_kernel loads its tokens' ids and
+// mask bytes and writes the workgroup's per-expert counts to a row of the
+// workspace; group_place_kernel loads them again, sums every workgroup's row
+// for each expert (and the rows of the workgroups before it), scans the
+// experts for the offsets and tile bases (workgroup 0 writes them and the
+// tile list) and places its rows at offset + rows of earlier workgroups +
+// an LDS cursor.  Each CU then loads 1/G of the ids instead of one CU all
+// of them.
+constexpr int kGrpThreads = 256;
+constexpr int kGrpTok = 64;            // tokens per workgroup: 4 threads per token, 2 slots each
+constexpr int kGrpMaxSlots = 8;        // top_k
+constexpr int kGrpMaxExperts = 256;    // one expert per thread in the scan
+constexpr int kGrpMaxWgs = 128;        // n_tokens <= 8192
+constexpr int kGrpBatch = 16;          // count rows loaded per round trip
+
+// The two (token, slot) entries of this thread: expert id, or -1 when the
+// pair is not recomputed.  Clamped addresses (no load is conditional).
+__device__ __forceinline__ void grp_entries(const int64_t *__restrict__ ids, int64_t n, int top_k, int64_t ld_ids,
+                                            const uint8_t *__restrict__ mask, int64_t ms_b, int64_t ms_s,
+                                            int n_experts, int64_t b, int s0, int (&ex)[2]) {
+  const int64_t bb = b < n ? b : n - 1;
+  int64_t e[2];
+  uint8_t m[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int s = s0 + u;
+    const int ss = s < top_k ? s : top_k - 1;
+    e[u] = ids[bb * ld_ids + ss];
+    m[u] = mask[bb * ms_b + ss * ms_s];
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const bool use = b < n && s0 + u < top_k && m[u] && e[u] >= 0 && e[u] < n_experts;
+    ex[u] = use ? (int)e[u] : -1;
+  }
+}
+
+__global__ __launch_bounds__(kGrpThreads) void group_count_kernel(const int64_t *__restrict__ ids, int64_t n,
+                                                                  int top_k, int64_t ld_ids,
+                                                                  const uint8_t *__restrict__ mask, int64_t ms_b,
+                                                                  int64_t ms_s, int n_experts,
+                                                                  int32_t *__restrict__ counts) {
+  __shared__ int32_t h[kGrpMaxExperts];
+  const int tid = threadIdx.x;
+  int ex[2];
+  grp_entries(ids, n, top_k, ld_ids, mask, ms_b, ms_s, n_experts, (int64_t)blockIdx.x * kGrpTok + tid / 4,
+              2 * (tid % 4), ex);
+  for (int e = tid; e < n_experts; e += kGrpThreads) h[e] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    if (ex[u] >= 0) atomicAdd(&h[ex[u]], 1);
+  __syncthreads();
+  for (int e = tid; e < n_experts; e += kGrpThreads) counts[(int64_t)blockIdx.x * n_experts + e] = h[e];
+}
+
+__global__ __launch_bounds__(kGrpThreads) void group_place_kernel(
+    const int64_t *__restrict__ ids, int64_t n, int top_k, int64_t ld_ids, const uint8_t *__restrict__ mask,
+    int64_t ms_b, int64_t ms_s, int n_experts, int64_t so_b, int64_t so_s, const int32_t *__restrict__ counts,
+    int32_t *__restrict__ offsets, int32_t *__restrict__ row_token, int64_t *__restrict__ row_out,
+    int32_t *__restrict__ tiles, int64_t t_max) {
+  __shared__ int32_t part_tot[kGrpThreads], part_bef[kGrpThreads];
+  __shared__ int32_t cur[kGrpMaxExperts];
+  __shared__ int32_t wave_rows[kGrpThreads / 64], wave_tiles[kGrpThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = (int)gridDim.x, g0 = (int)blockIdx.x;
+  const int64_t b = (int64_t)g0 * kGrpTok + tid / 4;
+  const int s0 = 2 * (tid % 4);
+  int ex[2];
+  grp_entries(ids, n, top_k, ld_ids, mask, ms_b, ms_s, n_experts, b, s0, ex);
+  // Thread (e, p) of ep = pow2 >= n_experts columns sums the count rows
+  // g = p, p + P, .. (P = 256 / ep) of expert e: kGrpBatch rows per round
+  // trip (clamped rows, masked by a select).
+  int ep = 1;
+  while (ep < n_experts) ep <<= 1;
+  const int P = kGrpThreads / ep;
+  const int e = tid % ep, p = tid / ep;
+  const int ec = e < n_experts ? e : n_experts - 1;
+  int32_t tot = 0, bef = 0;
+  for (int g = p; g < G; g += P * kGrpBatch) {
+    int32_t v[kGrpBatch];
+#pragma unroll
+    for (int j = 0; j < kGrpBatch; ++j) {
+      const int gj = g + P * j;
+      v[j] = counts[(int64_t)(gj < G ? gj : G - 1) * n_experts + ec];
+    }
+#pragma unroll
+    for (int j = 0; j < kGrpBatch; ++j) {
+      const int gj = g + P * j;
+      const int32_t c = (gj < G && e < n_experts) ? v[j] : 0;
+      tot += c;
+      bef += gj < g0 ? c : 0;
+    }
+  }
+  part_tot[tid] = tot;
+  part_bef[tid] = bef;
+  __syncthreads();
+  // thread x owns expert x: its total and the rows of the earlier workgroups
+  int32_t h = 0, hb = 0;
+  if (tid < n_experts)
+    for (int q = 0; q < P; ++q) {
+      h += part_tot[q * ep + tid];
+      hb += part_bef[q * ep + tid];
+    }
+  // exclusive scans over the experts (rows and 256-row tiles): wave scans,
+  // then the waves' totals in wave order
+  const int32_t tc = (h + BM - 1) / BM;
+  int32_t ih = h, it = tc;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t oh = __shfl_up(ih, d, 64), ot = __shfl_up(it, d, 64);
+    if (lane >= d) {
+      ih += oh;
+      it += ot;
+    }
+  }
+  if (lane == 63) {
+    wave_rows[wave] = ih;
+    wave_tiles[wave] = it;
+  }
+  __syncthreads();
+  int32_t bh = 0, bt = 0;
+  for (int w = 0; w < wave; ++w) {
+    bh += wave_rows[w];
+    bt += wave_tiles[w];
+  }
+  const int32_t eh = bh + ih - h, et = bt + it - tc;  // exclusive
+  if (tid < n_experts) {
+    cur[tid] = eh + hb;
+    if (g0 == 0) {
+      offsets[tid] = eh;
+      for (int32_t t = 0; t < tc; ++t) {
+        tiles[2 + et + t] = tid;
+        tiles[2 + t_max + et + t] = eh + t * BM;
+      }
+      if (tid == n_experts - 1) {
+        offsets[n_experts] = eh + h;
+        tiles[0] = eh + h;
+        tiles[1] = et + tc;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    if (ex[u] >= 0) {
+      const int32_t pos = atomicAdd(&cur[ex[u]], 1);
+      row_token[pos] = (int32_t)b;
+      row_out[pos] = b * so_b + (int64_t)(s0 + u) * so_s;
+    }
+}
+
 template <int DT, int NB, int MODE, int BN, bool PB>
 void launch_gemm(const void *A, int64_t lda, const int32_t *a_rows, const void *B0, const void *B1, int64_t b_expert,
                  int K, int N, const TileSrc &ts, int64_t grid_y, void *C, int64_t ldc, const int64_t *c_rows,
@@ -577,6 +730,46 @@ extern "C" int tm_group_slots(const int64_t *ids, int64_t n_tokens, int32_t top_
                      top_k, ld_ids, mask, ms_b, ms_s, n_experts, so_b, so_s, expert_offsets, row_token, row_out,
                      tiles, t_max);
   TM_LAUNCH_CHECK("tm_group_slots");
+  return TM_OK;
+}
+
+namespace {
+bool group_multi_ok(int64_t n_tokens, int32_t top_k, int32_t n_experts) {
+  return n_tokens > 0 && n_tokens <= (int64_t)kGrpTok * kGrpMaxWgs && top_k >= 1 && top_k <= kGrpMaxSlots &&
+         n_experts >= 1 && n_experts <= kGrpMaxExperts;
+}
+}  // namespace
+
+extern "C" size_t tm_group_slots_workspace_size(int64_t n_tokens, int32_t top_k, int32_t n_experts) {
+  if (!group_multi_ok(n_tokens, top_k, n_experts)) return 0;
+  return (size_t)tm_cdiv(n_tokens, kGrpTok) * (size_t)n_experts * sizeof(int32_t);
+}
+
+extern "C" int tm_group_slots_ws(const int64_t *ids, int64_t n_tokens, int32_t top_k, int64_t ld_ids,
+                                 const uint8_t *mask, int64_t ms_b, int64_t ms_s, int32_t n_experts, int64_t so_b,
+                                 int64_t so_s, int32_t *expert_offsets, int32_t *row_token, int64_t *row_out,
+                                 int32_t *tiles, void *workspace, size_t workspace_bytes, tm_stream_t stream) {
+  const size_t need = tm_group_slots_workspace_size(n_tokens, top_k, n_experts);
+  if (need == 0)  // outside the multi-workgroup shapes: the one-workgroup grouping
+    return tm_group_slots(ids, n_tokens, top_k, ld_ids, mask, ms_b, ms_s, n_experts, so_b, so_s, expert_offsets,
+                          row_token, row_out, tiles, stream);
+  TM_REQUIRE(ld_ids >= top_k && top_k >= 1, TM_EINVAL_SHAPE, "tm_group_slots_ws: bad sizes");
+  TM_REQUIRE(ids && mask && expert_offsets && row_token && row_out && tiles, TM_EINVAL_ARG,
+             "tm_group_slots_ws: null pointer");
+  TM_REQUIRE(so_b % 8 == 0 && so_s % 8 == 0, TM_EINVAL_SHAPE,
+             "tm_group_slots_ws: output strides (%lld, %lld) must be multiples of 8 elements", (long long)so_b,
+             (long long)so_s);
+  TM_REQUIRE(workspace != nullptr && workspace_bytes >= need && tm_aligned16(workspace), TM_EWORKSPACE,
+             "tm_group_slots_ws: workspace %zu bytes < %zu", workspace_bytes, need);
+  const int64_t t_max = tm_group_slots_tiles(n_tokens * top_k, n_experts);
+  const unsigned G = (unsigned)tm_cdiv(n_tokens, kGrpTok);
+  hipStream_t s = tm_hip_stream(stream);
+  int32_t *counts = static_cast<int32_t *>(workspace);
+  hipLaunchKernelGGL(group_count_kernel, dim3(G), dim3(kGrpThreads), 0, s, ids, n_tokens, top_k, ld_ids, mask, ms_b,
+                     ms_s, n_experts, counts);
+  hipLaunchKernelGGL(group_place_kernel, dim3(G), dim3(kGrpThreads), 0, s, ids, n_tokens, top_k, ld_ids, mask, ms_b,
+                     ms_s, n_experts, so_b, so_s, counts, expert_offsets, row_token, row_out, tiles, t_max);
+  TM_LAUNCH_CHECK("tm_group_slots_ws");
   return TM_OK;
 }
 

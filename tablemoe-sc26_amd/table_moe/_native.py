@@ -100,6 +100,8 @@ PROTOTYPES = {
     "tm_expert_swiglu_add": (C.c_int, [i32, vp, i64, i32, i64, vp, vp, vp, i32, vp, i64, vp, i64, vp, sz, vp]),
     "tm_group_slots_tiles": (i64, [i64, i32]),
     "tm_group_slots": (C.c_int, [vp, i64, i32, i64, vp, i64, i64, i32, i64, i64, vp, vp, vp, vp, vp]),
+    "tm_group_slots_workspace_size": (sz, [i64, i32, i32]),
+    "tm_group_slots_ws": (C.c_int, [vp, i64, i32, i64, vp, i64, i64, i32, i64, i64, vp, vp, vp, vp, vp, sz, vp]),
     "tm_grouped_swiglu": (C.c_int, [i32, vp, i64, i32, i32, i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, sz, vp]),
     "tm_grouped_swiglu_packed": (C.c_int, [i32, vp, i64, i32, i32, i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, sz,
                                            vp]),

@@ -2,7 +2,7 @@
 pair selected by ``mask`` runs its routed expert's SwiGLU MLP and writes
 ``slot_out[token, slot]`` — the collected[token, slot] rows the reference
 fills one expert at a time (models/qwen3_vl_moe/cached_layers.py:431-437)
-and the combine consumes.  Two C-ABI calls: tm_group_slots (bucket the pairs
+and the combine consumes.  Two C-ABI calls: tm_group_slots_ws (bucket the pairs
 by expert on the device, no host sync) and tm_grouped_swiglu (two grouped
 GEMMs on the matrix cores).  Weights are stacked per expert as nn.Linear
 keeps them: w1, w3 [E, I, H], w2 [E, H, I]; by default a packed copy of
@@ -60,9 +60,11 @@ class GroupedExperts:
         row_token = self._buf("row_token", n * k, torch.int32)
         row_out = self._buf("row_out", n * k, torch.int64)
         tiles = self._buf("tiles", 2 + 2 * t_max, torch.int32)
-        N.call("tm_group_slots", N.ptr(ids), n, k, ids.stride(0), N.ptr(m), ms_b, ms_s, self.n_experts,
+        nbytes = N.lib().tm_group_slots_workspace_size(n, k, self.n_experts)
+        ws = self._buf("group_ws", max(nbytes, 1), torch.uint8)
+        N.call("tm_group_slots_ws", N.ptr(ids), n, k, ids.stride(0), N.ptr(m), ms_b, ms_s, self.n_experts,
                slot_out.stride(0), slot_out.stride(1), N.ptr(offs), N.ptr(row_token), N.ptr(row_out), N.ptr(tiles),
-               N.stream(self.device))
+               N.ptr(ws), ws.numel(), N.stream(self.device))
         return offs, row_token, row_out, tiles
 
     def forward(self, hidden: torch.Tensor, ids: torch.Tensor, mask: torch.Tensor, slot_out: torch.Tensor):

@@ -122,6 +122,14 @@ def test_argument_validation_without_device(lib):
     # the packed path's intermediate is whole 256-row tiles of the tile list
     assert lib.tm_grouped_swiglu_packed_workspace_size(24576, 1536, 64, N.TM_DT_BF16) == (96 + 64) * 256 * 1536 * 2
     assert lib.tm_swiglu_workspace_size(24576, 1536, N.TM_DT_BF16) == 24576 * 1536 * 2
+    # the multi-workgroup grouping: one count row per 64 tokens, 0 (the one-workgroup kernel) outside its shapes
+    assert lib.tm_group_slots_workspace_size(4096, 6, 64) == 64 * 64 * 4
+    assert lib.tm_group_slots_workspace_size(8192, 8, 256) == 128 * 256 * 4
+    for n_, k_, e_ in ((0, 6, 64), (8193, 6, 64), (4096, 9, 64), (4096, 6, 257), (4096, 6, 0)):
+        assert lib.tm_group_slots_workspace_size(n_, k_, e_) == 0
+    q = C.c_void_p(256)
+    assert lib.tm_group_slots_ws(q, 4096, 6, 6, q, 6, 1, 64, 6 * 2560, 2560, q, q, q, q, q, 4096,
+                                 None) == N.TM_EWORKSPACE
     # grouped rows are written in 16-byte pieces: output strides off a multiple of 8 elements are rejected
     p = C.c_void_p(256)
     assert lib.tm_group_slots(p, 16, 6, 6, p, 6, 1, 64, 6 * 2564, 2564, p, p, p, p, None) == N.TM_EINVAL_SHAPE

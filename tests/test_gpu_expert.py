@@ -95,6 +95,58 @@ def test_group_slots_buckets_every_pair(hip_device, n, k):
         assert np.all(ids.numpy()[bb, ss] == ex)
 
 
+@pytest.mark.parametrize("n,k,e,per_slot", [(4096, 6, 64, False), (8192, 8, 256, True), (37, 6, 64, True),
+                                             (64, 8, 5, False), (8193, 6, 64, False)])
+def test_group_slots_ws_matches_one_workgroup(hip_device, n, k, e, per_slot):
+    """tm_group_slots_ws (per-workgroup counts, then placement) against the
+    one-workgroup tm_group_slots on the same ids and mask: the same offsets
+    and tile list, and the same set of (token, slot) rows in each expert's
+    range (the order inside an expert is unspecified), ids out of range
+    skipped; 8193 tokens are past the multi-workgroup limit and take the
+    one-workgroup kernel."""
+    dev = hip_device
+    g = torch.Generator().manual_seed(41 + n + e)
+    ids = torch.randint(0, e, (n, k), generator=g)
+    ids[3 % n, 1] = -1
+    ids[5 % n, 0] = e
+    mask = (torch.rand(n, k, generator=g) < 0.6) if per_slot else (torch.rand(n, generator=g) < 0.6)
+    ids, m = ids.to(dev), mask.to(torch.uint8).to(dev)
+    ms_b, ms_s = (k, 1) if per_slot else (1, 0)
+    h = 128
+    so_b, so_s = k * h, h
+    t_max = N.lib().tm_group_slots_tiles(n * k, e)
+    nbytes = N.lib().tm_group_slots_workspace_size(n, k, e)
+    assert (nbytes > 0) == (n <= 8192)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    outs = []
+    for multi in (False, True):
+        offs = torch.full((e + 1,), -7, dtype=torch.int32, device=dev)
+        tiles = torch.full((2 + 2 * t_max,), -7, dtype=torch.int32, device=dev)
+        rt = torch.full((n * k,), -7, dtype=torch.int32, device=dev)
+        ro = torch.full((n * k,), -7, dtype=torch.int64, device=dev)
+        args = (N.ptr(ids), n, k, k, N.ptr(m), ms_b, ms_s, e, so_b, so_s, N.ptr(offs), N.ptr(rt), N.ptr(ro),
+                N.ptr(tiles))
+        if multi:
+            N.call("tm_group_slots_ws", *args, N.ptr(ws), ws.numel(), N.stream(dev))
+        else:
+            N.call("tm_group_slots", *args, N.stream(dev))
+        torch.cuda.synchronize()
+        outs.append((offs.cpu().numpy(), tiles.cpu().numpy(), rt.cpu().numpy(), ro.cpu().numpy()))
+    (o1, t1, rt1, ro1), (o2, t2, rt2, ro2) = outs
+    np.testing.assert_array_equal(o1, o2)
+    total, n_tiles = int(t1[0]), int(t1[1])
+    assert total == int(o1[e]) and total > 0
+    np.testing.assert_array_equal(t1[:2 + n_tiles], t2[:2 + n_tiles])
+    np.testing.assert_array_equal(t1[2 + t_max:2 + t_max + n_tiles], t2[2 + t_max:2 + t_max + n_tiles])
+    np.testing.assert_array_equal(rt2[:total], ro2[:total] // so_b)
+    for ex in range(e):
+        a, z = int(o1[ex]), int(o1[ex + 1])
+        assert sorted(ro1[a:z].tolist()) == sorted(ro2[a:z].tolist()), ex
+    # every selected pair once, in its expert's range
+    sel = (mask[:, None].expand(n, k) if not per_slot else mask) & (ids.cpu() >= 0) & (ids.cpu() < e)
+    assert total == int(sel.sum())
+
+
 def test_group_slots_empty_batch(hip_device):
     """An empty recompute batch (no tokens, null id/mask pointers) groups
     nothing: zero offsets and a zero row/tile count, and the grouped MLP after
