@@ -476,13 +476,15 @@ __device__ __forceinline__ uint32_t coh_add(uint32_t *p) {
 
 // Phase A of decode_fused_kernel: project_split_kernel's wave (hidden ==
 // 32 * kSlices * KPW).  fused_project_loads issues every operand load of
-// task `task` at once -- x, both modalities' P (so no load waits for the
-// modality byte) and the biases -- and fused_project_task multiplies,
-// publishes and, in the group's last wave, reduces; its hand-offs are
-// coherent stores, and that wave raises the group's q-ready flag.
+// task `task` at once -- x, the first modality's P (text with a modality
+// mask, vision without; no load waits for the modality byte) and the biases
+// -- and fused_project_task multiplies (loading the other modality's P only
+// when the tile holds a row of it), publishes and, in the group's last wave,
+// reduces; its hand-offs are coherent stores, and that wave raises the
+// group's q-ready flag.
 template <int DT, int KPW>
 struct ProjOps {
-  uint4 x[KPW], pv[KPW], pt[KPW];
+  uint4 x[KPW], p1[KPW];  // p1: the first modality's P (text with a modality mask, else vision)
   typename Elem<DT>::T bias_v, bias_t;  // raw: converted where used
   uint8_t vis;
 };
@@ -507,13 +509,14 @@ __device__ __forceinline__ void fused_project_loads(const FusedArgs &a, int64_t 
   const int col = cb * 16 + (lane & 15);
   o.bias_v = static_cast<const T *>(a.bv)[col];
   o.bias_t = static_cast<const T *>(a.bt)[col];
-  const uint4 *pvf = reinterpret_cast<const uint4 *>(a.pv) + lane;
-  const uint4 *ptf = reinterpret_cast<const uint4 *>(a.pt) + lane;
+  // the first modality's P only (text when there is a modality mask: decode
+  // batches are text; vision without one); fused_project_task loads the
+  // other when its tile holds a row of it
+  const uint4 *p1f = reinterpret_cast<const uint4 *>(a.is_vision ? a.pt : a.pv) + lane;
 #pragma unroll
   for (int j = 0; j < KPW; ++j) {
     o.x[j] = *reinterpret_cast<const uint4 *>(xrow + (ks_begin + j) * 32 + kq);
-    o.pv[j] = pvf[((int64_t)(ks_begin + j) * NCB + cb) * 64];
-    o.pt[j] = ptf[((int64_t)(ks_begin + j) * NCB + cb) * 64];
+    o.p1[j] = p1f[((int64_t)(ks_begin + j) * NCB + cb) * 64];
   }
 }
 
@@ -542,8 +545,19 @@ __device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t t
     for (int i = 0; i < 4; ++i)
       if ((rows_of_pass >> (4 * (lane >> 4) + i)) & 1u) fin[i] = acc[i];
   };
-  if (vis_bits) run_pass(o.pv, vis_bits);  // uniform branches
-  if (txt_bits) run_pass(o.pt, txt_bits);
+  // uniform branches: the first modality's rows from the loaded P; rows of
+  // the other (vision rows of a masked batch) after a load of its P
+  const uint32_t first_bits = a.is_vision ? txt_bits : vis_bits;
+  const uint32_t second_bits = a.is_vision ? vis_bits : 0u;
+  if (first_bits) run_pass(o.p1, first_bits);
+  if (second_bits) {
+    const int ks_begin = sl * KPW;
+    const uint4 *pvf = reinterpret_cast<const uint4 *>(a.pv) + lane;
+    uint4 p2[KPW];
+#pragma unroll
+    for (int j = 0; j < KPW; ++j) p2[j] = pvf[((int64_t)(ks_begin + j) * NCB + cb) * 64];
+    run_pass(p2, second_bits);
+  }
   const float bias_v = Elem<DT>::to_f(o.bias_v), bias_t = Elem<DT>::to_f(o.bias_t);
 
   // reset the tile's best keys (every replica) for phase B
