@@ -352,10 +352,12 @@ def test_engine_rejects_host_tensors():
 # ------------------------------------------------ mode G: gather + combine
 @pytest.mark.parametrize("k,nn,hidden,with_residual", [(8, 1, 2048, True), (8, 4, 2048, True), (8, 4, 1004, False),
                                                         (6, 1, 2560, True), (6, 4, 2560, False), (5, 2, 2048, True),
-                                                        (8, 1, 4096, False)])
+                                                        (8, 1, 4096, False), (8, 1, 8, True), (6, 4, 520, True),
+                                                        (8, 1, 8192, True), (6, 4, 8200, False)])
 def test_gather_combine_vs_oracle(hip_device, k, nn, hidden, with_residual):
-    """Shape-specialised kernels (top-8/top-6 x 1/4 nearest, 16-byte rows),
-    hidden sizes that take several or partial 2048-wide chunks, and the
+    """Shape-specialised kernels (top-8/top-6 x 1/4 nearest, 16-byte rows):
+    one 8-element chunk per thread up to hidden 8192 (a single chunk, a
+    partial last wave, 1024 threads), the chunk loop beyond it; and the
     general kernels (other shapes, unaligned rows)."""
     from table_moe.cache_engine import GlobalTable
 
