@@ -380,9 +380,11 @@ __global__ __launch_bounds__(64) void decode_finish_kernel(
 // One-launch decode plan (decode_fused_kernel): the three launches above as
 // three phases of one launch of kFusedWGs four-wave workgroups.  A phase
 // whose inputs come from other workgroups waits on a grid-wide flag.
-//   A  projection tasks (project_split_kernel's work; task t runs on wave
-//      t / G of workgroup t % G).  The last wave of a (tile, column block)
-//      group writes q and the block's |q|^2 and raises the group's flag; a
+//   A  projection (project_split_kernel's work): one row tile: (tile, column
+//      block) group g runs on workgroup G - 1 - g, two slices per wave, added
+//      through LDS; more rows: one slice per wave, spread over workgroups, the
+//      group's last wave adds the partials.  The wave that finishes a group
+//      writes q and the block's |q|^2 and raises the group's flag; a
 //      workgroup goes on once one wave saw every group's flag.
 //   B  workgroup s < nsplit searches split s (search_stream_kernel's work) and
 //      publishes its lists and best keys; every workgroup then counts itself
@@ -474,35 +476,44 @@ __device__ __forceinline__ uint32_t coh_add(uint32_t *p) {
   return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Phase A of decode_fused_kernel: project_split_kernel's wave (hidden ==
-// 32 * kSlices * KPW).  fused_project_loads issues every operand load of
-// task `task` at once -- x, the first modality's P (text with a modality
-// mask, vision without; no load waits for the modality byte) and the biases
-// -- and fused_project_task multiplies (loading the other modality's P only
-// when the tile holds a row of it), publishes and, in the group's last wave,
-// reduces; its hand-offs are coherent stores, and that wave raises the
+// Phase A of decode_fused_kernel: project_split_kernel's work (hidden ==
+// 32 * kSlices * KPW) in one of two layouts, chosen by the batch:
+//  - one row tile (n <= 16): (tile, column block) group g runs on one
+//    workgroup, wave w taking slices 2w and 2w + 1; the group's kSlices fp32
+//    partials are added in slice order through LDS and wave 0 finishes q.
+//  - more rows: one slice per wave, the slices of a group spread over
+//    workgroups; each publishes its partial by coherent stores and counts it
+//    on the group, and the group's last wave adds the partials in slice order
+//    and finishes q.  (A whole group on one workgroup moves 160 KB of operands
+//    through one CU at 16 real rows, which costs more than the hand-off.)
+// Both add the same partials in the same order: the same q, bit for bit.
+// fused_project_loads issues every operand load of the wave at once -- x, the
+// first modality's P (text with a modality mask, vision without; no load waits
+// for the modality byte) and the biases -- and fused_project_task multiplies
+// (loading the other modality's P only when the tile holds a row of it),
+// reduces, writes q and the block's |q|^2 by coherent stores and raises the
 // group's q-ready flag.
-template <int DT, int KPW>
+template <int DT, int KPW, bool OT>
 struct ProjOps {
-  uint4 x[KPW], p1[KPW];  // p1: the first modality's P (text with a modality mask, else vision)
+  static constexpr int NK = OT ? 2 * KPW : KPW;  // k-steps per wave: two slices in the one-tile layout
+  uint4 x[NK], p1[NK];  // p1: the first modality's P (text with a modality mask, else vision)
   typename Elem<DT>::T bias_v, bias_t;  // raw: converted where used
   uint8_t vis;
 };
 
-template <int DT, int DIM, int KPW>
-__device__ __forceinline__ void fused_project_loads(const FusedArgs &a, int64_t task, int lane, ProjOps<DT, KPW> &o) {
+// k-steps ks0 .. ks0 + NK - 1 of group g
+template <int DT, int DIM, int KPW, bool OT>
+__device__ __forceinline__ void fused_project_loads(const FusedArgs &a, int64_t g, int ks0, int lane,
+                                                    ProjOps<DT, KPW, OT> &o) {
+  constexpr int NK = ProjOps<DT, KPW, OT>::NK;
   using T = typename Elem<DT>::T;
   constexpr int NCB = DIM / 16;
-  constexpr int S = kSlices;
   const int64_t n = a.n;
-  const int sl = (int)(task % S);
-  const int64_t g = task / S;
   const int cb = (int)(g % NCB);
   const int64_t arow = (g / NCB) * 16 + (lane & 15);
   const bool arow_ok = arow < n;
   const T *x = static_cast<const T *>(a.x);
   const T *xrow = x + (arow_ok ? arow : 0) * a.ld_x;
-  const int ks_begin = sl * KPW;
   const int kq = 8 * (lane >> 4);
   const uint8_t *vsrc = a.is_vision ? a.is_vision + (arow_ok ? arow : 0) : reinterpret_cast<const uint8_t *>(x);
   o.vis = *vsrc;
@@ -514,36 +525,45 @@ __device__ __forceinline__ void fused_project_loads(const FusedArgs &a, int64_t 
   // other when its tile holds a row of it
   const uint4 *p1f = reinterpret_cast<const uint4 *>(a.is_vision ? a.pt : a.pv) + lane;
 #pragma unroll
-  for (int j = 0; j < KPW; ++j) {
-    o.x[j] = *reinterpret_cast<const uint4 *>(xrow + (ks_begin + j) * 32 + kq);
-    o.p1[j] = p1f[((int64_t)(ks_begin + j) * NCB + cb) * 64];
+  for (int j = 0; j < NK; ++j) {
+    o.x[j] = *reinterpret_cast<const uint4 *>(xrow + (ks0 + j) * 32 + kq);
+    o.p1[j] = p1f[((int64_t)(ks0 + j) * NCB + cb) * 64];
   }
 }
 
-template <int DT, int DIM, int KPW>
-__device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t task, uint32_t g0v, int lane,
-                                                   const ProjOps<DT, KPW> &o) {
+// OT: the one-tile layout (every wave of the workgroup calls it: it holds a
+// barrier), `sw` = the wave; else slice `sw` of the spread layout.
+template <int DT, int DIM, int KPW, bool OT>
+__device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t g, int sw, uint32_t g0v, int lane,
+                                                   const ProjOps<DT, KPW, OT> &o, tm_f32x4 (*red)[64]) {
+  constexpr int NK = ProjOps<DT, KPW, OT>::NK;
+  constexpr bool two = OT;
   using T = typename Elem<DT>::T;
   constexpr int NCB = DIM / 16;
   constexpr int S = kSlices;
+  static_assert(S == 8 && kKeyRep == S, "4 waves x 2 slices; slice s resets key replica s");
   const int64_t n = a.n;
-  const int sl = (int)(task % S);
-  const int64_t g = task / S;
   const int cb = (int)(g % NCB);
   const int64_t row0 = (g / NCB) * 16;
   const int64_t arow = row0 + (lane & 15);
   const bool arow_ok = arow < n;
+  const int sl0 = two ? 2 * sw : sw;  // first slice of this wave
   const int amod = !arow_ok ? 2 : ((a.is_vision == nullptr || o.vis) ? 0 : 1);
   const uint32_t vis_bits = (uint32_t)(__ballot(amod == 0) & 0xFFFFull);
   const uint32_t txt_bits = (uint32_t)(__ballot(amod == 1) & 0xFFFFull);
-  tm_f32x4 fin = tm_f32x4{0.f, 0.f, 0.f, 0.f};
-  auto run_pass = [&](const uint4 (&br)[KPW], uint32_t rows_of_pass) {
-    tm_f32x4 acc = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+  tm_f32x4 fin[2];
+  fin[0] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+  fin[1] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
+  auto run_pass = [&](const uint4 (&br)[NK], uint32_t rows_of_pass) {
 #pragma unroll
-    for (int j = 0; j < KPW; ++j) acc = tm_mfma16x16x32<DT>(o.x[j], br[j], acc);
+    for (int h = 0; h < NK / KPW; ++h) {  // one fp32 partial per slice, as project_split_kernel's waves
+      tm_f32x4 acc = tm_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if ((rows_of_pass >> (4 * (lane >> 4) + i)) & 1u) fin[i] = acc[i];
+      for (int j = 0; j < KPW; ++j) acc = tm_mfma16x16x32<DT>(o.x[h * KPW + j], br[h * KPW + j], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if ((rows_of_pass >> (4 * (lane >> 4) + i)) & 1u) fin[h][i] = acc[i];
+    }
   };
   // uniform branches: the first modality's rows from the loaded P; rows of
   // the other (vision rows of a masked batch) after a load of its P
@@ -551,46 +571,62 @@ __device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t t
   const uint32_t second_bits = a.is_vision ? vis_bits : 0u;
   if (first_bits) run_pass(o.p1, first_bits);
   if (second_bits) {
-    const int ks_begin = sl * KPW;
+    const int ks0 = sl0 * KPW;
     const uint4 *pvf = reinterpret_cast<const uint4 *>(a.pv) + lane;
-    uint4 p2[KPW];
+    uint4 p2[NK];
 #pragma unroll
-    for (int j = 0; j < KPW; ++j) p2[j] = pvf[((int64_t)(ks_begin + j) * NCB + cb) * 64];
+    for (int j = 0; j < NK; ++j) p2[j] = pvf[((int64_t)(ks0 + j) * NCB + cb) * 64];
     run_pass(p2, second_bits);
   }
-  const float bias_v = Elem<DT>::to_f(o.bias_v), bias_t = Elem<DT>::to_f(o.bias_t);
 
-  // reset the tile's best keys (every replica) for phase B
-  if (cb == 0 && lane < 16 && arow_ok)
-    for (int r = sl; r < kKeyRep; r += S) coh_st(a.keys + (int64_t)r * n + arow, ~0ull);
-
-  // publish this slice's partial, count it on the group
-  uint64_t *pp = reinterpret_cast<uint64_t *>(a.part) + ((g * S + sl) * 64 + lane) * 2;
-  coh_st(pp, ((uint64_t)__float_as_uint(fin[1]) << 32) | __float_as_uint(fin[0]));
-  coh_st(pp + 1, ((uint64_t)__float_as_uint(fin[3]) << 32) | __float_as_uint(fin[2]));
-  __builtin_amdgcn_s_waitcnt(0);
-  uint32_t ticket = 0;
-  if (lane == 0) ticket = coh_add(a.sync + kWGrp + g * kLine);
-  ticket = (uint32_t)__builtin_amdgcn_readfirstlane((int)ticket);
-  if (ticket != S - 1) return;  // uniform: not the group's last slice
-  if (lane == 0) coh_st32(a.sync + kWGrp + g * kLine, 0u);
-
-  // the group's last wave: the S partials added in slice order, bias, one rounding
-  uint64_t pv2[S][2];
-#pragma unroll
-  for (int s2 = 0; s2 < S; ++s2) {
-    const uint64_t *src = reinterpret_cast<const uint64_t *>(a.part) + ((g * S + s2) * 64 + lane) * 2;
-    pv2[s2][0] = coh_ld(src);
-    pv2[s2][1] = coh_ld(src + 1);
+  // reset the tile's best keys (replica s for slice s) for phase B
+  if (cb == 0 && lane < 16 && arow_ok) {
+    coh_st(a.keys + (int64_t)sl0 * n + arow, ~0ull);
+    if constexpr (two) coh_st(a.keys + (int64_t)(sl0 + 1) * n + arow, ~0ull);
   }
   float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (two) {
+    red[sl0][lane] = fin[0];
+    red[sl0 + 1][lane] = fin[1];
+    __builtin_amdgcn_s_waitcnt(0);  // the key resets acknowledged before the group's flag
+    __syncthreads();
+    if (sw != 0) return;
+    // wave 0: the S partials added in slice order
 #pragma unroll
-  for (int s2 = 0; s2 < S; ++s2) {
-    v[0] += __uint_as_float((uint32_t)pv2[s2][0]);
-    v[1] += __uint_as_float((uint32_t)(pv2[s2][0] >> 32));
-    v[2] += __uint_as_float((uint32_t)pv2[s2][1]);
-    v[3] += __uint_as_float((uint32_t)(pv2[s2][1] >> 32));
+    for (int s2 = 0; s2 < S; ++s2) {
+      const tm_f32x4 p = red[s2][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += p[i];
+    }
+  } else {
+    // publish this slice's partial, count it on the group
+    uint64_t *pp = reinterpret_cast<uint64_t *>(a.part) + ((g * S + sl0) * 64 + lane) * 2;
+    coh_st(pp, ((uint64_t)__float_as_uint(fin[0][1]) << 32) | __float_as_uint(fin[0][0]));
+    coh_st(pp + 1, ((uint64_t)__float_as_uint(fin[0][3]) << 32) | __float_as_uint(fin[0][2]));
+    __builtin_amdgcn_s_waitcnt(0);
+    uint32_t ticket = 0;
+    if (lane == 0) ticket = coh_add(a.sync + kWGrp + g * kLine);
+    ticket = (uint32_t)__builtin_amdgcn_readfirstlane((int)ticket);
+    if (ticket != S - 1) return;  // uniform: not the group's last slice
+    if (lane == 0) coh_st32(a.sync + kWGrp + g * kLine, 0u);
+    // the group's last wave: the S partials added in slice order
+    uint64_t pv2[S][2];
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) {
+      const uint64_t *src = reinterpret_cast<const uint64_t *>(a.part) + ((g * S + s2) * 64 + lane) * 2;
+      pv2[s2][0] = coh_ld(src);
+      pv2[s2][1] = coh_ld(src + 1);
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2) {
+      v[0] += __uint_as_float((uint32_t)pv2[s2][0]);
+      v[1] += __uint_as_float((uint32_t)(pv2[s2][0] >> 32));
+      v[2] += __uint_as_float((uint32_t)pv2[s2][1]);
+      v[3] += __uint_as_float((uint32_t)(pv2[s2][1] >> 32));
+    }
   }
+  // bias, one rounding
+  const float bias_v = Elem<DT>::to_f(o.bias_v), bias_t = Elem<DT>::to_f(o.bias_t);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * (lane >> 4) + i;
@@ -621,7 +657,7 @@ __device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t t
   if (lane == 0) coh_st32(a.sync + kWFlagA + g * kLine, gen + 1);
 }
 
-template <int DT, int DIM, int KPW, int K, int TK>
+template <int DT, int DIM, int KPW, int K, int TK, bool OT>
 __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   using T = typename Elem<DT>::T;
   constexpr int KS = DIM / 16;
@@ -630,6 +666,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   constexpr int NN = K;
   __shared__ uint64_t merge_buf[4][K][64];
   __shared__ uint4 q_lds[64 * DIM / 8];
+  __shared__ tm_f32x4 red[kSlices][64];  // the projection group's slice partials
   __shared__ uint32_t s_ok;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -644,19 +681,21 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   // finishing task's rows, then this call's generation.  Every one is
   // unconditional (clamped or redirected addresses): a load under a branch
   // makes the compiler wait for it, and for all loads before it, right there.
-  // Task of (wave, workgroup): position L = wave * G + wg holds group
+  // Projection, one row tile (n <= 16): group ga = G - 1 - wg (16-row tile,
+  // 16-column block) on the last workgroups (the finishing tasks, and the
+  // routing they do, start at workgroup 0), two slices per wave.  More rows:
+  // task of (wave, workgroup): position L = wave * G + wg holds group
   // 8 (L / 64) + L % 8, slice (L / 8) % 8, so a group's S slices run on
   // workgroups congruent mod 8 (one XCD under the dispatcher's round robin).
-  // Measured against consecutive slices on 8 XCDs: 0.1 us faster at N = 1,
-  // the same at N = 8 and 32 -- the hand-offs' coherent accesses go to the
-  // point of coherence from any XCD.
+  static_assert(S == 8 && NCB == 8, "64 slices per row tile");
+  constexpr bool one_tile = OT;  // the launch picks it: n <= 16
   const int64_t la = (int64_t)wave * G + wg;
   const int64_t ta = (8 * (la / 64) + la % 8) * S + (la / 8) % 8;
-  const int64_t ta_n = ((n + 15) / 16) * NCB * S;
-  static_assert(S == 8 && NCB == 8, "64 tasks per row tile");
-  const bool has_a = ta < ta_n;  // uniform per wave
-  ProjOps<DT, KPW> po;
-  if (has_a) fused_project_loads<DT, DIM, KPW>(a, ta, lane, po);
+  const int64_t ga = one_tile ? (int64_t)(G - 1 - wg) : ta / S;
+  const int sw = one_tile ? wave : (int)(ta % S);
+  const bool has_a = one_tile ? ga < NCB : ta < ((n + 15) / 16) * NCB * S;  // uniform per wave
+  ProjOps<DT, KPW, OT> po;
+  if (has_a) fused_project_loads<DT, DIM, KPW, OT>(a, ga, (one_tile ? 2 * sw : sw) * KPW, lane, po);
 
   const bool has_split = wg < a.nsplit;  // uniform
   const int64_t c_begin = (int64_t)wg * kStreamChunkD;
@@ -706,7 +745,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   auto g0 = [&] { return (uint32_t)__builtin_amdgcn_readfirstlane((int)g0v); };
 
   // ---- phase A: projection task ----
-  if (has_a) fused_project_task<DT, DIM, KPW>(a, ta, g0v, lane, po);
+  if (has_a) fused_project_task<DT, DIM, KPW, OT>(a, ga, sw, g0v, lane, po, red);
   if (!a.l2) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) pen[i] = 0.f;
@@ -1164,7 +1203,10 @@ void launch_fused(const tm_table_layer *t, const tm_layer_io *io, const tm_decod
   a.out_qn = io->q_sqnorm;
   a.out_keep = io->keep;
   a.sync = w.cnt;
-  hipLaunchKernelGGL((decode_fused_kernel<DT, 128, KPW, K, TK>), dim3(kFusedWGs), dim3(256), 0, s, a);
+  if (a.n <= 16)  // one row tile: the projection groups reduce in LDS
+    hipLaunchKernelGGL((decode_fused_kernel<DT, 128, KPW, K, TK, true>), dim3(kFusedWGs), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_fused_kernel<DT, 128, KPW, K, TK, false>), dim3(kFusedWGs), dim3(256), 0, s, a);
 }
 
 template <int DT, int KPW>

@@ -755,7 +755,7 @@ def _gen_word(table):
 @pytest.mark.parametrize("cfg,n,nn,variant", [
     (3, 1, 4, "base"), (3, 8, 4, "base"), (3, 32, 4, "base"), (3, 33, 1, "mix"), (3, 64, 4, "mix"),
     (5, 17, 4, "base"), (5, 64, 1, "nores"), (3, 24, 4, "fp16"), (3, 40, 4, "dot"), (3, 32, 4, "small_c"),
-    (5, 5, 1, "fp16")])
+    (5, 5, 1, "fp16"), (3, 12, 4, "mix"), (5, 16, 1, "mix")])
 def test_decode_one_launch_matches_three_launches(hip_device, cfg, n, nn, variant):
     """Decode batches with d = 128, hidden 2048 or 2560 and at most 128
     search splits run as one launch whose three phases hand q and the search
@@ -764,9 +764,11 @@ def test_decode_one_launch_matches_three_launches(hip_device, cfg, n, nn, varian
     in a row on one workspace (new tokens each call: the flags' generation
     advances every call), the one-launch plan really ran (its generation word
     counts the calls), and no bounded wait ran out.  Covers 1 to 64 tokens
-    (one and two query slabs), top-1 and top-4, 64 and 128 experts (top-6 and
-    top-8), mixed modalities, no residual, fp16, the dot metric and a table of
-    8 splits (most workgroups idle in the search phase)."""
+    (one and two query slabs; one row tile, whose projection groups reduce in
+    LDS, and more, whose slices reduce through device memory), top-1 and
+    top-4, 64 and 128 experts (top-6 and top-8), mixed modalities in both
+    projection layouts, no residual, fp16, the dot metric and a table of 8
+    splits (most workgroups idle in the search phase)."""
     from table_moe.cache_engine import GlobalTable
     from synth import make_workload
 
