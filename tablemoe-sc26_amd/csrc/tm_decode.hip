@@ -227,6 +227,55 @@ __device__ __forceinline__ void merge_min_k(uint64_t (&a)[K], const uint64_t (&b
       }
 }
 
+// Wave minimum of a 64-bit value, in every lane: DPP exchanges inside each
+// 16-lane row (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror: every lane then holds its row's minimum), then the four row
+// minima read into scalars.  Every lane of the wave must call it.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_min64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  return o < v ? o : v;
+}
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+  v = dpp_min64<0xB1>(v);
+  v = dpp_min64<0x4E>(v);
+  v = dpp_min64<0x141>(v);
+  v = dpp_min64<0x140>(v);
+  uint64_t m = ~0ull;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint64_t x = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r) |
+                       ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 16 * r) << 32);
+    m = x < m ? x : m;
+  }
+  return m;
+}
+
+// The K smallest keys of the wave, ascending, in every lane, from each lane's
+// ascending K-list: K rounds of a wave minimum over the lists' heads, the lane
+// that holds it popping its head.  Keys are unique (the centroid index is the
+// low word), so one lane pops; empty entries (~0) pop in every lane holding
+// one and stay ~0.  The same K keys as a merge of all the lists.
+template <int K>
+__device__ __forceinline__ void wave_min_k(uint64_t (&l)[K]) {
+  uint64_t top[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const uint64_t m = wave_min_u64(l[0]);
+    top[j] = m;
+    if (j + 1 < K) {
+      const bool pop = l[0] == m;
+#pragma unroll
+      for (int i = 0; i + 1 < K; ++i) l[i] = pop ? l[i + 1] : l[i];
+      l[K - 1] = pop ? ~0ull : l[K - 1];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j) l[j] = top[j];
+}
+
 template <int DT, int TK, int NN, int NCB, int ML>
 __global__ __launch_bounds__(64) void decode_finish_kernel(
     int64_t n, int hidden, int n_chunks, const uint64_t *__restrict__ keys, const float *__restrict__ qn_blk,
@@ -302,13 +351,7 @@ __global__ __launch_bounds__(64) void decode_finish_kernel(
 
   // top-NN keys of token b
   if constexpr (K > 1) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      uint64_t other[K];
-#pragma unroll
-      for (int j = 0; j < K; ++j) other[j] = __shfl_xor(lst[j], o, 64);
-      merge_min_k<K>(lst, other);
-    }
+    wave_min_k<K>(lst);
   } else {
     lst[0] = (uint64_t)__builtin_amdgcn_readlane((int)(uint32_t)kj, b) |
              ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(kj >> 32), b) << 32);
@@ -982,13 +1025,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   const bool kept = n_keep >= n ? true : (n_keep <= 0 ? false : rank < n_keep);
 
   if constexpr (K > 1) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      uint64_t other[K];
-#pragma unroll
-      for (int j = 0; j < K; ++j) other[j] = __shfl_xor(lst[j], o, 64);
-      merge_min_k<K>(lst, other);
-    }
+    wave_min_k<K>(lst);
   } else {
     lst[0] = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)kj, b) |
              ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(kj >> 32), b) << 32);
