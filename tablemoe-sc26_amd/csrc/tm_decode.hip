@@ -584,7 +584,7 @@ __device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t g
   using T = typename Elem<DT>::T;
   constexpr int NCB = DIM / 16;
   constexpr int S = kSlices;
-  static_assert(S == 8 && kKeyRep == S, "4 waves x 2 slices; slice s resets key replica s");
+  static_assert(S == 8, "4 waves x 2 slices");
   const int64_t n = a.n;
   const int cb = (int)(g % NCB);
   const int64_t row0 = (g / NCB) * 16;
@@ -622,18 +622,21 @@ __device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t g
     run_pass(p2, second_bits);
   }
 
-  // reset the tile's best keys (replica s for slice s) for phase B
-  if (cb == 0 && lane < 16 && arow_ok) {
-    coh_st(a.keys + (int64_t)sl0 * n + arow, ~0ull);
-    if constexpr (two) coh_st(a.keys + (int64_t)(sl0 + 1) * n + arow, ~0ull);
-  }
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   if constexpr (two) {
     red[sl0][lane] = fin[0];
     red[sl0 + 1][lane] = fin[1];
-    __builtin_amdgcn_s_waitcnt(0);  // the key resets acknowledged before the group's flag
     __syncthreads();
     if (sw != 0) return;
+    // the tile's best keys (every replica) reset for phase B, acknowledged
+    // with q before the group's flag
+    if (cb == 0) {
+#pragma unroll
+      for (int e = lane; e < 16 * kKeyRep; e += 64) {
+        const int64_t r = row0 + (e & 15);
+        if (r < n) coh_st(a.keys + (int64_t)(e >> 4) * n + r, ~0ull);
+      }
+    }
     // wave 0: the S partials added in slice order
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2) {
@@ -642,6 +645,10 @@ __device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t g
       for (int i = 0; i < 4; ++i) v[i] += p[i];
     }
   } else {
+    // reset the tile's best keys (replicas s, s + S, ... for slice s) for
+    // phase B, acknowledged with the partial before the count
+    if (cb == 0 && lane < 16 && arow_ok)
+      for (int r = sl0; r < kKeyRep; r += S) coh_st(a.keys + (int64_t)r * n + arow, ~0ull);
     // publish this slice's partial, count it on the group
     uint64_t *pp = reinterpret_cast<uint64_t *>(a.part) + ((g * S + sl0) * 64 + lane) * 2;
     coh_st(pp, ((uint64_t)__float_as_uint(fin[0][1]) << 32) | __float_as_uint(fin[0][0]));
