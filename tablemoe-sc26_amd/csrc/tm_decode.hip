@@ -142,7 +142,7 @@ __global__ __launch_bounds__(64) void project_split_kernel(
 
   // reset the tile's best keys (every replica) for the search launch
   if (cb == 0 && lane < 16 && arow_ok)
-    for (int r = sl; r < kKeyRep; r += S) keys[(int64_t)r * n + arow] = ~0ull;
+    for (int r = sl; r < kKeyRep; r += S) keys[(int64_t)r * tm_key_stride(n) + arow] = ~0ull;
 
   // Publish this slice's 16 x 16 partial (fragment order), then count the
   // arrival.  The partials and the counter move through agent-scope relaxed
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(64) void decode_finish_kernel(
   const int jl = lane < n ? lane : (int)n - 1;
   uint64_t kr[kKeyRep];
 #pragma unroll
-  for (int r = 0; r < kKeyRep; ++r) kr[r] = keys[(int64_t)r * n + jl];
+  for (int r = 0; r < kKeyRep; ++r) kr[r] = keys[(int64_t)r * tm_key_stride(n) + jl];
   float qb[NCB];
 #pragma unroll
   for (int c = 0; c < NCB; c += 4) {
@@ -634,7 +634,7 @@ __device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t g
 #pragma unroll
       for (int e = lane; e < 16 * kKeyRep; e += 64) {
         const int64_t r = row0 + (e & 15);
-        if (r < n) coh_st(a.keys + (int64_t)(e >> 4) * n + r, ~0ull);
+        if (r < n) coh_st(a.keys + (int64_t)(e >> 4) * tm_key_stride(n) + r, ~0ull);
       }
     }
     // wave 0: the S partials added in slice order
@@ -648,7 +648,7 @@ __device__ __forceinline__ void fused_project_task(const FusedArgs &a, int64_t g
     // reset the tile's best keys (replicas s, s + S, ... for slice s) for
     // phase B, acknowledged with the partial before the count
     if (cb == 0 && lane < 16 && arow_ok)
-      for (int r = sl0; r < kKeyRep; r += S) coh_st(a.keys + (int64_t)r * n + arow, ~0ull);
+      for (int r = sl0; r < kKeyRep; r += S) coh_st(a.keys + (int64_t)r * tm_key_stride(n) + arow, ~0ull);
     // publish this slice's partial, count it on the group
     uint64_t *pp = reinterpret_cast<uint64_t *>(a.part) + ((g * S + sl0) * 64 + lane) * 2;
     coh_st(pp, ((uint64_t)__float_as_uint(fin[0][1]) << 32) | __float_as_uint(fin[0][0]));
@@ -942,7 +942,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
 #pragma unroll
           for (int j = 0; j < K; ++j) coh_st(dst + j, l[j]);
         }
-        atomicMin(reinterpret_cast<unsigned long long *>(a.keys + (int64_t)(wg % kKeyRep) * n + r),
+        atomicMin(reinterpret_cast<unsigned long long *>(a.keys + (int64_t)(wg % kKeyRep) * tm_key_stride(n) + r),
                   (unsigned long long)l[0]);
       }
     }
@@ -987,7 +987,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   const int jl = lane < n ? lane : (int)n - 1;
   uint64_t kr[kKeyRep];
 #pragma unroll
-  for (int r = 0; r < kKeyRep; ++r) kr[r] = coh_ld(a.keys + (int64_t)r * n + jl);
+  for (int r = 0; r < kKeyRep; ++r) kr[r] = coh_ld(a.keys + (int64_t)r * tm_key_stride(n) + jl);
   float qb[NCB];
 #pragma unroll
   for (int c = 0; c < NCB; c += 2) {
@@ -1281,7 +1281,7 @@ bool rows16(const void *base, int64_t ld) {
 }  // namespace
 
 size_t tm_internal_decode_qn_floats(int64_t n, int32_t dim) { return (size_t)n * (size_t)(dim / 16); }
-size_t tm_internal_decode_keys(int64_t n) { return (size_t)kKeyRep * (size_t)n; }
+size_t tm_internal_decode_keys(int64_t n) { return (size_t)kKeyRep * (size_t)tm_key_stride(n); }
 size_t tm_internal_decode_part_bytes(int64_t n, int32_t dim) {
   return (size_t)tm_cdiv(n, 16) * (size_t)(dim / 16) * kSlices * 64 * sizeof(float4);
 }

@@ -95,11 +95,16 @@ __attribute__((visibility("hidden"))) int tm_internal_keep_keys(const uint64_t *
                                                                 int64_t *out_idx, float *out_qn,
                                                                 uint8_t *out_keep, hipStream_t stream);
 
+// Leading dimension of the decode plan's best-key replicas: each replica
+// starts on a 128-byte line of its own (16 keys), so the atomic minima on
+// different replicas never meet on one line.
+__host__ __device__ inline int64_t tm_key_stride(int64_t n) { return (n + 15) / 16 * 16; }
+
 // Decode plan, search stage: the small-batch stream kernel (n <= 64) alone.
 // Split s writes the sorted top-k lists of its centroid range into
 // lists[(s * n + r) * list_len] and the best key of each query into
-// keys[(s % key_rep) * n + r] by atomic minimum (every replica reset to ~0
-// beforehand).  tm_internal_stream_nsplit gives the split count (0 when the
+// keys[(s % key_rep) * tm_key_stride(n) + r] by atomic minimum (every replica
+// reset to ~0 beforehand).  tm_internal_stream_nsplit gives the split count (0 when the
 // shape is not a stream shape); list_len is 1, 4 or 8 for top_k 1, 2..4, 5..8.
 __attribute__((visibility("hidden"))) int64_t tm_internal_stream_nsplit(int64_t n, int64_t n_cent, int32_t dim,
                                                                         int32_t top_k);

@@ -1123,7 +1123,8 @@ __global__ __launch_bounds__(kThreads) void search_stream_kernel(
       for (int j = 0; j < K; ++j) dst[j] = l[j];
       // the query's best key over the splits of replica split % key_rep (reset to ~0 before the launch)
       if (keys != nullptr)
-        atomicMin(reinterpret_cast<unsigned long long *>(keys + (split % key_rep) * n + r), (unsigned long long)l[0]);
+        atomicMin(reinterpret_cast<unsigned long long *>(keys + (split % key_rep) * tm_key_stride(n) + r),
+                  (unsigned long long)l[0]);
     }
   }
 }
