@@ -819,6 +819,39 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
       }
     }
   }
+  // A kept token's row chunk: the residual plus its recomputed slot rows
+  // weighted by the renormalised router weights.
+  T *const dst = static_cast<T *>(a.out) + (int64_t)b * a.ld_o + hl;
+  auto kept_row = [&](float (&acc)[8]) {
+    const T *e = reinterpret_cast<const T *>(&rrow);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = a.has_res ? Elem<DT>::to_f(e[i]) : 0.f;
+    float sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < TK; ++s) sum += wv[s];
+    const bool any = sum > 0.f;
+    float coef[TK];
+#pragma unroll
+    for (int s = 0; s < TK; ++s) coef[s] = wv[s] / sum;
+    if (any) {
+#pragma unroll
+      for (int s = 0; s < TK; ++s) {
+        const T *es = reinterpret_cast<const T *>(&srow[s]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], Elem<DT>::to_f(es[i]), acc[i]);
+      }
+    }
+  };
+  // Every token kept (n_keep >= n, as for one token at the reference keep
+  // rates): the rows need nothing from the search, so the finishing waves
+  // store them now; after the waits only chunk 0 of each token writes the
+  // search outputs (and a wait that ran out rewrites the rows as NaN).
+  const bool all_kept = a.n_keep >= n;  // uniform
+  if (has_c && all_kept) {
+    float acc[8];
+    kept_row(acc);
+    if (h0 < a.hidden) tm_store8_nt<DT>(dst, acc);
+  }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t cm = c0 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
@@ -982,6 +1015,15 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
   __syncthreads();
   poison = poison || s_ok == 0u;
   if (!has_c) return;  // uniform per wave
+  if (all_kept && ch != 0) {  // the row chunk is stored
+    if (poison && h0 < a.hidden) {
+      float nan8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) nan8[i] = __builtin_nanf("");
+      tm_store8_nt<DT>(dst, nan8);
+    }
+    return;
+  }
 
   // ---- phase C: token b, row chunk ch ----
   const int jl = lane < n ? lane : (int)n - 1;
@@ -1052,30 +1094,16 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(FusedArgs a) {
     a.out_qn[b] = qn_b;
   }
 
+  if (all_kept && !poison) return;  // the row chunk is stored
   float acc[8];
-  {
-    const T *e = reinterpret_cast<const T *>(&rrow);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = a.has_res ? Elem<DT>::to_f(e[i]) : 0.f;
-  }
-  T *dst = static_cast<T *>(a.out) + (int64_t)b * a.ld_o + hl;
   if (kept) {  // uniform
-    float sum = 0.f;
-#pragma unroll
-    for (int s = 0; s < TK; ++s) sum += wv[s];
-    const bool any = sum > 0.f;
-    float coef[TK];
-#pragma unroll
-    for (int s = 0; s < TK; ++s) coef[s] = wv[s] / sum;
-    if (any) {
-#pragma unroll
-      for (int s = 0; s < TK; ++s) {
-        const T *e = reinterpret_cast<const T *>(&srow[s]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = fmaf(coef[s], Elem<DT>::to_f(e[i]), acc[i]);
-      }
-    }
+    kept_row(acc);
   } else {
+    {
+      const T *e = reinterpret_cast<const T *>(&rrow);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = a.has_res ? Elem<DT>::to_f(e[i]) : 0.f;
+    }
     const T *values = static_cast<const T *>(a.values);
     const T *src[NN];
     float coef[NN];
