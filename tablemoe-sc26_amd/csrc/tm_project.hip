@@ -548,22 +548,29 @@ __global__ __launch_bounds__(256, 2) void project_cols_kernel(
 // 384 KiB).  The groups' partial |q|^2 are subtrees of the direct kernel's
 // lane tree either way (8 or 4 lanes of 8 columns), so qn_sum adds them to
 // the same bits.
-template <int DT, int DIM, int RVPL, int NCH, int CB>
+template <int DT, int DIM, int RVPL, int NCH, int CB, int RB = 2>
 __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
     const typename Elem<DT>::T *__restrict__ x, int64_t n, int hidden, int64_t ld_x,
     const uint8_t *__restrict__ is_vision, const typename Elem<DT>::T *__restrict__ pv,
     const typename Elem<DT>::T *__restrict__ bv, const typename Elem<DT>::T *__restrict__ pt,
     const typename Elem<DT>::T *__restrict__ bt, typename Elem<DT>::T *__restrict__ q, int64_t ld_q,
-    float *__restrict__ qn_part, uint64_t *__restrict__ keys, int64_t n_tiles, ColsRoute cr) {
+    float *__restrict__ qn_part, uint64_t *__restrict__ keys, int64_t n_tiles, ColsRoute cr, int normalize,
+    float eps, float *__restrict__ q_sqnorm) {
   using T = typename Elem<DT>::T;
   constexpr int G = DIM / (16 * CB);  // column groups
   constexpr int NCB = ColsCfg<DIM>::NCB;
   static_assert(NCH >= 1 && NCH <= 8, "chunks per wave");
   constexpr int kRowPad = 64 + 4;
-  static_assert(DIM == 128 && (CB == 4 || CB == 2), "CB column blocks of 1 KiB per k-step and wave");
+  static_assert((DIM == 128 && (CB == 4 || CB == 2)) || (DIM == 64 && CB == 4),
+                "CB column blocks of 1 KiB per k-step and wave");
   constexpr int TPRW = 2 * CB;  // epilogue threads per row (8 columns each)
-  // per wave: 2 ring slots of 32 rows x 16 x 16 bytes; the wave partials
-  // (32 x kRowPad floats) reuse the wave's own slots after its last chunk
+  static_assert(RB == 1 || RB == 2, "16 or 32 rows per tile");
+  constexpr int TR = 16 * RB;    // rows per tile
+  constexpr int XS = TR * 16;    // 16-byte chunks per ring slot (TR rows x 4 k-steps)
+  constexpr int NXL = 4 * RB;    // x loads per chunk and wave (4 rows each)
+  // per wave: 2 ring slots of up to 32 rows x 16 x 16 bytes; the wave
+  // partials (TR x kRowPad floats) reuse the wave's own slots after its last
+  // chunk
   __shared__ uint4 ring[4][2 * 512];
   static_assert(32 * kRowPad * 4 <= 2 * 512 * 16, "partials fit the wave's ring");
 
@@ -582,7 +589,7 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
 
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t row0 = tile * 32;
+  const int64_t row0 = tile * TR;
 
   const int ks_begin = wave * 4 * NCH;  // hidden == 512 * NCH (checked by the launcher)
 
@@ -597,24 +604,24 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
   const uint32_t lds_w = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&ring[wave][0]);
   auto issue_x = [&](int c) {  // chunk c into slot c & 1: load i brings rows 4i .. 4i + 3
 #pragma unroll
-    for (int i = 0; i < 8; ++i) tm_dma16_s(x_src(i, c), lds_w + (uint32_t)(((c & 1) * 512 + 64 * i) * 16));
+    for (int i = 0; i < NXL; ++i) tm_dma16_s(x_src(i, c), lds_w + (uint32_t)(((c & 1) * XS + 64 * i) * 16));
   };
   auto read_a = [&](int c, int rb, int t) {  // A fragment of k-step t of chunk c, rows 16*rb + lane%16
     const int r = 16 * rb + (lane & 15);
-    return ring[wave][(c & 1) * 512 + r * 16 + ((4 * t + (lane >> 4)) ^ (r & 15))];
+    return ring[wave][(c & 1) * XS + r * 16 + ((4 * t + (lane >> 4)) ^ (r & 15))];
   };
 
   // modality byte of row (lane & 31), then the first two x chunks; the byte
-  // is in once at most 8 * X0 loads remain outstanding
+  // is in once at most NXL * X0 loads remain outstanding
   const int64_t vr = row0 + (lane & 31);
-  const bool vr_ok = vr < n;
+  const bool vr_ok = (lane & 31) < TR && vr < n;
   const uint8_t *vsrc = is_vision ? is_vision + (vr_ok ? vr : 0) : reinterpret_cast<const uint8_t *>(x);
   uint32_t vb;
   asm volatile("global_load_ubyte %0, %1, off" : "=v"(vb) : "v"(vsrc) : "memory");
   constexpr int X0 = NCH > 1 ? 2 : 1;  // x chunks issued ahead of the loop
   issue_x(0);
   if constexpr (X0 > 1) issue_x(1);
-  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(vb) : "n"(8 * X0) : "memory");
+  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(vb) : "n"(NXL * X0) : "memory");
   const int amod = !vr_ok ? 2 : ((is_vision == nullptr || (vb & 0xffu)) ? 0 : 1);
   const uint32_t vis_bits = (uint32_t)(__ballot(amod == 0) & 0xFFFFFFFFull);  // bit r: tile row r uses P_vis
   const uint32_t txt_bits = (uint32_t)(__ballot(amod == 1) & 0xFFFFFFFFull);
@@ -626,9 +633,9 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
   const uint4 braw_t = *reinterpret_cast<const uint4 *>(bt + col);
 
   tm_u32x4 pb[2][4][CB];  // P of two chunks: [c & 1][k-step][column block]
-  tm_f32x4 fin[2][CB];    // each row's result from the pass of its modality
+  tm_f32x4 fin[RB][CB];   // each row's result from the pass of its modality
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int c = 0; c < CB; ++c) fin[rb][c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -663,9 +670,9 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t) issue_p(1, t);
     }
-    tm_f32x4 acc[2][CB];
+    tm_f32x4 acc[RB][CB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int c = 0; c < CB; ++c) acc[rb][c] = tm_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -673,9 +680,9 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
       // x(c) and P(c) are in once only the loads issued after both remain:
       // P(1) for chunk 0 (x(1) precedes P(0)); for chunk c >= 1 the P and x of
       // chunk c + 1, issued while chunk c - 1 was multiplied (4 k-steps of CB
-      // P loads, 8 x loads a chunk)
+      // P loads, NXL x loads a chunk)
       constexpr int kAfter0 = NCH > 1 ? 4 * CB : 0;
-      constexpr int kAfterMid = 4 * CB + 8;
+      constexpr int kAfterMid = 4 * CB + NXL;
       if (c == 0)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfter0) : "memory");
       else if (c + 1 < NCH)
@@ -689,7 +696,7 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
+        for (int rb = 0; rb < RB; ++rb) {
           const uint4 a = read_a(c, rb, t);
 #pragma unroll
           for (int u = 0; u < CB; ++u) {
@@ -707,7 +714,7 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // nothing of this pass still lands in the ring
     // D row of acc[rb][u][i] is 16*rb + 4*(lane>>4) + i
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool mine = (rows_of_pass >> (16 * rb + 4 * (lane >> 4) + i)) & 1u;
@@ -719,10 +726,10 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
   if (txt_bits) run_pass(pt, txt_bits, vis_bits == 0);
   if (!vis_bits && !txt_bits) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no row: drain the x loads
 
-  float *red = reinterpret_cast<float *>(&ring[0][0]);  // [4][32][kRowPad], wave w inside its own ring
+  float *red = reinterpret_cast<float *>(&ring[0][0]);  // [4][TR][kRowPad], wave w inside its own ring
   auto red_at = [&](int w, int r, int c) { return red + w * (2 * 512 * 4) + r * kRowPad + c; };
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + 4 * (lane >> 4) + i;
@@ -730,7 +737,7 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
       for (int u = 0; u < CB; ++u) *red_at(wave, r, 16 * u + (lane & 15)) = fin[rb][u][i];
     }
   __syncthreads();
-  if (erow >= 32) return;  // CB = 2: waves 2 and 3 have no row (no barrier follows)
+  if (erow >= TR) return;  // threads past the tile's rows (waves 2 and 3 when TR * TPRW = 128; no barrier follows)
 
   const int64_t gr = row0 + erow;
   const bool ok = gr < n;
@@ -749,16 +756,13 @@ __global__ __launch_bounds__(256, 2) void project_cols_pipe_kernel(
   const T *be = reinterpret_cast<const T *>(&braw);
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = tm_round<DT>(v[i] + Elem<DT>::to_f(be[i]));
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
-#pragma unroll
-  for (int o = 1; o < TPRW; o <<= 1) ss += __shfl_xor(ss, o, 64);
-  if (ok) {
-    tm_store8<DT>(q + gr * ld_q + col, v);
-    if (part == 0) qn_part[(int64_t)g * n + gr] = ss;
-    if (keys != nullptr && g == 0 && part == 1) keys[gr] = ~0ull;
-  }
+  // the row epilogue of project_direct_kernel (normalisation needs the whole
+  // row: one column group, which the host ensures); the column group's
+  // partial |q|^2 (qn_part) or the row's (q_sqnorm)
+  float *sq_dst = nullptr;
+  if (ok && part == 0) sq_dst = qn_part != nullptr ? qn_part + (int64_t)g * n + gr : (q_sqnorm ? q_sqnorm + gr : nullptr);
+  finish_row<DT, TPRW>(v, normalize, eps, ok ? q + gr * ld_q + col : nullptr, sq_dst);
+  if (ok && keys != nullptr && g == 0 && part == 1) keys[gr] = ~0ull;
 }
 
 // tm_project_pack: one thread per 16-byte chunk of the packed layout.
@@ -1196,6 +1200,9 @@ int launch_mfma(const ProjPlan &pl, bool split, bool pk, const typename Elem<DT>
   return TM_OK;
 }
 
+// Rows from which tm_project's packed d = 64 path takes the pipelined kernel.
+constexpr int64_t kPipeMinRows64 = 2048;
+
 template <int DT>
 int launch_project(const void *x, int64_t n, int hidden, int64_t ld_x, const uint8_t *is_vision,
                    const void *pv, const void *bv, const void *pt, const void *bt, int64_t ps_h,
@@ -1221,6 +1228,20 @@ int launch_project(const void *x, int64_t n, int hidden, int64_t ld_x, const uin
   }
   if constexpr (DT != TM_DT_F32) {
   if (packed) {
+    // d = 64 at the model hidden sizes with many rows: the pipelined column
+    // kernel with one 64-column group per 16-row tile (its operand loads in
+    // flight two chunks ahead; the direct kernel's tiles, slices, MFMA chains,
+    // wave order and row epilogue, so the same bits)
+    if (dim == 64 && (hidden == 2048 || hidden == 2560) && n >= kPipeMinRows64 &&
+        n < ((int64_t)1 << 31) / 32) {
+      const int64_t n_tiles = tm_cdiv(n, 16);
+      auto kern = hidden == 2048 ? project_cols_pipe_kernel<DT, 64, 0, 4, 4, 1> : project_cols_pipe_kernel<DT, 64, 0, 5, 4, 1>;
+      hipLaunchKernelGGL(kern, dim3((unsigned)(tm_cdiv(n_tiles, 8) * 8)), dim3(256), 0, stream, X, n, hidden, ld_x,
+                         is_vision, PV, BV, PT, BT, Q, ld_q, nullptr, nullptr, n_tiles, ColsRoute{}, normalize, eps,
+                         q_sqnorm);
+      TM_LAUNCH_CHECK("tm_project");
+      return TM_OK;
+    }
     // 16 rows per workgroup, 4 waves splitting hidden
     const dim3 grid((unsigned)tm_cdiv(n, 16));
     switch (dim) {
@@ -1385,7 +1406,7 @@ void launch_cols(const void *x, int64_t n, int hidden, int64_t ld_x, const uint8
       hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, static_cast<const T *>(x), n, hidden,
                          ld_x, is_vision, static_cast<const T *>(pv), static_cast<const T *>(bv),
                          static_cast<const T *>(pt ? pt : pv), static_cast<const T *>(pt ? bt : bv),
-                         static_cast<T *>(q), ld_q, qn_part, keys, n_tiles, cr);
+                         static_cast<T *>(q), ld_q, qn_part, keys, n_tiles, cr, 0, 0.f, nullptr);
       return;
     }
   }

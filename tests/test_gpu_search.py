@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import tm_oracle as O
-from parity_util import ODT, assert_projection_close, assert_within_ulps, check_pick, check_topk_rows, np64, proj_abssum
+from parity_util import ODT, assert_projection_close, assert_within_ulps, check_pick, check_topk_rows, np64, proj_abssum, ulp
 from table_moe import _native as N
 
 pytestmark = pytest.mark.gpu
@@ -145,6 +145,65 @@ def test_project_packed_normalized_fp16(hip_device):
     abssum = proj_abssum(np64(x), np.ones(n, bool), np64(p), np64(p))
     abssum = abssum / np.maximum(np.linalg.norm(raw, axis=1, keepdims=True), 1e-6)
     assert_projection_close(np64(q), ref, abssum, dtype, min_exact=0.95)
+
+
+@pytest.mark.parametrize("n,hidden,dtype,normalize,mix", [
+    (4096, 2048, torch.bfloat16, 1, "mixed"), (2048, 2048, torch.bfloat16, 0, "vision"),
+    (2100, 2560, torch.float16, 1, "mixed"), (3000, 2048, torch.bfloat16, 1, "text")])
+def test_project_packed_d64_pipelined_matches_direct(hip_device, n, hidden, dtype, normalize, mix):
+    """From 2048 rows tm_project takes packed d = 64 projections at hidden
+    2048 / 2560 through the pipelined column kernel (32-row tiles, one
+    64-column group), below that through the direct kernel (16-row tiles).
+    Both add the same per-slice MFMA chains in the same order and run the same
+    row epilogue, so q and |q|^2 match bit for bit: the whole batch in one
+    call against the same rows in calls of 1000 (mixed modalities inside the
+    tiles, normalised and not, bf16 and fp16, a ragged last tile), and the
+    oracle checks the values (a normalised component within two ulps: one
+    from its unnormalised value, one from a norm rounded the other way)."""
+    g = _gen(n + hidden)
+    dim = 64
+    x = torch.randn(n, hidden, generator=g).to(dtype)
+    pv, pt = _rand_proj(g, hidden, dim).to(dtype), _rand_proj(g, hidden, dim).to(dtype)
+    bv, bt = (torch.randn(dim, generator=g) * 0.1).to(dtype), (torch.randn(dim, generator=g) * 0.1).to(dtype)
+    vis = {"mixed": torch.rand(n, generator=g) < 0.5, "vision": torch.ones(n, dtype=torch.bool),
+           "text": torch.zeros(n, dtype=torch.bool)}[mix]
+    dev = hip_device
+    xd, visd = x.to(dev), vis.to(dev)
+    bvd, btd = bv.to(dev), bt.to(dev)
+    Pv, Pt = N.pack_projection(pv.to(dev), bvd), N.pack_projection(pt.to(dev), btd)
+
+    def project(lo, hi, q, qn):
+        N.call("tm_project", N.dtype_tag(dtype), xd[lo:hi].data_ptr(), hi - lo, hidden, hidden,
+               N.as_u8(visd[lo:hi]).data_ptr(), Pv.data_ptr(), bvd.data_ptr(), Pt.data_ptr(), btd.data_ptr(), 0, 0,
+               dim, normalize, 1e-6, q[lo:hi].data_ptr(), dim, qn[lo:hi].data_ptr(), None, 0, N.stream(dev))
+
+    q_one = torch.empty(n, dim, dtype=dtype, device=dev)
+    qn_one = torch.empty(n, dtype=torch.float32, device=dev)
+    project(0, n, q_one, qn_one)
+    q_parts = torch.empty_like(q_one)
+    qn_parts = torch.empty_like(qn_one)
+    for lo in range(0, n, 1000):
+        project(lo, min(lo + 1000, n), q_parts, qn_parts)
+    torch.cuda.synchronize()
+    assert torch.equal(q_one.view(torch.int16), q_parts.view(torch.int16))
+    assert torch.equal(qn_one, qn_parts)
+    ref = O.project_queries(np64(x), vis.numpy(), (np64(pv), np64(bv)), (np64(pt), np64(bt)), bool(normalize),
+                            ODT[dtype])
+    abssum = proj_abssum(np64(x), vis.numpy(), np64(pv), np64(pt))
+    if normalize:
+        raw = O.project_queries(np64(x), vis.numpy(), (np64(pv), np64(bv)), (np64(pt), np64(bt)), False, ODT[dtype])
+        abssum = abssum / np.maximum(np.linalg.norm(raw, axis=1, keepdims=True), 1e-6)
+    got = np64(q_one)
+    if normalize:
+        # a normalised component: one ulp from the unnormalised one (fp32
+        # accumulation order) and one more when the rounded norm it divides by
+        # came out on the other side
+        tol = 2.0 * ulp(ref, dtype) + 2.0**-18 * abssum
+        assert not (np.abs(got - ref) > tol).any()
+        assert float(np.mean(got == ref)) >= 0.95
+    else:
+        assert_projection_close(got, ref, abssum, dtype, min_exact=0.97)
+    np.testing.assert_allclose(np64(qn_one), (got * got).sum(1), rtol=2e-6, atol=1e-6)
 
 
 @pytest.mark.parametrize("dtype,dim", [(torch.float32, 2), (torch.float32, 64), (torch.bfloat16, 48)])
