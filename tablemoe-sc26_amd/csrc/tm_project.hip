@@ -81,12 +81,12 @@ ProjPlan plan_project_f32(int64_t n, int hidden, int dim) {
 template <int DT, int TPR>
 __device__ __forceinline__ void finish_row(float (&v)[8], int normalize, float eps,
                                            typename Elem<DT>::T *dst, float *sq_dst) {
-  float ss = 0.f;
+  if (normalize) {  // uniform
+    float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
+    for (int i = 0; i < 8; ++i) ss = fmaf(v[i], v[i], ss);
 #pragma unroll
-  for (int o = 1; o < TPR; o <<= 1) ss += __shfl_xor(ss, o, 64);
-  if (normalize) {
+    for (int o = 1; o < TPR; o <<= 1) ss += __shfl_xor(ss, o, 64);
     const float norm = tm_round<DT>(sqrtf(ss));
     const float eps_dt = tm_round<DT>(eps);
     const bool zero_row = !(norm > eps_dt);
