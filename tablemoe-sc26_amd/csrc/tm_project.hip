@@ -950,14 +950,18 @@ __global__ __launch_bounds__(kThreads) void project_mfma_kernel(
   }
 }
 
-// Split epilogue: q[r] = finish(dtype(sum_s partial[s][r] + bias_m)).
+// Split epilogue: q[r] = finish(dtype(sum_s partial[s][r] + bias_m)).  One
+// 64-thread workgroup per 64 / (DIM / 8) rows, so the partials (L2-resident:
+// the split kernel just wrote them) spread over many CUs.
+constexpr int kEpiThreads = 64;
 template <int DT, int DIM>
-__global__ __launch_bounds__(kThreads) void project_epilogue_kernel(
+__global__ __launch_bounds__(kEpiThreads) void project_epilogue_kernel(
     const float *__restrict__ partial, int nsplit, int64_t n, const uint8_t *__restrict__ is_vision,
     const typename Elem<DT>::T *__restrict__ bv, const typename Elem<DT>::T *__restrict__ bt, int normalize,
     float eps, typename Elem<DT>::T *__restrict__ q, int64_t ld_q, float *__restrict__ q_sqnorm) {
   constexpr int TPR = DIM / 8;
-  constexpr int RPB = kThreads / TPR;
+  constexpr int RPB = kEpiThreads / TPR;
+  constexpr int kRound = 16;  // splits whose loads are issued together
   const int tid = threadIdx.x;
   const int64_t r = (int64_t)blockIdx.x * RPB + tid / TPR;
   const int part = tid % TPR;
@@ -966,11 +970,11 @@ __global__ __launch_bounds__(kThreads) void project_epilogue_kernel(
   for (int i = 0; i < 8; ++i) v[i] = 0.f;
   const bool ok = r < n;
   if (ok) {
-    // splits summed in order; loads of up to 8 splits issued before the adds
-    for (int s0 = 0; s0 < nsplit; s0 += 8) {
-      float4 a[8], b[8];
+    // splits summed in order; the loads of kRound splits issued before the adds
+    for (int s0 = 0; s0 < nsplit; s0 += kRound) {
+      float4 a[kRound], b[kRound];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < kRound; ++u) {
         if (s0 + u < nsplit) {
           const float4 *src = reinterpret_cast<const float4 *>(partial + ((int64_t)(s0 + u) * n + r) * DIM + part * 8);
           a[u] = src[0];
@@ -978,7 +982,7 @@ __global__ __launch_bounds__(kThreads) void project_epilogue_kernel(
         }
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < kRound; ++u) {
         if (s0 + u < nsplit) {
           v[0] += a[u].x; v[1] += a[u].y; v[2] += a[u].z; v[3] += a[u].w;
           v[4] += b[u].x; v[5] += b[u].y; v[6] += b[u].z; v[7] += b[u].w;
@@ -1184,9 +1188,9 @@ int launch_mfma(const ProjPlan &pl, bool split, bool pk, const typename Elem<DT>
       hipLaunchKernelGGL((project_mfma_kernel<DT, DIM, false, true>), grid, block, 0, stream, X, n, hidden, ld_x,
                          is_vision, PV, BV, PT, BT, ps_h, ps_d, normalize, eps, Q, ld_q, q_sqnorm, k_chunk, partial);
     TM_LAUNCH_CHECK("tm_project");
-    constexpr int RPB = kThreads / (DIM / 8);
-    hipLaunchKernelGGL((project_epilogue_kernel<DT, DIM>), dim3((unsigned)tm_cdiv(n, RPB)), block, 0, stream,
-                       partial, nsplit, n, is_vision, BV, BT, normalize, eps, Q, ld_q, q_sqnorm);
+    constexpr int RPB = kEpiThreads / (DIM / 8);
+    hipLaunchKernelGGL((project_epilogue_kernel<DT, DIM>), dim3((unsigned)tm_cdiv(n, RPB)), dim3(kEpiThreads), 0,
+                       stream, partial, nsplit, n, is_vision, BV, BT, normalize, eps, Q, ld_q, q_sqnorm);
     TM_LAUNCH_CHECK("tm_project(epilogue)");
     return TM_OK;
   }
@@ -1295,8 +1299,8 @@ int launch_project(const void *x, int64_t n, int hidden, int64_t ld_x, const uin
     hipLaunchKernelGGL((project_f32_kernel<D>), grid, dim3(kThreads), 0, stream, X, n, hidden, ld_x, is_vision, \
                        PV, PT, ps_h, ps_d, pl.k_chunk, partial);                                                \
     TM_LAUNCH_CHECK("tm_project");                                                                             \
-    hipLaunchKernelGGL((project_epilogue_kernel<DT, D>), dim3((unsigned)tm_cdiv(n, kThreads / (D / 8))),        \
-                       dim3(kThreads), 0, stream, partial, pl.nsplit, n, is_vision, BV, BT, normalize, eps, Q,  \
+    hipLaunchKernelGGL((project_epilogue_kernel<DT, D>), dim3((unsigned)tm_cdiv(n, kEpiThreads / (D / 8))),     \
+                       dim3(kEpiThreads), 0, stream, partial, pl.nsplit, n, is_vision, BV, BT, normalize, eps, Q, \
                        ld_q, q_sqnorm);                                                                         \
     TM_LAUNCH_CHECK("tm_project(epilogue)");                                                                   \
     return TM_OK;
