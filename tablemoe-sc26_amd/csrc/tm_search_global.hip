@@ -1371,15 +1371,27 @@ SplitPlan plan_f32(int64_t n, int64_t c) {
   return p;
 }
 
-template <int DIM, int K, int METRIC>
+// RVPL > 0: rows y >= mr.first of the grid are router workgroups (32 tokens
+// each, numbered along x): the router's DPP chain runs beside the search
+// instead of in the short merge launch after it.
+template <int DIM, int K, int METRIC, int RVPL>
 __global__ __launch_bounds__(kThreads) void search_f32_kernel(const float *__restrict__ q, int64_t n, int64_t ld_q,
                                                               const float *__restrict__ cents, int64_t n_cent,
                                                               int64_t ld_c, const float *__restrict__ c_sqnorm,
-                                                              int64_t chunk, uint64_t *__restrict__ ws) {
+                                                              int64_t chunk, uint64_t *__restrict__ ws,
+                                                              MergeRoute mr) {
   constexpr int V4 = DIM / 4;  // float4 per centroid row
   __shared__ float4 cs[kF32Block * V4];
   __shared__ float pen_s[kF32Block];
   __shared__ uint64_t lists[3][K][kF32Rows];  // waves 1..3 hand their lists to wave 0
+  if constexpr (RVPL > 0) {
+    if ((int64_t)blockIdx.y >= mr.first) {  // uniform: router workgroup
+      const int64_t w = ((int64_t)blockIdx.y - mr.first) * gridDim.x + blockIdx.x;
+      const int64_t tok = w * (kThreads / 8) + (threadIdx.x >> 3);
+      tm_route_token<RVPL, 8>(mr.a.logits, n, mr.a.ld, mr.a.top_k, 0, mr.a.out_w, mr.a.out_ids, tok, threadIdx.x & 7);
+      return;
+    }
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t r = (int64_t)blockIdx.x * kF32Rows + lane;
   const float4 *qrow = reinterpret_cast<const float4 *>(q + (r < n ? r : n - 1) * ld_q);
@@ -1441,16 +1453,28 @@ int launch_search_f32(int top_k, const void *q, int64_t n, int64_t ld_q, const f
                       uint64_t *ws, const tm_route_args *ra, hipStream_t stream) {
   const SplitPlan p = plan_f32(n, n_cent);
   const float *Q = static_cast<const float *>(q);
-  hipLaunchKernelGGL((search_f32_kernel<DIM, K, METRIC>), dim3((unsigned)p.row_blocks, (unsigned)p.nsplit),
-                     dim3(kThreads), 0, stream, Q, n, ld_q, static_cast<const float *>(cents), n_cent, ld_c, c_sqnorm,
-                     p.chunk, ws);
-  TM_LAUNCH_CHECK("tm_search_global(f32)");
+  // the router (when fused) in extra grid rows of the search launch
+  MergeRoute mr{};
+  int64_t rows = p.nsplit;
+  if (ra != nullptr) {
+    mr.a = *ra;
+    mr.first = p.nsplit;
+    rows += tm_cdiv(tm_cdiv(n, kThreads / 8), p.row_blocks);
+  }
+  auto go = [&](auto rvpl_tag) {
+    constexpr int RVPL = decltype(rvpl_tag)::value;
+    hipLaunchKernelGGL((search_f32_kernel<DIM, K, METRIC, RVPL>), dim3((unsigned)p.row_blocks, (unsigned)rows),
+                       dim3(kThreads), 0, stream, Q, n, ld_q, static_cast<const float *>(cents), n_cent, ld_c,
+                       c_sqnorm, p.chunk, ws, mr);
+  };
   if (ra == nullptr)
-    launch_merge<TM_DT_F32, K, METRIC, 0>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, ra, stream);
+    go(std::integral_constant<int, 0>{});
   else if (ra->n_experts == 64)
-    launch_merge<TM_DT_F32, K, METRIC, 8>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, ra, stream);
+    go(std::integral_constant<int, 8>{});
   else
-    launch_merge<TM_DT_F32, K, METRIC, 16>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, ra, stream);
+    go(std::integral_constant<int, 16>{});
+  TM_LAUNCH_CHECK("tm_search_global(f32)");
+  launch_merge<TM_DT_F32, K, METRIC, 0>(p, top_k, Q, n, ld_q, DIM, q_sqnorm, out_dist, out_idx, ws, nullptr, stream);
   TM_LAUNCH_CHECK("tm_search_global(merge)");
   return TM_OK;
 }

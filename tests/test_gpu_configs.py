@@ -93,6 +93,26 @@ def test_config1_fp32_layer_vs_oracle_and_staged(hip_device):
     np.testing.assert_allclose(np64(ra["out"]), ref["out"], rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("n,n_experts,top_k", [(77, 64, 6), (300, 128, 8)])
+def test_fp32_layer_router_in_search_launch(hip_device, n, n_experts, top_k):
+    """The fp32 layer's router rides in the search launch (extra grid rows of
+    32 tokens each, numbered along the row blocks): token counts that leave
+    the last router workgroup and row block ragged, 64 and 128 experts, the
+    one-call layer against the stage calls (router launched on its own) bit
+    for bit."""
+    from synth import make_workload
+
+    wl = make_workload(1, n=n, n_experts=n_experts, router_top_k=top_k)
+    d = wl.to(hip_device)
+    a, b = _table(d), _table(d)
+    ra = a.layer_forward(d.x, d.is_vision, d.logits, d.slot_out, d.residual, top_k, 1, 0.6)
+    rb = b.layer_forward_staged(d.x, d.is_vision, d.logits, d.slot_out, d.residual, top_k, 1, 0.6)
+    torch.cuda.synchronize()
+    for key in KEYS:
+        assert torch.equal(ra[key], rb[key]), key
+    assert int(ra["keep"].sum()) == O.keep_count(n, 0.6)
+
+
 def test_config1_fp32_search_topk_and_dot(hip_device):
     """The fp32 search path beyond config 1's top-1 L2: top-4 and top-8 lists,
     the dot metric, d = 128/256, ragged centroid ranges and a decode-sized
