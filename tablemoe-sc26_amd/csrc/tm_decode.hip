@@ -15,12 +15,13 @@
 //     rows' best keys and carries the router's workgroups.
 //  2. search_stream_kernel (tm_search_global.hip): per-split sorted lists,
 //     and each query's best key by 64-bit atomic minimum into one of kKeyRep
-//     replicas (split % kKeyRep), so few workgroups contend for an address.
+//     replicas (split % kKeyRep, each replica on a 128-byte line of its
+//     own), so few workgroups contend for a line.
 //  3. decode_finish_kernel: one wave per (token, 512-element row chunk).  It
 //     ranks the token's best distance among the n tokens' (keep rule of
 //     tm_keep_select: larger distance first, ties to the lower token index),
-//     merges the token's split lists (the K smallest packed keys, a set, so
-//     the same keys as merge_kernel), and combines its row chunk exactly as
+//     takes the K smallest keys of the token's split lists (wave_min_k: a
+//     set, so the same keys as merge_kernel), and combines its row chunk exactly as
 //     gather_combine_tk_kernel does (fp32 from the residual, sources in order,
 //     one rounding).  The chunk-0 wave also writes dist, idx, keep and |q|^2.
 //
