@@ -755,7 +755,7 @@ def _gen_word(table):
 @pytest.mark.parametrize("cfg,n,nn,variant", [
     (3, 1, 4, "base"), (3, 8, 4, "base"), (3, 32, 4, "base"), (3, 33, 1, "mix"), (3, 64, 4, "mix"),
     (5, 17, 4, "base"), (5, 64, 1, "nores"), (3, 24, 4, "fp16"), (3, 40, 4, "dot"), (3, 32, 4, "small_c"),
-    (5, 5, 1, "fp16"), (3, 12, 4, "mix"), (5, 16, 1, "mix")])
+    (5, 5, 1, "fp16"), (3, 12, 4, "mix"), (5, 16, 1, "mix"), (3, 8, 4, "small_c")])
 def test_decode_one_launch_matches_three_launches(hip_device, cfg, n, nn, variant):
     """Decode batches with d = 128, hidden 2048 or 2560 and at most 128
     search splits run as one launch whose three phases hand q and the search
