@@ -177,30 +177,45 @@ def dtype_tag(dtype: torch.dtype) -> int:
 
 def require_hip(*tensors: torch.Tensor | None) -> torch.device:
     """All given tensors must live on the same HIP device; return it."""
-    dev = None
+    first = None
     for t in tensors:
         if t is None:
             continue
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise RuntimeError(
                 f"table_moe kernels run on a HIP device only; got a tensor on {t.device} "
                 "(there is no CPU fallback)"
             )
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
-    if dev is None:
+        if first is None:
+            first, idx = t, t.get_device()
+        elif t.get_device() != idx:
+            raise ValueError(f"tensors on different devices: {first.device} and {t.device}")
+    if first is None:
         raise ValueError("no tensor given")
-    return dev
+    return first.device
 
 
 def ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
+# the current stream's handle without building a torch.cuda.Stream object
+# (a few microseconds per call on the eager decode path)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(device: torch.device) -> int:
+    if _raw_stream is not None and device.index is not None:
+        return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def mask_bytes(mask: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """A token mask as contiguous bytes on ``device``: the tensor itself when
+    it already is a contiguous bool tensor there, else a bool copy."""
+    if mask.dtype == torch.bool and mask.is_cuda and mask.is_contiguous() and mask.get_device() == device.index:
+        return mask
+    return mask.reshape(-1).to(device=device, dtype=torch.bool).contiguous()
 
 
 def as_u8(mask: torch.Tensor) -> torch.Tensor:

@@ -30,6 +30,8 @@ def _round_cap(batch_size: int) -> int:
     return ((cap + 127) // 128) * 128
 
 
+_BYTE_MASKS = (torch.bool, torch.uint8)
+
 class VectorSearchEngine:
     def __init__(self, manager):
         self.manager = manager
@@ -269,14 +271,24 @@ class VectorSearchEngine:
     def _hybrid_into(self, hidden_states, selected_experts, is_vision_mask, keep_k, on_hit, on_idx, off_hit,
                      off_idx, on_slot):
         dev = N.require_hip(hidden_states, selected_experts, on_hit, off_idx)
-        dims = self._get_search_dims()
-        dtype = self.manager.keys_buffer.dtype
-        if hidden_states.dtype != dtype:
-            raise RuntimeError(f"hidden_states dtype {hidden_states.dtype} != table dtype {dtype}")
         x = hidden_states if hidden_states.stride(-1) == 1 else hidden_states.contiguous()
         n, hidden = x.shape
-        top_k = selected_experts.shape[1]
         sel = selected_experts if selected_experts.dtype == torch.long else selected_experts.long()
+        self._hybrid_call(dev, x, n, hidden, x.stride(0), is_vision_mask, sel, sel.shape[1], sel.stride(0),
+                          sel.stride(1), keep_k, on_hit, on_idx, off_hit, off_idx, on_slot, on_hit.stride(0),
+                          on_hit.stride(1))
+
+    def _hybrid_call(self, dev, x, n, hidden, ld_x, is_vision_mask, sel, top_k, sel_s0, sel_s1, keep_k, on_hit,
+                     on_idx, off_hit, off_idx, on_slot, out_s0, out_s1):
+        """tm_search_hybrid on plain pointers and strides (the four [n, top_k]
+        outputs share the element strides out_s0/out_s1); the bs1 path calls
+        it on its 1-D tensors without building 2-D views."""
+        dims = self._get_search_dims()
+        dtype = self.manager.keys_buffer.dtype
+        if x.dtype != dtype:
+            raise RuntimeError(f"hidden_states dtype {x.dtype} != table dtype {dtype}")
+        if on_hit.dtype not in _BYTE_MASKS or off_hit.dtype not in _BYTE_MASKS:
+            raise ValueError("on_hit/off_hit must be bool (or uint8) tensors")
         num_search = max(top_k - keep_k, 0)
         on_keys, on_ids, n_valid = self._online_state()
         if num_search <= 0:
@@ -284,20 +296,27 @@ class VectorSearchEngine:
         if on_ids is not None and on_ids.stride(-1) != 1:
             raise ValueError("online_expert_ids must have a unit stride along slots")
         keys = self.manager.keys_buffer
-        isv = N.as_u8(is_vision_mask.reshape(-1).to(device=dev, dtype=torch.bool))
-        q_ws = self._ensure_decode_query_workspace(n, dims["compressed_dim"])
-        ws = self._scratch("hybrid", N.lib().tm_search_hybrid_workspace_size(n, hidden, dims["compressed_dim"]))
+        isv = N.mask_bytes(is_vision_mask, dev)
+        d = dims["compressed_dim"]
+        q_ws = self.decode_query_workspace
+        if q_ws is None or n > self.decode_query_workspace_capacity or q_ws.shape[1] != d or q_ws.dtype != dtype:
+            q_ws = self._ensure_decode_query_workspace(n, d)
+        sizes = self.__dict__.setdefault("_hybrid_ws_sizes", {})
+        nbytes = sizes.get((n, hidden, d))
+        if nbytes is None:
+            nbytes = sizes[(n, hidden, d)] = N.lib().tm_search_hybrid_workspace_size(n, hidden, d)
+        ws = self._scratch("hybrid", nbytes)
         pv, pt = dims["pca_vis"], dims["pca_txt"]
         tv, tt = dims["proj_t"]
         N.call(
-            "tm_search_hybrid", N.dtype_tag(dtype), N.ptr(x), n, hidden, x.stride(0), N.ptr(isv),
-            N.ptr(tv), N.ptr(pv["bias"]), N.ptr(tt), N.ptr(pt["bias"]), 1, hidden, dims["compressed_dim"],
+            "tm_search_hybrid", N.dtype_tag(dtype), x.data_ptr(), n, hidden, ld_x, isv.data_ptr(),
+            N.ptr(tv), N.ptr(pv["bias"]), N.ptr(tt), N.ptr(pt["bias"]), 1, hidden, d,
             N.ptr(on_keys), 0 if on_keys is None else on_keys.stride(0), n_valid, N.ptr(on_ids),
             0 if on_ids is None else on_ids.shape[1], 0 if on_ids is None else on_ids.stride(0),
-            N.ptr(keys), keys.shape[0], keys.shape[2], keys.stride(0), keys.stride(1), keys.stride(2),
-            N.ptr(sel), top_k, sel.stride(0), sel.stride(1), int(keep_k), N.ptr(N.as_u8(on_hit)), N.ptr(on_idx),
-            N.ptr(N.as_u8(off_hit)), N.ptr(off_idx), N.ptr(on_slot), on_hit.stride(0), on_hit.stride(1),
-            N.ptr(q_ws), q_ws.stride(0), N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(dev),
+            keys.data_ptr(), keys.shape[0], keys.shape[2], keys.stride(0), keys.stride(1), keys.stride(2),
+            sel.data_ptr(), top_k, sel_s0, sel_s1, int(keep_k), on_hit.data_ptr(), on_idx.data_ptr(),
+            off_hit.data_ptr(), off_idx.data_ptr(), on_slot.data_ptr(), out_s0, out_s1,
+            q_ws.data_ptr(), q_ws.stride(0), N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(dev),
         )
 
     def search_decode_hybrid(self, layer_idx, hidden_states, selected_experts, is_vision_mask, keep_k=None):
@@ -337,8 +356,15 @@ class VectorSearchEngine:
             out_on_idx.fill_(-1)
             return
         keep_k = max(0, min(int(keep_k), top_k))
-        self._hybrid_into(
-            hidden_state.view(1, -1), selected_experts_row.view(1, top_k), is_vision.view(1), keep_k,
-            out_on_hit.view(1, top_k), out_on_idx.view(1), out_off_hit.view(1, top_k), out_off_idx.view(1, top_k),
-            out_on_slot.view(1, top_k),
-        )
+        # one token: the 1-D tensors go straight to the call (no 2-D views),
+        # which keeps the eager per-call host time near the kernels' own
+        dev = N.require_hip(hidden_state, selected_experts_row, out_on_hit, out_off_idx)
+        x = hidden_state if hidden_state.stride(-1) == 1 else hidden_state.contiguous()
+        hidden = x.shape[-1]
+        if x.numel() != hidden:
+            raise ValueError(f"hidden_state must hold one token; got shape {tuple(hidden_state.shape)}")
+        sel = selected_experts_row if selected_experts_row.dtype == torch.long else selected_experts_row.long()
+        s1 = sel.stride(0)
+        o1 = out_on_hit.stride(0)
+        self._hybrid_call(dev, x, 1, hidden, hidden, is_vision, sel, top_k, top_k * s1, s1, keep_k, out_on_hit,
+                          out_on_idx, out_off_hit, out_off_idx, out_on_slot, top_k * o1, o1)
