@@ -94,6 +94,8 @@ class GlobalTable:
             # zero-filled: the search workspace starts with counters that must be zero
             t = torch.zeros(max(numel, 1), dtype=dtype, device=self.device)
             self._bufs[name] = t
+            # layer-call descriptions cached on the old buffers are stale now
+            self.__dict__.pop("_io_cache", None)
         return t[:numel].view(shape)
 
     def _side_stream(self) -> torch.cuda.Stream:
@@ -224,26 +226,56 @@ class GlobalTable:
             out = self._out_buf(n, residual)
         if not combine:
             slot_out = residual = out = None
-        w = self._buf("route_w", (n, router_top_k), torch.float32)
-        ids = self._buf("route_ids", (n, router_top_k), torch.long)
-        q = self._buf("q", (n, self.dim), self.dtype)
-        qn = self._buf("qn", (n,), torch.float32)
-        dist = self._buf("dist", (n, n_nearest), torch.float32)
-        idx = self._buf("idx", (n, n_nearest), torch.long)
-        keep = self._buf("keep", (n,), torch.bool)
-        isv = None if is_vision is None else N.as_u8(is_vision.reshape(-1).to(dtype=torch.bool))
-        io = N.LayerIO(
-            n_tokens=n, x=N.ptr(x), ld_x=x.stride(0), is_vision=N.ptr(isv), router_logits=N.ptr(logits),
-            ld_logits=logits.stride(0), n_experts=logits.shape[1], router_top_k=router_top_k, n_nearest=n_nearest,
-            keep_rate=float(keep_rate), flags=int(flags), slot_out=N.ptr(slot_out),
-            so_b=0 if slot_out is None else slot_out.stride(0), so_s=0 if slot_out is None else slot_out.stride(1),
-            residual=N.ptr(residual), ld_r=0 if residual is None else residual.stride(0), out=N.ptr(out),
-            ld_o=0 if out is None else out.stride(0), weights=N.ptr(w), expert_ids=N.ptr(ids), q=N.ptr(q),
-            q_sqnorm=N.ptr(qn), dist=N.ptr(dist), idx=N.ptr(idx), keep=N.ptr(N.as_u8(keep)))
+        isv = None if is_vision is None else N.mask_bytes(is_vision, x.device)
+        # the stage buffers and their pointers depend on (n, top_k, n_nearest)
+        # only: built once per shape (a decode loop calls this per token) and
+        # dropped whenever _buf reallocates a buffer
+        cache = self.__dict__.setdefault("_io_cache", {})
+        key = (n, router_top_k, n_nearest)
+        entry = cache.get(key)
+        if entry is None:
+            stages = {
+                "weights": self._buf("route_w", (n, router_top_k), torch.float32),
+                "ids": self._buf("route_ids", (n, router_top_k), torch.long),
+                "q": self._buf("q", (n, self.dim), self.dtype),
+                "qn": self._buf("qn", (n,), torch.float32),
+                "dist": self._buf("dist", (n, n_nearest), torch.float32),
+                "idx": self._buf("idx", (n, n_nearest), torch.long),
+                "keep": self._buf("keep", (n,), torch.bool),
+            }
+            io = N.LayerIO(
+                n_tokens=n, router_top_k=router_top_k, n_nearest=n_nearest, weights=N.ptr(stages["weights"]),
+                expert_ids=N.ptr(stages["ids"]), q=N.ptr(stages["q"]), q_sqnorm=N.ptr(stages["qn"]),
+                dist=N.ptr(stages["dist"]), idx=N.ptr(stages["idx"]), keep=N.ptr(stages["keep"]))
+            entry = (io, stages)
+            cache = self.__dict__.setdefault("_io_cache", {})  # a _buf above may have dropped it
+            cache[key] = entry
+        io, stages = entry
+        io.x, io.ld_x, io.is_vision = x.data_ptr(), x.stride(0), N.ptr(isv)
+        io.router_logits, io.ld_logits, io.n_experts = logits.data_ptr(), logits.stride(0), logits.shape[1]
+        io.keep_rate, io.flags = float(keep_rate), int(flags)
+        io.slot_out = N.ptr(slot_out)
+        io.so_b, io.so_s = (0, 0) if slot_out is None else (slot_out.stride(0), slot_out.stride(1))
+        io.residual, io.ld_r = N.ptr(residual), 0 if residual is None else residual.stride(0)
+        io.out, io.ld_o = N.ptr(out), 0 if out is None else out.stride(0)
         # the tensors the io points at stay referenced by the returned dict
-        res = {"weights": w, "ids": ids, "q": q, "qn": qn, "dist": dist, "idx": idx, "keep": keep, "out": out,
-               "_inputs": (x, logits, slot_out, isv)}
+        res = dict(stages)
+        res["out"] = out
+        res["_inputs"] = (x, logits, slot_out, isv)
         return io, res
+
+    def _layer_ws(self, n, n_nearest):
+        """The layer call's workspace (at least tm_table_forward_workspace_size
+        bytes; the size is queried once per shape)."""
+        sizes = self.__dict__.setdefault("_ws_sizes", {})
+        nbytes = sizes.get((n, n_nearest))
+        if nbytes is None:
+            nbytes = sizes[(n, n_nearest)] = max(
+                N.lib().tm_table_forward_workspace_size(C.byref(self._desc), n, n_nearest), 1)
+        ws = self._bufs.get("layer_ws")
+        if ws is None or ws.numel() < nbytes:
+            ws = self._buf("layer_ws", (nbytes,), torch.uint8)
+        return ws
 
     def layer_forward(self, hidden, is_vision, router_logits, slot_out, residual, router_top_k: int = 8,
                       n_nearest: int = 1, keep_rate: float = 0.6, out=None, stage_events=None):
@@ -254,9 +286,7 @@ class GlobalTable:
         ``out`` to keep an output)."""
         io, res = self._layer_io(hidden, is_vision, router_logits, slot_out, residual, router_top_k, n_nearest,
                                  keep_rate, out)
-        n = io.n_tokens
-        nbytes = N.lib().tm_table_forward_workspace_size(C.byref(self._desc), n, n_nearest)
-        ws = self._buf("layer_ws", (max(nbytes, 1),), torch.uint8)
+        ws = self._layer_ws(io.n_tokens, n_nearest)
         evs = None
         if stage_events is not None:
             evs = (C.c_void_p * 6)(*[e.cuda_event for e in stage_events])
@@ -301,8 +331,7 @@ class GlobalTable:
         combining (layer_forward_recompute)."""
         io, res = self._layer_io(hidden, is_vision, router_logits, None, None, router_top_k, n_nearest, keep_rate,
                                  None, flags=N.TM_LAYER_NO_COMBINE)
-        nbytes = N.lib().tm_table_forward_workspace_size(C.byref(self._desc), io.n_tokens, n_nearest)
-        ws = self._buf("layer_ws", (max(nbytes, 1),), torch.uint8)
+        ws = self._layer_ws(io.n_tokens, n_nearest)
         N.check(N.lib().tm_table_forward(C.byref(self._desc), C.byref(io), N.ptr(ws), ws.numel(), None,
                                          N.stream(self.device)), "tm_table_forward")
         if self.check_waits:
