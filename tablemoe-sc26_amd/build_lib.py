@@ -7,11 +7,12 @@ linked into one shared library that sits in-tree at
 ``table_moe/_lib/libtablemoe_hip.so``.
 
 The library links the HIP runtime that PyTorch-ROCm ships (torch/lib/
-libamdhip64.so, recorded as NEEDED "libamdhip64.so").  That copy has no SONAME,
-so a process that already loaded torch resolves our dependency to the SAME
-runtime instance: streams and device pointers from torch are valid in our
-kernels.  Linking /opt/rocm's libamdhip64.so.7 instead would load a second HIP
-runtime into the process.
+libamdhip64.so, torch's lib/ as the run path).  Its SONAME is libamdhip64.so.7,
+which becomes our NEEDED entry; in a process that already loaded torch the
+loader matches it to that SAME runtime instance by SONAME, so streams and device
+pointers from torch are valid in our kernels.  Loaded before torch, the name
+would be looked up as a file (torch's lib/ has no libamdhip64.so.7) and could
+resolve to /opt/rocm's copy, a second HIP runtime: import torch first.
 """
 
 from __future__ import annotations
