@@ -137,7 +137,7 @@ class VectorSearchEngine:
         n, hidden = x.shape
         pv, pt = search_dims["pca_vis"], search_dims["pca_txt"]
         tv, tt = search_dims["proj_t"]
-        isv = N.as_u8(is_vision_mask.reshape(-1).to(device=dev, dtype=torch.bool))
+        isv = N.mask_bytes(is_vision_mask, dev)
         d = search_dims["compressed_dim"]
         pk = search_dims["proj_pk"]
         if pk is not None and x.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0 and query_low.data_ptr() % 16 == 0 \
@@ -183,16 +183,18 @@ class VectorSearchEngine:
         dev = N.require_hip(query_low, keys, selected_experts, out_hit, out_idx)
         n, top_k = selected_experts.shape
         sel = selected_experts if selected_experts.dtype == torch.long else selected_experts.long()
-        isv = N.as_u8(is_vision_mask.reshape(-1).to(device=dev, dtype=torch.bool))
+        isv = N.mask_bytes(is_vision_mask, dev)
         rs = None if reuse_mask is None else N.as_u8(reuse_mask.to(device=dev, dtype=torch.bool))
         if keys.stride(-1) != 1:
             raise ValueError("keys must have a unit stride along the PCA dimension")
+        if out_hit.dtype not in _BYTE_MASKS:
+            raise ValueError("out_hit must be a bool (or uint8) tensor")
         N.call(
             "tm_search_gated", N.dtype_tag(keys.dtype), N.ptr(query_low), n, query_low.stride(0), N.ptr(keys),
             keys.shape[0], keys.shape[2], keys.shape[3], keys.stride(0), keys.stride(1), keys.stride(2),
             N.ptr(sel), top_k, sel.stride(0), sel.stride(1), N.ptr(isv), N.ptr(rs),
             0 if rs is None else rs.stride(0), 0 if rs is None else rs.stride(1), col_offset,
-            float(thr_vision), float(thr_text), cmp, N.ptr(N.as_u8(out_hit)), N.ptr(out_idx),
+            float(thr_vision), float(thr_text), cmp, out_hit.data_ptr(), N.ptr(out_idx),
             out_hit.stride(0), out_hit.stride(1), N.stream(dev),
         )
 
