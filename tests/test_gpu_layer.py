@@ -744,6 +744,29 @@ def test_layer_forward_config3_decode_end_to_end(hip_device, n):
     assert_bf16_output(np64(res["out"]), exact, abssum)
 
 
+def test_layer_forward_alternating_shapes_match_fresh_tables(hip_device):
+    """One table serving calls of changing shape (token count, n_nearest),
+    its stage buffers growing part-way (the per-shape layer descriptions it
+    keeps must follow the reallocations), equals a fresh table on every call,
+    bit for bit, in every stage output."""
+    from table_moe.cache_engine import GlobalTable
+    from synth import make_workload
+
+    d = make_workload(3, n=64).to(hip_device)
+    tables = lambda: GlobalTable(d.centroids, d.values, (d.proj_vis, d.bias_vis), (d.proj_txt, d.bias_txt))
+    tbl = tables()
+    for n, nn, off in [(1, 4, 0), (8, 4, 3), (1, 4, 7), (32, 4, 1), (8, 1, 20), (64, 4, 0), (1, 1, 9), (8, 4, 3)]:
+        sl = slice(off, off + n)
+        args = (d.x[sl], d.is_vision[sl], d.logits[sl], d.slot_out[sl], d.residual[sl])
+        got = tbl.layer_forward(*args, router_top_k=8, n_nearest=nn, keep_rate=0.6)
+        got = {k: v.clone() for k, v in got.items()}
+        want = tables().layer_forward(*args, router_top_k=8, n_nearest=nn, keep_rate=0.6)
+        torch.cuda.synchronize()
+        for k in ("weights", "ids", "q", "dist", "idx", "keep", "out"):
+            assert got[k].shape == want[k].shape, (n, nn, k)
+            assert torch.equal(got[k], want[k]), (n, nn, off, k)
+
+
 def _gen_word(table):
     """Generation word of the one-launch decode plan in a table's layer workspace
     (byte 256 of the sync region): advanced once by every one-launch call."""
