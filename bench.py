@@ -295,6 +295,24 @@ def traffic_from_profile(kernel_prefix, summary):
 
 
 # --------------------------------------------------------------------------- config 3 (decode)
+def eager_us(fn, calls=1024, reps=3):
+    """Wall time per call of `calls` back-to-back eager calls (no graph), one
+    synchronisation at the end: what a loop calling the entry point once per
+    token pays, host work or device time, whichever bounds it."""
+    import torch
+
+    fn(0)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for i in range(calls):
+            fn(i)
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) / calls * 1e6)
+    return statistics.median(ts)
+
+
 def run_decode(replicas=DECODE_REPLICAS, replays=5):
     """Config 3 at N = 1, 8, 32: one HIP graph of `replicas` consecutive layer
     calls, each on its own table (centroids 4 MiB + norms + packed
@@ -321,6 +339,13 @@ def run_decode(replicas=DECODE_REPLICAS, replays=5):
         g = graph_of(layers)
         per = [t / replicas for t in replay_times_us(g, replays)]
         del g
+        args = [(r.x[:n], r.is_vision[:n], r.logits[:n], r.slot_out[:n], r.residual[:n]) for r in reps]
+
+        def eager_layer(i):
+            j = i % len(tables)
+            tables[j].layer_forward(*args[j], 8, 4, 0.6, out=outs[j])
+
+        eager = eager_us(eager_layer)
         n_keep = max(1, int(n * 0.6))
         by = _stage_bytes(cfg, n, n_keep, 4, 8)
         layer_bytes = (cfg["n_cent"] * cfg["dim"] * 2 + cfg["n_cent"] * 4 + cfg["hidden"] * cfg["dim"] * 2
@@ -333,8 +358,10 @@ def run_decode(replicas=DECODE_REPLICAS, replays=5):
             "layer_hbm_GBps": layer_bytes / (us * 1e-6) / 1e9,
             "layer_hbm_frac": layer_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
             "search_bytes": by["search"] + cfg["hidden"] * cfg["dim"] * 2,
+            "eager_us_per_layer": eager,
         }
-        log(f"decode N={n}: {us:.2f} us/layer (median of {replays} replays of {replicas} layers)")
+        log(f"decode N={n}: {us:.2f} us/layer (median of {replays} replays of {replicas} layers); "
+            f"eager loop {eager:.2f} us per call")
     # the one-launch decode plan's bounded waits: a wait that ran out leaves
     # undefined rows, so a timing it took part in is not a valid measurement
     wait_errors = sum(t.wait_errors() for t in tables)
@@ -538,6 +565,8 @@ def run_mode_r(replays=20):
     g = graph_of(decode)
     dec_us = statistics.median(replay_times_us(g, replays)) / 64
     del g
+    dec_eager_us = eager_us(lambda i: eng.search_decode_hybrid_bs1_into(xs[i % 64], sel[i % 64],
+                                                                        wl.is_vision[i % 64], 4, *outs))
     # the decode step's tail for one token (the slot combine with the online
     # window, offline table and recomputed slots, then the ring write:
     # tm_decode_combine_update), after the hybrid search of that token
@@ -552,17 +581,20 @@ def run_mode_r(replays=20):
     pairs = int(reuse.sum().item())
     table_bytes = 128 * 2 * 256 * 64 * 2
     log(f"mode R: search_prefill_offline {prefill_us:.1f} us (gated search {gated_us:.1f} us, {pairs} pairs), "
-        f"decode bs1 hybrid {dec_us:.2f} us, decode step combine + ring write {step_us:.2f} us")
+        f"decode bs1 hybrid {dec_us:.2f} us (eager loop {dec_eager_us:.2f} us per call), decode step combine + "
+        f"ring write {step_us:.2f} us")
     return {
         "workload": "mode R (the reference's per-(expert, modality) tables) at Qwen3-VL-30B-A3B shapes: E=128 x 2 "
                     "modalities x K=256 centroids, d=64, hidden 2048 bf16, N=4096 (3584 vision + 512 text), top-8; "
                     "reuse = slots of experts outside the top 60 % by importance",
         "reuse_frac": reuse_frac, "searched_pairs": pairs, "hit_frac": hit_frac,
         "search_prefill_offline_us": prefill_us, "gated_search_us": gated_us,
-        "timing": "graphs of 16 back-to-back calls on the same tables (device time per call); decode: 64 calls per graph",
+        "timing": "graphs of 16 back-to-back calls on the same tables (device time per call); decode: 64 calls per "
+                  "graph; *_eager_us: 1024 eager calls, one synchronisation at the end (host wall clock)",
         "gated_pairs_per_s": pairs / (gated_us * 1e-6),
         "gated_table_GBps": table_bytes / (gated_us * 1e-6) / 1e9,
         "search_decode_hybrid_bs1_us": dec_us,
+        "search_decode_hybrid_bs1_eager_us": dec_eager_us,
         "decode_combine_update_bs1_us": step_us,
     }
 
