@@ -339,6 +339,22 @@ def test_engine_decode_hybrid_with_window(hip_device):
     assert int(bufs[1].item()) == int(on_idx[1].item())
     assert torch.equal(bufs[0], on_hit[1]) and torch.equal(bufs[4], on_slot[1])
     assert torch.equal(bufs[2], off_hit[1]) and torch.equal(bufs[3], off_idx[1])
+    # every token through the bs1 entry, outputs as strided columns (element
+    # stride 2, the other column untouched), a non-unit-stride expert row and
+    # 0-d vision flags: the same values as the batch call
+    for t in range(n):
+        cols = [torch.zeros(k, 2, dtype=torch.bool, device=dev), torch.full((1,), -7, dtype=torch.long, device=dev),
+                torch.zeros(k, 2, dtype=torch.bool, device=dev), torch.full((k, 2), -7, dtype=torch.long, device=dev),
+                torch.full((k, 2), -7, dtype=torch.long, device=dev)]
+        outs = [c[:, 1] if c.dim() == 2 else c for c in cols]
+        sel_row = torch.stack([sel[t], sel[t]], 1).to(dev)[:, 0]
+        eng.search_decode_hybrid_bs1_into(x[t].to(dev), sel_row, vis[t].to(dev), 4, *outs)
+        torch.cuda.synchronize()
+        assert int(outs[1].item()) == int(on_idx[t].item()), t
+        assert torch.equal(outs[0], on_hit[t]) and torch.equal(outs[4], on_slot[t]), t
+        assert torch.equal(outs[2], off_hit[t]) and torch.equal(outs[3], off_idx[t]), t
+        assert not cols[0][:, 0].any() and not cols[2][:, 0].any(), t
+        assert bool((cols[3][:, 0] == -7).all()) and bool((cols[4][:, 0] == -7).all()), t
 
 
 def test_engine_rejects_host_tensors():
