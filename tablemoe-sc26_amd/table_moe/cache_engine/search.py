@@ -130,29 +130,35 @@ class VectorSearchEngine:
         """q = dtype(x @ P_m + bias_m) (+ L2 normalisation) into ``query_low``
         (reference search.py:476-498)."""
         dev = N.require_hip(hidden_states, query_low)
-        dtype = self.manager.keys_buffer.dtype
-        if hidden_states.dtype != dtype:
-            raise RuntimeError(f"hidden_states dtype {hidden_states.dtype} != table dtype {dtype}")
         x = hidden_states if hidden_states.stride(-1) == 1 else hidden_states.contiguous()
         n, hidden = x.shape
+        self._project_call(dev, x, n, hidden, x.stride(0), is_vision_mask, search_dims, query_low,
+                           query_low.stride(0), normalize)
+        return query_low
+
+    def _project_call(self, dev, x, n, hidden, ld_x, is_vision_mask, search_dims, query_low, ld_q, normalize):
+        """tm_project on plain pointers and row strides (the bs1 path passes its
+        1-D row without a 2-D view)."""
+        dtype = self.manager.keys_buffer.dtype
+        if x.dtype != dtype:
+            raise RuntimeError(f"hidden_states dtype {x.dtype} != table dtype {dtype}")
         pv, pt = search_dims["pca_vis"], search_dims["pca_txt"]
         tv, tt = search_dims["proj_t"]
         isv = N.mask_bytes(is_vision_mask, dev)
         d = search_dims["compressed_dim"]
         pk = search_dims["proj_pk"]
-        if pk is not None and x.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0 and query_low.data_ptr() % 16 == 0 \
-                and query_low.stride(0) % 8 == 0:
+        x_ptr, q_ptr = x.data_ptr(), query_low.data_ptr()
+        if pk is not None and x_ptr % 16 == 0 and ld_x % 8 == 0 and q_ptr % 16 == 0 and ld_q % 8 == 0:
             (tv, tt), ps_h, ps_d, ws = pk, 0, 0, None  # packed layout, no workspace
         else:
             ps_h, ps_d = 1, hidden
             ws = self._scratch("project", N.lib().tm_project_workspace_size(n, hidden, d))
         N.call(
-            "tm_project", N.dtype_tag(dtype), N.ptr(x), n, hidden, x.stride(0), N.ptr(isv),
+            "tm_project", N.dtype_tag(dtype), x_ptr, n, hidden, ld_x, isv.data_ptr(),
             N.ptr(tv), N.ptr(pv["bias"]), N.ptr(tt), N.ptr(pt["bias"]), ps_h, ps_d, d,
-            1 if normalize else 0, float(CacheConfig.OFFLINE_COSINE_EPS), N.ptr(query_low), query_low.stride(0),
+            1 if normalize else 0, float(CacheConfig.OFFLINE_COSINE_EPS), q_ptr, ld_q,
             None, N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(dev),
         )
-        return query_low
 
     def _scratch(self, name, nbytes):
         """Reusable device workspace of at least ``nbytes`` (None for 0)."""
@@ -183,19 +189,27 @@ class VectorSearchEngine:
         dev = N.require_hip(query_low, keys, selected_experts, out_hit, out_idx)
         n, top_k = selected_experts.shape
         sel = selected_experts if selected_experts.dtype == torch.long else selected_experts.long()
-        isv = N.mask_bytes(is_vision_mask, dev)
         rs = None if reuse_mask is None else N.as_u8(reuse_mask.to(device=dev, dtype=torch.bool))
+        self._gated_call(dev, query_low, n, query_low.stride(0), keys, sel, top_k, sel.stride(0), sel.stride(1),
+                         is_vision_mask, rs, 0 if rs is None else rs.stride(0), 0 if rs is None else rs.stride(1),
+                         out_hit, out_idx, out_hit.stride(0), out_hit.stride(1), thr_vision, thr_text, cmp,
+                         col_offset)
+
+    def _gated_call(self, dev, query_low, n, ld_q, keys, sel, top_k, sel_s0, sel_s1, is_vision_mask, rs, rs_s0,
+                    rs_s1, out_hit, out_idx, out_s0, out_s1, thr_vision, thr_text, cmp, col_offset):
+        """tm_search_gated on plain pointers and strides (out_hit and out_idx
+        share the element strides out_s0/out_s1)."""
+        isv = N.mask_bytes(is_vision_mask, dev)
         if keys.stride(-1) != 1:
             raise ValueError("keys must have a unit stride along the PCA dimension")
         if out_hit.dtype not in _BYTE_MASKS:
             raise ValueError("out_hit must be a bool (or uint8) tensor")
         N.call(
-            "tm_search_gated", N.dtype_tag(keys.dtype), N.ptr(query_low), n, query_low.stride(0), N.ptr(keys),
+            "tm_search_gated", N.dtype_tag(keys.dtype), query_low.data_ptr(), n, ld_q, keys.data_ptr(),
             keys.shape[0], keys.shape[2], keys.shape[3], keys.stride(0), keys.stride(1), keys.stride(2),
-            N.ptr(sel), top_k, sel.stride(0), sel.stride(1), N.ptr(isv), N.ptr(rs),
-            0 if rs is None else rs.stride(0), 0 if rs is None else rs.stride(1), col_offset,
-            float(thr_vision), float(thr_text), cmp, out_hit.data_ptr(), N.ptr(out_idx),
-            out_hit.stride(0), out_hit.stride(1), N.stream(dev),
+            sel.data_ptr(), top_k, sel_s0, sel_s1, isv.data_ptr(), N.ptr(rs), rs_s0, rs_s1, col_offset,
+            float(thr_vision), float(thr_text), cmp, out_hit.data_ptr(), out_idx.data_ptr(), out_s0, out_s1,
+            N.stream(dev),
         )
 
     def _search_prefill_offline_into(self, query_low, selected_experts, is_vision_mask, reuse_mask,
@@ -343,13 +357,24 @@ class VectorSearchEngine:
         if top_k == 0:
             return
         keep_k = max(0, min(int(keep_k), top_k))
-        hidden = hidden_state.view(1, -1)
-        q = self._build_decode_queries(hidden, is_vision.view(1), self._get_search_dims())
+        # one token: the 1-D tensors go straight to the two calls (no 2-D views)
+        dev = N.require_hip(hidden_state, selected_experts_row, out_off_hit, out_off_idx)
+        x = hidden_state if hidden_state.stride(-1) == 1 else hidden_state.contiguous()
+        hidden = x.shape[-1]
+        if x.numel() != hidden:
+            raise ValueError(f"hidden_state must hold one token; got shape {tuple(hidden_state.shape)}")
+        dims = self._get_search_dims()
+        d = dims["compressed_dim"]
+        q = self.decode_query_workspace
+        if q is None or q.shape[1] != d or q.dtype != self.manager.keys_buffer.dtype:
+            q = self._ensure_decode_query_workspace(1, d)
+        self._project_call(dev, x, 1, hidden, hidden, is_vision, dims, q, q.stride(0), False)
+        sel = selected_experts_row if selected_experts_row.dtype == torch.long else selected_experts_row.long()
+        s1, o1 = sel.stride(0), out_off_hit.stride(0)
         thr = float(CacheConfig.OFFLINE_DOT_THRESHOLD)
-        self._gated_into(
-            q, self.manager.raw_keys_buffer, selected_experts_row.view(1, top_k), is_vision.view(1), None,
-            out_off_hit.view(1, top_k), out_off_idx.view(1, top_k), thr, thr, N.TM_CMP_GT, col_offset=keep_k,
-        )
+        self._gated_call(dev, q, 1, q.stride(0), self.manager.raw_keys_buffer, sel, top_k, top_k * s1, s1,
+                         is_vision, None, 0, 0, out_off_hit, out_off_idx, top_k * o1, o1, thr, thr, N.TM_CMP_GT,
+                         keep_k)
 
     def search_decode_hybrid_bs1_into(self, hidden_state, selected_experts_row, is_vision, keep_k, out_on_hit,
                                       out_on_idx, out_off_hit, out_off_idx, out_on_slot):
